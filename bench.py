@@ -1,0 +1,256 @@
+"""Verify-step benchmark of the MI355X speculative verify path.
+
+Workload (the north-star metric): one session, K=4
+draft tokens (M = 5 verify rows) through the 36-layer INT4-g32 slow-AR
+backbone against a bf16 KV cache of 2048 tokens, the INT4 lm head
+2560 -> 155,776, then device acceptance sampling (T 0.8, top-p 0.8) of the 4
+drafted tokens against draft logits = target logits + N(0, 0.5).  Random-init
+weights, synthetic inputs resident in HBM before the timed region.  A step is
+one replay of the captured hipGraph (forward + acceptance).
+
+Prints one JSON line (see README of the driver contract): value = verify
+steps/s, plus `roofline` for the dominant kernel (the INT4 GEMV engine) timed
+with HIP events on its own stream, and `cpu_baseline` (the scalar C oracle on
+one host core over a bounded sample: one backbone layer + the head GEMV,
+extrapolated to 36 layers).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "s2pro-native_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "verify steps/s (36L INT4, K=4, b=1) + achieved HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+N_LAYERS, CTX, K = 36, 2048, 4
+# algorithmic bytes of one config-3 step (weights + KV + activations + logits)
+W_LAYER = [(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)]
+
+
+def int4_bytes(N, Kd):
+    return N * Kd // 2 + 2 * N * Kd // 32
+
+
+def step_alg_bytes():
+    w = N_LAYERS * sum(int4_bytes(n, k) for n, k in W_LAYER) + int4_bytes(155776, 2560)
+    kv = N_LAYERS * 2 * 8 * 128 * 2 * CTX
+    act = 17_879_040 + 1_557_760
+    return w, kv, w + kv + act
+
+
+def cpu_baseline(budget_s=20.0):
+    """Scalar C oracle (one core): one layer (4 GEMVs in the reference lane
+    order, norms, RoPE, attention over 2048 slots, SwiGLU) plus the head GEMV,
+    extrapolated as 36 x layer + head."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    r = np.random.default_rng(0)
+    M = K + 1
+    lins, keep = [], []
+    for n, k in W_LAYER:
+        w = r.integers(0, 256, (n, k // 2), dtype=np.uint8)
+        s = np.abs(r.standard_normal((n, k // 32)) * 0.02).astype(np.float16).view(np.uint16)
+        keep.append((w, s))
+        lins.append(po.make_linear(w, s, n, k, 32))
+    norms = [po.f32_to_bf16(np.ones(d, np.float32)) for d in (2560, 2560, 128, 128)]
+    lw = po.OrLayerW(*lins, *(po.ptr(x) for x in norms))
+    kc = po.f32_to_bf16(r.standard_normal((8, CTX + M, 128)).astype(np.float32))
+    vc = po.f32_to_bf16(r.standard_normal((8, CTX + M, 128)).astype(np.float32))
+    x = po.f32_to_bf16(r.standard_normal((M, 2560)).astype(np.float32))
+    pos = np.arange(CTX, CTX + M, dtype=np.int32)
+    t0 = time.perf_counter()
+    po.layer(lw, x, M, kc, vc, CTX + M, CTX, pos)
+    t_layer = time.perf_counter() - t0
+    hw = r.integers(0, 256, (155776 // 8, 1280), dtype=np.uint8)  # 1/8 of the head rows
+    hs = np.abs(r.standard_normal((155776 // 8, 80)) * 0.02).astype(np.float16).view(np.uint16)
+    t0 = time.perf_counter()
+    po.int4p_gemv(x, hw, hs, M, 155776 // 8, 2560)
+    t_head = (time.perf_counter() - t0) * 8
+    step = N_LAYERS * t_layer + t_head
+    return {"value": round(1.0 / step, 6), "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"1 of 36 layers ({t_layer:.2f} s) + 1/8 of the head GEMV, scalar C "
+                      f"oracle at -O2, extrapolated to 36 layers + full head "
+                      f"({step:.1f} s per step)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one MI355X; --gpus must be 1 "
+                          "(sessions shard across GPUs with no collectives, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+    import s2pamd
+    lib = s2pamd.load()
+    dev = torch.device("cuda:0")
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        S = s2pamd.stream_ptr()
+        opts = s2pamd.BackboneOpts(N_LAYERS, s2pamd.WQ_INT4, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB,
+                                   16, 1, CTX + 64)
+        bb = ctypes.c_void_p()
+        s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(opts), 2026, S, ctypes.byref(bb)))
+        kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0, 5, S))
+        parent = np.array([-1, 0, 1, 2, 3], np.int32)
+        R = K + 1
+        kvp = (ctypes.c_void_p * 1)(kv.data_ptr())
+        ln = np.array([CTX], np.int32)
+        vb = s2pamd.VerifyBatch(1, R, parent.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
+        s2pamd.check(lib.s2p_verify_plan(bb, ctypes.byref(vb), S))
+        x = torch.empty((R, 2560), dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(x), x.numel(), 0.0, 1.0, 9, S))
+        logits = torch.empty((R, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
+        s2pamd.check(lib.s2p_verify_forward(bb, s2pamd.dptr(x), s2pamd.dptr(logits), S))
+        # draft logits: target + N(0, 0.5); drafted ids by the device sampler
+        noise = torch.empty_like(logits)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(noise), noise.numel(), 0.0, 0.5,
+                                                   13, S))
+        drf = (logits.view(torch.bfloat16).float() + noise.view(torch.bfloat16).float()).to(
+            torch.bfloat16).view(torch.int16)
+        st = StateBytes.make(0.8, 0.8, 1.1, 16, seed=0, entropy=0)
+        d_state = torch.from_numpy(np.frombuffer(bytes(st), np.uint8).copy()).to(dev)
+        d_sptr = torch.tensor([d_state.data_ptr()], dtype=torch.int64, device=dev)
+        d_draft_state = d_state.clone()
+        d_dptr = torch.tensor([d_draft_state.data_ptr()], dtype=torch.int64, device=dev)
+        tok = torch.zeros(R, dtype=torch.int64, device=dev)
+        sem = torch.zeros(1, dtype=torch.int32, device=dev)
+        eos = torch.zeros(1, dtype=torch.uint8, device=dev)
+        for i in range(K):
+            s2pamd.hip_check(lib.s2pk_sample(s2pamd.dptr(drf[i]), s2pamd.S2P_VOCAB, None,
+                                             s2pamd.dptr(d_dptr), 1,
+                                             ctypes.c_void_p(tok.data_ptr() + 8 * (i + 1)),
+                                             s2pamd.dptr(sem), None, s2pamd.dptr(eos), S))
+        d_parent = torch.from_numpy(parent).to(dev)
+        work = torch.empty(lib.s2p_verify_accept_work_bytes(1, R), dtype=torch.uint8, device=dev)
+        path = torch.zeros(R, dtype=torch.int32, device=dev)
+        nacc = torch.zeros(1, dtype=torch.int32, device=dev)
+        emit = torch.zeros(R + 1, dtype=torch.int64, device=dev)
+        nemit = torch.zeros(1, dtype=torch.int32, device=dev)
+        io = s2pamd.StepIO(x.data_ptr(), logits.data_ptr(), drf.data_ptr(), s2pamd.S2P_VOCAB,
+                           d_parent.data_ptr(), tok.data_ptr(), d_sptr.data_ptr(), path.data_ptr(),
+                           nacc.data_ptr(), emit.data_ptr(), nemit.data_ptr(), work.data_ptr())
+
+        def step():
+            s2pamd.check(lib.s2p_verify_step(bb, ctypes.byref(io), 1, S), "verify step")
+
+        for _ in range(args.warmup):
+            step()
+        side.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        e1.record(side)
+        side.synchronize()
+        wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1) / args.steps
+
+        # dominant kernel: the GEMV engine, every weight GEMV of one step
+        # (36 x {wqkv, wo, gate_up, w2} + head at M = 5), launched eagerly on
+        # this stream and bracketed by HIP events
+        lins = []
+        for l in range(N_LAYERS):
+            L = lib.s2p_backbone_layer(bb, l).contents
+            lins += [L.wqkv, L.wo, L.gate_up, L.w2]
+        lins.append(lib.s2p_backbone_head(bb).contents)
+        ybuf = torch.empty((R, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
+        xbuf = torch.empty((R, 9728), dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(xbuf), xbuf.numel(), 0.0, 1.0, 3, S))
+
+        def gemvs():
+            for lin in lins:
+                s2pamd.check(lib.s2p_linear_forward(ctypes.byref(lin), s2pamd.dptr(xbuf),
+                                                    s2pamd.dptr(ybuf), R, 2, S), "gemv")
+        gemvs()
+        reps = 5
+        side.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record(side)
+        for _ in range(reps):
+            gemvs()
+        g1.record(side)
+        side.synchronize()
+        n_launch = reps * len(lins)
+        avg_launch_s = g0.elapsed_time(g1) / 1e3 / n_launch
+        wbytes = sum(lin.w_pack.bytes + lin.w_iscale.bytes for lin in lins)
+        abytes = sum(2 * R * (lin.in_features + lin.out_features) for lin in lins)
+        per_launch = (wbytes + abytes) / len(lins)
+        gemv_gbs = per_launch / avg_launch_s / 1e9
+        lib.s2p_backbone_free(bb)
+
+    w, kvb, alg = step_alg_bytes()
+    step_gbs = alg / (ms / 1e3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(1e3 / ms, 3),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init INT4-g32 weights, N(0,1) KV cache and inputs)",
+        "config": {"workload": "config3: 36L INT4-g32 backbone + INT4 head 2560->155776, "
+                               "K=4 chain (M=5), b=1, bf16 KV 2048, device acceptance T0.8 p0.8",
+                   "global_batch": 1, "seq_len": CTX, "parallelism": "single GPU"},
+        "step_alg_bytes": alg,
+        "step_hbm_gbs": round(step_gbs, 1),
+        "step_frac_of_peak": round(step_gbs / PEAK_GBS, 4),
+        "wall_s_timed": round(wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv_mfma<INT4, MT=1> (all 145 weight GEMVs of a step)",
+                     "avg_launch_us": round(avg_launch_s * 1e6, 3),
+                     "alg_bytes_per_launch": int(per_launch)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+class StateBytes(ctypes.Structure):
+    """s2ps_dev_state byte layout (include/s2pro/slowar_kernels.h)."""
+    _fields_ = [("prev", ctypes.c_int64 * 64), ("count", ctypes.c_uint64),
+                ("rng", ctypes.c_uint64 * 4), ("temperature", ctypes.c_float),
+                ("top_p", ctypes.c_float), ("rep_penalty", ctypes.c_float),
+                ("window", ctypes.c_int32), ("seeded", ctypes.c_int32),
+                ("seed31", ctypes.c_uint32), ("pad_", ctypes.c_uint32)]
+
+    @classmethod
+    def make(cls, temperature, top_p, rep_penalty, window, seed, entropy):
+        """Initial sampler state (reference sampling.c:95-112)."""
+        st = cls()
+        st.temperature, st.top_p, st.rep_penalty = temperature, top_p, rep_penalty
+        st.window = window
+        st.seeded = 1 if seed else 0
+        st.seed31 = seed & 0x7FFFFFFF
+        sm = (entropy ^ 0xD1B54A32D192ED03) & (2 ** 64 - 1)
+        for i in range(4):
+            sm = (sm + 0x9E3779B97F4A7C15) & (2 ** 64 - 1)
+            z = sm
+            z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & (2 ** 64 - 1)
+            z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & (2 ** 64 - 1)
+            st.rng[i] = z ^ (z >> 31)
+        return st
+
+
+if __name__ == "__main__":
+    main()

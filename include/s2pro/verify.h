@@ -1,0 +1,152 @@
+/* s2pro MI355X — speculative verify pass for the slow-AR backbone.
+ *
+ * New API (the reference designed but never built this stage:
+ * docs/SPECULATIVE.md:249-256).  It follows the reference contract
+ * conventions: s2p_status returns, device pointers, an explicit stream, no
+ * host synchronisation or allocation inside the per-step calls, so a whole
+ * verify step can be captured in one hipGraph and replayed.
+ *
+ * A verify step takes n_sess sessions that share one draft shape of R rows:
+ * row 0 is the root (the last accepted token, whose K/V is not in the cache
+ * yet) and rows 1..R-1 are drafted nodes with parent[i] < i (a chain
+ * parent[i] = i-1 for K-token drafts, or a tree).  For session s with kv_len
+ * L tokens in its cache, node i is written to KV slot L + i, has RoPE
+ * position L + depth(i), and attends slots [0, L) plus the slots of its
+ * ancestors and itself.  This is the reference's decode contract extended to
+ * rows: s2pk_kv_append(rows=K+1, pos=L) + s2pk_attention(rows=K+1, pos=L)
+ * (kernels.cu:172-209, 250) for the chain.  After acceptance the cache holds
+ * the accepted path at L + 1 .. L + n (s2p_verify_kv_commit moves tree nodes
+ * there) and the session's kv_len advances by 1 + n_accepted: rejected slots
+ * are simply overwritten later (rollback by length, slowar.c:751).
+ */
+#ifndef S2P_VERIFY_H
+#define S2P_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#include "s2pro/gemm.h"
+#include "s2pro/slowar_kernels.h"
+#include "s2pro/status.h"
+#include "s2pro/tensor.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S2P_DIM 2560
+#define S2P_Q_HEADS 32
+#define S2P_KV_HEADS 8
+#define S2P_HEAD_DIM 128
+#define S2P_QKV_WIDTH 6144
+#define S2P_FFN_DIM 9728
+#define S2P_VOCAB 155776
+#define S2P_HEAD_SLICE 4097 /* 4096 semantic rows + EOS */
+#define S2P_VERIFY_MAX_ROWS 64 /* R per session (visibility masks are 64-bit) */
+
+/* One backbone layer (reference src/slowar/slowar_internal.h:72-81). */
+typedef struct {
+    s2p_linear wqkv;    /* [6144, 2560] fused q,k,v */
+    s2p_linear wo;      /* [2560, 4096] */
+    s2p_linear gate_up; /* [19456, 2560] = w1 rows then w3 rows */
+    s2p_linear w2;      /* [2560, 9728] */
+    s2p_tensor attn_norm, ffn_norm; /* [2560] bf16 */
+    s2p_tensor q_norm, k_norm;      /* [128] bf16 */
+} s2p_slow_layer;
+
+typedef enum { S2P_WQ_INT4_G32 = 0, S2P_WQ_INT8 = 1 } s2p_weight_q;
+
+typedef struct {
+    int          n_layers;      /* 36 for the S2-Pro backbone */
+    s2p_weight_q quant;         /* backbone linears */
+    s2p_weight_q head_quant;    /* lm head */
+    int          head_rows;     /* S2P_VOCAB (full head) or S2P_HEAD_SLICE */
+    int          max_rows;      /* rows per verify call: sessions x R (<= 128) */
+    int          max_sessions;
+    int          ctx_len;       /* per-session KV capacity (slots) */
+} s2p_backbone_opts;
+
+typedef struct s2p_backbone s2p_backbone;
+
+/* Random-init backbone (synthetic workloads): INT4-g32 weights uniform in
+ * [-8,7] with f16 group scales |N(0,0.02)|, or INT8 uniform in [-127,127]
+ * with f32 row scales |N(0,0.001)|; norm weights bf16 1 + N(0,0.02).
+ * Calls s2p_gemm_init.  Synchronises `st`. */
+s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t seed,
+                                      hipStream_t st, s2p_backbone** out);
+void       s2p_backbone_free(s2p_backbone* b);
+s2p_slow_layer* s2p_backbone_layer(s2p_backbone* b, int layer);
+s2p_linear*     s2p_backbone_head(s2p_backbone* b);
+void*           s2p_backbone_final_norm(s2p_backbone* b);
+/* bytes of one session's KV: [n_layers][2 * 8][ctx_len][128] bf16 */
+size_t          s2p_backbone_kv_bytes(const s2p_backbone* b);
+/* weight bytes streamed by one verify step (backbone + head) */
+size_t          s2p_backbone_weight_bytes(const s2p_backbone* b);
+
+typedef struct {
+    int            n_sess;
+    int            rows;     /* R */
+    const int32_t* parent;   /* host [R]; parent[0] = -1 */
+    void* const*   kv;       /* host [n_sess] device KV bases */
+    const int32_t* kv_len;   /* host [n_sess] */
+} s2p_verify_batch;
+
+/* Upload the per-row plan (positions, slots, visibility) and per-session KV
+ * bases.  Host -> device copy; call outside graph capture, before each step
+ * whose plan changed.  Fails with S2P_ERR_FULL if a session would overflow
+ * ctx_len. */
+s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStream_t st);
+
+/* Verify forward over the planned rows: x_in [n_sess*R, 2560] bf16 input
+ * embeddings (read only); logits [n_sess*R, head_rows] bf16.  Appends every
+ * row's K/V to its slot.  Asynchronous, capturable. */
+s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, hipStream_t st);
+
+/* Workspace of s2p_verify_accept. */
+size_t s2p_verify_accept_work_bytes(int n_sess, int rows);
+
+/* Acceptance (device).  tgt/drf rows follow s2pk_sample's layout (full vocab
+ * with eos == NULL, else 4096 semantic logits + eos[row]); draft row i holds
+ * the draft logits whose samples are node i's children; parent [R] and tok
+ * [n_sess*R] (drafted vocab ids, entry 0 of each session unused) and states
+ * [n_sess] are device arrays.  Writes the accepted node ids (out_path
+ * [n_sess*R]), their count, the emitted vocab ids (out_emit [n_sess*(R+1)]:
+ * accepted drafts then the corrected or bonus token) and their count, and
+ * advances each state.  Asynchronous, capturable. */
+s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const void* drf_logits,
+                             const void* drf_eos, int64_t row_stride, const int32_t* parent,
+                             const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
+                             int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
+                             int32_t* out_n_emit, void* work, hipStream_t st);
+
+/* Move the K/V of accepted tree nodes from slot L + node to L + depth for
+ * every layer (no-op for chains).  Uses the current plan. */
+s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,
+                                const int32_t* out_n_acc, hipStream_t st);
+
+/* One verify step (forward + acceptance) replayed from a hipGraph captured
+ * on first use for the current plan shape; falls back to eager launches
+ * when use_graph == 0. */
+typedef struct {
+    const void* x_in;
+    void* logits;                       /* target logits out */
+    const void* drf_logits;             /* draft rows, layout of the target logits */
+    int64_t drf_stride;                 /* == head rows */
+    const int32_t* parent_dev;
+    const int64_t* tok_dev;
+    s2ps_dev_state* const* states_dev;
+    int32_t* out_path;
+    int32_t* out_n_acc;
+    int64_t* out_emit;
+    int32_t* out_n_emit;
+    void* work;
+} s2p_verify_step_io;
+
+s2p_status s2p_verify_step(s2p_backbone* b, const s2p_verify_step_io* io, int use_graph,
+                           hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,62 @@
+/* s2pro MI355X — device helpers shared by the HIP kernels (gfx950 only). */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define S2P_DEV static __device__ __forceinline__
+
+typedef __attribute__((ext_vector_type(8))) __bf16 s2p_bf16x8;
+typedef __attribute__((ext_vector_type(4))) float s2p_f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t s2p_u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t s2p_u32x2;
+
+/* bf16 bit pattern -> float (exact) */
+S2P_DEV float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+S2P_DEV float bf2f_lo(uint32_t w) { return __uint_as_float(w << 16); }
+S2P_DEV float bf2f_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+/* float -> bf16 bit pattern, round to nearest even (NaN stays NaN) */
+S2P_DEV uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
+        return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+/* IEEE f16 bit pattern <-> float (hardware conversions, RNE) */
+S2P_DEV float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+S2P_DEV uint16_t f2h(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+/* 1/sqrt(v) as two correctly rounded operations: the rule's rsqrt value for
+ * every norm in this build (the reference calls the approximate rsqrtf). */
+S2P_DEV float rsqrt_rule(float v) { return 1.0f / __fsqrt_rn(v); }
+
+S2P_DEV s2p_bf16x8 as_bf16x8(s2p_u32x4 v) { return __builtin_bit_cast(s2p_bf16x8, v); }
+
+/* D = A(16x32) * B(32x16) + C, bf16 in, f32 accumulate (v_mfma_f32_16x16x32_bf16).
+ * Lane l supplies A row (l % 16) and B column (l % 16), 8 k-slots each from
+ * k-group (l / 16); D row 4*(l/16)+i, column l % 16 lands in C[i]. */
+S2P_DEV s2p_f32x4 mfma16x16x32(s2p_u32x4 a, s2p_u32x4 b, s2p_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+/* Wave-wide (64 lanes) reductions through cross-lane shuffles.  The sum
+ * follows the shuffle-down tree (offsets 32,16,...,1): lane 0 ends with
+ * ((x0+x32)+(x16+x48))+... */
+S2P_DEV float wave_sum_down(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    return v;
+}
+S2P_DEV float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}

@@ -1,0 +1,49 @@
+/* s2pro MI355X — internal launch descriptor of the GEMV engine (gemv.hip),
+ * shared by the C host code (gemm.c, verify.c).  Not part of the public ABI. */
+#ifndef S2P_GEMV_INTERNAL_H
+#define S2P_GEMV_INTERNAL_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEMV_MAX_M 128         /* rows per call (8 MFMA column tiles) */
+
+enum { GEMV_W_INT4 = 0, GEMV_W_INT8 = 1 };            /* weight formats */
+enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1, GEMV_X_SILU = 2 }; /* staging */
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1 };       /* epilogues */
+
+typedef struct {
+    const uint8_t*  w;       /* INT4: packed [N][K/2]; INT8: [N][K] */
+    const void*     s;       /* INT4: f16 [N][K/32]; INT8: f32 [N] */
+    const uint16_t* x;       /* bf16 activations, row stride ldx */
+    int             ldx;
+    uint16_t*       y;       /* bf16 output (or residual stream), stride ldy */
+    int             ldy;
+    int             M, N, K;
+    int             wfmt;
+    int             gps;     /* 32-k groups per split (multiple of 4) */
+    int             splits;  /* derived by the launcher */
+    int             xmode;
+    const uint16_t* norm_w;  /* NORM: bf16 [K] */
+    float           norm_eps;
+    const float*    ssq_in;  /* NORM: [ssq_in_blocks][GEMV_MAX_M] */
+    int             ssq_in_blocks;
+    int             epi;
+    float*          ssq_out; /* RESID: [ceil(N/64)][GEMV_MAX_M] (may be NULL) */
+    float*          part;    /* [splits][M][N] fp32 */
+    unsigned*       counters;/* [ceil(N/64)], zero between calls */
+} GemvArgs;
+
+hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
+hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,
+                                   const void* x, void* y, int M, int N, int K,
+                                   int gshift, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,458 @@
+/* s2pro MI355X — the speculative verify pass (C11 host side).
+ *
+ * Per backbone layer the forward issues (reference run_layer,
+ * src/slowar/slowar.c:156-260, with its elementwise ops fused):
+ *   1. GEMV wqkv    staging = RMSNorm(attn_norm) of the residual stream
+ *   2. qk-norm + RoPE + KV append of every row (one launch)
+ *   3. attention over each session's cache with the row visibility masks
+ *      (+ split combine)
+ *   4. GEMV wo      epilogue = residual add, sums of squares for the next norm
+ *   5. GEMV gate_up staging = RMSNorm(ffn_norm)
+ *   6. GEMV w2      staging = silu(gate) * up, epilogue = residual add
+ * then the final RMSNorm is fused into the head GEMV.  The plan (per-row
+ * positions, slots, visibility; per-session KV bases; attention segments)
+ * lives in device memory, so a captured graph replays for any plan of the
+ * same shape.
+ */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "s2pro/verify.h"
+#include "../gemv_internal.h"
+#include "../prims_internal.h"
+#include "../sample_internal.h"
+#include "../synth_internal.h"
+
+float* s2p_gemm_ctx_part(void);
+unsigned* s2p_gemm_ctx_counters(void);
+int s2p_gemv_pick_gps(int M, int N, int K);
+
+#define NORM_EPS 1e-6f
+#define ROPE_BASE 1000000.0f
+#define SPAN_BUCKET 512
+
+struct s2p_backbone {
+    s2p_backbone_opts o;
+    s2p_slow_layer* layers;
+    s2p_tensor final_norm;
+    s2p_linear head;
+    /* activations */
+    void* x;      /* [max_rows][2560] residual stream */
+    void* qkv;    /* [max_rows][6144] */
+    void* q;      /* [max_rows][4096] */
+    void* attn;   /* [max_rows][4096] */
+    void* gu;     /* [max_rows][19456] */
+    float* ssq;   /* [2][64][GEMV_MAX_M] per-block sums of squares */
+    float* attn_part;
+    int64_t attn_part_floats;
+    /* plan (device + pinned host staging) */
+    int32_t* d_pos;
+    int32_t* d_slot;
+    int32_t* d_sess;
+    uint64_t* d_vis;
+    void** d_kv;
+    S2pAttnSeg* d_segs;
+    void* h_stage;
+    size_t stage_bytes;
+    int planned, rows, n_sess, R, n_seg, max_span;
+    int seg_rows_max;
+    /* graph of one verify step */
+    hipGraphExec_t gexec;
+    int g_rows, g_nseg, g_span, g_valid;
+    s2p_verify_step_io g_io;
+};
+
+static s2p_status hip_ok(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        fprintf(stderr, "[s2pro] %s: %s\n", what, hipGetErrorString(e));
+        return S2P_ERR_CUDA;
+    }
+    return S2P_OK;
+}
+
+static uint64_t seed_of(uint64_t base, int layer, int which) {
+    uint64_t z = base ^ (0x9E3779B97F4A7C15ULL * (uint64_t)(layer * 16 + which + 1));
+    z = (z ^ (z >> 31)) * 0xBF58476D1CE4E5B9ULL;
+    return z ^ (z >> 29);
+}
+
+static s2p_status norm_weight(s2p_tensor* t, int n, uint64_t seed, hipStream_t st) {
+    int64_t shape[1] = {n};
+    S2P_TRY(s2p_tensor_device_alloc(t, S2P_DT_BF16, 1, shape));
+    return hip_ok(s2p_synth_bf16_normal(t->data, n, 1.0f, 0.02f, seed, st), "norm init");
+}
+
+static s2p_status rand_linear(s2p_linear* l, s2p_weight_q q, int in, int out, uint64_t seed,
+                              hipStream_t st) {
+    if (q == S2P_WQ_INT4_G32) return s2p_linear_init_random_int4(l, in, out, 32, 0.02f, seed, st);
+    return s2p_linear_init_random_int8(l, in, out, 0.001f, seed, st);
+}
+
+static s2p_status dalloc(void** p, size_t bytes) {
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        *p = NULL;
+        return S2P_ERR_OOM;
+    }
+    return S2P_OK;
+}
+
+s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t seed,
+                                      hipStream_t st, s2p_backbone** out) {
+    if (!opts || !out || opts->n_layers <= 0 || opts->max_rows <= 0 ||
+        opts->max_rows > GEMV_MAX_M || opts->max_sessions <= 0 || opts->ctx_len <= 0 ||
+        opts->head_rows <= 0)
+        return S2P_ERR_INVALID;
+    S2P_TRY(s2p_gemm_init(opts->max_rows));
+    s2p_backbone* b = (s2p_backbone*)calloc(1, sizeof(*b));
+    if (!b) return S2P_ERR_OOM;
+    b->o = *opts;
+    b->layers = (s2p_slow_layer*)calloc((size_t)opts->n_layers, sizeof(s2p_slow_layer));
+    s2p_status rc = b->layers ? S2P_OK : S2P_ERR_OOM;
+    for (int l = 0; l < opts->n_layers && rc == S2P_OK; l++) {
+        s2p_slow_layer* L = &b->layers[l];
+        rc = rand_linear(&L->wqkv, opts->quant, S2P_DIM, S2P_QKV_WIDTH, seed_of(seed, l, 0), st);
+        if (rc == S2P_OK)
+            rc = rand_linear(&L->wo, opts->quant, S2P_Q_HEADS * S2P_HEAD_DIM, S2P_DIM,
+                             seed_of(seed, l, 1), st);
+        if (rc == S2P_OK)
+            rc = rand_linear(&L->gate_up, opts->quant, S2P_DIM, 2 * S2P_FFN_DIM,
+                             seed_of(seed, l, 2), st);
+        if (rc == S2P_OK)
+            rc = rand_linear(&L->w2, opts->quant, S2P_FFN_DIM, S2P_DIM, seed_of(seed, l, 3), st);
+        if (rc == S2P_OK) rc = norm_weight(&L->attn_norm, S2P_DIM, seed_of(seed, l, 4), st);
+        if (rc == S2P_OK) rc = norm_weight(&L->ffn_norm, S2P_DIM, seed_of(seed, l, 5), st);
+        if (rc == S2P_OK) rc = norm_weight(&L->q_norm, S2P_HEAD_DIM, seed_of(seed, l, 6), st);
+        if (rc == S2P_OK) rc = norm_weight(&L->k_norm, S2P_HEAD_DIM, seed_of(seed, l, 7), st);
+    }
+    if (rc == S2P_OK) rc = norm_weight(&b->final_norm, S2P_DIM, seed_of(seed, 999, 0), st);
+    if (rc == S2P_OK)
+        rc = rand_linear(&b->head, opts->head_quant, S2P_DIM, opts->head_rows,
+                         seed_of(seed, 999, 1), st);
+    const size_t R = (size_t)opts->max_rows;
+    if (rc == S2P_OK) rc = dalloc(&b->x, R * S2P_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc(&b->qkv, R * S2P_QKV_WIDTH * 2);
+    if (rc == S2P_OK) rc = dalloc(&b->q, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc(&b->attn, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc(&b->gu, R * 2 * S2P_FFN_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * 64 * GEMV_MAX_M);
+    b->attn_part_floats = s2p_attn_plan_part_floats((int)R, opts->ctx_len);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->attn_part, sizeof(float) * b->attn_part_floats);
+    const int S = opts->max_sessions;
+    const int nseg_max = (int)R + S; /* segments of <= 8 rows per session */
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_pos, R * 4);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_slot, R * 4);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_sess, R * 4);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_vis, R * 8);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_kv, (size_t)S * sizeof(void*));
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_segs, (size_t)nseg_max * sizeof(S2pAttnSeg));
+    b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)S * sizeof(void*) +
+                     (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
+    if (rc == S2P_OK && hipHostMalloc(&b->h_stage, b->stage_bytes, 0) != hipSuccess) {
+        b->h_stage = NULL;
+        rc = S2P_ERR_OOM;
+    }
+    if (rc == S2P_OK) rc = hip_ok(hipStreamSynchronize(st), "backbone init sync");
+    if (rc != S2P_OK) {
+        s2p_backbone_free(b);
+        return rc;
+    }
+    *out = b;
+    return S2P_OK;
+}
+
+void s2p_backbone_free(s2p_backbone* b) {
+    if (!b) return;
+    (void)hipDeviceSynchronize();
+    if (b->g_valid) (void)hipGraphExecDestroy(b->gexec);
+    if (b->layers) {
+        for (int l = 0; l < b->o.n_layers; l++) {
+            s2p_slow_layer* L = &b->layers[l];
+            s2p_linear_free(&L->wqkv);
+            s2p_linear_free(&L->wo);
+            s2p_linear_free(&L->gate_up);
+            s2p_linear_free(&L->w2);
+            s2p_tensor_free(&L->attn_norm);
+            s2p_tensor_free(&L->ffn_norm);
+            s2p_tensor_free(&L->q_norm);
+            s2p_tensor_free(&L->k_norm);
+        }
+        free(b->layers);
+    }
+    s2p_tensor_free(&b->final_norm);
+    s2p_linear_free(&b->head);
+    void* bufs[] = {b->x, b->qkv, b->q, b->attn, b->gu, b->ssq, b->attn_part, b->d_pos,
+                    b->d_slot, b->d_sess, b->d_vis, (void*)b->d_kv, (void*)b->d_segs};
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+        if (bufs[i]) (void)hipFree(bufs[i]);
+    if (b->h_stage) (void)hipHostFree(b->h_stage);
+    free(b);
+}
+
+s2p_slow_layer* s2p_backbone_layer(s2p_backbone* b, int layer) {
+    if (!b || layer < 0 || layer >= b->o.n_layers) return NULL;
+    return &b->layers[layer];
+}
+s2p_linear* s2p_backbone_head(s2p_backbone* b) { return b ? &b->head : NULL; }
+void* s2p_backbone_final_norm(s2p_backbone* b) { return b ? b->final_norm.data : NULL; }
+
+size_t s2p_backbone_kv_bytes(const s2p_backbone* b) {
+    return (size_t)b->o.n_layers * 2 * S2P_KV_HEADS * (size_t)b->o.ctx_len * S2P_HEAD_DIM * 2;
+}
+
+static size_t lin_bytes(const s2p_linear* l) {
+    return l->w_pack.bytes + l->w_int8.bytes + l->w_iscale.bytes;
+}
+
+size_t s2p_backbone_weight_bytes(const s2p_backbone* b) {
+    size_t t = lin_bytes(&b->head);
+    for (int l = 0; l < b->o.n_layers; l++) {
+        const s2p_slow_layer* L = &b->layers[l];
+        t += lin_bytes(&L->wqkv) + lin_bytes(&L->wo) + lin_bytes(&L->gate_up) + lin_bytes(&L->w2);
+    }
+    return t;
+}
+
+/* ------------------------------------------------------------------ plan */
+
+s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStream_t st) {
+    if (!b || !vb || vb->n_sess <= 0 || vb->rows <= 0 || vb->rows > S2P_VERIFY_MAX_ROWS ||
+        !vb->parent || !vb->kv || !vb->kv_len)
+        return S2P_ERR_INVALID;
+    const int n = vb->n_sess, R = vb->rows, rows = n * R;
+    if (n > b->o.max_sessions || rows > b->o.max_rows) return S2P_ERR_INVALID;
+    if (vb->parent[0] != -1) return S2P_ERR_INVALID;
+    int depth[S2P_VERIFY_MAX_ROWS];
+    uint64_t anc[S2P_VERIFY_MAX_ROWS];
+    depth[0] = 0;
+    anc[0] = 1ull;
+    for (int i = 1; i < R; i++) {
+        const int p = vb->parent[i];
+        if (p < 0 || p >= i) return S2P_ERR_INVALID;
+        depth[i] = depth[p] + 1;
+        anc[i] = anc[p] | (1ull << i);
+    }
+    unsigned char* h = (unsigned char*)b->h_stage;
+    int32_t* pos = (int32_t*)h;
+    int32_t* slot = pos + rows;
+    int32_t* sess = slot + rows;
+    uint64_t* vis = (uint64_t*)(((uintptr_t)(sess + rows) + 7) & ~(uintptr_t)7);
+    void** kv = (void**)(vis + rows);
+    S2pAttnSeg* segs = (S2pAttnSeg*)(kv + n);
+    int nseg = 0, max_span = 0;
+    for (int s = 0; s < n; s++) {
+        const int L = vb->kv_len[s];
+        if (L < 0 || !vb->kv[s]) return S2P_ERR_INVALID;
+        if (L + R > b->o.ctx_len) return S2P_ERR_FULL;
+        kv[s] = vb->kv[s];
+        for (int i = 0; i < R; i++) {
+            const int r = s * R + i;
+            pos[r] = L + depth[i];
+            slot[r] = L + i;
+            sess[r] = s;
+            vis[r] = anc[i];
+        }
+        for (int r0 = 0; r0 < R; r0 += 8) {
+            S2pAttnSeg* g = &segs[nseg++];
+            g->sess = s;
+            g->L = L;
+            g->row0 = s * R + r0;
+            g->nrows = R - r0 < 8 ? R - r0 : 8;
+            g->span = L + R;
+            g->pad_ = 0;
+        }
+        if (L + R > max_span) max_span = L + R;
+    }
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_pos, pos, (size_t)rows * 4, hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_slot, slot, (size_t)rows * 4, hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_sess, sess, (size_t)rows * 4, hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_vis, vis, (size_t)rows * 8, hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_kv, kv, (size_t)n * sizeof(void*), hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_segs, segs, (size_t)nseg * sizeof(S2pAttnSeg),
+                                  hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipStreamSynchronize(st), "plan sync"));
+    b->planned = 1;
+    b->rows = rows;
+    b->n_sess = n;
+    b->R = R;
+    b->n_seg = nseg;
+    /* bucketed so that a graph captured for one span serves nearby spans */
+    b->max_span = ((max_span + SPAN_BUCKET - 1) / SPAN_BUCKET) * SPAN_BUCKET;
+    if (b->max_span > b->o.ctx_len) b->max_span = b->o.ctx_len;
+    return S2P_OK;
+}
+
+static S2pRowPlan row_plan(const s2p_backbone* b) {
+    S2pRowPlan p;
+    p.pos = b->d_pos;
+    p.slot = b->d_slot;
+    p.sess = b->d_sess;
+    p.vis = b->d_vis;
+    p.kv = b->d_kv;
+    p.layer_stride = (int64_t)2 * S2P_KV_HEADS * b->o.ctx_len * S2P_HEAD_DIM;
+    p.max_seq = b->o.ctx_len;
+    return p;
+}
+
+/* --------------------------------------------------------------- forward */
+
+static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, void* y, int ldy,
+                       int xmode, const void* norm_w, const float* ssq_in, int epi, float* ssq_out,
+                       hipStream_t st) {
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wfmt = lin->q_packed ? GEMV_W_INT4 : GEMV_W_INT8;
+    a.w = (const uint8_t*)(lin->q_packed ? lin->w_pack.data : lin->w_int8.data);
+    a.s = lin->w_iscale.data;
+    a.x = (const uint16_t*)x;
+    a.ldx = ldx;
+    a.y = (uint16_t*)y;
+    a.ldy = ldy;
+    a.M = M;
+    a.N = lin->out_features;
+    a.K = lin->in_features;
+    a.gps = s2p_gemv_pick_gps(M, a.N, a.K);
+    a.xmode = xmode;
+    a.norm_w = (const uint16_t*)norm_w;
+    a.norm_eps = NORM_EPS;
+    a.ssq_in = ssq_in;
+    a.ssq_in_blocks = S2P_DIM / 64;
+    a.epi = epi;
+    a.ssq_out = ssq_out;
+    a.part = s2p_gemm_ctx_part();
+    a.counters = s2p_gemm_ctx_counters();
+    return hip_ok(s2p_gemv_launch(&a, st), "verify gemv");
+}
+
+s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, hipStream_t st) {
+    if (!b || !x_in || !logits) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    const int M = b->rows;
+    const S2pRowPlan plan = row_plan(b);
+    float* ssq_a = b->ssq;
+    float* ssq_b = b->ssq + 64 * GEMV_MAX_M;
+    S2P_TRY(hip_ok(s2p_resid_init_launch(x_in, b->x, ssq_a, M, S2P_DIM, st), "resid init"));
+    for (int l = 0; l < b->o.n_layers; l++) {
+        const s2p_slow_layer* L = &b->layers[l];
+        S2P_TRY(gemv(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
+                     L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st));
+        S2P_TRY(hip_ok(s2p_qkrope_append_launch(b->qkv, b->q, L->q_norm.data, L->k_norm.data, &plan,
+                                                M, l, NORM_EPS, ROPE_BASE, st), "qkrope"));
+        S2P_TRY(hip_ok(s2p_attn_plan_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
+                                            b->max_span, b->attn_part, st), "attention"));
+        S2P_TRY(gemv(&L->wo, M, b->attn, S2P_Q_HEADS * S2P_HEAD_DIM, b->x, S2P_DIM, GEMV_X_PLAIN,
+                     NULL, NULL, GEMV_EPI_RESID, ssq_b, st));
+        S2P_TRY(gemv(&L->gate_up, M, b->x, S2P_DIM, b->gu, 2 * S2P_FFN_DIM, GEMV_X_NORM,
+                     L->ffn_norm.data, ssq_b, GEMV_EPI_STORE, NULL, st));
+        S2P_TRY(gemv(&L->w2, M, b->gu, 2 * S2P_FFN_DIM, b->x, S2P_DIM, GEMV_X_SILU, NULL, NULL,
+                     GEMV_EPI_RESID, ssq_a, st));
+    }
+    return gemv(&b->head, M, b->x, S2P_DIM, logits, b->head.out_features, GEMV_X_NORM,
+                b->final_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st);
+}
+
+/* ------------------------------------------------------------ acceptance */
+
+size_t s2p_verify_accept_work_bytes(int n_sess, int rows) {
+    return s2p_accept_work_bytes(n_sess, rows);
+}
+
+static s2p_status accept_run(const void* tgt, const void* tgt_eos, int64_t tgt_eos_stride,
+                             int64_t tgt_stride, const void* drf, const void* drf_eos,
+                             int64_t drf_eos_stride, int64_t drf_stride, const int32_t* parent,
+                             const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
+                             int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
+                             int32_t* out_n_emit, void* work, hipStream_t st) {
+    if (tgt_stride != drf_stride) return S2P_ERR_INVALID;
+    AcceptArgs a;
+    memset(&a, 0, sizeof(a));
+    a.tgt = (const uint16_t*)tgt;
+    a.tgt_eos = (const uint16_t*)tgt_eos;
+    a.drf = (const uint16_t*)drf;
+    a.drf_eos = (const uint16_t*)drf_eos;
+    a.row_stride = tgt_stride;
+    a.tgt_eos_stride = tgt_eos_stride;
+    a.drf_eos_stride = drf_eos_stride;
+    a.parent = parent;
+    a.tok = tok;
+    a.states = states;
+    a.n_sess = n_sess;
+    a.R = rows;
+    a.out_path = out_path;
+    a.out_n_acc = out_n_acc;
+    a.out_emit = out_emit;
+    a.out_n_emit = out_n_emit;
+    a.work = work;
+    return hip_ok(s2p_accept_launch(&a, st), "accept");
+}
+
+s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const void* drf_logits,
+                             const void* drf_eos, int64_t row_stride, const int32_t* parent,
+                             const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
+                             int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
+                             int32_t* out_n_emit, void* work, hipStream_t st) {
+    if (!tgt_logits || !drf_logits || !parent || !tok || !states || !out_path || !out_n_acc ||
+        !out_emit || !out_n_emit || !work || n_sess <= 0 || rows <= 0 ||
+        rows > S2P_VERIFY_MAX_ROWS || (!tgt_eos) != (!drf_eos))
+        return S2P_ERR_INVALID;
+    if (!tgt_eos && row_stride < 155774) return S2P_ERR_INVALID;
+    if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
+    return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
+                      parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
+                      work, st);
+}
+
+s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,
+                                const int32_t* out_n_acc, hipStream_t st) {
+    if (!b || !out_path || !out_n_acc) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    const S2pRowPlan plan = row_plan(b);
+    return hip_ok(s2p_kv_commit_launch(&plan, out_path, out_n_acc, b->n_sess, b->R,
+                                       b->o.n_layers, st), "kv commit");
+}
+
+/* ------------------------------------------------------------------ step */
+
+static s2p_status step_enqueue(s2p_backbone* b, const s2p_verify_step_io* io, hipStream_t st) {
+    S2P_TRY(s2p_verify_forward(b, io->x_in, io->logits, st));
+    const int sliced = b->head.out_features == S2P_HEAD_SLICE;
+    const uint16_t* lg = (const uint16_t*)io->logits;
+    const int64_t ts = b->head.out_features;
+    const uint16_t* dg = (const uint16_t*)io->drf_logits;
+    return accept_run(lg, sliced ? lg + 4096 : NULL, ts, ts, dg, sliced ? dg + 4096 : NULL, ts,
+                      io->drf_stride, io->parent_dev, io->tok_dev,
+                      io->states_dev, b->n_sess, b->R, io->out_path, io->out_n_acc,
+                      io->out_emit, io->out_n_emit, io->work, st);
+}
+
+s2p_status s2p_verify_step(s2p_backbone* b, const s2p_verify_step_io* io, int use_graph,
+                           hipStream_t st) {
+    if (!b || !io) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    if (io->drf_stride != b->head.out_features) return S2P_ERR_INVALID;
+    if (!use_graph) return step_enqueue(b, io, st);
+    const int same = b->g_valid && b->g_rows == b->rows && b->g_nseg == b->n_seg &&
+                     b->g_span == b->max_span && memcmp(&b->g_io, io, sizeof(*io)) == 0;
+    if (!same) {
+        if (b->g_valid) {
+            (void)hipGraphExecDestroy(b->gexec);
+            b->g_valid = 0;
+        }
+        hipGraph_t graph;
+        S2P_TRY(hip_ok(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture"));
+        s2p_status rc = step_enqueue(b, io, st);
+        hipError_t ce = hipStreamEndCapture(st, &graph);
+        if (rc != S2P_OK) return rc;
+        S2P_TRY(hip_ok(ce, "end capture"));
+        ce = hipGraphInstantiate(&b->gexec, graph, NULL, NULL, 0);
+        (void)hipGraphDestroy(graph);
+        S2P_TRY(hip_ok(ce, "graph instantiate"));
+        b->g_valid = 1;
+        b->g_rows = b->rows;
+        b->g_nseg = b->n_seg;
+        b->g_span = b->max_span;
+        b->g_io = *io;
+    }
+    return hip_ok(hipGraphLaunch(b->gexec, st), "graph launch");
+}

@@ -1,0 +1,408 @@
+/* s2pro MI355X — transformer primitives on the verify path.
+ *
+ * Contract launchers of the reference include/s2pro/kernels.h and
+ * src/slowar/slowar_kernels.h (rms_norm, qk_norm, rope, rope_pos, kv_append,
+ * kv_append_ptrs, qkv_split, silu_mul, add) plus the fused per-layer kernels
+ * the verify forward uses (qk-norm + RoPE + KV append in one launch, residual
+ * stream init).  Rounding points follow the reference (kernels.cu:4-17):
+ *  - RMSNorm / qk-norm: fp32 sum of squares with the reference's reduction
+ *    tree, inverse RMS = 1/sqrt(mean + eps) (two correctly rounded ops; the
+ *    reference's rsqrtf is approximate), y = bf16((x * inv) * w);
+ *  - RoPE: interleaved pairs, inv_freq = 1/powf(base, 2i/d), cos/sin of the
+ *    fp32 angle rounded through bf16, butterfly with one rounding per op;
+ *    pow/cos/sin are evaluated in binary64 and rounded once to float (the
+ *    correctly rounded value);
+ *  - silu: 1/(1+exp(-g)) with the rule's exp, two bf16 roundings;
+ *  - adds in fp32, one rounding.
+ */
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "common.h"
+#include "prims_internal.h"
+#include "s2pro/kernels.h"
+#include "s2pro/s2p_fmath.h"
+#include "s2pro/slowar_kernels.h"
+
+#define PR_THREADS 256
+#define PR_MAX_GRID 4096
+
+static inline int pr_blocks(int64_t total, int threads) {
+    int64_t b = (total + threads - 1) / threads;
+    if (b > PR_MAX_GRID) b = PR_MAX_GRID;
+    if (b < 1) b = 1;
+    return (int)b;
+}
+
+/* --------------------------------------------------------------- rms_norm */
+
+__global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w,
+                                                  uint16_t* __restrict__ y, int width,
+                                                  float eps) {
+    __shared__ float red[256];
+    const int row = blockIdx.x;
+    const size_t base = (size_t)row * width;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < width; i += 256) {
+        const float v = bf2f(x[base + i]);
+        s = fmaf(v, v, s);
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = 128; off > 0; off >>= 1) {
+        if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    const float inv = rsqrt_rule(red[0] / (float)width + eps);
+    for (int i = threadIdx.x; i < width; i += 256)
+        y[base + i] = f2bf(__fmul_rn(__fmul_rn(bf2f(x[base + i]), inv), bf2f(w[i])));
+}
+
+extern "C" hipError_t s2pk_rms_norm(const s2p_bf16* x, const s2p_bf16* w, s2p_bf16* y,
+                                    int rows, int width, float eps, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)w, (uint16_t*)y, width, eps);
+    return hipGetLastError();
+}
+
+/* ---------------------------------------------------------------- qk_norm */
+
+/* block = (row, head), 128 threads = one element each (head_dim <= 128) */
+__global__ __launch_bounds__(128) void k_qk_norm(uint16_t* __restrict__ qk,
+                                                 const uint16_t* __restrict__ w,
+                                                 int head_dim, float eps) {
+    __shared__ float red[128];
+    const size_t base = (size_t)blockIdx.x * head_dim;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < head_dim; i += 128) {
+        const float v = bf2f(qk[base + i]);
+        s = fmaf(v, v, s);
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = 64; off > 0; off >>= 1) {
+        if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    const float inv = rsqrt_rule(red[0] / (float)head_dim + eps);
+    for (int i = threadIdx.x; i < head_dim; i += 128)
+        qk[base + i] = f2bf(__fmul_rn(__fmul_rn(bf2f(qk[base + i]), inv), bf2f(w[i])));
+}
+
+extern "C" hipError_t s2pk_qk_norm(s2p_bf16* qk, const s2p_bf16* w, int rows, int heads,
+                                   int head_dim, float eps, hipStream_t st) {
+    if (rows <= 0 || w == NULL) return hipSuccess;
+    if (head_dim > 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_qk_norm, dim3(rows * heads), dim3(128), 0, st, (uint16_t*)qk,
+                       (const uint16_t*)w, head_dim, eps);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------- rope */
+
+/* cos/sin (bf16-rounded, as float) of pair i at position p */
+S2P_DEV void rope_cs(int p, int i, int head_dim, float base, float* c, float* s) {
+    const float ex = __fdiv_rn((float)(2 * i), (float)head_dim);
+    const float pw = (float)pow((double)base, (double)ex);
+    const float inv = __fdiv_rn(1.0f, pw);
+    const float ang = __fmul_rn((float)p, inv);
+    *c = bf2f(f2bf((float)cos((double)ang)));
+    *s = bf2f(f2bf((float)sin((double)ang)));
+}
+
+__global__ __launch_bounds__(256) void k_rope(uint16_t* __restrict__ x, int rows, int heads,
+                                              int head_dim, int pos0,
+                                              const int32_t* __restrict__ pos_arr,
+                                              float base) {
+    const int pairs = head_dim / 2;
+    const int64_t total = (int64_t)rows * heads * pairs;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int r = (int)(idx / ((int64_t)heads * pairs));
+        const int rem = (int)(idx % ((int64_t)heads * pairs));
+        const int h = rem / pairs, i = rem % pairs;
+        const int p = pos_arr ? pos_arr[r] : pos0 + r;
+        float c, s;
+        rope_cs(p, i, head_dim, base, &c, &s);
+        const size_t o = ((size_t)r * heads + h) * head_dim + 2 * i;
+        const float x0 = bf2f(x[o]), x1 = bf2f(x[o + 1]);
+        x[o] = f2bf(__fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s)));
+        x[o + 1] = f2bf(__fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s)));
+    }
+}
+
+static hipError_t rope_launch(s2p_bf16* q, s2p_bf16* k, int rows, int qh, int kvh, int hd,
+                              int pos0, const int32_t* pos, float base, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t tq = (int64_t)rows * qh * (hd / 2);
+    hipLaunchKernelGGL(k_rope, dim3(pr_blocks(tq, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (uint16_t*)q, rows, qh, hd, pos0, pos, base);
+    const int64_t tk = (int64_t)rows * kvh * (hd / 2);
+    hipLaunchKernelGGL(k_rope, dim3(pr_blocks(tk, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (uint16_t*)k, rows, kvh, hd, pos0, pos, base);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2pk_rope(s2p_bf16* q, s2p_bf16* k, int rows, int q_heads, int kv_heads,
+                                int head_dim, int pos, float rope_base, hipStream_t st) {
+    return rope_launch(q, k, rows, q_heads, kv_heads, head_dim, pos, NULL, rope_base, st);
+}
+
+extern "C" hipError_t s2pk_rope_pos(s2p_bf16* q, s2p_bf16* k, int rows, int q_heads,
+                                    int kv_heads, int head_dim, const int32_t* pos,
+                                    float rope_base, hipStream_t st) {
+    return rope_launch(q, k, rows, q_heads, kv_heads, head_dim, 0, pos, rope_base, st);
+}
+
+/* -------------------------------------------------------------- kv append */
+
+__global__ __launch_bounds__(256) void k_kv_append(const uint16_t* __restrict__ k,
+                                                   const uint16_t* __restrict__ v,
+                                                   uint16_t* kc0, uint16_t* vc0,
+                                                   uint16_t* const* kcs, uint16_t* const* vcs,
+                                                   int rows, int kv_heads, int head_dim,
+                                                   int pos0, const int32_t* pos_arr,
+                                                   int max_seq) {
+    /* one thread per 8 elements (16 bytes) */
+    const int per_row = kv_heads * head_dim / 8;
+    const int64_t total = (int64_t)rows * per_row;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int r = (int)(idx / per_row);
+        const int e = (int)(idx % per_row) * 8;
+        const int h = e / head_dim, d = e % head_dim;
+        const int p = pos_arr ? pos_arr[r] : pos0 + r;
+        uint16_t* kc = kcs ? kcs[r] : kc0;
+        uint16_t* vc = vcs ? vcs[r] : vc0;
+        const size_t src = (size_t)r * kv_heads * head_dim + e;
+        const size_t dst = ((size_t)h * max_seq + p) * head_dim + d;
+        *(s2p_u32x4*)(kc + dst) = *(const s2p_u32x4*)(k + src);
+        *(s2p_u32x4*)(vc + dst) = *(const s2p_u32x4*)(v + src);
+    }
+}
+
+extern "C" hipError_t s2pk_kv_append(const s2p_bf16* k, const s2p_bf16* v, s2p_bf16* k_cache,
+                                     s2p_bf16* v_cache, int rows, int kv_heads, int head_dim,
+                                     int pos, int max_seq, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim % 8) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)rows * kv_heads * head_dim / 8;
+    hipLaunchKernelGGL(k_kv_append, dim3(pr_blocks(total, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)k_cache,
+                       (uint16_t*)v_cache, (uint16_t* const*)NULL, (uint16_t* const*)NULL, rows,
+                       kv_heads, head_dim, pos, (const int32_t*)NULL, max_seq);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2pk_kv_append_ptrs(const s2p_bf16* k, const s2p_bf16* v,
+                                          s2p_bf16* const* k_caches, s2p_bf16* const* v_caches,
+                                          int rows, int kv_heads, int head_dim,
+                                          const int32_t* pos, int max_seq, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim % 8) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)rows * kv_heads * head_dim / 8;
+    hipLaunchKernelGGL(k_kv_append, dim3(pr_blocks(total, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)NULL, (uint16_t*)NULL,
+                       (uint16_t* const*)k_caches, (uint16_t* const*)v_caches, rows, kv_heads,
+                       head_dim, 0, pos, max_seq);
+    return hipGetLastError();
+}
+
+/* -------------------------------------------------------------- qkv split */
+
+__global__ __launch_bounds__(256) void k_qkv_split(const uint16_t* __restrict__ qkv,
+                                                   uint16_t* __restrict__ q,
+                                                   uint16_t* __restrict__ k,
+                                                   uint16_t* __restrict__ v, int64_t total,
+                                                   int qw, int kvw) {
+    const int w = qw + 2 * kvw;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = idx / w;
+        const int c = (int)(idx % w);
+        const uint16_t val = qkv[idx];
+        if (c < qw) q[r * qw + c] = val;
+        else if (c < qw + kvw) k[r * kvw + (c - qw)] = val;
+        else v[r * kvw + (c - qw - kvw)] = val;
+    }
+}
+
+extern "C" hipError_t s2pk_qkv_split(const s2p_bf16* qkv, s2p_bf16* q, s2p_bf16* k,
+                                     s2p_bf16* v, int rows, int q_width, int kv_width,
+                                     hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t total = (int64_t)rows * (q_width + 2 * kv_width);
+    hipLaunchKernelGGL(k_qkv_split, dim3(pr_blocks(total, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (const uint16_t*)qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, total,
+                       q_width, kv_width);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------- silu / add */
+
+__global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* __restrict__ gu,
+                                                  uint16_t* __restrict__ h, int64_t total,
+                                                  int ffn) {
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = idx / ffn;
+        const int c = (int)(idx % ffn);
+        const float g = bf2f(gu[(size_t)r * 2 * ffn + c]);
+        const float u = bf2f(gu[(size_t)r * 2 * ffn + ffn + c]);
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, s2p_expf(-g)));
+        const float sil = bf2f(f2bf(__fmul_rn(g, sig)));
+        h[idx] = f2bf(__fmul_rn(sil, u));
+    }
+}
+
+extern "C" hipError_t s2pk_silu_mul(const s2p_bf16* gu, s2p_bf16* h, int rows, int ffn,
+                                    hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t total = (int64_t)rows * ffn;
+    hipLaunchKernelGGL(k_silu_mul, dim3(pr_blocks(total, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (const uint16_t*)gu, (uint16_t*)h, total, ffn);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_add(uint16_t* __restrict__ y,
+                                             const uint16_t* __restrict__ x, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = f2bf(__fadd_rn(bf2f(y[i]), bf2f(x[i])));
+}
+
+extern "C" hipError_t s2pk_add(s2p_bf16* y, const s2p_bf16* x, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add, dim3(pr_blocks(n, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (uint16_t*)y, (const uint16_t*)x, n);
+    return hipGetLastError();
+}
+
+/* ----------------------------------------------- fused verify-layer kernels */
+
+/* One wave per (row, head), heads 0..q_heads-1 are query heads, then the
+ * kv heads.  Per-head RMSNorm (reference tree order: lane i holds elements
+ * i and i+64, exactly the first level of the 128-thread tree), RoPE at the
+ * row's position, query -> q_out, key/value -> the row's cache slot.
+ * Cache planes of layer l of a session: base + l * layer_stride, k head h at
+ * plane h, v head h at plane kv_heads + h, each [max_seq][128]. */
+__global__ __launch_bounds__(64) void k_qkrope_append(const uint16_t* __restrict__ qkv,
+                                                      uint16_t* __restrict__ q_out,
+                                                      const uint16_t* __restrict__ qn_w,
+                                                      const uint16_t* __restrict__ kn_w,
+                                                      S2pRowPlan plan, int layer, float eps,
+                                                      float base) {
+    const int row = blockIdx.x;
+    const int head = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int QH = 32, KVH = 8, HD = 128;
+    const int qkv_w = (QH + 2 * KVH) * HD;
+    const bool is_q = head < QH;
+    const int kh = head - QH;
+    const uint16_t* src = qkv + (size_t)row * qkv_w + (is_q ? head * HD : QH * HD + kh * HD);
+    const uint16_t* nw = is_q ? qn_w : kn_w;
+    float v0 = bf2f(src[lane]), v1 = bf2f(src[lane + 64]);
+    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
+    s = wave_sum_down(s);
+    s = __shfl(s, 0, 64);
+    const float inv = rsqrt_rule(s / (float)HD + eps);
+    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(nw[lane]))));
+    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(nw[lane + 64]))));
+    /* RoPE: element e = lane + 64*slot, partner e ^ 1 lives in lane ^ 1 */
+    const int p = plan.pos[row];
+    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
+    float o[2];
+#pragma unroll
+    for (int slot = 0; slot < 2; slot++) {
+        const int e = lane + 64 * slot;
+        const float me = slot ? v1 : v0, pa = slot ? pv1 : pv0;
+        float c, sn;
+        rope_cs(p, e >> 1, HD, base, &c, &sn);
+        if ((e & 1) == 0) o[slot] = __fsub_rn(__fmul_rn(me, c), __fmul_rn(pa, sn)); /* x0' */
+        else o[slot] = __fadd_rn(__fmul_rn(me, c), __fmul_rn(pa, sn));              /* x1' */
+    }
+    if (is_q) {
+        uint16_t* dst = q_out + (size_t)row * QH * HD + head * HD;
+        dst[lane] = f2bf(o[0]);
+        dst[lane + 64] = f2bf(o[1]);
+    } else {
+        uint16_t* kvb = (uint16_t*)plan.kv[plan.sess[row]] + (size_t)layer * plan.layer_stride;
+        const size_t slot = (size_t)plan.slot[row];
+        uint16_t* kd = kvb + ((size_t)kh * plan.max_seq + slot) * HD;
+        uint16_t* vd = kvb + ((size_t)(KVH + kh) * plan.max_seq + slot) * HD;
+        kd[lane] = f2bf(o[0]);
+        kd[lane + 64] = f2bf(o[1]);
+        const uint16_t* vs = qkv + (size_t)row * qkv_w + (QH + KVH) * HD + kh * HD;
+        vd[lane] = vs[lane];
+        vd[lane + 64] = vs[lane + 64];
+    }
+}
+
+extern "C" hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
+                                               const void* kn_w, const S2pRowPlan* plan,
+                                               int rows, int layer, float eps, float base,
+                                               hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_qkrope_append, dim3(rows, 40), dim3(64), 0, st, (const uint16_t*)qkv,
+                       (uint16_t*)q_out, (const uint16_t*)qn_w, (const uint16_t*)kn_w, *plan,
+                       layer, eps, base);
+    return hipGetLastError();
+}
+
+/* Residual stream init: x = x_in and per-64-column sums of squares of x
+ * (layout [N/64][GEMV_MAX_M]) for the first RMSNorm. */
+__global__ __launch_bounds__(64) void k_resid_init(const uint16_t* __restrict__ xin,
+                                                   uint16_t* __restrict__ x,
+                                                   float* __restrict__ ssq, int width) {
+    const int blk = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    const size_t i = (size_t)m * width + blk * 64 + lane;
+    const uint16_t v = xin[i];
+    x[i] = v;
+    const float f = bf2f(v);
+    const float t = wave_sum_down(f * f);
+    if (lane == 0) ssq[(size_t)blk * 128 + m] = t;
+}
+
+extern "C" hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq, int rows,
+                                            int width, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (width % 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_resid_init, dim3(width / 64, rows), dim3(64), 0, st,
+                       (const uint16_t*)xin, (uint16_t*)x, ssq, width);
+    return hipGetLastError();
+}
+
+/* Tree commit: session s, layer l, plane h (16 = 8 K + 8 V heads).  Accepted
+ * node path[d-1] (index >= d) moves to slot L + d in increasing d, so no
+ * source is overwritten before it is read. */
+__global__ __launch_bounds__(64) void k_kv_commit(S2pRowPlan plan, const int32_t* __restrict__ path,
+                                                  const int32_t* __restrict__ n_acc, int R) {
+    const int s = blockIdx.x, layer = blockIdx.y, plane = blockIdx.z, lane = threadIdx.x;
+    const int n = n_acc[s];
+    const int L = plan.slot[s * R];
+    uint16_t* base = (uint16_t*)plan.kv[s] + (size_t)layer * plan.layer_stride +
+                     (size_t)plane * plan.max_seq * 128;
+    for (int d = 1; d <= n; d++) {
+        const int node = path[(size_t)s * R + d - 1];
+        if (node == d) continue;
+        const uint32_t* src = (const uint32_t*)(base + (size_t)(L + node) * 128);
+        uint32_t* dst = (uint32_t*)(base + (size_t)(L + d) * 128);
+        dst[lane] = src[lane];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+extern "C" hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t* path,
+                                           const int32_t* n_acc, int n_sess, int R, int n_layers,
+                                           hipStream_t st) {
+    if (n_sess <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_kv_commit, dim3(n_sess, n_layers, 16), dim3(64), 0, st, *plan, path,
+                       n_acc, R);
+    return hipGetLastError();
+}

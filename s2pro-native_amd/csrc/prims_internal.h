@@ -1,0 +1,55 @@
+/* s2pro MI355X — internal launch descriptors of the fused verify kernels
+ * (prims.hip, attention.hip), shared with the C host code.  Not public ABI. */
+#ifndef S2P_PRIMS_INTERNAL_H
+#define S2P_PRIMS_INTERNAL_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-row plan of one verify call (device arrays). */
+typedef struct {
+    const int32_t*  pos;          /* [rows] RoPE position */
+    const int32_t*  slot;         /* [rows] KV cache slot written by the row */
+    const int32_t*  sess;         /* [rows] session index */
+    const uint64_t* vis;          /* [rows] visible node slots relative to L */
+    void* const*    kv;           /* [n_sess] KV base, [layers][2*8][max_seq][128] */
+    int64_t         layer_stride; /* elements per layer in a session KV */
+    int             max_seq;
+} S2pRowPlan;
+
+/* Attention segment: up to 8 consecutive rows sharing one cache. */
+typedef struct {
+    int32_t sess;   /* session index (KV base in plan.kv) */
+    int32_t L;      /* prefix length: slots [0, L) visible to every row */
+    int32_t row0;   /* first row */
+    int32_t nrows;  /* rows in this segment (<= 8) */
+    int32_t span;   /* slots [0, span) may be visible to some row */
+    int32_t pad_;
+} S2pAttnSeg;
+
+hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
+                                    const void* kn_w, const S2pRowPlan* plan, int rows,
+                                    int layer, float eps, float base, hipStream_t st);
+/* Move accepted tree nodes' K/V from slot L + node to L + depth. */
+hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t* path,
+                                const int32_t* n_acc, int n_sess, int R, int n_layers,
+                                hipStream_t st);
+hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq, int rows,
+                                 int width, hipStream_t st);
+
+/* Verify-plan attention over the per-layer caches of the plan's sessions.
+ * segs: device [n_seg]; max_span: host bound of max(span) (grid sizing);
+ * part: scratch of s2p_attn_plan_part_floats(rows, max_span) floats. */
+hipError_t s2p_attn_plan_launch(const void* q, void* out, const S2pRowPlan* plan,
+                                const S2pAttnSeg* segs, int n_seg, int rows, int layer,
+                                int max_span, float* part, hipStream_t st);
+int64_t    s2p_attn_plan_part_floats(int rows, int max_span);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

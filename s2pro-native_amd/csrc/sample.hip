@@ -1,0 +1,545 @@
+/* s2pro MI355X — device sampler and speculative acceptance.
+ *
+ * Compiled with FP contraction off: every float operation of the rule is one
+ * IEEE rounding, in the order of the reference sampler (sampling.c:119-282),
+ * and exp/log are the rule's s2p_expf/s2p_logf (binary64 evaluation, one
+ * rounding), so sampled ids and accept/reject decisions are bit-identical to
+ * the host restatement for the same state and logits.
+ *
+ * k_transform: one workgroup per (row, target|draft).
+ *   1. sampler state of the row: the session state plus, for a verify tree
+ *      node, the drafted tokens on its root path pushed as emitted tokens
+ *      (sampling.c:269-281), so node i sees the history with d_1..d_i;
+ *   2. gather the 4096 semantic logits + EOS (bf16 -> f32, exact);
+ *   3. RAS detect and repetition penalty on one lane (gather then scatter);
+ *   4. top-30 by value desc / index asc: a 4-pass 8-bit radix select finds
+ *      the 30th largest value, ties at the threshold are taken in index
+ *      order through a block prefix count, and the 30 survivors are ranked;
+ *   5. top-p over the un-tempered softmax and the temperature softmax: the
+ *      exps are elementwise across lanes, every sum is sequential on lane 0.
+ *   s2pk_sample then draws (seeded hash-Gumbel or xoshiro inverse CDF,
+ *   sampling.c:221-262) and updates the state; the verify path writes the
+ *   30 (candidate, probability) pairs to the workspace.
+ * k_accept: one wave per session walks the draft tree root-first
+ *   (Leviathan et al. 2211.17192; SpecInfer multi-candidate form for
+ *   siblings): child c of node v with drafted id d is accepted iff
+ *   u * q_v(d) < p_v(d) (u a 24-bit uniform, compared exactly in binary64);
+ *   on rejection p_v <- norm(max(0, p_v - q_v)) and the next sibling is
+ *   tried; when no child is accepted the corrected token is drawn from the
+ *   residual, and at an accepted leaf the bonus token is drawn from p exactly
+ *   as s2ps_sample would.  An accepted EOS ends generation.  The state
+ *   advances over every emitted non-EOS id.
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "common.h"
+#include "s2pro/s2p_fmath.h"
+#include "s2pro/slowar_kernels.h"
+#include "sample_internal.h"
+
+#define N_SEM 4096
+#define N_CAND 4097
+#define CAND_EOS 4096
+#define TOP_K 30
+#define TOK_EOS 151645LL
+#define SEM_START 151678LL
+#define SEM_END 155773LL
+#define TX_THREADS 256
+
+/* ------------------------------------------------------------ RNG pieces */
+
+S2P_DEV uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+S2P_DEV uint64_t xoshiro_next(uint64_t* s) {
+    const uint64_t result = rotl64(s[1] * 5, 7) * 9;
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl64(s[3], 45);
+    return result;
+}
+
+/* reference seeded draw, sampling.c:221-243 */
+S2P_DEV int gumbel_draw(const s2ps_dev_state* sp, const float* prob) {
+    const uint64_t step_seed = ((uint64_t)sp->seed31 * 19349663ULL) ^ (sp->count * 73856093ULL);
+    float best = -INFINITY;
+    int choice = 0;
+    for (int j = 0; j < TOP_K; j++) {
+        const uint64_t hashed = (step_seed * 8589934591ULL) ^ ((uint64_t)j * 479001599ULL);
+        float u = (float)(uint32_t)(hashed & 0xFFFFFFULL) / 16777216.0f;
+        if (u < 1e-10f) u = 1e-10f;
+        const float g = -s2p_logf(-s2p_logf(u));
+        const float pert = s2p_logf(prob[j] + 1e-10f) + g;
+        if (pert > best) {
+            best = pert;
+            choice = j;
+        }
+    }
+    return choice;
+}
+
+/* reference unseeded draw, sampling.c:244-262 */
+S2P_DEV int xoshiro_draw(s2ps_dev_state* sp, const float* prob) {
+    const double r = (double)(xoshiro_next(sp->rng) >> 11) * 0x1.0p-53;
+    double cum2 = 0.0;
+    int lastnz = 0, choice = -1;
+    for (int j = 0; j < TOP_K; j++) {
+        if (prob[j] <= 0.f) continue;
+        lastnz = j;
+        cum2 += (double)prob[j];
+        if (r < cum2) {
+            choice = j;
+            break;
+        }
+    }
+    return choice < 0 ? lastnz : choice;
+}
+
+/* acceptance-rule uniform: splitmix64 finaliser of (seed31, count, slot) */
+S2P_DEV uint32_t rule_u24(const s2ps_dev_state* sp, uint32_t slot) {
+    uint64_t z = ((uint64_t)sp->seed31 * 0x9E3779B97F4A7C15ULL) ^
+                 (sp->count * 0xBF58476D1CE4E5B9ULL) ^
+                 ((uint64_t)(slot + 1) * 0x94D049BB133111EBULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    z ^= z >> 31;
+    return (uint32_t)(z >> 40);
+}
+
+S2P_DEV int residual_draw(s2ps_dev_state* sp, const float* prob) {
+    if (!sp->seeded) return xoshiro_draw(sp, prob);
+    float best = -INFINITY;
+    int choice = 0;
+    for (int j = 0; j < TOP_K; j++) {
+        if (!(prob[j] > 0.f)) continue;
+        float u = (float)rule_u24(sp, (uint32_t)j) / 16777216.0f;
+        if (u < 1e-10f) u = 1e-10f;
+        const float g = -s2p_logf(-s2p_logf(u));
+        const float pert = s2p_logf(prob[j] + 1e-10f) + g;
+        if (pert > best) {
+            best = pert;
+            choice = j;
+        }
+    }
+    return choice;
+}
+
+S2P_DEV void state_push(s2ps_dev_state* sp, int64_t tok) {
+    if (tok == TOK_EOS) return;
+    if (sp->count < (uint64_t)sp->window) {
+        sp->prev[sp->count] = tok;
+    } else {
+        for (int j = 0; j < sp->window - 1; j++) sp->prev[j] = sp->prev[j + 1];
+        sp->prev[sp->window - 1] = tok;
+    }
+    sp->count++;
+}
+
+S2P_DEV int64_t cand_to_vocab(int ci) { return ci == CAND_EOS ? TOK_EOS : SEM_START + ci; }
+S2P_DEV int vocab_to_cand(int64_t t) {
+    if (t >= SEM_START && t <= SEM_END) return (int)(t - SEM_START);
+    if (t == TOK_EOS) return CAND_EOS;
+    return -1;
+}
+
+/* orderable key of a float (-0 folded onto +0): unsigned order == value order */
+S2P_DEV uint32_t okey(float v) {
+    uint32_t u = __float_as_uint(v + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* --------------------------------------------------------------- transform */
+
+struct TxShared {
+    float cand[N_CAND];
+    uint32_t key[N_CAND];
+    s2ps_dev_state st;
+    unsigned hist[256];
+    uint32_t prefix;
+    int need;       /* survivors still to take at the threshold key */
+    int n_gt;       /* collected strictly above the threshold */
+    int eq_base[TX_THREADS];
+    float tv[32];
+    int ti[32];
+    float e[32];
+    float p2[32];
+    int greedy;
+    float temp, topp, m, sum, t, m2, s2;
+    int masked[32];
+};
+
+/* Sampler transform of one logits row into sh.ti / sh.p2 (ranks 0..29). */
+__device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t* eos_ptr) {
+    const int tid = threadIdx.x;
+    /* gather */
+    if (eos_ptr) {
+        for (int i = tid; i < N_SEM; i += TX_THREADS) sh.cand[i] = bf2f(lrow[i]);
+        if (tid == 0) sh.cand[CAND_EOS] = bf2f(*eos_ptr);
+    } else {
+        for (int i = tid; i < N_SEM; i += TX_THREADS) sh.cand[i] = bf2f(lrow[SEM_START + i]);
+        if (tid == 0) sh.cand[CAND_EOS] = bf2f(lrow[TOK_EOS]);
+    }
+    __syncthreads();
+    /* RAS + repetition penalty (sampling.c:129-174), lane 0 */
+    if (tid == 0) {
+        const s2ps_dev_state* sp = &sh.st;
+        const int greedy = sp->temperature == 0.0f;
+        const int capped = sp->count < (uint64_t)sp->window ? (int)sp->count : sp->window;
+        int use_ras = 0;
+        if (!greedy && capped >= 4) {
+            int64_t last4[4];
+            for (int r = 0; r < 4; r++) {
+                int idx = capped - (4 - r);
+                if (idx < 0) idx = 0;
+                last4[r] = sp->prev[idx];
+            }
+            for (int a = 0; a < 3; a++)
+                for (int b = a + 1; b < 4; b++)
+                    if (last4[b] < last4[a]) {
+                        const int64_t t = last4[a];
+                        last4[a] = last4[b];
+                        last4[b] = t;
+                    }
+            for (int a = 0; a < 3; a++)
+                if (last4[a] == last4[a + 1]) use_ras = 1;
+        }
+        sh.greedy = greedy;
+        sh.temp = use_ras ? 1.0f : sp->temperature;
+        sh.topp = use_ras ? 0.9f : sp->top_p;
+        if (capped > 0) {
+            int ridx[64];
+            float rval[64];
+            int rn = 0;
+            for (int j = 0; j < capped; j++) {
+                const int ci = vocab_to_cand(sp->prev[j]);
+                if (ci < 0) continue;
+                const float v = sh.cand[ci];
+                ridx[rn] = ci;
+                rval[rn] = v < 0.f ? v * sp->rep_penalty : v / sp->rep_penalty;
+                rn++;
+            }
+            for (int j = 0; j < rn; j++) sh.cand[ridx[j]] = rval[j];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < N_CAND; i += TX_THREADS) sh.key[i] = okey(sh.cand[i]);
+    if (tid == 0) {
+        sh.prefix = 0;
+        sh.need = TOP_K;
+    }
+    __syncthreads();
+    /* radix select of the 30th largest key, 8 bits per pass from the top */
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
+        sh.hist[tid] = 0;
+        __syncthreads();
+        const uint32_t pre = sh.prefix;
+        for (int i = tid; i < N_CAND; i += TX_THREADS) {
+            const uint32_t k = sh.key[i];
+            if ((k & hmask) == pre) atomicAdd(&sh.hist[(k >> shift) & 0xFFu], 1u);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            /* lane l owns bins 255-4l .. 252-4l (descending) */
+            unsigned b4[4], own = 0;
+            for (int i = 0; i < 4; i++) {
+                b4[i] = sh.hist[255 - 4 * tid - i];
+                own += b4[i];
+            }
+            /* exclusive prefix over lanes in descending-bin order */
+            unsigned incl = own;
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned o = __shfl_up(incl, off, 64);
+                if (tid >= off) incl += o;
+            }
+            const unsigned excl = incl - own;
+            const int need = sh.need;
+            if (excl < (unsigned)need && incl >= (unsigned)need) {
+                unsigned cum = excl;
+                for (int i = 0; i < 4; i++) {
+                    if (cum + b4[i] >= (unsigned)need) {
+                        const uint32_t bin = 255u - 4u * tid - i;
+                        sh.prefix = pre | (bin << shift);
+                        sh.need = need - (int)cum;
+                        break;
+                    }
+                    cum += b4[i];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    /* collect: keys above the threshold, then the first `need` equal keys in
+     * index order (contiguous index ranges per thread + block prefix count) */
+    const uint32_t T = sh.prefix;
+    const int need = sh.need;
+    if (tid == 0) sh.n_gt = 0;
+    const int per = (N_CAND + TX_THREADS - 1) / TX_THREADS; /* 17 */
+    const int i0 = tid * per, i1 = min(N_CAND, i0 + per);
+    int n_eq = 0;
+    __syncthreads();
+    for (int i = i0; i < i1; i++) {
+        const uint32_t k = sh.key[i];
+        if (k > T) {
+            const int s = atomicAdd(&sh.n_gt, 1);
+            sh.ti[s] = i;
+        } else if (k == T) {
+            n_eq++;
+        }
+    }
+    sh.eq_base[tid] = n_eq;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int t = 0; t < TX_THREADS; t++) {
+            const int c = sh.eq_base[t];
+            sh.eq_base[t] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    {
+        int r = sh.eq_base[tid];
+        const int ngt = TOP_K - need; /* == sh.n_gt */
+        for (int i = i0; i < i1 && r < need; i++)
+            if (sh.key[i] == T) {
+                sh.ti[ngt + r] = i;
+                r++;
+            }
+    }
+    __syncthreads();
+    /* rank the 30 survivors: value desc, index asc */
+    int my_i = 0, rank = 0;
+    float my_v = 0.f;
+    if (tid < TOP_K) {
+        my_i = sh.ti[tid];
+        my_v = sh.cand[my_i];
+        const uint32_t mk = okey(my_v);
+        for (int j = 0; j < TOP_K; j++) {
+            const int oi = sh.ti[j];
+            const uint32_t ok = okey(sh.cand[oi]);
+            rank += (ok > mk) || (ok == mk && oi < my_i);
+        }
+    }
+    __syncthreads();
+    if (tid < TOP_K) {
+        sh.tv[rank] = my_v;
+        sh.ti[rank] = my_i;
+    }
+    __syncthreads();
+    /* two softmaxes (sampling.c:196-219) */
+    if (sh.greedy) {
+        if (tid < 32) sh.p2[tid] = tid == 0 ? 1.0f : 0.0f;
+        __syncthreads();
+        return;
+    }
+    if (tid < TOP_K) sh.e[tid] = s2p_expf(sh.tv[tid] - sh.tv[0]);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.f;
+        for (int j = 0; j < TOP_K; j++) sum += sh.e[j];
+        float cum = 0.f;
+        for (int j = 0; j < TOP_K; j++) {
+            cum += sh.e[j] / sum;
+            sh.masked[j] = (j > 0 && cum > sh.topp) ? 1 : 0;
+        }
+        const float t = sh.temp < 1e-5f ? 1e-5f : sh.temp;
+        sh.t = t;
+        sh.m2 = sh.tv[0] / t;
+    }
+    __syncthreads();
+    if (tid < TOP_K) sh.p2[tid] = sh.masked[tid] ? 0.f : s2p_expf(sh.tv[tid] / sh.t - sh.m2);
+    __syncthreads();
+    if (tid == 0) {
+        float s2 = 0.f;
+        for (int j = 0; j < TOP_K; j++) s2 += sh.p2[j];
+        sh.s2 = s2;
+    }
+    __syncthreads();
+    if (tid < TOP_K) sh.p2[tid] = sh.p2[tid] / sh.s2;
+    __syncthreads();
+}
+
+/* ------------------------------------------------------------ s2pk_sample */
+
+__global__ __launch_bounds__(TX_THREADS) void k_sample(const uint16_t* __restrict__ logits,
+                                                       int64_t vocab_stride,
+                                                       const uint16_t* __restrict__ eos_logits,
+                                                       s2ps_dev_state* const* states,
+                                                       int64_t* out_tok, int32_t* out_sem,
+                                                       int32_t* out_codes, uint8_t* out_eos) {
+    __shared__ TxShared sh;
+    const int row = blockIdx.x;
+    s2ps_dev_state* sp = states[row];
+    if (threadIdx.x == 0) sh.st = *sp;
+    __syncthreads();
+    transform_row(sh, logits + (size_t)row * vocab_stride, eos_logits ? eos_logits + row : nullptr);
+    if (threadIdx.x != 0) return;
+    int choice = 0;
+    if (!sh.greedy) choice = sh.st.seeded ? gumbel_draw(&sh.st, sh.p2) : xoshiro_draw(&sh.st, sh.p2);
+    const int ci = sh.ti[choice];
+    const int64_t tok = cand_to_vocab(ci);
+    out_tok[row] = tok;
+    if (tok == TOK_EOS) {
+        out_sem[row] = 0;
+        if (out_codes) out_codes[(size_t)row * 10] = 0;
+        out_eos[row] = 1;
+    } else {
+        out_sem[row] = ci;
+        if (out_codes) out_codes[(size_t)row * 10] = ci;
+        out_eos[row] = 0;
+        state_push(&sh.st, tok);
+    }
+    *sp = sh.st;
+}
+
+extern "C" hipError_t s2pk_sample(const s2p_bf16* logits, int64_t vocab_stride,
+                                  const s2p_bf16* eos_logits, s2ps_dev_state* const* states,
+                                  int rows, int64_t* out_tok, int32_t* out_sem,
+                                  int32_t* out_codes, uint8_t* out_eos, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_sample, dim3(rows), dim3(TX_THREADS), 0, st, (const uint16_t*)logits,
+                       vocab_stride, (const uint16_t*)eos_logits, states, out_tok, out_sem,
+                       out_codes, out_eos);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------- acceptance */
+
+/* workspace entry per (session, node, target|draft) */
+struct TxOut {
+    int32_t ti[32];
+    float p[32];
+    int32_t greedy;
+    int32_t pad_[31];
+};
+
+__global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
+    __shared__ TxShared sh;
+    const int gr = blockIdx.x;          /* global node row s * R + v */
+    const int which = blockIdx.y;       /* 0 target, 1 draft */
+    const int s = gr / a.R, v = gr - s * a.R;
+    /* leaves need no draft transform */
+    if (which == 1) {
+        bool has_child = false;
+        for (int c = v + 1; c < a.R; c++) has_child |= a.parent[c] == v;
+        if (!has_child) return;
+    }
+    if (threadIdx.x == 0) {
+        sh.st = *a.states[s];
+        /* push the drafted tokens of the root path (root excluded) */
+        int path[64];
+        int n = 0;
+        for (int u = v; u > 0 && n < 64; u = a.parent[u]) path[n++] = u;
+        for (int i = n - 1; i >= 0; i--) state_push(&sh.st, a.tok[(size_t)s * a.R + path[i]]);
+    }
+    __syncthreads();
+    const uint16_t* base = which ? a.drf : a.tgt;
+    const uint16_t* eos = which ? a.drf_eos : a.tgt_eos;
+    const int64_t es = which ? a.drf_eos_stride : a.tgt_eos_stride;
+    transform_row(sh, base + (size_t)gr * a.row_stride, eos ? eos + (size_t)gr * es : nullptr);
+    TxOut* o = (TxOut*)a.work + ((size_t)gr * 2 + which);
+    if (threadIdx.x < 32) {
+        o->ti[threadIdx.x] = threadIdx.x < TOP_K ? sh.ti[threadIdx.x] : -1;
+        o->p[threadIdx.x] = threadIdx.x < TOP_K ? sh.p2[threadIdx.x] : 0.f;
+    }
+    if (threadIdx.x == 0) o->greedy = sh.greedy;
+}
+
+S2P_DEV float prob_of(const int32_t* ti, const float* p, int ci) {
+    for (int j = 0; j < TOP_K; j++)
+        if (ti[j] == ci) return p[j];
+    return 0.f;
+}
+
+__global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
+    const int s = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    s2ps_dev_state st = *a.states[s];
+    const TxOut* work = (const TxOut*)a.work;
+    const int R = a.R;
+    const int64_t* tok = a.tok + (size_t)s * R;
+    int32_t* path = a.out_path + (size_t)s * R;
+    int64_t* emit = a.out_emit + (size_t)s * (R + 1);
+    int n_acc = 0, n_emit = 0;
+    int v = 0;
+    for (;;) {
+        const TxOut* tp = work + ((size_t)(s * R + v) * 2 + 0);
+        const TxOut* tq = work + ((size_t)(s * R + v) * 2 + 1);
+        float p[TOP_K];
+        int32_t pti[TOP_K];
+        for (int k = 0; k < TOP_K; k++) {
+            p[k] = tp->p[k];
+            pti[k] = tp->ti[k];
+        }
+        const int greedy = tp->greedy;
+        int accepted = -1, rejected_any = 0, j = 0;
+        for (int c = v + 1; c < R && accepted < 0; c++) {
+            if (a.parent[c] != v) continue;
+            const int ci = vocab_to_cand(tok[c]);
+            const float pc = ci < 0 ? 0.f : prob_of(pti, p, ci);
+            const float qc = ci < 0 ? 0.f : prob_of(tq->ti, tq->p, ci);
+            const uint32_t u = greedy ? 0u
+                                      : (st.seeded ? rule_u24(&st, 64u + (uint32_t)j)
+                                                   : (uint32_t)(xoshiro_next(st.rng) >> 40));
+            if ((double)u * (double)qc < (double)pc * 16777216.0) {
+                accepted = c;
+                break;
+            }
+            rejected_any = 1;
+            float rsd[TOP_K], z = 0.f;
+            for (int k = 0; k < TOP_K; k++) {
+                const float d = p[k] - prob_of(tq->ti, tq->p, pti[k]);
+                rsd[k] = d > 0.f ? d : 0.f;
+                z += rsd[k];
+            }
+            if (z > 0.f)
+                for (int k = 0; k < TOP_K; k++) p[k] = rsd[k] / z;
+            j++;
+        }
+        if (accepted >= 0) {
+            path[n_acc++] = accepted;
+            emit[n_emit++] = tok[accepted];
+            if (tok[accepted] == TOK_EOS) break;
+            state_push(&st, tok[accepted]);
+            v = accepted;
+            continue;
+        }
+        int choice = 0;
+        if (greedy) {
+            for (int k = 1; k < TOP_K; k++)
+                if (p[k] > p[choice]) choice = k;
+        } else if (rejected_any) {
+            choice = residual_draw(&st, p);
+        } else {
+            choice = st.seeded ? gumbel_draw(&st, p) : xoshiro_draw(&st, p);
+        }
+        const int64_t t = cand_to_vocab(pti[choice]);
+        emit[n_emit++] = t;
+        state_push(&st, t);
+        break;
+    }
+    a.out_n_acc[s] = n_acc;
+    a.out_n_emit[s] = n_emit;
+    *a.states[s] = st;
+}
+
+extern "C" size_t s2p_accept_work_bytes(int n_sess, int rows) {
+    return (size_t)n_sess * rows * 2 * sizeof(TxOut);
+}
+
+extern "C" hipError_t s2p_accept_launch(const AcceptArgs* ap, hipStream_t st) {
+    const AcceptArgs a = *ap;
+    if (a.n_sess <= 0) return hipSuccess;
+    if (a.R < 1 || a.R > 64 || !a.work) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_accept_transform, dim3(a.n_sess * a.R, 2), dim3(TX_THREADS), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_accept_walk, dim3(a.n_sess), dim3(64), 0, st, a);
+    return hipGetLastError();
+}

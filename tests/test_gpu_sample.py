@@ -1,0 +1,193 @@
+"""Device sampler and acceptance vs the host rule, bit-exact: same sampled
+ids, same accept/reject decisions, same emitted tokens and same sampler
+state bytes afterwards, for the same state and logits."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+import s2pamd
+from gpu_util import P, S, bf16_bits, empty, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+SEM0, EOS = 151678, 151645
+# config 5 draft tree: root + 16 nodes, depth counts 2/4/6/4
+TREE16 = [-1, 0, 0, 1, 1, 2, 2, 3, 3, 4, 5, 6, 6, 7, 8, 10, 11]
+SB = ctypes.sizeof(po.OrState)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return s2pamd.load()
+
+
+def states_to_dev(states):
+    buf = np.frombuffer(b"".join(bytes(s) for s in states), np.uint8).copy()
+    d = to_dev(buf)
+    ptrs = to_dev(np.array([d.data_ptr() + i * SB for i in range(len(states))], np.int64))
+    return d, ptrs
+
+
+def states_from_dev(d, n):
+    raw = to_host(d).tobytes()
+    out = []
+    for i in range(n):
+        s = po.OrState()
+        ctypes.memmove(ctypes.addressof(s), raw[i * SB:(i + 1) * SB], SB)
+        out.append(s)
+    return out
+
+
+def make_state(i, r):
+    temp = [0.8, 0.0, 1.0, 0.8, 0.5][i % 5]
+    topp = [0.8, 0.8, 1.0, 0.9, 0.3][i % 5]
+    seed = 0 if i % 3 == 0 else 1000 + i
+    st = po.state(temperature=temp, top_p=topp, rep_penalty=1.1, window=16, seed=seed, entropy=i)
+    hist = r.integers(0, 4096, int(r.integers(0, 24)))
+    if i % 4 == 1 and len(hist) >= 4:
+        hist[-2] = hist[-4]  # duplicate in the last four -> RAS
+    for t in hist:
+        po.state_push(st, SEM0 + int(t))
+    return st
+
+
+@pytest.mark.parametrize("compact", [True, False])
+def test_sample_bit_exact(lib, compact):
+    r = np.random.default_rng(11 if compact else 12)
+    n = 48
+    states = [make_state(i, r) for i in range(n)]
+    if compact:
+        logits = bf16_bits((r.standard_normal((n, 4096)) * 2).astype(np.float32))
+        eos = bf16_bits((r.standard_normal(n) * 2 - 1).astype(np.float32))
+        eos[5] = bf16_bits(np.array([40.0], np.float32))[0]  # an EOS draw
+        stride = 4096
+    else:
+        logits = bf16_bits((r.standard_normal((n, 155776)) * 2).astype(np.float32))
+        eos = None
+        stride = 155776
+    d_states, d_ptrs = states_to_dev(states)
+    out_tok = torch.zeros(n, dtype=torch.int64, device="cuda")
+    out_sem = torch.zeros(n, dtype=torch.int32, device="cuda")
+    out_codes = torch.zeros(n * 10, dtype=torch.int32, device="cuda")
+    out_eos = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    s2pamd.hip_check(lib.s2pk_sample(P(to_dev(logits)), stride,
+                                     P(to_dev(eos)) if eos is not None else None, P(d_ptrs), n,
+                                     P(out_tok), P(out_sem), P(out_codes), P(out_eos), S()))
+    got_tok = to_host(out_tok)
+    got_states = states_from_dev(d_states, n)
+    for i in range(n):
+        tok, sem, e = po.sample(states[i], logits[i], None if eos is None else int(eos[i]))
+        assert got_tok[i] == tok, (i, got_tok[i], tok)
+        assert bytes(got_states[i]) == bytes(states[i]), i
+    assert to_host(out_eos)[5] == 1 if compact else True
+
+
+def chain_inputs(r, K, n_sess, mode):
+    """Target logits N(0,2); draft = target + N(0,0.5) (config 1 recipe)."""
+    R = K + 1
+    tgt = (r.standard_normal((n_sess * R, 4096)) * 2).astype(np.float32)
+    drf = tgt + (r.standard_normal((n_sess * R, 4096)) * 0.5).astype(np.float32)
+    if mode == "disjoint":
+        drf = -tgt
+    tgt_b, drf_b = bf16_bits(tgt), bf16_bits(drf)
+    te = bf16_bits((r.standard_normal(n_sess * R) - 6).astype(np.float32))
+    de = bf16_bits((r.standard_normal(n_sess * R) - 6).astype(np.float32))
+    return tgt_b, drf_b, te, de
+
+
+def draft_tokens(states, drf, de, parent, R):
+    """Draft ids drawn by the reference sampler from the draft rows."""
+    tok = np.zeros(len(states) * R, np.int64)
+    for s, st in enumerate(states):
+        for i in range(1, R):
+            sd = po.copy_state(st)
+            path = []
+            u = parent[i]
+            while u > 0:
+                path.append(u)
+                u = parent[u]
+            for u in reversed(path):
+                po.state_push(sd, tok[s * R + u])
+            row, eos = drf[s * R + parent[i]], int(de[s * R + parent[i]])
+            first_child = min(c for c in range(1, R) if parent[c] == parent[i]) == i
+            if first_child:
+                tok[s * R + i] = po.sample(sd, row, eos)[0]
+            else:  # later siblings: another candidate of the draft's top-30
+                ti, _, p2, _ = po.transform(sd, row, eos)
+                tok[s * R + i] = SEM0 + int(ti[(i * 7) % 30])
+    return tok
+
+
+def run_accept(lib, states, tgt, drf, te, de, parent, tok, n_sess, R):
+    d_states, d_ptrs = states_to_dev(states)
+    work = torch.empty(lib.s2p_verify_accept_work_bytes(n_sess, R), dtype=torch.uint8,
+                       device="cuda")
+    path = torch.full((n_sess * R,), -1, dtype=torch.int32, device="cuda")
+    nacc = torch.zeros(n_sess, dtype=torch.int32, device="cuda")
+    emit = torch.zeros(n_sess * (R + 1), dtype=torch.int64, device="cuda")
+    nemit = torch.zeros(n_sess, dtype=torch.int32, device="cuda")
+    s2pamd.check(lib.s2p_verify_accept(P(to_dev(tgt)), P(to_dev(te)), P(to_dev(drf)),
+                                       P(to_dev(de)), 4096, P(to_dev(np.asarray(parent, np.int32))),
+                                       P(to_dev(tok)), P(d_ptrs), n_sess, R, P(path), P(nacc),
+                                       P(emit), P(nemit), P(work), S()), "accept")
+    return (to_host(path).reshape(n_sess, R), to_host(nacc), to_host(emit).reshape(n_sess, R + 1),
+            to_host(nemit), states_from_dev(d_states, n_sess))
+
+
+@pytest.mark.parametrize("mode", ["config1", "disjoint"])
+def test_accept_chain_bit_exact(lib, mode):
+    """Config 1: K=4, 4096-way logits, T0.8 p0.8, seed 0 (unseeded xoshiro)
+    plus seeded sessions; decisions and emitted ids equal the host rule."""
+    r = np.random.default_rng(21)
+    K, n_sess = 4, 24
+    R = K + 1
+    parent = [-1, 0, 1, 2, 3]
+    tgt, drf, te, de = chain_inputs(r, K, n_sess, mode)
+    states = []
+    for s in range(n_sess):
+        st = po.state(temperature=[0.8, 0.8, 0.0, 1.0][s % 4], top_p=0.8,
+                      seed=0 if s % 2 == 0 else 7 + s, entropy=s)
+        for t in r.integers(0, 4096, s % 9):
+            po.state_push(st, SEM0 + int(t))
+        states.append(st)
+    tok = draft_tokens(states, drf, de, parent, R)
+    path, nacc, emit, nemit, new_states = run_accept(lib, states, tgt, drf, te, de, parent, tok,
+                                                     n_sess, R)
+    total_acc = 0
+    for s in range(n_sess):
+        st = po.copy_state(states[s])
+        p_ref, e_ref = po.accept_tree(st, tgt[s * R:(s + 1) * R], drf[s * R:(s + 1) * R], parent,
+                                      tok[s * R:(s + 1) * R], te[s * R:(s + 1) * R],
+                                      de[s * R:(s + 1) * R])
+        assert nacc[s] == len(p_ref) and list(path[s, :nacc[s]]) == list(p_ref), s
+        assert nemit[s] == len(e_ref) and list(emit[s, :nemit[s]]) == list(e_ref), s
+        assert bytes(new_states[s]) == bytes(st), s
+        total_acc += nacc[s]
+    if mode == "disjoint":
+        assert total_acc <= n_sess // 4  # only greedy rows can agree by chance
+    else:
+        assert total_acc > 0
+
+
+def test_accept_tree_bit_exact(lib):
+    """16-node tree (depth 4) + root: parent array of the tree config."""
+    parent = TREE16
+    R = len(parent)
+    r = np.random.default_rng(31)
+    n_sess = 4
+    tgt, drf, te, de = chain_inputs(r, R - 1, n_sess, "config1")
+    states = [po.state(temperature=0.8, top_p=0.8, seed=100 + s, entropy=s) for s in range(n_sess)]
+    tok = draft_tokens(states, drf, de, parent, R)
+    path, nacc, emit, nemit, new_states = run_accept(lib, states, tgt, drf, te, de, parent, tok,
+                                                     n_sess, R)
+    for s in range(n_sess):
+        st = po.copy_state(states[s])
+        p_ref, e_ref = po.accept_tree(st, tgt[s * R:(s + 1) * R], drf[s * R:(s + 1) * R], parent,
+                                      tok[s * R:(s + 1) * R], te[s * R:(s + 1) * R],
+                                      de[s * R:(s + 1) * R])
+        assert list(path[s, :nacc[s]]) == list(p_ref), s
+        assert list(emit[s, :nemit[s]]) == list(e_ref), s
+        assert bytes(new_states[s]) == bytes(st), s

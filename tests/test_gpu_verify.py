@@ -1,0 +1,227 @@
+"""Verify forward (s2p_verify_plan + s2p_verify_forward) vs the oracle's
+layer composition (run_layer restated, slowar.c:156-260), and properties of
+the full-size 36-layer step.
+
+Logits tolerance (north star): within 1e-2 relative (+1e-2 of the row RMS for
+near-zero logits) of the oracle's reference-order forward on the same
+weights, caches and inputs."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+import s2pamd
+from gpu_util import P, S, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+TREE16 = [-1, 0, 0, 1, 1, 2, 2, 3, 3, 4, 5, 6, 6, 7, 8, 10, 11]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return s2pamd.load()
+
+
+def make_backbone(lib, n_layers, quant, head_rows, max_rows, max_sessions, ctx, seed):
+    o = s2pamd.BackboneOpts(n_layers, quant, quant, head_rows, max_rows, max_sessions, ctx)
+    bb = ctypes.c_void_p()
+    s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(o), seed, S(), ctypes.byref(bb)),
+                 "backbone")
+    return bb
+
+
+def host_linear(lin):
+    if lin.q_packed:
+        w = d2h(lin.w_pack.data, lin.w_pack.bytes, np.uint8)
+        s = d2h(lin.w_iscale.data, lin.w_iscale.bytes, np.uint16)
+        keep = (w, s)
+        return po.make_linear(w, s, lin.out_features, lin.in_features, 32), keep
+    w = d2h(lin.w_int8.data, lin.w_int8.bytes, np.int8)
+    s = d2h(lin.w_iscale.data, lin.w_iscale.bytes, np.float32)
+    return po.make_linear(w, s, lin.out_features, lin.in_features, 0), (w, s)
+
+
+def host_layer(lib, bb, l):
+    L = lib.s2p_backbone_layer(bb, l).contents
+    keep = []
+    lins = []
+    for name in ("wqkv", "wo", "gate_up", "w2"):
+        li, k = host_linear(getattr(L, name))
+        lins.append(li)
+        keep.append(k)
+    norms = [d2h(getattr(L, n).data, getattr(L, n).bytes, np.uint16)
+             for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm")]
+    keep.append(norms)
+    lw = po.OrLayerW(lins[0], lins[1], lins[2], lins[3], *(po.ptr(n) for n in norms))
+    return lw, keep
+
+
+def new_kv(lib, bb, seed):
+    nbytes = lib.s2p_backbone_kv_bytes(bb)
+    kv = torch.empty(nbytes // 2, dtype=torch.int16, device="cuda")
+    s2pamd.hip_check(lib.s2p_synth_bf16_normal(P(kv), kv.numel(), 0.0, 1.0, seed, S()))
+    return kv
+
+
+def plan(lib, bb, parent, kvs, lens):
+    n = len(kvs)
+    par = np.asarray(parent, np.int32)
+    kvp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in kvs])
+    ln = np.asarray(lens, np.int32)
+    vb = s2pamd.VerifyBatch(n, len(parent), par.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
+    s2pamd.check(lib.s2p_verify_plan(bb, ctypes.byref(vb), S()), "plan")
+
+
+def oracle_forward(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_rows):
+    """Oracle forward of one session (rows = len(parent)) on host copies."""
+    R = len(parent)
+    depth = [0] * R
+    vis = np.zeros(R, np.uint64)
+    for i in range(R):
+        if i:
+            depth[i] = depth[parent[i]] + 1
+        m, j = 0, i
+        while j >= 0:
+            m |= 1 << j
+            j = parent[j]
+        vis[i] = m
+    pos = np.array([L + d for d in depth], np.int32)
+    x = np.array(x, np.uint16, copy=True)
+    kv = kv_host.reshape(n_layers, 16, ctx, 128)
+    chain = all(parent[i] == i - 1 for i in range(1, R))
+    for l in range(n_layers):
+        lw, keep = host_layer(lib, bb, l)
+        kc = np.ascontiguousarray(kv[l, :8])
+        vc = np.ascontiguousarray(kv[l, 8:])
+        po.layer(lw, x, R, kc, vc, ctx, L, pos, None if chain else vis)
+        kv[l, :8] = kc
+        kv[l, 8:] = vc
+    fnorm = d2h(lib.s2p_backbone_final_norm(bb), 2560 * 2, np.uint16)
+    xn = po.rms_norm(x, fnorm, R, 2560)
+    head, keep = host_linear(lib.s2p_backbone_head(bb).contents)
+    return po.linear_fwd(head, xn, R), kv
+
+
+@pytest.mark.parametrize("quant,n_layers,L", [(s2pamd.WQ_INT4, 2, 100), (s2pamd.WQ_INT8, 1, 512)])
+def test_verify_chain_vs_oracle(lib, quant, n_layers, L):
+    """Config 1/2 shapes: K=4 chain (M=5) over one session's cache."""
+    ctx = 640
+    bb = make_backbone(lib, n_layers, quant, s2pamd.S2P_HEAD_SLICE, 16, 2, ctx, 1234)
+    try:
+        parent = [-1, 0, 1, 2, 3]
+        R = len(parent)
+        kv = new_kv(lib, bb, 77)
+        kv_host = to_host(kv, np.uint16).copy()
+        plan(lib, bb, parent, [kv], [L])
+        x = bf16_bits(np.random.default_rng(5).standard_normal((R, 2560)).astype(np.float32))
+        logits = empty((R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
+        got = bf16_vals(to_host(logits, np.uint16))
+        want, kv_ref = oracle_forward(lib, bb, n_layers, x, kv_host, ctx, L, parent,
+                                      s2pamd.S2P_HEAD_SLICE)
+        assert_close_rel(got, bf16_vals(want), what="chain logits")
+        # the verify rows' K/V landed in slots L..L+R-1; everything else untouched
+        kv_dev = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
+        kv_ref = kv_ref.reshape(n_layers, 16, ctx, 128)
+        assert np.array_equal(kv_dev[:, :, :L], kv_ref[:, :, :L])
+        assert np.array_equal(kv_dev[:, :, L + R:], kv_ref[:, :, L + R:])
+        assert_close_rel(bf16_vals(kv_dev[:, :, L:L + R]), bf16_vals(kv_ref[:, :, L:L + R]),
+                         rel=2e-2, floor_frac=2e-2, what="appended K/V")
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+def test_verify_tree_two_sessions_vs_oracle(lib):
+    """Config 5 shape on 2 layers: 16-node tree + root, two sessions with
+    different prefix lengths, tree visibility masks."""
+    ctx, n_layers = 512, 2
+    R = len(TREE16)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 2 * R, 2, ctx, 99)
+    try:
+        kvs = [new_kv(lib, bb, 5), new_kv(lib, bb, 6)]
+        hosts = [to_host(k, np.uint16).copy() for k in kvs]
+        lens = [130, 301]
+        plan(lib, bb, TREE16, kvs, lens)
+        x = bf16_bits(np.random.default_rng(8).standard_normal((2 * R, 2560)).astype(np.float32))
+        logits = empty((2 * R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
+        got = bf16_vals(to_host(logits, np.uint16))
+        for s in range(2):
+            want, _ = oracle_forward(lib, bb, n_layers, x[s * R:(s + 1) * R], hosts[s], ctx,
+                                     lens[s], TREE16, s2pamd.S2P_HEAD_SLICE)
+            assert_close_rel(got[s * R:(s + 1) * R], bf16_vals(want), what=f"tree session {s}")
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+def test_verify_full_size_step_properties(lib):
+    """Config 3: 36L INT4-g32, full 155,776-row head, K=4, ctx 2048.
+    Deterministic, finite, graph replay == eager, acceptance sane."""
+    ctx = 2304
+    side = torch.cuda.Stream()  # graphs cannot be captured on the legacy default stream
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        _full_size_body(lib, ctx)
+    torch.cuda.synchronize()
+
+
+def _full_size_body(lib, ctx):
+    bb = make_backbone(lib, 36, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB, 16, 1, ctx, 7)
+    try:
+        kv = new_kv(lib, bb, 11)
+        parent = [-1, 0, 1, 2, 3]
+        R = 5
+        plan(lib, bb, parent, [kv], [2048])
+        x = to_dev(bf16_bits(np.random.default_rng(1).standard_normal((R, 2560)).astype(np.float32)))
+        l1 = empty((R, s2pamd.S2P_VOCAB))
+        l2 = empty((R, s2pamd.S2P_VOCAB))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(x), P(l1), S()))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(x), P(l2), S()))
+        a, b = to_host(l1, np.uint16), to_host(l2, np.uint16)
+        assert np.array_equal(a, b), "forward is not deterministic"
+        v = bf16_vals(a)
+        assert np.all(np.isfinite(v)) and v.std() > 0.1
+        # full step through the graph path, twice, equals the eager path
+        drf = to_dev(bf16_bits(bf16_vals(a) + np.random.default_rng(3).standard_normal(
+            a.shape).astype(np.float32) * 0.5))
+        st = po.state(temperature=0.8, top_p=0.8, seed=0, entropy=0)
+        states = [st]
+        outs = []
+        for use_graph in (0, 1, 1):
+            d_states = to_dev(np.frombuffer(bytes(st), np.uint8).copy())
+            d_ptrs = to_dev(np.array([d_states.data_ptr()], np.int64))
+            tok = np.zeros(R, np.int64)
+            sd = po.copy_state(st)
+            dv = to_host(drf, np.uint16)
+            for i in range(1, R):
+                tok[i] = po.sample(sd, dv[i - 1])[0]
+            work = torch.empty(lib.s2p_verify_accept_work_bytes(1, R), dtype=torch.uint8,
+                               device="cuda")
+            path = torch.zeros(R, dtype=torch.int32, device="cuda")
+            nacc = torch.zeros(1, dtype=torch.int32, device="cuda")
+            emit = torch.zeros(R + 1, dtype=torch.int64, device="cuda")
+            nemit = torch.zeros(1, dtype=torch.int32, device="cuda")
+            logits = empty((R, s2pamd.S2P_VOCAB))
+            io = s2pamd.StepIO(x.data_ptr(), logits.data_ptr(), drf.data_ptr(), s2pamd.S2P_VOCAB,
+                               to_dev(np.array(parent, np.int32)).data_ptr(),
+                               to_dev(tok).data_ptr(), d_ptrs.data_ptr(), path.data_ptr(),
+                               nacc.data_ptr(), emit.data_ptr(), nemit.data_ptr(),
+                               work.data_ptr())
+            keep = (d_states, d_ptrs, work, path, nacc, emit, nemit, logits)
+            s2pamd.check(lib.s2p_verify_step(bb, ctypes.byref(io), use_graph, S()), "step")
+            lg = to_host(logits, np.uint16)
+            assert np.array_equal(lg, a)
+            n = int(to_host(nemit)[0])
+            outs.append((int(to_host(nacc)[0]), list(to_host(emit)[:n])))
+            # host rule on the same logits
+            st_ref = po.copy_state(st)
+            p_ref, e_ref = po.accept_tree(st_ref, lg, to_host(drf, np.uint16), parent, tok)
+            assert outs[-1] == (len(p_ref), list(e_ref))
+            del keep
+        assert outs[0] == outs[1] == outs[2]
+        assert states
+    finally:
+        lib.s2p_backbone_free(bb)
