@@ -20,7 +20,8 @@
  * The waves merge through LDS; a block writes its (m, l, O) partial, and a
  * combine kernel merges splits (log-sum-exp) unless there is one split.
  * Scores are (q . k) * 1/sqrt(128) with q, k bf16 exact products and fp32
- * sums; P enters the PV product rounded to bf16.  Parity is by tolerance
+ * sums; P enters the PV product as a bf16 hi + lo pair (two MFMAs), so the
+ * PV sum sees P to ~2^-16 relative.  Parity is by tolerance
  * against the reference order (oracle or_attention / or_attention_split).
  */
 #include <hip/hip_runtime.h>
@@ -80,14 +81,15 @@ S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
         s.row0 = seg * AT_SEG_ROWS;
         s.nrows = min(AT_SEG_ROWS, a.rows - s.row0);
         s.L = a.pos0 + s.row0;
-        s.span = s.L + s.nrows;
+        s.span = min(s.L + s.nrows, a.max_seq); /* never read past the cache */
         s.kp = a.kc + (size_t)kvh * a.max_seq * AT_HD;
         s.vp = a.vc + (size_t)kvh * a.max_seq * AT_HD;
     } else if (a.mode == AM_PTRS) {
         s.row0 = seg;
-        s.nrows = 1;
         s.L = a.pos[seg];
-        s.span = s.L + 1;
+        /* a position outside the cache attends nothing (and reads nothing) */
+        s.nrows = (s.L >= 0 && s.L < a.max_seq) ? 1 : 0;
+        s.span = s.nrows ? s.L + 1 : 0;
         s.kp = a.kcs[seg] + (size_t)kvh * a.max_seq * AT_HD;
         s.vp = a.vcs[seg] + (size_t)kvh * a.max_seq * AT_HD;
     } else {
@@ -138,6 +140,7 @@ template <int MQT>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     __shared__ __align__(16) uint16_t s_v[AT_WAVES][AT_TILE][AT_VSTRIDE];
     __shared__ __align__(16) uint16_t s_p[AT_WAVES][32][AT_PSTRIDE];
+    __shared__ __align__(16) uint16_t s_pl[AT_WAVES][32][AT_PSTRIDE];
     __shared__ float s_ml[AT_WAVES][32][2];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -234,14 +237,21 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
                 m[qt][v] = mn;
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
-                s_p[wave][16 * qt + 4 * qq + v][c] = f2bf(p0);
-                s_p[wave][16 * qt + 4 * qq + v][16 + c] = f2bf(p1);
+                /* P = hi + lo, both bf16: 16 significant bits into the PV MFMA */
+                const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
+                s_p[wave][16 * qt + 4 * qq + v][c] = h0;
+                s_p[wave][16 * qt + 4 * qq + v][16 + c] = h1;
+                s_pl[wave][16 * qt + 4 * qq + v][c] = f2bf(p0 - bf2f(h0));
+                s_pl[wave][16 * qt + 4 * qq + v][16 + c] = f2bf(p1 - bf2f(h1));
             }
         }
         wave_sync_lds();
-        s2p_u32x4 pa[MQT];
+        s2p_u32x4 pa[MQT], pl[MQT];
 #pragma unroll
-        for (int qt = 0; qt < MQT; qt++) pa[qt] = *(const s2p_u32x4*)&s_p[wave][16 * qt + c][8 * qq];
+        for (int qt = 0; qt < MQT; qt++) {
+            pa[qt] = *(const s2p_u32x4*)&s_p[wave][16 * qt + c][8 * qq];
+            pl[qt] = *(const s2p_u32x4*)&s_pl[wave][16 * qt + c][8 * qq];
+        }
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             uint32_t b[4];
@@ -251,7 +261,10 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
                        ((uint32_t)s_v[wave][8 * qq + 2 * e + 1][16 * dt + c] << 16);
             const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
 #pragma unroll
-            for (int qt = 0; qt < MQT; qt++) o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+            for (int qt = 0; qt < MQT; qt++) {
+                o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+            }
         }
         wave_sync_lds();
     }

@@ -31,6 +31,10 @@ S2P_DEV float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
 S2P_DEV uint16_t f2h(float f) {
+    /* materialise f as a float first: without the barrier the compiler may
+     * fold a preceding multiply and this conversion into one v_fma_mix
+     * (a single rounding where the reference rounds to f32, then to f16) */
+    asm volatile("" : "+v"(f));
     return __half_as_ushort(__float2half_rn(f));
 }
 

@@ -12,10 +12,10 @@
  *    A 4x4 transpose across lane quarters (v_permlane32_swap then
  *    v_permlane16_swap) turns four such loads into the A operands of four
  *    v_mfma_f32_16x16x32_bf16, one per group, 16 rows x 32 k each.
- *  - INT4 -> bf16 in registers: nibbles XOR 8 are OR-ed into the mantissa of
- *    bf16 128.0, giving 136 + w exactly (one v_and_or per two weights); the
- *    bias is removed per group with the activation group sum:
- *        sum_k (136 + w_k) x_k  -  136 * sum_k x_k.
+ *  - INT4 -> bf16 in registers: nibbles XOR 8 are OR-ed into the top
+ *    mantissa bits of bf16 1.0, giving 1.5 + w/16 exactly (a shift and one
+ *    v_and_or per two weights); the bias is removed per group with the
+ *    activation group sum:  16 * (sum_k (1.5 + w_k/16) x_k - 1.5 sum_k x_k).
  *    The f16 group scale is applied per group in fp32 (as the reference's
  *    acc += s * gs, int8_gemv.cu:312), not folded into bf16 weights.
  *  - INT8 per channel: bytes XOR 0x80 converted with v_cvt_f32_ubyte*, the
@@ -70,15 +70,17 @@ S2P_DEV void xpose4(uint32_t& d0, uint32_t& d1, uint32_t& d2, uint32_t& d3) {
     d3 = s23[1];
 }
 
-/* 8 nibbles (two's complement) -> 8 bf16 holding 136 + w, in k-slot order
- * 0,4,1,5,2,6,3,7. */
+/* 8 nibbles (two's complement w) -> 8 bf16 holding 1.5 + w/16 exactly (the
+ * nibble XOR 8 lands in the top 4 mantissa bits of bf16 1.0), in k-slot order
+ * 0,4,1,5,2,6,3,7.  The dot product is then 16 * (raw - 1.5 * sum(x)); the
+ * 1.5 bias keeps the cancellation small (|1.5 sum x| ~ 5 |w.x / 16|). */
 S2P_DEV s2p_u32x4 deq_int4(uint32_t d) {
     d ^= 0x88888888u;
     s2p_u32x4 a;
-    a.x = (d & 0x000F000Fu) | 0x43004300u;
-    a.y = ((d >> 4) & 0x000F000Fu) | 0x43004300u;
-    a.z = ((d >> 8) & 0x000F000Fu) | 0x43004300u;
-    a.w = ((d >> 12) & 0x000F000Fu) | 0x43004300u;
+    a.x = ((d << 3) & 0x00780078u) | 0x3F803F80u;
+    a.y = ((d >> 1) & 0x00780078u) | 0x3F803F80u;
+    a.z = ((d >> 5) & 0x00780078u) | 0x3F803F80u;
+    a.w = ((d >> 9) & 0x00780078u) | 0x3F803F80u;
     return a;
 }
 
@@ -98,6 +100,7 @@ S2P_DEV s2p_u32x2 deq_int8(uint32_t d) {
 /* silu(g) * u with the two bf16 roundings of kernels.cu:1216-1229; exp is
  * the rule's s2p_expf so the value matches the host oracle bit for bit. */
 S2P_DEV uint16_t silu_mul_bf16(uint16_t g16, uint16_t u16) {
+#pragma clang fp contract(off)
     const float g = bf2f(g16);
     const float u = bf2f(u16);
     const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, s2p_expf(-g)));
@@ -117,6 +120,7 @@ struct GemvSmem {
 template <int WFMT>
 __device__ void stage_chunk(const GemvArgs& a, GemvSmem& sm, int g0, int gn, int M,
                             int Mpad, int rb) {
+#pragma clang fp contract(off)
     const int tid = threadIdx.x;
     const int chk = gn * 32; /* k elements in this chunk */
     /* activations: one thread per (m, 8-block) */
@@ -287,10 +291,10 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
                             *(const s2p_u32x4*)(sm.x + (size_t)m * sm.xstride + gl * 32 + q * 8);
                         const float xsum = sm.xs[m * GEMV_CHUNK_GROUPS + gl];
                         const s2p_f32x4 raw = mfma16x16x32(av, bv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
-                        acc[t][0] = fmaf(s0, fmaf(-136.0f, xsum, raw[0]), acc[t][0]);
-                        acc[t][1] = fmaf(s1, fmaf(-136.0f, xsum, raw[1]), acc[t][1]);
-                        acc[t][2] = fmaf(s2, fmaf(-136.0f, xsum, raw[2]), acc[t][2]);
-                        acc[t][3] = fmaf(s3, fmaf(-136.0f, xsum, raw[3]), acc[t][3]);
+                        acc[t][0] = fmaf(s0, fmaf(-1.5f, xsum, raw[0]), acc[t][0]);
+                        acc[t][1] = fmaf(s1, fmaf(-1.5f, xsum, raw[1]), acc[t][1]);
+                        acc[t][2] = fmaf(s2, fmaf(-1.5f, xsum, raw[2]), acc[t][2]);
+                        acc[t][3] = fmaf(s3, fmaf(-1.5f, xsum, raw[3]), acc[t][3]);
                     }
                 }
             } else {
@@ -319,7 +323,13 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         }
     }
 
-    if (WFMT == GEMV_W_INT8) {
+    if (WFMT == GEMV_W_INT4) {
+        /* undo the 1/16 of the dequantised weights (exact power of two) */
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[t][i] *= 16.0f;
+    } else {
         /* remove the 128 * sum(x) bias; the lanes of quarter 0 carry the
          * column sums, broadcast them to the other quarters */
 #pragma unroll
@@ -348,6 +358,12 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         return;
     }
 
+    /* Split-K handoff without cache maintenance.  The 8 XCD L2s are not
+     * coherent, and an agent-scope fence would write back / invalidate the
+     * whole L2 per workgroup.  Instead every access to the partials and the
+     * counter is an agent-scope atomic (device-coherent loads and stores),
+     * and each workgroup waits for its partial stores to complete before it
+     * signals arrival; the last arrival then reads every split. */
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         const int m = t * 16 + r;
@@ -356,20 +372,20 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         for (int i = 0; i < 4; i++) {
             const int n = n0 + q * 4 + i;
             if (n >= a.N) continue;
-            a.part[((size_t)sp * M + m) * a.N + n] = acc[t][i];
+            __hip_atomic_store(&a.part[((size_t)sp * M + m) * a.N + n], acc[t][i],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __shared__ int s_last;
-    __threadfence();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_ACQ_REL,
+        const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == (unsigned)(a.splits - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
     /* last workgroup of this row block: deterministic split-order sum */
     for (int base = 0; base < M * 64; base += 256) {
@@ -380,7 +396,8 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         if (m < M && n < a.N) {
             float s = 0.f;
             for (int k = 0; k < a.splits; k++)
-                s += __builtin_nontemporal_load(&a.part[((size_t)k * M + m) * a.N + n]);
+                s += __hip_atomic_load(&a.part[((size_t)k * M + m) * a.N + n],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (WFMT == GEMV_W_INT8) s *= ((const float*)a.s)[n];
             const uint16_t yb = f2bf(s);
             uint16_t* yp = a.y + (size_t)m * a.ldy + n;

@@ -14,6 +14,7 @@
  * lives in device memory, so a captured graph replays for any plan of the
  * same shape.
  */
+#include <math.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -84,10 +85,16 @@ static s2p_status norm_weight(s2p_tensor* t, int n, uint64_t seed, hipStream_t s
     return hip_ok(s2p_synth_bf16_normal(t->data, n, 1.0f, 0.02f, seed, st), "norm init");
 }
 
+/* Random weights at rms 1/sqrt(in), the scale of trained projections, so a
+ * synthetic stack keeps activations O(1) layer to layer.  The scale sigma is
+ * the group / row scale; the code rms is sqrt(255/12) for uniform nibbles
+ * (offset 8) and ~73.9 for uniform bytes (offset 128). */
 static s2p_status rand_linear(s2p_linear* l, s2p_weight_q q, int in, int out, uint64_t seed,
                               hipStream_t st) {
-    if (q == S2P_WQ_INT4_G32) return s2p_linear_init_random_int4(l, in, out, 32, 0.02f, seed, st);
-    return s2p_linear_init_random_int8(l, in, out, 0.001f, seed, st);
+    const float w_rms = 1.0f / sqrtf((float)in);
+    if (q == S2P_WQ_INT4_G32)
+        return s2p_linear_init_random_int4(l, in, out, 32, w_rms / 4.61f, seed, st);
+    return s2p_linear_init_random_int8(l, in, out, w_rms / 73.9f, seed, st);
 }
 
 static s2p_status dalloc(void** p, size_t bytes) {
@@ -212,6 +219,17 @@ size_t s2p_backbone_weight_bytes(const s2p_backbone* b) {
         t += lin_bytes(&L->wqkv) + lin_bytes(&L->wo) + lin_bytes(&L->gate_up) + lin_bytes(&L->w2);
     }
     return t;
+}
+
+/* Activation buffers of the last forward (diagnostics and stage-level parity
+ * tests; not part of the public header). */
+void s2p_backbone_debug_ptrs(s2p_backbone* b, void** x, void** qkv, void** q, void** attn,
+                             void** gu) {
+    if (x) *x = b->x;
+    if (qkv) *qkv = b->qkv;
+    if (q) *q = b->q;
+    if (attn) *attn = b->attn;
+    if (gu) *gu = b->gu;
 }
 
 /* ------------------------------------------------------------------ plan */

@@ -176,6 +176,7 @@ __global__ __launch_bounds__(256) void k_kv_append(const uint16_t* __restrict__ 
         const int e = (int)(idx % per_row) * 8;
         const int h = e / head_dim, d = e % head_dim;
         const int p = pos_arr ? pos_arr[r] : pos0 + r;
+        if (p < 0 || p >= max_seq) continue; /* out-of-range position: nothing written */
         uint16_t* kc = kcs ? kcs[r] : kc0;
         uint16_t* vc = vcs ? vcs[r] : vc0;
         const size_t src = (size_t)r * kv_heads * head_dim + e;
@@ -382,13 +383,14 @@ extern "C" hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq
 __global__ __launch_bounds__(64) void k_kv_commit(S2pRowPlan plan, const int32_t* __restrict__ path,
                                                   const int32_t* __restrict__ n_acc, int R) {
     const int s = blockIdx.x, layer = blockIdx.y, plane = blockIdx.z, lane = threadIdx.x;
-    const int n = n_acc[s];
+    int n = n_acc[s];
+    n = n < 0 ? 0 : (n > R - 1 ? R - 1 : n);
     const int L = plan.slot[s * R];
     uint16_t* base = (uint16_t*)plan.kv[s] + (size_t)layer * plan.layer_stride +
                      (size_t)plane * plan.max_seq * 128;
     for (int d = 1; d <= n; d++) {
         const int node = path[(size_t)s * R + d - 1];
-        if (node == d) continue;
+        if (node == d || node < d || node >= R) continue; /* chain slot, or invalid */
         const uint32_t* src = (const uint32_t*)(base + (size_t)(L + node) * 128);
         uint32_t* dst = (uint32_t*)(base + (size_t)(L + d) * 128);
         dst[lane] = src[lane];

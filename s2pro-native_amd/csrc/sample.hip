@@ -433,9 +433,16 @@ __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
     if (threadIdx.x == 0) {
         sh.st = *a.states[s];
         /* push the drafted tokens of the root path (root excluded) */
+        /* root path; parent indices are validated (parent[u] in [0, u)) so a
+         * malformed tree ends the walk instead of reading out of bounds */
         int path[64];
         int n = 0;
-        for (int u = v; u > 0 && n < 64; u = a.parent[u]) path[n++] = u;
+        for (int u = v; u > 0 && u < a.R && n < 64;) {
+            path[n++] = u;
+            const int p = a.parent[u];
+            if (p < 0 || p >= u) break;
+            u = p;
+        }
         for (int i = n - 1; i >= 0; i--) state_push(&sh.st, a.tok[(size_t)s * a.R + path[i]]);
     }
     __syncthreads();

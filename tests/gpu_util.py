@@ -9,6 +9,11 @@ import s2pamd
 
 DEV = "cuda:0"
 _hip = None
+# Every device buffer made by to_dev()/empty() stays referenced until the test
+# ends (conftest clears it after a device synchronisation): pointers handed to
+# the C ABI must never outlive their torch tensor, whose block the caching
+# allocator would otherwise hand to the next allocation.
+LIVE = []
 
 
 def hip():
@@ -46,12 +51,13 @@ def to_dev(a):
     """numpy -> device tensor (uint16 travels as int16 bits)."""
     a = np.ascontiguousarray(a)
     if a.dtype == np.uint16:
-        return torch.from_numpy(a.view(np.int16)).to(DEV)
-    if a.dtype == np.uint8:
-        return torch.from_numpy(a).to(DEV)
-    if a.dtype == np.uint64:
-        return torch.from_numpy(a.view(np.int64)).to(DEV)
-    return torch.from_numpy(a).to(DEV)
+        t = torch.from_numpy(a.view(np.int16)).to(DEV)
+    elif a.dtype == np.uint64:
+        t = torch.from_numpy(a.view(np.int64)).to(DEV)
+    else:
+        t = torch.from_numpy(a).to(DEV)
+    LIVE.append(t)
+    return t
 
 
 def to_host(t, dtype=None):
@@ -63,7 +69,9 @@ def to_host(t, dtype=None):
 
 
 def empty(shape, dtype=torch.int16):
-    return torch.empty(shape, dtype=dtype, device=DEV)
+    t = torch.empty(shape, dtype=dtype, device=DEV)
+    LIVE.append(t)
+    return t
 
 
 def P(t):
@@ -94,3 +102,19 @@ def assert_close_rel(got, want, rel=1e-2, floor_frac=1e-2, what=""):
     assert not bad.any(), (
         f"{what}: {int(bad.sum())}/{bad.size} beyond tolerance; max err {err.max():.4g} "
         f"(rms {rms:.4g}); worst at {np.unravel_index(np.argmax(err - bound), err.shape)}")
+
+
+def assert_close_norm(got, want, rel=1e-2, what=""):
+    """Per row: ||got - want||_2 <= rel ||want||_2 and
+    max|got - want| <= rel max|want| (norm-relative error); rel may be a
+    per-row array."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    d = got - want
+    l2 = np.linalg.norm(d, axis=-1) / np.maximum(np.linalg.norm(want, axis=-1), 1e-30)
+    mx = np.abs(d).max(axis=-1) / np.maximum(np.abs(want).max(axis=-1), 1e-30)
+    rel = np.broadcast_to(np.asarray(rel, np.float64), l2.shape)
+    assert (l2 <= rel).all() and (mx <= rel).all(), (
+        f"{what}: worst row L2 rel {l2.max():.3g} (row {int(l2.argmax())}), "
+        f"worst row max-norm rel {mx.max():.3g} (row {int(mx.argmax())}), "
+        f"tolerance {rel.min():.3g}..{rel.max():.3g}")

