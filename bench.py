@@ -217,7 +217,7 @@ def main():
         "wall_s_timed": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_mfma<INT4, MT=1> (all 145 weight GEMVs of a step)",
+                     "kernel": "k_gemv<INT4, MT=1> (all 145 weight GEMVs of a step)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "alg_bytes_per_launch": int(per_launch)},
     }

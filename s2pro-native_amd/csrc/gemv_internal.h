@@ -13,8 +13,11 @@ extern "C" {
 #define GEMV_MAX_M 128         /* rows per call (8 MFMA column tiles) */
 
 enum { GEMV_W_INT4 = 0, GEMV_W_INT8 = 1 };            /* weight formats */
-enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1, GEMV_X_SILU = 2 }; /* staging */
-enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1 };       /* epilogues */
+enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1 };            /* activation staging */
+/* STORE: y = bf16(W x); RESID: y = bf16(y + bf16(W x)) plus per-64-column
+ * sums of squares; SWIGLU: W = [gate; up] (2F rows), y[m][F] =
+ * silu(bf16(gate)) * bf16(up) with the rule's roundings. */
+enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1, GEMV_EPI_SWIGLU = 2 };
 
 typedef struct {
     const uint8_t*  w;       /* INT4: packed [N][K/2]; INT8: [N][K] */
@@ -25,8 +28,10 @@ typedef struct {
     int             ldy;
     int             M, N, K;
     int             wfmt;
-    int             gps;     /* 32-k groups per split (multiple of 4) */
+    int             gps;     /* 32-k groups per split (multiple of 4); 0 = auto */
     int             splits;  /* derived by the launcher */
+    int             win;     /* derived: staged groups per LDS window */
+    int             nrb;     /* derived: 64-row blocks */
     int             xmode;
     const uint16_t* norm_w;  /* NORM: bf16 [K] */
     float           norm_eps;
@@ -34,7 +39,8 @@ typedef struct {
     int             ssq_in_blocks;
     int             epi;
     float*          ssq_out; /* RESID: [ceil(N/64)][GEMV_MAX_M] (may be NULL) */
-    float*          part;    /* [splits][M][N] fp32 */
+    float*          part;    /* [splits][M][nrb][64] fp32 */
+    int64_t         part_cap;/* floats available at part */
     unsigned*       counters;/* [ceil(N/64)], zero between calls */
 } GemvArgs;
 

@@ -73,27 +73,9 @@ void s2p_gemm_shutdown(void) {
 
 /* internal accessors for the verify forward (same scratch, same rules) */
 float* s2p_gemm_ctx_part(void) { return g.part; }
+int64_t s2p_gemm_ctx_part_cap(void) { return CTX_PART_FLOATS; }
 unsigned* s2p_gemm_ctx_counters(void) { return g.counters; }
 int s2p_gemm_ctx_ready(void) { return g.inited; }
-
-/* 32-k groups per split for an [N, K] GEMV at M rows. */
-int s2p_gemv_pick_gps(int M, int N, int K) {
-    const int G = K / 32;
-    const int rb = (N + 63) / 64;
-    int S = (g.target_wg + rb - 1) / rb;
-    if (S < 1) S = 1;
-    int gps = (G + S - 1) / S;
-    if (gps < 8) gps = 8;
-    gps = (gps + 3) & ~3;
-    if (gps > G) gps = (G + 3) & ~3;
-    /* the partials of all splits must fit the context buffer */
-    for (;;) {
-        const int splits = (G + gps - 1) / gps;
-        if (splits <= 1 || (size_t)splits * M * N <= CTX_PART_FLOATS) break;
-        gps += 4;
-    }
-    return gps;
-}
 
 /* Fill the descriptor of a plain GEMV on the context scratch. */
 void s2p_gemv_args_plain(GemvArgs* a, int wfmt, const void* w, const void* s, const void* x,
@@ -109,10 +91,11 @@ void s2p_gemv_args_plain(GemvArgs* a, int wfmt, const void* w, const void* s, co
     a->N = N;
     a->K = K;
     a->wfmt = wfmt;
-    a->gps = s2p_gemv_pick_gps(M, N, K);
+    a->gps = 0; /* the launcher sizes the splits */
     a->xmode = GEMV_X_PLAIN;
     a->epi = GEMV_EPI_STORE;
     a->part = g.part;
+    a->part_cap = CTX_PART_FLOATS;
     a->counters = g.counters;
 }
 

@@ -27,8 +27,8 @@
 #include "../synth_internal.h"
 
 float* s2p_gemm_ctx_part(void);
+int64_t s2p_gemm_ctx_part_cap(void);
 unsigned* s2p_gemm_ctx_counters(void);
-int s2p_gemv_pick_gps(int M, int N, int K);
 
 #define NORM_EPS 1e-6f
 #define ROPE_BASE 1000000.0f
@@ -44,7 +44,7 @@ struct s2p_backbone {
     void* qkv;    /* [max_rows][6144] */
     void* q;      /* [max_rows][4096] */
     void* attn;   /* [max_rows][4096] */
-    void* gu;     /* [max_rows][19456] */
+    void* gu;     /* [max_rows][9728] SwiGLU output h */
     float* ssq;   /* [2][64][GEMV_MAX_M] per-block sums of squares */
     float* attn_part;
     int64_t attn_part_floats;
@@ -330,7 +330,7 @@ static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, voi
     a.M = M;
     a.N = lin->out_features;
     a.K = lin->in_features;
-    a.gps = s2p_gemv_pick_gps(M, a.N, a.K);
+    a.gps = 0;
     a.xmode = xmode;
     a.norm_w = (const uint16_t*)norm_w;
     a.norm_eps = NORM_EPS;
@@ -339,6 +339,7 @@ static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, voi
     a.epi = epi;
     a.ssq_out = ssq_out;
     a.part = s2p_gemm_ctx_part();
+    a.part_cap = s2p_gemm_ctx_part_cap();
     a.counters = s2p_gemm_ctx_counters();
     return hip_ok(s2p_gemv_launch(&a, st), "verify gemv");
 }
@@ -361,9 +362,9 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
                                             b->max_span, b->attn_part, st), "attention"));
         S2P_TRY(gemv(&L->wo, M, b->attn, S2P_Q_HEADS * S2P_HEAD_DIM, b->x, S2P_DIM, GEMV_X_PLAIN,
                      NULL, NULL, GEMV_EPI_RESID, ssq_b, st));
-        S2P_TRY(gemv(&L->gate_up, M, b->x, S2P_DIM, b->gu, 2 * S2P_FFN_DIM, GEMV_X_NORM,
-                     L->ffn_norm.data, ssq_b, GEMV_EPI_STORE, NULL, st));
-        S2P_TRY(gemv(&L->w2, M, b->gu, 2 * S2P_FFN_DIM, b->x, S2P_DIM, GEMV_X_SILU, NULL, NULL,
+        S2P_TRY(gemv(&L->gate_up, M, b->x, S2P_DIM, b->gu, S2P_FFN_DIM, GEMV_X_NORM,
+                     L->ffn_norm.data, ssq_b, GEMV_EPI_SWIGLU, NULL, st));
+        S2P_TRY(gemv(&L->w2, M, b->gu, S2P_FFN_DIM, b->x, S2P_DIM, GEMV_X_PLAIN, NULL, NULL,
                      GEMV_EPI_RESID, ssq_a, st));
     }
     return gemv(&b->head, M, b->x, S2P_DIM, logits, b->head.out_features, GEMV_X_NORM,

@@ -295,7 +295,7 @@ def test_verify_stages_one_layer(lib, quant, L):
         g_qkv = d2h(ptrs[1].value, R * 6144 * 2, np.uint16).reshape(R, 6144)
         g_q = d2h(ptrs[2].value, R * 4096 * 2, np.uint16).reshape(R, 4096)
         g_attn = d2h(ptrs[3].value, R * 4096 * 2, np.uint16).reshape(R, 4096)
-        g_gu = d2h(ptrs[4].value, R * 19456 * 2, np.uint16).reshape(R, 19456)
+        g_h = d2h(ptrs[4].value, R * 9728 * 2, np.uint16).reshape(R, 9728)
         g_kv = to_host(kv, np.uint16).reshape(1, 16, ctx, 128)
         lw, keep = host_layer(lib, bb, 0)
         norms = keep[-1]  # attn_norm, ffn_norm, q_norm, k_norm
@@ -317,14 +317,13 @@ def test_verify_stages_one_layer(lib, quant, L):
         exact = po.attention_f64(g_q, np.ascontiguousarray(g_kv[0, :8]),
                                  np.ascontiguousarray(g_kv[0, 8:]), R, 32, 8, 128, L, ctx)
         assert np.max(np.abs(bf16_vals(g_attn) - exact)) < 2e-2, "attention"
-        # (d) wo + residual, ffn norm + gate_up
+        # (d) wo + residual, ffn norm + gate_up with the fused SwiGLU epilogue
         x_mid = po.add(x_in, po.linear_fwd(lw.wo, g_attn, R))
         xn2 = po.rms_norm(x_mid, norms[1], R, 2560)
-        assert_close_rel(bf16_vals(g_gu), bf16_vals(po.linear_fwd(lw.gate_up, xn2, R)),
-                         what="gate_up")
-        # (e) SwiGLU + w2 + residual on the GPU's gate_up output
-        h = po.silu_mul(g_gu, R, 9728)
-        x_out = po.add(x_mid, po.linear_fwd(lw.w2, h, R))
+        h_ref = po.silu_mul(po.linear_fwd(lw.gate_up, xn2, R), R, 9728)
+        assert_close_rel(bf16_vals(g_h), bf16_vals(h_ref), what="gate_up + SwiGLU")
+        # (e) w2 + residual on the GPU's SwiGLU output
+        x_out = po.add(x_mid, po.linear_fwd(lw.w2, g_h, R))
         assert_close_rel(bf16_vals(g_x), bf16_vals(x_out), what="layer output")
     finally:
         lib.s2p_backbone_free(bb)
