@@ -85,6 +85,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a plain 256 MiB device copy (3 launches): the reference "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; --gpus must be 1 "
@@ -92,6 +95,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calib:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        a.fill_(1)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": a.numel(), "copy_calib_bytes_written": b.numel(),
+                          "launches": 3}))
+        return
     import s2pamd
     lib = s2pamd.load()
     dev = torch.device("cuda:0")

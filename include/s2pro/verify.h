@@ -69,9 +69,10 @@ typedef struct {
 
 typedef struct s2p_backbone s2p_backbone;
 
-/* Random-init backbone (synthetic workloads): INT4-g32 weights uniform in
- * [-8,7] with f16 group scales |N(0,0.02)|, or INT8 uniform in [-127,127]
- * with f32 row scales |N(0,0.001)|; norm weights bf16 1 + N(0,0.02).
+/* Random-init backbone (synthetic workloads): INT4-g32 codes uniform in
+ * [-8,7] with f16 group scales |N(0, sigma)|, or INT8 codes uniform with f32
+ * row scales |N(0, sigma)|, sigma chosen so the weights have rms 1/sqrt(in)
+ * (the scale of trained projections); norm weights bf16 1 + N(0,0.02).
  * Calls s2p_gemm_init.  Synchronises `st`. */
 s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t seed,
                                       hipStream_t st, s2p_backbone** out);

@@ -630,20 +630,17 @@ __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : (MT == 2 ? 3 : 2)))) void k_gem
         }
         /* Split-K handoff without cache maintenance: the 8 XCD L2s are not
          * coherent and an agent-scope fence would write back / invalidate a
-         * whole L2, so the partials and the counter use agent-scope atomics
-         * (device-coherent accesses) and each workgroup waits for its partial
-         * stores to complete before it signals arrival. */
+         * whole L2, so the partials are written through to memory (sc1, the
+         * encoding of an agent-scope store; one 16-byte store per lane), read
+         * back with agent-scope atomic loads, and each workgroup waits for
+         * its partial stores to complete before it signals arrival. */
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const int m = t * 16 + r;
             if (m >= M) continue;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int l = wave * 16 + q * 4 + i;
-                __hip_atomic_store(
-                    &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + l], res[t][i],
-                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + wave * 16 + q * 4];
+            const s2p_f32x4 v4 = {res[t][0], res[t][1], res[t][2], res[t][3]};
+            asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst), "v"(v4) : "memory");
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
