@@ -44,6 +44,21 @@ def step_alg_bytes():
     return w, kv, w + kv + act
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_config3_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (copy-calibrated); None if the summary is absent."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s=20.0):
     """Scalar C oracle (one core): one layer (4 GEMVs in the reference lane
     order, norms, RoPE, attention over 2048 slots, SwiGLU) plus the head GEMV,
@@ -229,7 +244,9 @@ def main():
         "step_frac_of_peak": round(step_gbs / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "traffic_source": "profiles/gemv_int4_config3_traffic.md",
                      "kernel": "k_gemv<INT4, MT=1> (all 145 weight GEMVs of a step)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "alg_bytes_per_launch": int(per_launch)},
