@@ -1,0 +1,458 @@
+/* s2pro MI355X — device code of the decode / verify attention (see
+ * attention.hip for the design), shared by k_attn and the persistent verify
+ * kernel.  q, outputs and split partials go through the coherent accessors
+ * of coh.h; the KV cache is read with plain streaming loads (rows written in
+ * the same launch are written through before they are first read). */
+#ifndef S2P_ATTN_DEV_H
+#define S2P_ATTN_DEV_H
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "coh.h"
+#include "common.h"
+#include "prims_internal.h"
+
+#define AT_HD 128
+#define AT_TILE 32
+#define AT_WAVES 4
+#define AT_SEG_ROWS 8
+#define AT_VSTRIDE 136
+#define AT_PSTRIDE 40
+#define LDS(T) __attribute__((address_space(3))) T
+/* LDS carve-up of one attention block (bytes) */
+#define AT_SV_BYTES (AT_WAVES * AT_TILE * AT_VSTRIDE * 2)
+#define AT_SP_BYTES (AT_WAVES * 32 * AT_PSTRIDE * 2)
+#define AT_SML_BYTES (AT_WAVES * 32 * 2 * 4)
+#define AT_LDS_BYTES (AT_SV_BYTES + 2 * AT_SP_BYTES + AT_SML_BYTES + 16)
+
+enum { AM_CONTIG = 0, AM_PTRS = 1, AM_PLAN = 2 };
+
+struct AttnArgs {
+    int mode;
+    const uint16_t* q;
+    uint16_t* out;
+    int rows;
+    int qh, kvh_n;
+    /* CONTIG */
+    const uint16_t* kc;
+    const uint16_t* vc;
+    int pos0;
+    int max_seq;
+    /* PTRS */
+    const uint16_t* const* kcs;
+    const uint16_t* const* vcs;
+    const int32_t* pos;
+    /* PLAN */
+    S2pRowPlan plan;
+    const S2pAttnSeg* segs;
+    int layer;
+    /* splitting */
+    int nsplit;
+    int split_pos;
+    float* part;
+    /* non-NULL: the last split to finish a (segment, kv head) merges the
+     * splits itself (persistent kernel); NULL: k_attn_combine does */
+    unsigned* counters;
+};
+
+struct SegInfo {
+    const uint16_t* kp;
+    const uint16_t* vp;
+    int L, row0, nrows, span;
+    const uint64_t* vis; /* NULL: causal */
+};
+
+S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
+    SegInfo s;
+    s.vis = nullptr;
+    if (a.mode == AM_CONTIG) {
+        s.row0 = seg * AT_SEG_ROWS;
+        s.nrows = min(AT_SEG_ROWS, a.rows - s.row0);
+        s.L = a.pos0 + s.row0;
+        s.span = min(s.L + s.nrows, a.max_seq); /* never read past the cache */
+        s.kp = a.kc + (size_t)kvh * a.max_seq * AT_HD;
+        s.vp = a.vc + (size_t)kvh * a.max_seq * AT_HD;
+    } else if (a.mode == AM_PTRS) {
+        s.row0 = seg;
+        s.L = a.pos[seg];
+        /* a position outside the cache attends nothing (and reads nothing) */
+        s.nrows = (s.L >= 0 && s.L < a.max_seq) ? 1 : 0;
+        s.span = s.nrows ? s.L + 1 : 0;
+        s.kp = a.kcs[seg] + (size_t)kvh * a.max_seq * AT_HD;
+        s.vp = a.vcs[seg] + (size_t)kvh * a.max_seq * AT_HD;
+    } else {
+        const S2pAttnSeg g = a.segs[seg];
+        s.row0 = g.row0;
+        s.nrows = g.nrows;
+        s.L = g.L;
+        s.span = g.span;
+        const uint16_t* kv =
+            (const uint16_t*)a.plan.kv[g.sess] + (size_t)a.layer * a.plan.layer_stride;
+        s.kp = kv + (size_t)kvh * a.plan.max_seq * AT_HD;
+        s.vp = kv + (size_t)(a.kvh_n + kvh) * a.plan.max_seq * AT_HD;
+        s.vis = a.plan.vis;
+    }
+    return s;
+}
+
+S2P_DEV bool visible(const SegInfo& s, int rl, int j) {
+    if (rl >= s.nrows || j >= s.span) return false;
+    if (j < s.L) return true;
+    const int b = j - s.L;
+    if (!s.vis) return b <= rl;
+    return b < 64 && ((s.vis[s.row0 + rl] >> b) & 1ull);
+}
+
+S2P_DEV float max16(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1, 16));
+    v = fmaxf(v, __shfl_xor(v, 2, 16));
+    v = fmaxf(v, __shfl_xor(v, 4, 16));
+    v = fmaxf(v, __shfl_xor(v, 8, 16));
+    return v;
+}
+S2P_DEV float sum16(float v) {
+    v += __shfl_xor(v, 1, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 8, 16);
+    return v;
+}
+
+S2P_DEV void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* merge the split partials of (row, head h, dim d):
+ * out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s, in split order */
+S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, int nsplit,
+                            int row, int h, int d) {
+    const size_t p0 = ((size_t)row * qh + h) * nsplit;
+    const float* po = part + (size_t)rows * qh * nsplit * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, coh_ldf(part + (p0 + s) * 2));
+    const float Ms = M == -INFINITY ? 0.f : M;
+    float lt = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+        float mv[8], lv[8], ov[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool ok = s0 + j < nsplit;
+            mv[j] = ok ? coh_ldf(part + (p0 + s0 + j) * 2) : 0.f;
+            lv[j] = ok ? coh_ldf(part + (p0 + s0 + j) * 2 + 1) : 0.f;
+            ov[j] = ok ? coh_ldf(po + (p0 + s0 + j) * AT_HD + d) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (s0 + j >= nsplit) break;
+            const float w = __expf(mv[j] - Ms);
+            lt = fmaf(lv[j], w, lt);
+            acc = fmaf(ov[j], w, acc);
+        }
+    }
+    coh_st16(out + ((size_t)row * qh + h) * AT_HD + d, f2bf(acc / lt));
+}
+
+/* One (segment, kv head, position split) attention block; smem holds
+ * AT_LDS_BYTES.  Body of k_attn, also run by the persistent verify kernel. */
+template <int MQT>
+__device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
+    LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
+    LDS(uint16_t)* s_p = (LDS(uint16_t)*)(smem + AT_SV_BYTES);
+    LDS(uint16_t)* s_pl = (LDS(uint16_t)*)(smem + AT_SV_BYTES + AT_SP_BYTES);
+    LDS(float)* s_ml = (LDS(float)*)(smem + AT_SV_BYTES + 2 * AT_SP_BYTES);
+    LDS(int)* s_flag = (LDS(int)*)(smem + AT_SV_BYTES + 2 * AT_SP_BYTES + AT_SML_BYTES);
+#define SV(w, t, d) s_v[((w) * AT_TILE + (t)) * AT_VSTRIDE + (d)]
+#define SP(w, r, c) s_p[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
+#define SPL(w, r, c) s_pl[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
+#define SML(w, qv, k) s_ml[((w) * 32 + (qv)) * 2 + (k)]
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int qq = lane >> 4, c = lane & 15;
+    const SegInfo S = resolve(a, seg, kvh);
+    const int p_begin = sp * a.split_pos;
+    const int p_end = min(p_begin + a.split_pos, S.span);
+    const float scale = 0.08838834764831845f;
+    const int qrow_stride = a.qh * AT_HD;
+
+    /* Q operands: A row i = c -> query vector qv = 16 qt + c */
+    s2p_u32x4 qa[MQT][4];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++) {
+        const int qv = 16 * qt + c;
+        const int rl = qv >> 2, g = qv & 3;
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+            if (rl < S.nrows) {
+                qa[qt][ch] = coh_ld128(a.q + (size_t)(S.row0 + rl) * qrow_stride +
+                                       (4 * kvh + g) * AT_HD + 32 * ch + 8 * qq);
+            } else {
+                qa[qt][ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
+            }
+        }
+    }
+
+    float m[MQT][4], l[MQT][4];
+    s2p_f32x4 o[MQT][8];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            m[qt][v] = -INFINITY;
+            l[qt][v] = 0.f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int tb = p_begin + wave * AT_TILE; tb < p_end; tb += AT_WAVES * AT_TILE) {
+        /* K: 2 position subtiles x 4 dim chunks, one 16-byte load each */
+        s2p_u32x4 kr[2][4];
+#pragma unroll
+        for (int ps = 0; ps < 2; ps++) {
+            const int pos = min(tb + 16 * ps + c, p_end - 1);
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++)
+                kr[ps][ch] = __builtin_nontemporal_load(
+                    (const s2p_u32x4*)(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq));
+        }
+        /* V tile -> LDS [pos][dim], stored as soon as it arrives (keeps the
+         * tile out of registers during the score MFMAs) */
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int idx = i * 64 + lane;
+            const int pos = min(tb + (idx >> 4), p_end - 1);
+            *(LDS(s2p_u32x4)*)&SV(wave, idx >> 4, 8 * (idx & 15)) = __builtin_nontemporal_load(
+                (const s2p_u32x4*)(S.vp + (size_t)pos * AT_HD + 8 * (idx & 15)));
+        }
+        /* scores */
+        s2p_f32x4 sc[MQT][2];
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int ps = 0; ps < 2; ps++) {
+                s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(qa[qt][ch], kr[ps][ch], acc);
+                sc[qt][ps] = acc;
+            }
+        /* online softmax; lane (qq, c) holds rows 4 qq + v of each q tile */
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++) {
+            const int rl = 4 * qt + qq;
+            const bool vis0 = visible(S, rl, tb + c) && tb + c < p_end;
+            const bool vis1 = visible(S, rl, tb + 16 + c) && tb + 16 + c < p_end;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float t0 = vis0 ? sc[qt][0][v] * scale : -INFINITY;
+                const float t1 = vis1 ? sc[qt][1][v] * scale : -INFINITY;
+                const float tm = max16(fmaxf(t0, t1));
+                const float mn = fmaxf(m[qt][v], tm);
+                const float ms = mn == -INFINITY ? 0.f : mn;
+                const float corr = __expf(m[qt][v] - ms);
+                const float p0 = __expf(t0 - ms), p1 = __expf(t1 - ms);
+                l[qt][v] = l[qt][v] * corr + p0 + p1;
+                m[qt][v] = mn;
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
+                /* P = hi + lo, both bf16: 16 significant bits into the PV MFMA */
+                const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
+                SP(wave, 16 * qt + 4 * qq + v, c) = h0;
+                SP(wave, 16 * qt + 4 * qq + v, 16 + c) = h1;
+                SPL(wave, 16 * qt + 4 * qq + v, c) = f2bf(p0 - bf2f(h0));
+                SPL(wave, 16 * qt + 4 * qq + v, 16 + c) = f2bf(p1 - bf2f(h1));
+            }
+        }
+        wave_sync_lds();
+        s2p_u32x4 pa[MQT], pl[MQT];
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++) {
+            pa[qt] = *(const LDS(s2p_u32x4)*)&SP(wave, 16 * qt + c, 8 * qq);
+            pl[qt] = *(const LDS(s2p_u32x4)*)&SPL(wave, 16 * qt + c, 8 * qq);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            uint32_t b[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                b[e] = (uint32_t)SV(wave, 8 * qq + 2 * e, 16 * dt + c) |
+                       ((uint32_t)SV(wave, 8 * qq + 2 * e + 1, 16 * dt + c) << 16);
+            const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+#pragma unroll
+            for (int qt = 0; qt < MQT; qt++) {
+                o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+            }
+        }
+        wave_sync_lds();
+    }
+
+    /* ---- merge the 4 waves ---- */
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            l[qt][v] = sum16(l[qt][v]);
+            if (c == 0) {
+                SML(wave, 16 * qt + 4 * qq + v, 0) = m[qt][v];
+                SML(wave, 16 * qt + 4 * qq + v, 1) = l[qt][v];
+            }
+        }
+    __syncthreads();
+    float ltot[MQT][4], mtot[MQT][4];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int qv = 16 * qt + 4 * qq + v;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < AT_WAVES; w++) M = fmaxf(M, SML(w, qv, 0));
+            const float Ms = M == -INFINITY ? 0.f : M;
+            float lt = 0.f;
+#pragma unroll
+            for (int w = 0; w < AT_WAVES; w++) lt += __expf(SML(w, qv, 0) - Ms) * SML(w, qv, 1);
+            const float f = __expf(m[qt][v] - Ms);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= f;
+            ltot[qt][v] = lt;
+            mtot[qt][v] = M;
+        }
+    /* sum O over waves through LDS (reusing the V tiles: 2 x 16 KB) */
+    LDS(float)* s_o = (LDS(float)*)s_v;
+    const int ostride = 32 * AT_HD;
+    auto put = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c] = o[qt][dt][v];
+    };
+    auto add = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    o[qt][dt][v] += s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c];
+    };
+    __syncthreads();
+    if (wave >= 2) put(wave - 2);
+    __syncthreads();
+    if (wave < 2) add(wave);
+    __syncthreads();
+    if (wave == 1) put(0);
+    __syncthreads();
+    if (wave == 0) {
+        add(0);
+        /* ---- write ---- */
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int qv = 16 * qt + 4 * qq + v;
+                const int rl = qv >> 2, g = qv & 3;
+                if (rl >= S.nrows) continue;
+                const int row = S.row0 + rl;
+                const int h = 4 * kvh + g;
+                if (a.nsplit == 1) {
+                    const float inv = 1.0f / ltot[qt][v];
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++)
+                        coh_st16(a.out + (size_t)row * qrow_stride + h * AT_HD + 16 * dt + c,
+                                 f2bf(o[qt][dt][v] * inv));
+                } else {
+                    const size_t pi = ((size_t)row * a.qh + h) * a.nsplit + sp;
+                    float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++) coh_stf(po + 16 * dt + c, o[qt][dt][v]);
+                    if (c == 0) {
+                        coh_stf(a.part + pi * 2, mtot[qt][v]);
+                        coh_stf(a.part + pi * 2 + 1, ltot[qt][v]);
+                    }
+                }
+            }
+    }
+    if (a.nsplit == 1 || !a.counters) return;
+    /* last split of this (segment, kv head) to finish merges the splits */
+    vm_drain();
+    __syncthreads();
+    const int cidx = seg * a.kvh_n + kvh;
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.counters + cidx, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = prev == (unsigned)(a.nsplit - 1);
+    }
+    __syncthreads();
+    if (*s_flag && 2 * S.nrows * 4 * a.nsplit + S.nrows * 4 > AT_SV_BYTES / 4) {
+        /* too many splits for the LDS merge: one output at a time */
+        for (int idx = threadIdx.x; idx < S.nrows * 4 * AT_HD; idx += 256) {
+            const int rl = idx >> 9, g = (idx >> 7) & 3, d = idx & (AT_HD - 1);
+            attn_merge_one(a.part, a.out, a.rows, a.qh, a.nsplit, S.row0 + rl, 4 * kvh + g, d);
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (*s_flag) {
+        /* merge (same arithmetic and order as attn_merge_one): split weights
+         * e^(m_s - M) and the denominators per (row, head) once, in LDS
+         * (the V tiles' space), then every output with all of its split
+         * loads in flight */
+        const int npair = S.nrows * 4, ns = a.nsplit;
+        LDS(float)* wm = (LDS(float)*)s_v;   /* [npair][ns] m, then weights */
+        LDS(float)* wl = wm + npair * ns;    /* [npair][ns] l */
+        LDS(float)* lt = wl + npair * ns;    /* [npair] */
+        for (int idx = threadIdx.x; idx < npair * ns; idx += 256) {
+            const int pr = idx / ns, sp2 = idx - pr * ns;
+            const size_t pi = ((size_t)(S.row0 + (pr >> 2)) * a.qh + 4 * kvh + (pr & 3)) * ns + sp2;
+            wm[idx] = coh_ldf(a.part + pi * 2);
+            wl[idx] = coh_ldf(a.part + pi * 2 + 1);
+        }
+        __syncthreads();
+        if (threadIdx.x < npair) {
+            const int pr = threadIdx.x;
+            float M = -INFINITY;
+            for (int k = 0; k < ns; k++) M = fmaxf(M, wm[pr * ns + k]);
+            const float Ms = M == -INFINITY ? 0.f : M;
+            float l = 0.f;
+            for (int k = 0; k < ns; k++) {
+                const float w = __expf(wm[pr * ns + k] - Ms);
+                l = fmaf(wl[pr * ns + k], w, l);
+                wm[pr * ns + k] = w;
+            }
+            lt[pr] = l;
+        }
+        __syncthreads();
+        const float* po = a.part + (size_t)a.rows * a.qh * ns * 2;
+        for (int idx = threadIdx.x; idx < npair * AT_HD; idx += 256) {
+            const int pr = idx >> 7, d = idx & (AT_HD - 1);
+            const int row = S.row0 + (pr >> 2), h = 4 * kvh + (pr & 3);
+            const size_t p0 = ((size_t)row * a.qh + h) * ns;
+            float acc = 0.f;
+            for (int k0 = 0; k0 < ns; k0 += 16) {
+                float ov[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    ov[j] = k0 + j < ns ? coh_ldf(po + (p0 + k0 + j) * AT_HD + d) : 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (k0 + j < ns) acc = fmaf(ov[j], wm[pr * ns + k0 + j], acc);
+            }
+            coh_st16(a.out + ((size_t)row * a.qh + h) * AT_HD + d, f2bf(acc / lt[pr]));
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+#undef SV
+#undef SP
+#undef SPL
+#undef SML
+}
+
+#endif

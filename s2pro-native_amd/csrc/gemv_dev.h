@@ -1,0 +1,721 @@
+/* s2pro MI355X — device code of the INT4 / INT8 GEMV engine (see gemv.hip
+ * for the design), shared by the k_gemv kernel and the persistent verify
+ * kernel.  Outputs, split-K partials and sums of squares are written
+ * through (coh.h); activations are read around the L2 only in the
+ * persistent kernel (COH), where their producer ran in the same launch. */
+#ifndef S2P_GEMV_DEV_H
+#define S2P_GEMV_DEV_H
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "coh.h"
+#include "common.h"
+#include "gemv_internal.h"
+#include "s2pro/s2p_fmath.h"
+
+#define GV_SMAX 32                /* most K splits */
+#define GV_XPAD 8                 /* bf16 row padding of the staged x */
+#define GV_LDS_BUDGET (40 * 1024) /* staging bytes aimed for: 4 WGs per CU */
+#define GV_LDS_MAX (160 * 1024)
+#define GV_COUNTERS (1 << 16)     /* arrival counters at GemvArgs.counters */
+
+/* k-slot order of the INT4 A operand inside each 8-weight block: the
+ * and/or dequant yields nibble pairs (0,4) (1,5) (2,6) (3,7). */
+#define PERM4(e) ((((e) & 1) << 2) | ((e) >> 1))
+
+/* 4x4 transpose of one dword per lane across lane quarters:
+ * in: lane quarter q holds d[j] = A[q][j]; out: d[j] = A[j][q]. */
+S2P_DEV void xpose4(uint32_t& d0, uint32_t& d1, uint32_t& d2, uint32_t& d3) {
+    auto s02 = __builtin_amdgcn_permlane32_swap(d0, d2, false, false);
+    d0 = s02[0];
+    d2 = s02[1];
+    auto s13 = __builtin_amdgcn_permlane32_swap(d1, d3, false, false);
+    d1 = s13[0];
+    d3 = s13[1];
+    auto s01 = __builtin_amdgcn_permlane16_swap(d0, d1, false, false);
+    d0 = s01[0];
+    d1 = s01[1];
+    auto s23 = __builtin_amdgcn_permlane16_swap(d2, d3, false, false);
+    d2 = s23[0];
+    d3 = s23[1];
+}
+
+/* 8 nibbles (two's complement w) -> 8 bf16 holding 1.5 + w/16 exactly (the
+ * nibble XOR 8 lands in the top 4 mantissa bits of bf16 1.0), in k-slot order
+ * 0,4,1,5,2,6,3,7.  The 1.5 bias keeps the cancellation against the bias
+ * correction small (|1.5 sum x| ~ 5 |w.x / 16|). */
+S2P_DEV s2p_u32x4 deq_int4(uint32_t d, uint32_t mask, uint32_t one) {
+    /* mask / one live in VGPRs (gfx9 VOP3 takes no literal), so each pair
+     * is one shift and one v_and_or_b32 */
+    d ^= 0x88888888u;
+    s2p_u32x4 a;
+    a.x = ((d << 3) & mask) | one;
+    a.y = ((d >> 1) & mask) | one;
+    a.z = ((d >> 5) & mask) | one;
+    a.w = ((d >> 9) & mask) | one;
+    return a;
+}
+
+/* 4 int8 (dword) -> 2 bf16x2 holding 128 + w, natural k order */
+S2P_DEV s2p_u32x2 deq_int8(uint32_t d) {
+    d ^= 0x80808080u;
+    const uint32_t f0 = __float_as_uint((float)(d & 0xFFu));
+    const uint32_t f1 = __float_as_uint((float)((d >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((d >> 16) & 0xFFu));
+    const uint32_t f3 = __float_as_uint((float)(d >> 24));
+    s2p_u32x2 r;
+    r.x = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+    r.y = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+    return r;
+}
+
+/* silu(g) * u with the two bf16 roundings of kernels.cu:1216-1229; exp is
+ * the rule's s2p_expf so the value matches the host oracle bit for bit. */
+S2P_DEV uint16_t silu_mul_bf16(uint16_t g16, uint16_t u16) {
+#pragma clang fp contract(off)
+    const float g = bf2f(g16);
+    const float u = bf2f(u16);
+    const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, s2p_expf(-g)));
+    const float sil = bf2f(f2bf(__fmul_rn(g, sig)));
+    return f2bf(__fmul_rn(sil, u));
+}
+
+/* ----------------------------------------------------------------------- */
+
+/* LDS carve-up of one workgroup (dynamic shared memory). */
+/* LDS-typed pointers: every access compiles to ds_* (a generic pointer would
+ * become flat_*, whose vmcnt accounting waits behind the weight stream) */
+#define LDS(T) __attribute__((address_space(3))) T
+struct GvLds {
+    LDS(uint16_t)* x;   /* [M][xs] staged activations (INT4: PERM4 order) */
+    LDS(uint16_t)* X3;  /* [M][3][xg] bf16 hi/mid/lo of the f32 group sums */
+    LDS(float)* sc;     /* INT4: [4 waves][16 groups][16 rows] f32 scales */
+    LDS(float)* inv;    /* [GEMV_MAX_M] inverse RMS */
+    LDS(float)* xtot;   /* [GEMV_MAX_M] INT8: sum of the window's activations */
+    LDS(int)* flag;     /* last-arrival broadcast */
+    int xs, xg;
+};
+
+static __host__ __device__ inline int gv_round32(int v) { return (v + 31) & ~31; }
+
+static __host__ __device__ size_t gv_lds_bytes(int M, int win, int wfmt) {
+    const size_t xs = (size_t)win * 32 + GV_XPAD;
+    const size_t xg = (size_t)gv_round32(win) + 8;
+    size_t b = (size_t)M * xs * 2 + (size_t)M * 3 * xg * 2;
+    b = (b + 15) & ~(size_t)15;
+    if (wfmt == GEMV_W_INT4) b += 4 * 16 * 16 * 4;
+    b += 2 * GEMV_MAX_M * 4 + 16;
+    return b;
+}
+
+S2P_DEV GvLds gv_carve(LDS(unsigned char)* base, int M, int win, int wfmt) {
+    GvLds L;
+    L.xs = win * 32 + GV_XPAD;
+    L.xg = gv_round32(win) + 8;
+    uint32_t off = 0;
+    L.x = (LDS(uint16_t)*)(base + off);
+    off += (uint32_t)M * L.xs * 2;
+    L.X3 = (LDS(uint16_t)*)(base + off);
+    off += (uint32_t)M * 3 * L.xg * 2;
+    off = (off + 15) & ~15u;
+    L.sc = (LDS(float)*)(base + off);
+    if (wfmt == GEMV_W_INT4) off += 4 * 16 * 16 * 4;
+    L.inv = (LDS(float)*)(base + off);
+    off += GEMV_MAX_M * 4;
+    L.xtot = (LDS(float)*)(base + off);
+    off += GEMV_MAX_M * 4;
+    L.flag = (LDS(int)*)(base + off);
+    return L;
+}
+
+/* output row of local row l (0..63) of row block rb */
+S2P_DEV int gv_row(const GemvArgs& a, int rb, int l) {
+    if (a.epi == GEMV_EPI_SWIGLU) {
+        const int F = a.N >> 1;
+        return l < 32 ? rb * 32 + l : F + rb * 32 + (l - 32);
+    }
+    return rb * 64 + l;
+}
+
+/* exact split of an f32 into three bf16 (truncation: each remainder keeps
+ * the low bits, so hi + mid + lo == v) */
+S2P_DEV void split3(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+    const uint32_t b0 = __float_as_uint(v) & 0xFFFF0000u;
+    const float r1 = v - __uint_as_float(b0);
+    const uint32_t b1 = __float_as_uint(r1) & 0xFFFF0000u;
+    const float r2 = r1 - __uint_as_float(b1);
+    hi = (uint16_t)(b0 >> 16);
+    mid = (uint16_t)(b1 >> 16);
+    lo = (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+/* Activation reads: device-coherent (COH, the persistent kernel, where the
+ * producer ran in the same launch) or plain L2-cacheable (layer kernels:
+ * the producer was an earlier launch). */
+template <bool COH>
+S2P_DEV s2p_u32x4 ld_act128(const uint16_t* p) {
+    if constexpr (COH) return coh_ld128(p);
+    else return *(const s2p_u32x4*)p;
+}
+template <bool COH>
+S2P_DEV float ld_actf(const float* p) {
+    if constexpr (COH) return coh_ldf(p);
+    else return *p;
+}
+template <bool COH>
+S2P_DEV uint16_t ld_act16(const uint16_t* p) {
+    if constexpr (COH) return coh_ld16(p);
+    else return *p;
+}
+
+/* Transform one activation row m of 8-element column block b (RMSNorm with
+ * the rule's roundings when staging a norm), store it in LDS in the
+ * A-operand k-slot order, and its 32-k group sums (quad shuffle: the 4
+ * blocks of a group are in adjacent lanes). */
+template <int WFMT>
+S2P_DEV void gv_stage_one(const GemvArgs& a, const GvLds& L, int m, int b, bool valid,
+                          s2p_u32x4 raw, s2p_u32x4 wn4) {
+#pragma clang fp contract(off)
+    uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w}; /* bf16 pairs */
+    if (a.xmode == GEMV_X_NORM) {
+        const float inv = L.inv[m];
+        const uint32_t w4[4] = {wn4.x, wn4.y, wn4.z, wn4.w};
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t lo = f2bf(__fmul_rn(__fmul_rn(bf2f_lo(v[d]), inv), bf2f_lo(w4[d])));
+            const uint32_t hi = f2bf(__fmul_rn(__fmul_rn(bf2f_hi(v[d]), inv), bf2f_hi(w4[d])));
+            v[d] = lo | (hi << 16);
+        }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        s += bf2f_lo(v[d]);
+        s += bf2f_hi(v[d]);
+    }
+    s2p_u32x4 o;
+    if (WFMT == GEMV_W_INT4) { /* k-slot order 0,4,1,5,2,6,3,7 */
+        o.x = (v[0] & 0xFFFFu) | (v[2] << 16);
+        o.y = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
+        o.z = (v[1] & 0xFFFFu) | (v[3] << 16);
+        o.w = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
+    } else {
+        o = (s2p_u32x4){v[0], v[1], v[2], v[3]};
+    }
+    if (valid) *(LDS(s2p_u32x4)*)(L.x + m * L.xs + b * 8) = o;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (valid && (b & 3) == 0) {
+        uint16_t h, md, lo;
+        split3(s, h, md, lo);
+        const int g = b >> 2;
+        L.X3[(m * 3 + 0) * L.xg + g] = h;
+        L.X3[(m * 3 + 1) * L.xg + g] = md;
+        L.X3[(m * 3 + 2) * L.xg + g] = lo;
+    }
+}
+
+/* Stage groups [wg0, wg0 + wn) of every activation row into LDS (and, for a
+ * norm with with_inv, the rows' inverse RMS first): thread = one 8-element
+ * column block for all rows, loads for 4 rows in flight at once. */
+template <int WFMT, bool COH>
+__device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, bool with_inv) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = a.M;
+    const int nb8 = wn * 4;
+    const int wnp = gv_round32(wn);
+    if (with_inv && a.xmode == GEMV_X_NORM) {
+        /* inverse RMS per row from the producer's per-block sums of squares:
+         * lanes take blocks, fixed-order wave reduction */
+        for (int m = wave; m < M; m += 4) {
+            float s = 0.f;
+            for (int b = lane; b < a.ssq_in_blocks; b += 64)
+                s += ld_actf<COH>(a.ssq_in + (size_t)b * GEMV_MAX_M + m);
+            s = wave_sum_down(s);
+            if (lane == 0) L.inv[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
+        }
+        __syncthreads();
+    }
+    /* zero the group sums of the padded tail (read by the correction MFMA) */
+    for (int i = tid; i < M * 3 * (wnp - wn); i += 256) {
+        const int m = i / (3 * (wnp - wn)), rem = i - m * 3 * (wnp - wn);
+        const int p = rem / (wnp - wn), g = wn + rem - p * (wnp - wn);
+        L.X3[(m * 3 + p) * L.xg + g] = 0;
+    }
+    for (int bb = 0; bb < nb8; bb += 256) {
+        const int b = bb + tid;
+        const bool valid = b < nb8;
+        const int k = wg0 * 32 + b * 8;
+        int m0 = 0;
+        s2p_u32x4 wn4 = {0u, 0u, 0u, 0u};
+        if (m0 < M && valid && a.xmode == GEMV_X_NORM) wn4 = *(const s2p_u32x4*)(a.norm_w + k);
+        for (; m0 < M; m0 += 4) {
+            s2p_u32x4 raw[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                raw[j] = (valid && m0 + j < M) ? ld_act128<COH>(a.x + (size_t)(m0 + j) * a.ldx + k)
+                                               : (s2p_u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (m0 + j >= M) break; /* uniform */
+                gv_stage_one<WFMT>(a, L, m0 + j, b, valid, raw[j], wn4);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    if (WFMT == GEMV_W_INT8) {
+        __syncthreads();
+        /* window activation total per row, wave per row, fixed order */
+        for (int m = wave; m < M; m += 4) {
+            float s = 0.f;
+            for (int g = lane; g < wn; g += 64)
+                s += bf2f(L.X3[(m * 3 + 0) * L.xg + g]) +
+                     bf2f(L.X3[(m * 3 + 1) * L.xg + g]) +
+                     bf2f(L.X3[(m * 3 + 2) * L.xg + g]);
+            s = wave_sum_down(s);
+            if (lane == 0) L.xtot[m] = s;
+        }
+    }
+}
+
+/* one chunk of a wave's weight stream: INT4 4 loads x 4 groups plus the
+ * chunk's 16 group scales (lane (q, r): groups 4q..4q+3 of row r); INT8
+ * 2 x (2 loads x 4 groups) */
+#define GV_CHG_INT4 16
+#define GV_CHG_INT8 8
+struct GvBuf {
+    uint32_t w[16];
+    s2p_u32x2 s;
+};
+
+/* Branch-free: every load is issued (out-of-range groups read a clamped,
+ * valid address), so the compiler can keep the next chunk's loads in flight
+ * with a partial vmcnt while the current one is multiplied; conditional
+ * loads, or selects on the loaded data, make it wait for everything.  The
+ * out-of-range data is never used: the multiply stops at gn, and the bias
+ * correction pairs those groups' (finite) scales with zero-padded sums. */
+template <int WFMT>
+S2P_DEV void gv_load(GvBuf& B, const GemvArgs& a, int nrow, int gabs, int gn, int q) {
+    if constexpr (WFMT == GEMV_W_INT4) {
+        const uint8_t* wrow = a.w + (size_t)nrow * (a.K >> 1) + (size_t)gabs * 16;
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const bool ok = it * 4 < gn;
+            const s2p_u32x4 v = __builtin_nontemporal_load(
+                (const s2p_u32x4*)(wrow + (ok ? (it * 4 + q) * 16 : q * 16)));
+            B.w[it * 4 + 0] = v.x;
+            B.w[it * 4 + 1] = v.y;
+            B.w[it * 4 + 2] = v.z;
+            B.w[it * 4 + 3] = v.w;
+        }
+        const bool sok = 4 * q < gn;
+        const uint16_t* srow = (const uint16_t*)a.s + (size_t)nrow * (a.K >> 5) + gabs +
+                               (sok ? 4 * q : 0);
+        B.s = *(const s2p_u32x2*)srow;
+    } else {
+        const uint8_t* wrow = a.w + (size_t)nrow * a.K + (size_t)gabs * 32;
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            const bool ok = it * 4 < gn;
+            const uint8_t* src = wrow + (ok ? it * 128 + q * 32 : q * 32);
+            const s2p_u32x4 v0 = __builtin_nontemporal_load((const s2p_u32x4*)src);
+            const s2p_u32x4 v1 = __builtin_nontemporal_load((const s2p_u32x4*)(src + 16));
+            B.w[it * 8 + 0] = v0.x; B.w[it * 8 + 1] = v0.y;
+            B.w[it * 8 + 2] = v0.z; B.w[it * 8 + 3] = v0.w;
+            B.w[it * 8 + 4] = v1.x; B.w[it * 8 + 5] = v1.y;
+            B.w[it * 8 + 6] = v1.z; B.w[it * 8 + 7] = v1.w;
+        }
+    }
+}
+
+S2P_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* D = A(16x16) * B(16x16) + C (v_mfma_f32_16x16x16_bf16): lane l supplies A
+ * row l % 16 and B column l % 16, k-slots 4 (l / 16) .. +3; D as the x32 form */
+S2P_DEV s2p_f32x4 mfma16x16x16(s2p_u32x2 a, s2p_u32x2 b, s2p_f32x4 c) {
+    typedef __attribute__((ext_vector_type(4))) short s16x4;
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                      __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+}
+
+/* multiply one chunk: cg = chunk's first group within the staged window */
+template <int WFMT, int MT>
+S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, int wave, int q,
+                        int r, s2p_f32x4 (&acc)[MT], s2p_f32x4 (&corr)[MT]) {
+    int mrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) mrow[t] = min(t * 16 + r, M - 1);
+    if constexpr (WFMT == GEMV_W_INT4) {
+        /* scales of row r, groups 4q..4q+3: f32 to this wave's LDS slice in
+         * [group][row] order, and bf16 hi / lo as the correction's A operand */
+        LDS(float)* sc = L.sc + wave * GV_CHG_INT4 * 16;
+        uint32_t shi[2], slo[2];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t pair = B.s[d];
+            uint32_t hb[2], lb[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float f = h2f((uint16_t)(e ? pair >> 16 : pair & 0xFFFFu));
+                hb[e] = __float_as_uint(f) & 0xFFFF0000u;
+                lb[e] = __float_as_uint(f - __uint_as_float(hb[e])) >> 16;
+                sc[(4 * q + 2 * d + e) * 16 + r] = f;
+            }
+            shi[d] = (hb[0] >> 16) | hb[1];
+            slo[d] = lb[0] | (lb[1] << 16);
+        }
+        wave_lds_sync();
+        uint32_t kmask = 0x00780078u, kone = 0x3F803F80u;
+        asm volatile("" : "+v"(kmask), "+v"(kone));
+#pragma unroll
+        for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
+            if (it * 4 >= gn) break;
+            uint32_t d0 = B.w[it * 4 + 0], d1 = B.w[it * 4 + 1];
+            uint32_t d2 = B.w[it * 4 + 2], d3 = B.w[it * 4 + 3];
+            xpose4(d0, d1, d2, d3);
+            const uint32_t dj[4] = {d0, d1, d2, d3};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = it * 4 + j;
+                const s2p_u32x4 av = deq_int4(dj[j], kmask, kone);
+                const s2p_f32x4 s4 = *(const LDS(s2p_f32x4)*)(sc + g * 16 + 4 * q);
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const s2p_u32x4 bv =
+                        *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
+                    const s2p_f32x4 raw = mfma16x16x32(av, bv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(s4[i], raw[i], acc[t][i]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0); /* keep LDS reads from piling up */
+        }
+        /* bias correction: corr += S (16 rows x 16 groups) . X (16 groups x 16 cols) */
+        const s2p_u32x2 ah = {shi[0], shi[1]};
+        const s2p_u32x2 al = {slo[0], slo[1]};
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const s2p_u32x2 bx = *(const LDS(s2p_u32x2)*)(L.X3 + (mrow[t] * 3 + p) * L.xg +
+                                                         cg + 4 * q);
+                corr[t] = mfma16x16x16(ah, bx, corr[t]);
+                corr[t] = mfma16x16x16(al, bx, corr[t]);
+            }
+    } else {
+#pragma unroll
+        for (int it = 0; it < GV_CHG_INT8 / 4; it++) {
+            if (it * 4 >= gn) break;
+            uint32_t e0 = B.w[it * 8 + 0], e1 = B.w[it * 8 + 2], e2 = B.w[it * 8 + 4],
+                     e3 = B.w[it * 8 + 6];
+            uint32_t o0 = B.w[it * 8 + 1], o1 = B.w[it * 8 + 3], o2 = B.w[it * 8 + 5],
+                     o3 = B.w[it * 8 + 7];
+            xpose4(e0, e1, e2, e3);
+            xpose4(o0, o1, o2, o3);
+            const uint32_t ej[4] = {e0, e1, e2, e3};
+            const uint32_t oj[4] = {o0, o1, o2, o3};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = it * 4 + j;
+                const s2p_u32x2 lo = deq_int8(ej[j]);
+                const s2p_u32x2 hi = deq_int8(oj[j]);
+                const s2p_u32x4 av = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const s2p_u32x4 bv =
+                        *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
+                    acc[t] = mfma16x16x32(av, bv, acc[t]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+/* deterministic split-order sum of the partials p[k * stride], k < S, with
+ * the loads of 16 splits in flight at a time */
+S2P_DEV float gv_sum_splits(const float* p, size_t stride, int S) {
+    float s = 0.f;
+    for (int k0 = 0; k0 < S; k0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            v[j] = k0 + j < S ? __hip_atomic_load(p + (size_t)(k0 + j) * stride, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (k0 + j < S) s += v[j];
+    }
+    return s;
+}
+
+/* last arrival at row block rb: sum the splits and run the epilogue */
+template <int WFMT, bool COH>
+__device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int M = a.M, S = a.splits;
+    const size_t stride = (size_t)M * a.nrb * 64;
+    const float* part = a.part;
+    if (a.epi == GEMV_EPI_SWIGLU) {
+        const int F = a.N >> 1;
+        for (int idx = tid; idx < M * 32; idx += 256) {
+            const int m = idx >> 5, j = idx & 31;
+            const float* p0 = part + ((size_t)m * a.nrb + rb) * 64;
+            float g = gv_sum_splits(p0 + j, stride, S);
+            float u = gv_sum_splits(p0 + 32 + j, stride, S);
+            if (WFMT == GEMV_W_INT8) {
+                g *= ((const float*)a.s)[rb * 32 + j];
+                u *= ((const float*)a.s)[F + rb * 32 + j];
+            }
+            if (rb * 32 + j < F)
+                coh_st16(Y + (size_t)m * a.ldy + rb * 32 + j, silu_mul_bf16(f2bf(g), f2bf(u)));
+        }
+        return;
+    }
+    for (int base = 0; base < M * 64; base += 256) {
+        const int idx = base + tid;
+        const int m = idx >> 6, l = idx & 63;
+        const int n = rb * 64 + l;
+        float ssq = 0.f;
+        if (m < M && n < a.N) {
+            float s = gv_sum_splits(part + ((size_t)m * a.nrb + rb) * 64 + l, stride, S);
+            if (WFMT == GEMV_W_INT8) s *= ((const float*)a.s)[n];
+            const uint16_t yb = f2bf(s);
+            uint16_t* yp = Y + (size_t)m * a.ldy + n;
+            if (a.epi == GEMV_EPI_RESID) {
+                const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
+                coh_st16(yp, xo);
+                const float xv = bf2f(xo);
+                ssq = xv * xv;
+            } else {
+                coh_st16(yp, yb);
+            }
+        }
+        if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+            /* one wave = one row m = the block's 64 columns */
+            const float tot = wave_sum_down(ssq);
+            if (lane == 0 && m < M) coh_stf(a.ssq_out + (size_t)rb * GEMV_MAX_M + m, tot);
+        }
+    }
+}
+
+/* One (row-block stride p of P, K split sp) work unit of the GEMV engine:
+ * the body of a k_gemv workgroup, also run by the persistent verify kernel.
+ * WIN1: the split's activations fit one LDS window, staged once before the
+ * stream; otherwise every (row block, window) segment restages. */
+template <int WFMT, int MT, bool WIN1, bool COH>
+__device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned char)* smem,
+                         uint16_t* y_override = nullptr, uint64_t* probe = nullptr) {
+    /* probe (diagnostics): wall clock at the stages of the block */
+#define GV_PROBE(i)                                                   \
+    do {                                                              \
+        if (probe && threadIdx.x == 0) probe[i] = wall_clock64();     \
+    } while (0)
+    GV_PROBE(0);
+    uint16_t* const Y = y_override ? y_override : a.y;
+    constexpr int CHG = WFMT == GEMV_W_INT4 ? GV_CHG_INT4 : GV_CHG_INT8; /* groups per chunk */
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int q = lane >> 4, r = lane & 15;
+    const int M = a.M;
+    const int G = a.K >> 5;
+    const int gb = sp * a.gps;
+    const int ge = min(G, gb + a.gps);
+    const int nmine = p < a.nrb ? (a.nrb - p + P - 1) / P : 0;
+    if (nmine == 0 || gb >= ge) return; /* uniform over the workgroup */
+    const int win = a.win;
+    const int nwin = WIN1 ? 1 : (ge - gb + win - 1) / win;
+    const int nseg = nmine * nwin;
+    const bool handoff = a.splits > 1 || a.epi != GEMV_EPI_STORE;
+    const GvLds L = gv_carve(smem, M, win, WFMT);
+    const int lrow = wave * 16 + r; /* local row this lane loads */
+
+    if (!WIN1 && a.xmode == GEMV_X_NORM) {
+        /* inverse RMS per row from the producer's per-block sums of squares:
+         * lanes take blocks, fixed-order wave reduction */
+        for (int m = wave; m < M; m += 4) {
+            float s = 0.f;
+            for (int b = lane; b < a.ssq_in_blocks; b += 64)
+                s += ld_actf<COH>(a.ssq_in + (size_t)b * GEMV_MAX_M + m);
+            s = wave_sum_down(s);
+            if (lane == 0) L.inv[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
+        }
+    }
+    GV_PROBE(1);
+
+    s2p_f32x4 acc[MT], corr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+        corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    float corr8[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) corr8[t] = 0.f;
+
+    /* position of segment k's chunk c */
+    auto seg_rb = [&](int k) __attribute__((always_inline)) { return p + (k / nwin) * P; };
+    auto seg_g0 = [&](int k) { return gb + (k % nwin) * win; };
+    auto seg_gn = [&](int k) __attribute__((always_inline)) { return min(win, ge - seg_g0(k)); };
+    auto load_at = [&](GvBuf& B, int k, int c) __attribute__((always_inline)) {
+        const int rb = seg_rb(k);
+        const int nrow = min(gv_row(a, rb, lrow), a.N - 1);
+        const int g0 = seg_g0(k) + c * CHG;
+        const int gn = min(CHG, seg_g0(k) + seg_gn(k) - g0);
+        gv_load<WFMT>(B, a, nrow, g0, gn, q);
+    };
+
+    /* ---- end of row block rb: combine, then store or hand off ---- */
+    auto finish_rb = [&](int rb) __attribute__((always_inline)) {
+        /* ---- row block rb complete ---- */
+        float res[MT][4];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                res[t][i] = WFMT == GEMV_W_INT4 ? 16.0f * acc[t][i] - 24.0f * corr[t][i]
+                                                : fmaf(-128.0f, corr8[t], acc[t][i]);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            corr8[t] = 0.f;
+        }
+        if (!handoff) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int m = t * 16 + r;
+                if (m >= M) continue;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = rb * 64 + wave * 16 + q * 4 + i;
+                    if (n >= a.N) continue;
+                    float v = res[t][i];
+                    if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
+                    coh_st16(Y + (size_t)m * a.ldy + n, f2bf(v));
+                }
+            }
+            return;
+        }
+        /* Split-K handoff without cache maintenance: the 8 XCD L2s are not
+         * coherent and an agent-scope fence would write back / invalidate a
+         * whole L2, so the partials are written through to memory (sc1, the
+         * encoding of an agent-scope store; one 16-byte store per lane), read
+         * back with agent-scope atomic loads, and each workgroup waits for
+         * its partial stores to complete before it signals arrival. */
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int m = t * 16 + r;
+            if (m >= M) continue;
+            float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + wave * 16 + q * 4];
+            const s2p_f32x4 v4 = {res[t][0], res[t][1], res[t][2], res[t][3]};
+            coh_st128(dst, __builtin_bit_cast(s2p_u32x4, v4));
+        }
+        GV_PROBE(3);
+        vm_drain();
+        __syncthreads();
+        GV_PROBE(4);
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            *L.flag = prev == (unsigned)(a.splits - 1);
+        }
+        __syncthreads();
+        GV_PROBE(5);
+        const bool last = *L.flag != 0;
+        if (last) {
+            gv_fixup<WFMT, COH>(a, rb, Y);
+            vm_drain();
+            GV_PROBE(6);
+            if (tid == 0)
+                __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads(); /* flag is rewritten at the next block */
+    };
+
+    if constexpr (WIN1) {
+        /* Flattened (row block, chunk) stream with two named buffers and the
+         * next chunk in flight while one is multiplied (no buffer copy for
+         * the allocator to coalesce into one register set). */
+        const int gn_w = ge - gb;
+        const int nch = (gn_w + CHG - 1) / CHG;
+        const int T = nseg * nch;
+        auto load_t = [&](GvBuf& B, int t) __attribute__((always_inline)) { load_at(B, t / nch, t - (t / nch) * nch); };
+        auto step = [&](const GvBuf& B, int t) __attribute__((always_inline)) {
+            const int kk = t / nch, cc = t - kk * nch;
+            gv_compute<WFMT, MT>(B, L, cc * CHG, min(CHG, gn_w - cc * CHG), M, wave, q, r, acc,
+                                 corr);
+            if (cc == nch - 1) {
+                if (WFMT == GEMV_W_INT8) {
+#pragma unroll
+                    for (int t2 = 0; t2 < MT; t2++) corr8[t2] += L.xtot[min(t2 * 16 + r, M - 1)];
+                }
+                finish_rb(seg_rb(kk));
+            }
+        };
+        GvBuf b0, b1;
+        load_t(b0, 0); /* the first weight chunk is in flight while staging */
+        __syncthreads();
+        gv_stage<WFMT, COH>(a, L, gb, gn_w, true);
+        __syncthreads();
+        GV_PROBE(2);
+        /* every path into a step has the same loads outstanding, and no load
+         * is issued past the end (the handoff's vmcnt(0) would wait for it) */
+        int t = 0;
+        for (; t + 2 < T; t += 2) {
+            load_t(b1, t + 1);
+            step(b0, t);
+            load_t(b0, t + 2);
+            step(b1, t + 1);
+        }
+        if (T - t == 2) {
+            load_t(b1, t + 1);
+            step(b0, t);
+            step(b1, t + 1);
+        } else {
+            step(b0, t);
+        }
+        return;
+    }
+
+    GvBuf cur, nxt;
+    load_at(cur, 0, 0);
+    for (int k = 0; k < nseg; k++) {
+        const int rb = seg_rb(k);
+        const int w = k % nwin;
+        const int g0 = seg_g0(k), gn_w = seg_gn(k);
+        const int nch = (gn_w + CHG - 1) / CHG;
+        __syncthreads();
+        gv_stage<WFMT, COH>(a, L, g0, gn_w, false);
+        __syncthreads();
+        const bool last_w = w == nwin - 1;
+        for (int c = 0; c < nch; c++) {
+            const bool last_c = c == nch - 1;
+            const int nk = last_c ? (k + 1 < nseg ? k + 1 : k) : k;
+            const int nc = last_c ? (k + 1 < nseg ? 0 : c) : c + 1;
+            load_at(nxt, nk, nc);
+            gv_compute<WFMT, MT>(cur, L, c * CHG, min(CHG, gn_w - c * CHG), M, wave, q, r, acc,
+                                 corr);
+            cur = nxt;
+        }
+        if (WFMT == GEMV_W_INT8) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) corr8[t] += L.xtot[min(t * 16 + r, M - 1)];
+        }
+        if (!last_w) continue;
+        finish_rb(rb);
+    }
+}
+
+#undef GV_PROBE
+#endif

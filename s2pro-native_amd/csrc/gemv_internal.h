@@ -45,11 +45,15 @@ typedef struct {
 } GemvArgs;
 
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
+/* resident-workgroup target the launcher plans GEMVs for (env S2P_GEMV_TARGET_WG) */
+int s2p_gemv_slots(void);
 hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,
                                    const void* x, void* y, int M, int N, int K,
                                    int gshift, hipStream_t st);
 
 #ifdef __cplusplus
 }
+/* work decomposition for `slots` resident workgroups (gemv.hip) */
+extern "C" hipError_t s2p_gemv_plan(GemvArgs* a, int slots, dim3* grid, size_t* lds);
 #endif
 #endif

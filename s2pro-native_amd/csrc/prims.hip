@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "common.h"
+#include "prims_dev.h"
 #include "prims_internal.h"
 #include "s2pro/kernels.h"
 #include "s2pro/s2p_fmath.h"
@@ -103,16 +104,6 @@ extern "C" hipError_t s2pk_qk_norm(s2p_bf16* qk, const s2p_bf16* w, int rows, in
 }
 
 /* ------------------------------------------------------------------- rope */
-
-/* cos/sin (bf16-rounded, as float) of pair i at position p */
-S2P_DEV void rope_cs(int p, int i, int head_dim, float base, float* c, float* s) {
-    const float ex = __fdiv_rn((float)(2 * i), (float)head_dim);
-    const float pw = (float)pow((double)base, (double)ex);
-    const float inv = __fdiv_rn(1.0f, pw);
-    const float ang = __fmul_rn((float)p, inv);
-    *c = bf2f(f2bf((float)cos((double)ang)));
-    *s = bf2f(f2bf((float)sin((double)ang)));
-}
 
 __global__ __launch_bounds__(256) void k_rope(uint16_t* __restrict__ x, int rows, int heads,
                                               int head_dim, int pos0,
@@ -297,50 +288,8 @@ __global__ __launch_bounds__(64) void k_qkrope_append(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ kn_w,
                                                       S2pRowPlan plan, int layer, float eps,
                                                       float base) {
-    const int row = blockIdx.x;
-    const int head = blockIdx.y;
-    const int lane = threadIdx.x;
-    const int QH = 32, KVH = 8, HD = 128;
-    const int qkv_w = (QH + 2 * KVH) * HD;
-    const bool is_q = head < QH;
-    const int kh = head - QH;
-    const uint16_t* src = qkv + (size_t)row * qkv_w + (is_q ? head * HD : QH * HD + kh * HD);
-    const uint16_t* nw = is_q ? qn_w : kn_w;
-    float v0 = bf2f(src[lane]), v1 = bf2f(src[lane + 64]);
-    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
-    s = wave_sum_down(s);
-    s = __shfl(s, 0, 64);
-    const float inv = rsqrt_rule(s / (float)HD + eps);
-    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(nw[lane]))));
-    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(nw[lane + 64]))));
-    /* RoPE: element e = lane + 64*slot, partner e ^ 1 lives in lane ^ 1 */
-    const int p = plan.pos[row];
-    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
-    float o[2];
-#pragma unroll
-    for (int slot = 0; slot < 2; slot++) {
-        const int e = lane + 64 * slot;
-        const float me = slot ? v1 : v0, pa = slot ? pv1 : pv0;
-        float c, sn;
-        rope_cs(p, e >> 1, HD, base, &c, &sn);
-        if ((e & 1) == 0) o[slot] = __fsub_rn(__fmul_rn(me, c), __fmul_rn(pa, sn)); /* x0' */
-        else o[slot] = __fadd_rn(__fmul_rn(me, c), __fmul_rn(pa, sn));              /* x1' */
-    }
-    if (is_q) {
-        uint16_t* dst = q_out + (size_t)row * QH * HD + head * HD;
-        dst[lane] = f2bf(o[0]);
-        dst[lane + 64] = f2bf(o[1]);
-    } else {
-        uint16_t* kvb = (uint16_t*)plan.kv[plan.sess[row]] + (size_t)layer * plan.layer_stride;
-        const size_t slot = (size_t)plan.slot[row];
-        uint16_t* kd = kvb + ((size_t)kh * plan.max_seq + slot) * HD;
-        uint16_t* vd = kvb + ((size_t)(KVH + kh) * plan.max_seq + slot) * HD;
-        kd[lane] = f2bf(o[0]);
-        kd[lane + 64] = f2bf(o[1]);
-        const uint16_t* vs = qkv + (size_t)row * qkv_w + (QH + KVH) * HD + kh * HD;
-        vd[lane] = vs[lane];
-        vd[lane + 64] = vs[lane + 64];
-    }
+    qkrope_item(qkv, q_out, qn_w, kn_w, plan, layer, eps, base, blockIdx.x, blockIdx.y,
+                threadIdx.x);
 }
 
 extern "C" hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
@@ -359,13 +308,7 @@ extern "C" hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, con
 __global__ __launch_bounds__(64) void k_resid_init(const uint16_t* __restrict__ xin,
                                                    uint16_t* __restrict__ x,
                                                    float* __restrict__ ssq, int width) {
-    const int blk = blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
-    const size_t i = (size_t)m * width + blk * 64 + lane;
-    const uint16_t v = xin[i];
-    x[i] = v;
-    const float f = bf2f(v);
-    const float t = wave_sum_down(f * f);
-    if (lane == 0) ssq[(size_t)blk * 128 + m] = t;
+    resid_init_item(xin, x, ssq, width, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
 extern "C" hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq, int rows,

@@ -1,0 +1,112 @@
+/* s2pro MI355X — per-wave bodies of the fused verify primitives, shared by
+ * the prims.hip kernels and the persistent verify kernel.  Activations and
+ * the appended K/V go through the coherent accessors of coh.h (the K/V rows
+ * are read by other workgroups of the same launch).  Rounding points follow
+ * kernels.cu:4-17 (see prims.hip). */
+#ifndef S2P_PRIMS_DEV_H
+#define S2P_PRIMS_DEV_H
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "coh.h"
+#include "common.h"
+#include "prims_internal.h"
+
+/* cos/sin (bf16-rounded, as float) of pair i at position p */
+S2P_DEV void rope_cs(int p, int i, int head_dim, float base, float* c, float* s) {
+#pragma clang fp contract(off)
+    const float ex = __fdiv_rn((float)(2 * i), (float)head_dim);
+    const float pw = (float)pow((double)base, (double)ex);
+    const float inv = __fdiv_rn(1.0f, pw);
+    const float ang = __fmul_rn((float)p, inv);
+    *c = bf2f(f2bf((float)cos((double)ang)));
+    *s = bf2f(f2bf((float)sin((double)ang)));
+}
+
+/* qk-norm + RoPE of one (row, head) of the fused qkv output, one wave:
+ * q heads 0..31 go to q_out, k heads 32..39 (with the matching v head) to
+ * the row's KV slot of `layer` (kernels.cu:81-109, 114-168, 172-222). */
+template <bool TAB>
+S2P_DEV void qkrope_item_t(const uint16_t* qkv, uint16_t* q_out, const uint16_t* qn_w,
+                           const uint16_t* kn_w, const S2pRowPlan& plan, int layer, float eps,
+                           float base, int row, int head, int lane, const float* rope_tab) {
+#pragma clang fp contract(off)
+    const int QH = 32, KVH = 8, HD = 128;
+    const int qkv_w = (QH + 2 * KVH) * HD;
+    const bool is_q = head < QH;
+    const int kh = head - QH;
+    const uint16_t* src = qkv + (size_t)row * qkv_w + (is_q ? head * HD : QH * HD + kh * HD);
+    const uint16_t* nw = is_q ? qn_w : kn_w;
+    float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
+    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
+    s = wave_sum_down(s);
+    s = __shfl(s, 0, 64);
+    const float inv = rsqrt_rule(s / (float)HD + eps);
+    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(nw[lane]))));
+    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(nw[lane + 64]))));
+    /* RoPE: element e = lane + 64*slot, partner e ^ 1 lives in lane ^ 1 */
+    const int p = plan.pos[row];
+    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
+    float o[2];
+#pragma unroll
+    for (int slot = 0; slot < 2; slot++) {
+        const int e = lane + 64 * slot;
+        const float me = slot ? v1 : v0, pa = slot ? pv1 : pv0;
+        float c, sn;
+        if constexpr (TAB) { /* (cos, sin) of (row, pair), precomputed with rope_cs */
+            c = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2);
+            sn = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2 + 1);
+        } else {
+            rope_cs(p, e >> 1, HD, base, &c, &sn);
+        }
+        if ((e & 1) == 0) o[slot] = __fsub_rn(__fmul_rn(me, c), __fmul_rn(pa, sn)); /* x0' */
+        else o[slot] = __fadd_rn(__fmul_rn(me, c), __fmul_rn(pa, sn));              /* x1' */
+    }
+    if (is_q) {
+        uint16_t* dst = q_out + (size_t)row * QH * HD + head * HD;
+        coh_st16(dst + lane, f2bf(o[0]));
+        coh_st16(dst + lane + 64, f2bf(o[1]));
+    } else {
+        uint16_t* kvb = (uint16_t*)plan.kv[plan.sess[row]] + (size_t)layer * plan.layer_stride;
+        const size_t slot = (size_t)plan.slot[row];
+        uint16_t* kd = kvb + ((size_t)kh * plan.max_seq + slot) * HD;
+        uint16_t* vd = kvb + ((size_t)(KVH + kh) * plan.max_seq + slot) * HD;
+        coh_st16(kd + lane, f2bf(o[0]));
+        coh_st16(kd + lane + 64, f2bf(o[1]));
+        const uint16_t* vs = qkv + (size_t)row * qkv_w + (QH + KVH) * HD + kh * HD;
+        coh_st16(vd + lane, coh_ld16(vs + lane));
+        coh_st16(vd + lane + 64, coh_ld16(vs + lane + 64));
+    }
+}
+
+/* cos/sin computed in place (TAB = false) or read from the plan's table */
+S2P_DEV void qkrope_item(const uint16_t* qkv, uint16_t* q_out, const uint16_t* qn_w,
+                         const uint16_t* kn_w, const S2pRowPlan& plan, int layer, float eps,
+                         float base, int row, int head, int lane) {
+    qkrope_item_t<false>(qkv, q_out, qn_w, kn_w, plan, layer, eps, base, row, head, lane, nullptr);
+}
+
+/* RoPE table entry (row, pair i) for head_dim 128: the rule's cos/sin of
+ * position pos[row], layer-independent, so computed once per forward. */
+S2P_DEV void rope_tab_item(const S2pRowPlan& plan, float base, float* tab, int row, int i) {
+    float c, sn;
+    rope_cs(plan.pos[row], i, 128, base, &c, &sn);
+    coh_stf(tab + ((size_t)row * 64 + i) * 2, c);
+    coh_stf(tab + ((size_t)row * 64 + i) * 2 + 1, sn);
+}
+
+/* Residual stream init of one 64-column block of row m: x = x_in and the
+ * block's sum of squares (layout [width/64][GEMV_MAX_M = 128]). */
+S2P_DEV void resid_init_item(const uint16_t* xin, uint16_t* x, float* ssq, int width, int blk,
+                             int m, int lane) {
+    const size_t i = (size_t)m * width + blk * 64 + lane;
+    const uint16_t v = xin[i];
+    coh_st16(x + i, v);
+    const float f = bf2f(v);
+    const float t = wave_sum_down(f * f);
+    if (lane == 0) coh_stf(ssq + (size_t)blk * 128 + m, t);
+}
+
+#endif
