@@ -247,7 +247,7 @@ def main():
                      "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
                      "traffic": measured_traffic(),
                      "traffic_source": "profiles/gemv_int4_config3_traffic.md",
-                     "kernel": "k_gemv<INT4, MT=1> (all 145 weight GEMVs of a step)",
+                     "kernel": "k_gemv3<INT4, MT=1> (all 145 weight GEMVs of a step)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "alg_bytes_per_launch": int(per_launch)},
     }

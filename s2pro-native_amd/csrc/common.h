@@ -59,6 +59,13 @@ S2P_DEV float wave_sum_down(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
     return v;
 }
+/* sum over each aligned group of 16 lanes (fixed-order butterfly; every
+ * lane of the group gets the total) */
+S2P_DEV float sum_lanes16(float v) {
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
 S2P_DEV float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

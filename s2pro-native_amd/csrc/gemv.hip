@@ -52,6 +52,13 @@
 #include "gemv_dev.h"
 #include "s2pro/gemm.h"
 
+/* whole-K workgroups of up to 16 waves (MT = 1) or 8 waves */
+template <int WFMT, int MT>
+__global__ __launch_bounds__(MT == 1 ? 1024 : 512) void k_gemv3(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem3[];
+    gv3_block<WFMT, MT, false>(a, blockIdx.x, gridDim.x, (LDS(unsigned char)*)smem3, a.y);
+}
+
 template <int WFMT, int MT, bool WIN1>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : (MT == 2 ? 3 : 2)))) void k_gemv(GemvArgs a) {
@@ -142,15 +149,21 @@ static hipError_t gv_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStre
 /* Work decomposition of one GEMV for a target of `slots` resident
  * workgroups: fills a->nrb, gps, splits, win and returns the grid and the
  * dynamic LDS bytes. */
-extern "C" hipError_t s2p_gemv_plan(GemvArgs* ap, int slots, dim3* grid_out, size_t* lds_out) {
-    GemvArgs& a = *ap;
+static hipError_t s2p_gemv_plan_check(const GemvArgs* ap) {
+    const GemvArgs& a = *ap;
     if (a.M <= 0 || a.M > GEMV_MAX_M || a.N <= 0 || a.K <= 0 || (a.K & 127))
         return hipErrorInvalidValue;
     if (a.gps < 0 || (a.gps & 3)) return hipErrorInvalidValue;
     if (a.epi == GEMV_EPI_SWIGLU && ((a.N & 1) || ((a.N >> 1) & 31))) return hipErrorInvalidValue;
-    if (a.xmode == GEMV_X_NORM && (!a.norm_w || !a.ssq_in || a.ssq_in_blocks <= 0 ||
-                                  a.ssq_in_blocks > 64))
+    if (a.xmode == GEMV_X_NORM && (!a.norm_w || !a.ssq_in || a.ssq_in_blocks <= 0))
         return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+extern "C" hipError_t s2p_gemv_plan(GemvArgs* ap, int slots, dim3* grid_out, size_t* lds_out) {
+    GemvArgs& a = *ap;
+    const hipError_t ce = s2p_gemv_plan_check(ap);
+    if (ce != hipSuccess) return ce;
     const int G = a.K >> 5;
     a.nrb = a.epi == GEMV_EPI_SWIGLU ? (a.N >> 1) / 32 : (a.N + 63) / 64;
     const bool autos = a.gps == 0;
@@ -195,10 +208,121 @@ extern "C" hipError_t s2p_gemv_plan(GemvArgs* ap, int slots, dim3* grid_out, siz
     return hipSuccess;
 }
 
+#define GV3_LDS_MAX (160 * 1024)
+
+/* Whole-K plan: K slices of whole 16-group chunks where possible (at most 16
+ * waves), then as many tiles per group as the waves allow, fewer when the
+ * launch would not cover every CU; the grid is one resident round.  Returns
+ * hipErrorNotSupported when the activations do not fit in LDS (the split-K
+ * engine runs instead). */
+extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_t* lds_out) {
+    const int G = a->K >> 5;
+    const int mt = (a->M + 15) / 16;
+    const bool swiglu = a->epi == GEMV_EPI_SWIGLU;
+    const int tiles = swiglu ? (a->N >> 1) / 16 : (a->N + 15) / 16;
+    const int nwmax = mt == 1 ? 16 : 8;
+    const int chg = a->wfmt == GEMV_W_INT4 ? 16 : 8;
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    const int kmax = swiglu ? nwmax / 2 : nwmax;
+    int gps = chg;
+    while ((G + gps - 1) / gps > kmax) gps += 4;
+    int ks = (G + gps - 1) / gps;
+    /* units: output tiles per group (SWIGLU: a unit is a gate + up pair) */
+    const int per = swiglu ? 2 : 1;
+    int units = nwmax / (per * ks);
+    if (units < 1) units = 1;
+    while (units > 1 && (tiles + units - 1) / units < cus) units--;
+    /* still fewer groups than CUs: thinner K slices */
+    while ((tiles + units - 1) / units < cus && per * units * (ks + 1) <= nwmax && gps > 4) {
+        const int g2 = ((G + ks) / (ks + 1) + 3) & ~3;
+        if ((G + g2 - 1) / g2 <= ks) break;
+        gps = g2;
+        ks = (G + gps - 1) / gps;
+    }
+    for (;;) {
+        const int rt = per * units, nw = rt * ks;
+        const int ngroups = (tiles + units - 1) / units;
+        /* resident workgroups per CU: LDS, and waves at this kernel's
+         * register budget (16 waves per CU at MT = 1, else 8) */
+        const size_t lds1 = gv3_lds_bytes(a->M, gps, a->wfmt, ks, nw, 1);
+        int per_cu = (int)(GV3_LDS_MAX / lds1);
+        const int wcap = nwmax / nw;
+        if (per_cu > wcap) per_cu = wcap;
+        if (per_cu < 1) per_cu = 1;
+        int P = cus * per_cu;
+        if (P > ngroups) P = ngroups;
+        const size_t lds = gv3_lds_bytes(a->M, gps, a->wfmt, ks, nw, ngroups > P ? 2 : 1);
+        if (lds <= GV3_LDS_MAX) {
+            a->gps = gps;
+            a->ks = ks;
+            a->rt = rt;
+            a->splits = 1;
+            *grid = dim3((unsigned)P);
+            *block = dim3((unsigned)(64 * nw));
+            *lds_out = lds;
+            return hipSuccess;
+        }
+        if (units == 1) return hipErrorNotSupported;
+        units--;
+    }
+}
+
+static int g_engine = 0;
+extern "C" void s2p_gemv_set_engine(int engine) { g_engine = engine; }
+static uint64_t* g_probe = nullptr;
+static int g_probe_at = -1;
+extern "C" void s2p_gemv_set_probe(uint64_t* buf, int index) {
+    g_probe = buf;
+    g_probe_at = buf ? index : -1;
+}
+
+template <int WFMT, int MT>
+static hipError_t gv3_launch_mt(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
+                                hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)k_gemv3<WFMT, MT>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, GV3_LDS_MAX);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_gemv3<WFMT, MT>), grid, block, lds, st, a);
+    return hipGetLastError();
+}
+
+template <int WFMT>
+static hipError_t gv3_launch(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
+                             hipStream_t st) {
+    switch ((a.M + 15) / 16) {
+        case 1: return gv3_launch_mt<WFMT, 1>(a, grid, block, lds, st);
+        case 2: return gv3_launch_mt<WFMT, 2>(a, grid, block, lds, st);
+        case 3: return gv3_launch_mt<WFMT, 3>(a, grid, block, lds, st);
+        case 4: return gv3_launch_mt<WFMT, 4>(a, grid, block, lds, st);
+        case 5: return gv3_launch_mt<WFMT, 5>(a, grid, block, lds, st);
+        case 6: return gv3_launch_mt<WFMT, 6>(a, grid, block, lds, st);
+        case 7: return gv3_launch_mt<WFMT, 7>(a, grid, block, lds, st);
+        default: return gv3_launch_mt<WFMT, 8>(a, grid, block, lds, st);
+    }
+}
+
 extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
     GemvArgs a = *ap;
     dim3 grid;
     size_t lds = 0;
+    if (g_engine != 2 && a.gps == 0) {
+        GemvArgs a3 = a;
+        dim3 block;
+        const hipError_t e3 = s2p_gemv_plan_check(&a3);
+        if (e3 != hipSuccess) return e3;
+        if (s2p_gemv3_plan(&a3, &grid, &block, &lds) == hipSuccess) {
+            if (g_probe_at >= 0 && g_probe_at-- == 0) a3.probe = g_probe;
+            return a3.wfmt == GEMV_W_INT4 ? gv3_launch<GEMV_W_INT4>(a3, grid, block, lds, st)
+                                          : gv3_launch<GEMV_W_INT8>(a3, grid, block, lds, st);
+        }
+    }
     const hipError_t pe = s2p_gemv_plan(&a, s2p_gemv_slots(), &grid, &lds);
     if (pe != hipSuccess) return pe;
     const int mt = (a.M + 15) / 16;

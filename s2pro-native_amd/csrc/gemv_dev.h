@@ -151,6 +151,13 @@ S2P_DEV void split3(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
     lo = (uint16_t)(__float_as_uint(r2) >> 16);
 }
 
+/* LDS writes of a wave visible to all its lanes */
+S2P_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 /* Activation reads: device-coherent (COH, the persistent kernel, where the
  * producer ran in the same launch) or plain L2-cacheable (layer kernels:
  * the producer was an earlier launch). */
@@ -219,15 +226,19 @@ S2P_DEV void gv_stage_one(const GemvArgs& a, const GvLds& L, int m, int b, bool 
 
 /* Stage groups [wg0, wg0 + wn) of every activation row into LDS (and, for a
  * norm with with_inv, the rows' inverse RMS first): thread = one 8-element
- * column block for all rows, loads for 4 rows in flight at once. */
-template <int WFMT, bool COH>
+ * column block for all rows, loads for 4 rows in flight at once.  NT = 256:
+ * the whole (4-wave) workgroup stages a shared window; NT = 64: one wave
+ * stages its own window (the inverse RMS is already in L.inv). */
+template <int WFMT, bool COH, int NT = 256>
 __device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, bool with_inv) {
 #pragma clang fp contract(off)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int tid = NT == 256 ? (int)threadIdx.x : lane, wave = NT == 256 ? tid >> 6 : 0;
+    constexpr int NWS = NT / 64; /* waves staging */
     const int M = a.M;
     const int nb8 = wn * 4;
     const int wnp = gv_round32(wn);
-    if (with_inv && a.xmode == GEMV_X_NORM) {
+    if (NT == 256 && with_inv && a.xmode == GEMV_X_NORM) {
         /* inverse RMS per row from the producer's per-block sums of squares:
          * lanes take blocks, fixed-order wave reduction */
         for (int m = wave; m < M; m += 4) {
@@ -240,12 +251,12 @@ __device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, boo
         __syncthreads();
     }
     /* zero the group sums of the padded tail (read by the correction MFMA) */
-    for (int i = tid; i < M * 3 * (wnp - wn); i += 256) {
+    for (int i = tid; i < M * 3 * (wnp - wn); i += NT) {
         const int m = i / (3 * (wnp - wn)), rem = i - m * 3 * (wnp - wn);
         const int p = rem / (wnp - wn), g = wn + rem - p * (wnp - wn);
         L.X3[(m * 3 + p) * L.xg + g] = 0;
     }
-    for (int bb = 0; bb < nb8; bb += 256) {
+    for (int bb = 0; bb < nb8; bb += NT) {
         const int b = bb + tid;
         const bool valid = b < nb8;
         const int k = wg0 * 32 + b * 8;
@@ -267,9 +278,10 @@ __device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, boo
         }
     }
     if (WFMT == GEMV_W_INT8) {
-        __syncthreads();
+        if constexpr (NT == 256) __syncthreads();
+        else wave_lds_sync();
         /* window activation total per row, wave per row, fixed order */
-        for (int m = wave; m < M; m += 4) {
+        for (int m = wave; m < M; m += NWS) {
             float s = 0.f;
             for (int g = lane; g < wn; g += 64)
                 s += bf2f(L.X3[(m * 3 + 0) * L.xg + g]) +
@@ -331,11 +343,6 @@ S2P_DEV void gv_load(GvBuf& B, const GemvArgs& a, int nrow, int gabs, int gn, in
     }
 }
 
-S2P_DEV void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 /* D = A(16x16) * B(16x16) + C (v_mfma_f32_16x16x16_bf16): lane l supplies A
  * row l % 16 and B column l % 16, k-slots 4 (l / 16) .. +3; D as the x32 form */
@@ -501,9 +508,11 @@ __device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y) {
             }
         }
         if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
-            /* one wave = one row m = the block's 64 columns */
-            const float tot = wave_sum_down(ssq);
-            if (lane == 0 && m < M) coh_stf(a.ssq_out + (size_t)rb * GEMV_MAX_M + m, tot);
+            /* one wave = one row m = the block's 64 columns = four
+             * sum-of-squares blocks of 16 */
+            const float tot = sum_lanes16(ssq);
+            if ((lane & 15) == 0 && m < M)
+                coh_stf(a.ssq_out + (size_t)(rb * 4 + (lane >> 4)) * GEMV_MAX_M + m, tot);
         }
     }
 }
@@ -718,4 +727,308 @@ __device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned c
 }
 
 #undef GV_PROBE
+
+/* ===================================================================== */
+/* Whole-K engine (no cross-workgroup handoff).
+ *
+ * A workgroup of nw = rt * ks waves stays resident and walks tile groups
+ * p, p + P, ...: a tile group is rt 16-row tiles (SWIGLU: rt / 2 gate tiles
+ * and the matching up tiles), and the ks waves of a tile split K.  The
+ * activations are staged in LDS once per workgroup (ks K slices, shared by
+ * the rt waves of a slice) and reused by every tile group.  Each wave runs
+ * one flattened, double-buffered weight stream over its (tile, K slice)
+ * chunks of all its tile groups, so the next group's weights are in flight
+ * while a group is reduced: the waves' partial tiles meet in LDS (two
+ * buffers, one workgroup barrier per group), are summed in wave order
+ * (deterministic) and the epilogue runs.  Nothing but the outputs goes to
+ * global memory. */
+
+static __host__ __device__ inline size_t gv3_slice_bytes(int M, int gps, int wfmt) {
+    const size_t xs = (size_t)gps * 32 + GV_XPAD;
+    const size_t xg = (size_t)gv_round32(gps) + 8;
+    size_t b = ((size_t)M * xs * 2 + (size_t)M * 3 * xg * 2 + 15) & ~(size_t)15;
+    if (wfmt == GEMV_W_INT8) b += ((size_t)M * 4 + 15) & ~(size_t)15;
+    return b;
+}
+/* slices [ks], INT4 scale staging [nw][16 groups][16 rows] f32, inverse RMS
+ * [GEMV_MAX_M], partial tiles [nbuf][nw][MT][64 lanes][4] f32 (two buffers
+ * when a workgroup walks more than one tile group) */
+static __host__ __device__ inline size_t gv3_lds_bytes(int M, int gps, int wfmt, int ks, int nw,
+                                                       int nbuf) {
+    const int mt = (M + 15) / 16;
+    return (size_t)ks * gv3_slice_bytes(M, gps, wfmt) +
+           (wfmt == GEMV_W_INT4 ? (size_t)nw * 1024 : 0) + GEMV_MAX_M * 4 +
+           (size_t)nbuf * nw * mt * 1024;
+}
+
+/* Loads issued before the weight stream (waits are in issue order, so a
+ * load issued after the weights would wait for them too): the producer's
+ * sums of squares of row `wave` (blocks lane + 64 i), and rows 0..7 of the
+ * wave's first 64 column blocks of its K slice. */
+struct Gv3Pre {
+    s2p_u32x4 raw[8];
+    s2p_u32x4 wn4;
+    float ssq[3];
+};
+
+template <bool COH>
+S2P_DEV void gv3_pre_issue(const GemvArgs& a, Gv3Pre& pre, bool stager, int wave, int lane,
+                           int gb, int gn) {
+    const int M = a.M;
+    const bool norm = a.xmode == GEMV_X_NORM;
+    if (norm && wave < M) {
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            if (lane + 64 * i < a.ssq_in_blocks)
+                pre.ssq[i] = ld_actf<COH>(a.ssq_in + (size_t)(lane + 64 * i) * GEMV_MAX_M + wave);
+    }
+    if (stager && lane < gn * 4) {
+        const int k = gb * 32 + lane * 8;
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (m < M) pre.raw[m] = ld_act128<COH>(a.x + (size_t)m * a.ldx + k);
+        if (norm) pre.wn4 = *(const s2p_u32x4*)(a.norm_w + k);
+    }
+}
+
+template <bool COH>
+S2P_DEV void st_act16(uint16_t* p, uint16_t v) {
+    if constexpr (COH) coh_st16(p, v);
+    else *p = v;
+}
+
+template <int WFMT, int MT, bool COH>
+__device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* smem,
+                          uint16_t* Y) {
+#pragma clang fp contract(off)
+    constexpr int CHG = WFMT == GEMV_W_INT4 ? GV_CHG_INT4 : GV_CHG_INT8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q = lane >> 4, r = lane & 15;
+    const int M = a.M, G = a.K >> 5, ks = a.ks, rt = a.rt, gps = a.gps;
+    const int nw = rt * ks;
+    const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
+    const int F = a.N >> 1;
+    const int units = swiglu ? rt >> 1 : rt;             /* output tiles per group */
+    const int tiles = swiglu ? F >> 4 : (a.N + 15) >> 4; /* output tiles */
+    const int ngroups = (tiles + units - 1) / units;
+    const int niter = p < ngroups ? (ngroups - p + P - 1) / P : 0;
+    if (niter == 0) return; /* uniform over the workgroup */
+    const int j = wave / ks, sp = wave - j * ks; /* tile of the group, K slice */
+    const int gb = sp * gps, gn = min(G, gb + gps) - gb;
+    uint64_t* const probe = a.probe ? a.probe + (size_t)blockIdx.x * 8 : nullptr;
+    auto stamp = [&](int i) __attribute__((always_inline)) {
+        if (probe && tid == 0) probe[i] = wall_clock64();
+    };
+    stamp(0);
+
+    /* carve */
+    const size_t sb = gv3_slice_bytes(M, gps, WFMT);
+    LDS(unsigned char)* slice = smem + (size_t)sp * sb;
+    GvLds L;
+    L.xs = gps * 32 + GV_XPAD;
+    L.xg = gv_round32(gps) + 8;
+    L.x = (LDS(uint16_t)*)slice;
+    uint32_t off = (uint32_t)M * L.xs * 2;
+    L.X3 = (LDS(uint16_t)*)(slice + off);
+    off = (off + (uint32_t)M * 3 * L.xg * 2 + 15) & ~15u;
+    L.xtot = (LDS(float)*)(slice + off);
+    size_t o2 = (size_t)ks * sb;
+    L.sc = (LDS(float)*)(smem + o2 + (size_t)wave * 1024);
+    if (WFMT == GEMV_W_INT4) o2 += (size_t)nw * 1024;
+    L.inv = (LDS(float)*)(smem + o2);
+    o2 += GEMV_MAX_M * 4;
+    L.flag = nullptr;
+    LDS(s2p_f32x4)* red = (LDS(s2p_f32x4)*)(smem + o2);
+
+    /* weight rows of this wave in tile group g */
+    auto wrow = [&](int g) __attribute__((always_inline)) {
+        int t, base;
+        if (swiglu) {
+            const int h = units;
+            t = g * h + (j < h ? j : j - h);
+            base = (j < h ? 0 : F) + t * 16;
+        } else {
+            t = g * units + j;
+            base = t * 16;
+        }
+        return min(base + r, a.N - 1);
+    };
+    const int nch = (gn + CHG - 1) / CHG;
+    const int T = niter * nch;
+    auto load_t = [&](GvBuf& B, int t) __attribute__((always_inline)) {
+        const int it = t / nch, c = t - it * nch;
+        gv_load<WFMT>(B, a, wrow(p + it * P), gb + c * CHG, min(CHG, gn - c * CHG), q);
+    };
+
+    GvBuf b0, b1;
+    Gv3Pre pre;
+    gv3_pre_issue<COH>(a, pre, j == 0, wave, lane, gb, gn);
+    load_t(b0, 0);
+    if (a.xmode == GEMV_X_NORM) {
+        /* inverse RMS per row: lanes take the producer's blocks, fixed-order
+         * wave reduction */
+        for (int m = wave; m < M; m += nw) {
+            float s = 0.f;
+            if (m == wave && a.ssq_in_blocks <= 192) {
+#pragma unroll
+                for (int i = 0; i < 3; i++)
+                    if (lane + 64 * i < a.ssq_in_blocks) s += pre.ssq[i];
+            } else {
+                for (int b = lane; b < a.ssq_in_blocks; b += 64)
+                    s += ld_actf<COH>(a.ssq_in + (size_t)b * GEMV_MAX_M + m);
+            }
+            s = wave_sum_down(s);
+            if (lane == 0) L.inv[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
+        }
+        __syncthreads();
+    }
+    stamp(1);
+    if (j == 0) {
+        /* the slice's stager: rows < 8 of the first 64 column blocks from
+         * the registers, the rest loaded here */
+        const int nb8 = gn * 4;
+        const int wnp = gv_round32(gn);
+        for (int i = lane; i < M * 3 * (wnp - gn); i += 64) {
+            const int m = i / (3 * (wnp - gn)), rem = i - m * 3 * (wnp - gn);
+            const int pp = rem / (wnp - gn), g = gn + rem - pp * (wnp - gn);
+            L.X3[(m * 3 + pp) * L.xg + g] = 0;
+        }
+#pragma unroll
+        for (int m = 0; m < 8; m++)
+            if (m < M) gv_stage_one<WFMT>(a, L, m, lane, lane < nb8, pre.raw[m], pre.wn4);
+        for (int bb = 0; bb < nb8; bb += 64) {
+            const int b = bb + lane;
+            const bool valid = b < nb8;
+            const int k = gb * 32 + b * 8;
+            s2p_u32x4 wn4 = {0u, 0u, 0u, 0u};
+            if (valid && a.xmode == GEMV_X_NORM) wn4 = *(const s2p_u32x4*)(a.norm_w + k);
+            for (int m0 = bb == 0 ? 8 : 0; m0 < M; m0 += 4) {
+                s2p_u32x4 raw[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+                    raw[jj] = (valid && m0 + jj < M)
+                                  ? ld_act128<COH>(a.x + (size_t)(m0 + jj) * a.ldx + k)
+                                  : (s2p_u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+                    if (m0 + jj < M) gv_stage_one<WFMT>(a, L, m0 + jj, b, valid, raw[jj], wn4);
+            }
+        }
+        if (WFMT == GEMV_W_INT8) {
+            wave_lds_sync();
+            for (int m = 0; m < M; m++) {
+                float s = 0.f;
+                for (int g = lane; g < gn; g += 64)
+                    s += bf2f(L.X3[(m * 3 + 0) * L.xg + g]) + bf2f(L.X3[(m * 3 + 1) * L.xg + g]) +
+                         bf2f(L.X3[(m * 3 + 2) * L.xg + g]);
+                s = wave_sum_down(s);
+                if (lane == 0) L.xtot[m] = s;
+            }
+        }
+    }
+    __syncthreads();
+    stamp(2);
+
+    s2p_f32x4 acc[MT], corr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+        corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+
+    /* end of tile group it: partial tile to LDS, barrier, sum + epilogue */
+    auto finish = [&](int it) __attribute__((always_inline)) {
+        LDS(s2p_f32x4)* rb = red + (size_t)(it & 1) * nw * MT * 64;
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            s2p_f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[i] = WFMT == GEMV_W_INT4
+                           ? 16.0f * acc[t][i] - 24.0f * corr[t][i]
+                           : fmaf(-128.0f, L.xtot[min(t * 16 + r, M - 1)], acc[t][i]);
+            rb[(wave * MT + t) * 64 + lane] = v;
+            acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        if (it == 0) stamp(3);
+        __syncthreads();
+        if (it == 0) stamp(4);
+        /* output (row rho of unit u, column m): element rho % 4 of lane
+         * (rho / 4) * 16 + m % 16, column tile m / 16, of the unit's waves */
+        const LDS(float)* rf = (const LDS(float)*)rb;
+        const int g = p + it * P;
+        auto tsum = [&](int jw, int rho, int m) __attribute__((always_inline)) {
+            const int src = ((m >> 4) * 64 + (rho >> 2) * 16 + (m & 15)) * 4 + (rho & 3);
+            float v = 0.f;
+            for (int s = 0; s < ks; s++) v += rf[(size_t)(jw * ks + s) * MT * 256 + src];
+            return v;
+        };
+        const int nitems = units * M * 16;
+        for (int base = 0; base < nitems; base += nw * 64) {
+            const int idx = base + tid;
+            const int rho = idx & 15, um = idx >> 4;
+            const int u = um / M, m = um - u * M;
+            const int tile = g * units + u;
+            const int n = tile * 16 + rho;
+            const bool ok = u < units && tile < tiles;
+            if (swiglu) {
+                if (ok) {
+                    float gv = tsum(u, rho, m), uv = tsum(units + u, rho, m);
+                    if (WFMT == GEMV_W_INT8) {
+                        gv *= ((const float*)a.s)[n];
+                        uv *= ((const float*)a.s)[F + n];
+                    }
+                    st_act16<COH>(Y + (size_t)m * a.ldy + n, silu_mul_bf16(f2bf(gv), f2bf(uv)));
+                }
+                continue;
+            }
+            float ssq = 0.f;
+            if (ok && n < a.N) {
+                float v = tsum(u, rho, m);
+                if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
+                const uint16_t yb = f2bf(v);
+                uint16_t* yp = Y + (size_t)m * a.ldy + n;
+                if (a.epi == GEMV_EPI_RESID) {
+                    const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
+                    st_act16<COH>(yp, xo);
+                    const float xv = bf2f(xo);
+                    ssq = xv * xv;
+                } else {
+                    st_act16<COH>(yp, yb);
+                }
+            }
+            if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                const float tot = sum_lanes16(ssq); /* the 16 rows of (tile, m) */
+                if (rho == 0 && ok) coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+            }
+        }
+    };
+    auto step = [&](const GvBuf& B, int t) __attribute__((always_inline)) {
+        const int it = t / nch, c = t - it * nch;
+        gv_compute<WFMT, MT>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
+        if (c == nch - 1) finish(it);
+    };
+    /* every path into a step has the same loads outstanding, and no load is
+     * issued past the end */
+    int t = 0;
+    for (; t + 2 < T; t += 2) {
+        load_t(b1, t + 1);
+        step(b0, t);
+        load_t(b0, t + 2);
+        step(b1, t + 1);
+    }
+    if (T - t == 2) {
+        load_t(b1, t + 1);
+        step(b0, t);
+        step(b1, t + 1);
+    } else {
+        step(b0, t);
+    }
+    if (probe) {
+        vm_drain();
+        stamp(5);
+    }
+}
+
 #endif

@@ -11,10 +11,11 @@ extern "C" {
 #endif
 
 #define GEMV_MAX_M 128         /* rows per call (8 MFMA column tiles) */
+#define GEMV_SSQ_COLS 16       /* columns per sum-of-squares block */
 
 enum { GEMV_W_INT4 = 0, GEMV_W_INT8 = 1 };            /* weight formats */
 enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1 };            /* activation staging */
-/* STORE: y = bf16(W x); RESID: y = bf16(y + bf16(W x)) plus per-64-column
+/* STORE: y = bf16(W x); RESID: y = bf16(y + bf16(W x)) plus per-16-column
  * sums of squares; SWIGLU: W = [gate; up] (2F rows), y[m][F] =
  * silu(bf16(gate)) * bf16(up) with the rule's roundings. */
 enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1, GEMV_EPI_SWIGLU = 2 };
@@ -32,19 +33,26 @@ typedef struct {
     int             splits;  /* derived by the launcher */
     int             win;     /* derived: staged groups per LDS window */
     int             nrb;     /* derived: 64-row blocks */
+    int             ks;      /* derived (whole-K engine): K slices = waves per 16-row tile */
+    int             rt;      /* derived (whole-K engine): 16-row tiles per tile group */
     int             xmode;
     const uint16_t* norm_w;  /* NORM: bf16 [K] */
     float           norm_eps;
     const float*    ssq_in;  /* NORM: [ssq_in_blocks][GEMV_MAX_M] */
     int             ssq_in_blocks;
     int             epi;
-    float*          ssq_out; /* RESID: [ceil(N/64)][GEMV_MAX_M] (may be NULL) */
+    float*          ssq_out; /* RESID: [ceil(N/16)][GEMV_MAX_M] (may be NULL) */
     float*          part;    /* [splits][M][nrb][64] fp32 */
     int64_t         part_cap;/* floats available at part */
     unsigned*       counters;/* [ceil(N/64)], zero between calls */
+    uint64_t*       probe;   /* diagnostics (whole-K engine): [grid][8] stage clocks */
 } GemvArgs;
 
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
+/* test hook: 0 = launcher's choice, 2 = split-K engine only */
+void s2p_gemv_set_engine(int engine);
+/* diagnostics: stage clocks of the whole-K launch `index` launches from now */
+void s2p_gemv_set_probe(uint64_t* buf, int index);
 /* resident-workgroup target the launcher plans GEMVs for (env S2P_GEMV_TARGET_WG) */
 int s2p_gemv_slots(void);
 hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,

@@ -46,7 +46,7 @@ struct s2p_backbone {
     void* q;      /* [max_rows][4096] */
     void* attn;   /* [max_rows][4096] */
     void* gu;     /* [max_rows][9728] SwiGLU output h */
-    float* ssq;   /* [2][64][GEMV_MAX_M] per-block sums of squares */
+    float* ssq;   /* [2][S2P_DIM / GEMV_SSQ_COLS][GEMV_MAX_M] per-block sums of squares */
     float* attn_part;
     int64_t attn_part_floats;
     /* plan (device + pinned host staging) */
@@ -165,7 +165,7 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc(&b->q, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
     if (rc == S2P_OK) rc = dalloc(&b->attn, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
     if (rc == S2P_OK) rc = dalloc(&b->gu, R * 2 * S2P_FFN_DIM * 2);
-    if (rc == S2P_OK) rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * 64 * GEMV_MAX_M);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M);
     b->attn_part_floats = s2p_attn_plan_part_floats((int)R, opts->ctx_len);
     if (rc == S2P_OK) rc = dalloc((void**)&b->attn_part, sizeof(float) * b->attn_part_floats);
     const int S = opts->max_sessions;
@@ -440,7 +440,7 @@ static void gemv_args(GemvArgs* ap, const s2p_linear* lin, int M, const void* x,
     a.norm_w = (const uint16_t*)norm_w;
     a.norm_eps = NORM_EPS;
     a.ssq_in = ssq_in;
-    a.ssq_in_blocks = S2P_DIM / 64;
+    a.ssq_in_blocks = S2P_DIM / GEMV_SSQ_COLS;
     a.epi = epi;
     a.ssq_out = ssq_out;
     a.part = s2p_gemm_ctx_part();
@@ -469,7 +469,7 @@ static int mk_build(s2p_backbone* b) {
     MkGemv* head = (MkGemv*)(b->h_mk + mk_off_head(b->o.n_layers));
     memset(b->h_mk, 0, b->mk_bytes);
     float* ssq_a = b->ssq;
-    float* ssq_b = b->ssq + 64 * GEMV_MAX_M;
+    float* ssq_b = b->ssq + (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M;
     /* GEMVs planned for the kernel's own grid (one work unit per workgroup) */
     const int slots = b->mk_nwg;
     for (int l = 0; l < b->o.n_layers; l++) {
@@ -545,7 +545,7 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
     const int M = b->rows;
     const S2pRowPlan plan = row_plan(b);
     float* ssq_a = b->ssq;
-    float* ssq_b = b->ssq + 64 * GEMV_MAX_M;
+    float* ssq_b = b->ssq + (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M;
     S2P_TRY(hip_ok(s2p_resid_init_launch(x_in, b->x, ssq_a, M, S2P_DIM, st), "resid init"));
     for (int l = 0; l < b->o.n_layers; l++) {
         const s2p_slow_layer* L = &b->layers[l];

@@ -39,7 +39,7 @@ typedef struct {
     const MkGemv* head;    /* device */
     int wfmt;
     uint16_t* x;           /* residual stream [rows][2560] */
-    float* ssq_a;          /* sums of squares of x, [40][128] */
+    float* ssq_a;          /* sums of squares of x, [160][128] */
     float* ssq_b;
     uint16_t* qkv;
     uint16_t* q;

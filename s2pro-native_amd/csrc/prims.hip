@@ -303,8 +303,8 @@ extern "C" hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, con
     return hipGetLastError();
 }
 
-/* Residual stream init: x = x_in and per-64-column sums of squares of x
- * (layout [N/64][GEMV_MAX_M]) for the first RMSNorm. */
+/* Residual stream init: x = x_in and per-16-column sums of squares of x
+ * (layout [N/16][GEMV_MAX_M]) for the first RMSNorm. */
 __global__ __launch_bounds__(64) void k_resid_init(const uint16_t* __restrict__ xin,
                                                    uint16_t* __restrict__ x,
                                                    float* __restrict__ ssq, int width) {

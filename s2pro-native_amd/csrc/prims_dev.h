@@ -98,15 +98,16 @@ S2P_DEV void rope_tab_item(const S2pRowPlan& plan, float base, float* tab, int r
 }
 
 /* Residual stream init of one 64-column block of row m: x = x_in and the
- * block's sum of squares (layout [width/64][GEMV_MAX_M = 128]). */
+ * sums of squares of its four 16-column blocks (layout [width/16][GEMV_MAX_M
+ * = 128]). */
 S2P_DEV void resid_init_item(const uint16_t* xin, uint16_t* x, float* ssq, int width, int blk,
                              int m, int lane) {
     const size_t i = (size_t)m * width + blk * 64 + lane;
     const uint16_t v = xin[i];
     coh_st16(x + i, v);
     const float f = bf2f(v);
-    const float t = wave_sum_down(f * f);
-    if (lane == 0) coh_stf(ssq + (size_t)blk * 128 + m, t);
+    const float t = sum_lanes16(f * f);
+    if ((lane & 15) == 0) coh_stf(ssq + (size_t)(blk * 4 + (lane >> 4)) * 128 + m, t);
 }
 
 #endif

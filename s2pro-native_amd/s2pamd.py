@@ -121,6 +121,8 @@ SIGS = {
 EXTRA = {
     "s2p_backbone_set_mk": (None, [P, I]),
     "s2p_gemv_set_slots": (None, [I]),
+    "s2p_gemv_set_engine": (None, [I]),
+    "s2p_gemv_set_probe": (None, [P, I]),
     "s2p_backbone_mk_grid": (I, [P]),
     "s2p_backbone_mk_status": (I, [P]),
     "s2p_backbone_mk_times": (I, [P, P, I]),

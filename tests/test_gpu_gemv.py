@@ -24,6 +24,15 @@ def lib():
     return lib
 
 
+@pytest.fixture(params=[0, 2], ids=["auto", "splitk"])
+def engine(request, lib):
+    """launcher's engine choice (whole-K workgroups where they fit), then the
+    split-K engine forced"""
+    lib.s2p_gemv_set_engine(request.param)
+    yield request.param
+    lib.s2p_gemv_set_engine(0)
+
+
 def rand_int4(r, N, K):
     packed = r.integers(0, 256, (N, K // 2), dtype=np.uint8)
     scales = np.abs(r.standard_normal((N, K // 32)) * 0.02).astype(np.float16).view(np.uint16)
@@ -34,7 +43,7 @@ def rand_int4(r, N, K):
 @pytest.mark.parametrize("M,N,K", [(5, 9728, 2560), (1, 6144, 2560), (16, 2560, 4096),
                                    (5, 2560, 9728), (5, 19456, 2560), (3, 4097, 2560),
                                    (7, 100, 512)])
-def test_int4p_gemv_vs_oracle(lib, M, N, K):
+def test_int4p_gemv_vs_oracle(lib, engine, M, N, K):
     r = np.random.default_rng(1000 + M * 7 + N)
     packed, scales = rand_int4(r, N, K)
     x = bf16_bits(r.standard_normal((M, K)).astype(np.float32))
@@ -62,7 +71,7 @@ def test_int4p_gemm_large_m(lib, M, N, K):
     assert_close_rel(got, po.int4p_gemv_f64(x, packed, scales, M, N, K), what=f"M={M}")
 
 
-def test_int4p_gemv_closed_forms(lib):
+def test_int4p_gemv_closed_forms(lib, engine):
     """All weights -8, unit scales: y = -8 * sum(x); single nonzero weight."""
     M, N, K = 4, 64, 2560
     r = np.random.default_rng(3)
@@ -93,7 +102,7 @@ def test_int4p_gemv_closed_forms(lib):
 
 @pytest.mark.parametrize("M,N,K", [(5, 6144, 2560), (5, 2560, 9728), (16, 19456, 2560),
                                    (40, 2560, 4096)])
-def test_int8_gemv_vs_oracle(lib, M, N, K):
+def test_int8_gemv_vs_oracle(lib, engine, M, N, K):
     r = np.random.default_rng(3000 + M + N)
     q = r.integers(-127, 128, (N, K)).astype(np.int8)
     s = (np.abs(r.standard_normal(N)) * 1e-3).astype(np.float32)

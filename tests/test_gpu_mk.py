@@ -31,6 +31,7 @@ def test_mk_matches_layerwise(lib, quant, n_layers, L):
         out = {}
         # the layer-by-layer GEMVs planned for the persistent kernel's grid
         lib.s2p_gemv_set_slots(lib.s2p_backbone_mk_grid(bb))
+        lib.s2p_gemv_set_engine(2)  # the persistent kernel runs the split-K engine
         for mode in (1, 0):
             lib.s2p_backbone_set_mk(bb, mode)
             kv.copy_(__import__("torch").from_numpy(kv0.view(np.int16)).to(kv.device))
@@ -55,4 +56,5 @@ def test_mk_matches_layerwise(lib, quant, n_layers, L):
         assert np.array_equal(to_host(logits, np.uint16), out[1][0])
     finally:
         lib.s2p_gemv_set_slots(0)
+        lib.s2p_gemv_set_engine(0)
         lib.s2p_backbone_free(bb)
