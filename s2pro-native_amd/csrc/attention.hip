@@ -49,8 +49,17 @@ static int64_t part_floats(int rows, int qh, int nsplit) {
     return (int64_t)rows * qh * nsplit * (AT_HD + 2);
 }
 
+static uint64_t* g_attn_probe = nullptr;
+static int g_attn_probe_at = -1;
+/* diagnostics: stage clocks of the attention launch `index` launches from now */
+extern "C" void s2p_attn_set_probe(uint64_t* buf, int index) {
+    g_attn_probe = buf;
+    g_attn_probe_at = buf ? index : -1;
+}
+
 static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
                            int64_t part_cap, hipStream_t st) {
+    if (g_attn_probe_at >= 0 && g_attn_probe_at-- == 0) a.probe = g_attn_probe;
     const int tiles = (max_span + AT_TILE * AT_WAVES - 1) / (AT_TILE * AT_WAVES);
     int tpw = 1; /* tiles per wave per split */
     if (a.part && part_cap > 0) {

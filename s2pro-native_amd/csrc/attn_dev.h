@@ -55,6 +55,7 @@ struct AttnArgs {
     /* non-NULL: the last split to finish a (segment, kv head) merges the
      * splits itself (persistent kernel); NULL: k_attn_combine does */
     unsigned* counters;
+    uint64_t* probe; /* diagnostics: [grid][8] stage clocks */
 };
 
 struct SegInfo {
@@ -177,6 +178,12 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
     const int qrow_stride = a.qh * AT_HD;
+    uint64_t* const probe =
+        a.probe ? a.probe + ((size_t)(sp * gridDim.y + kvh) * gridDim.x + seg) * 8 : nullptr;
+    auto stamp = [&](int i) __attribute__((always_inline)) {
+        if (probe && threadIdx.x == 0) probe[i] = wall_clock64();
+    };
+    stamp(0);
 
     /* Q operands: A row i = c -> query vector qv = 16 qt + c */
     s2p_u32x4 qa[MQT][4];
@@ -216,17 +223,27 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             const int pos = min(tb + 16 * ps + c, p_end - 1);
 #pragma unroll
             for (int ch = 0; ch < 4; ch++)
-                kr[ps][ch] = __builtin_nontemporal_load(
-                    (const s2p_u32x4*)(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq));
+                kr[ps][ch] = gld_nt128(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq);
         }
-        /* V tile -> LDS [pos][dim], stored as soon as it arrives (keeps the
-         * tile out of registers during the score MFMAs) */
+        /* V tile -> LDS [pos][dim]: every load in flight, then the stores
+         * (keeps the tile out of registers during the score MFMAs) */
+        {
+            s2p_u32x4 vr[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int idx = i * 64 + lane;
-            const int pos = min(tb + (idx >> 4), p_end - 1);
-            *(LDS(s2p_u32x4)*)&SV(wave, idx >> 4, 8 * (idx & 15)) = __builtin_nontemporal_load(
-                (const s2p_u32x4*)(S.vp + (size_t)pos * AT_HD + 8 * (idx & 15)));
+            for (int i = 0; i < 8; i++) {
+                const int idx = i * 64 + lane;
+                const int pos = min(tb + (idx >> 4), p_end - 1);
+                vr[i] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * (idx & 15));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int idx = i * 64 + lane;
+                *(LDS(s2p_u32x4)*)&SV(wave, idx >> 4, 8 * (idx & 15)) = vr[i];
+            }
+        }
+        if (probe && tb == p_begin) {
+            vm_drain();
+            stamp(1);
         }
         /* scores */
         s2p_f32x4 sc[MQT][2];
@@ -290,6 +307,7 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         wave_sync_lds();
     }
 
+    stamp(2);
     /* ---- merge the 4 waves ---- */
 #pragma unroll
     for (int qt = 0; qt < MQT; qt++)
@@ -349,6 +367,7 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     __syncthreads();
     if (wave == 1) put(0);
     __syncthreads();
+    stamp(3);
     if (wave == 0) {
         add(0);
         /* ---- write ---- */
@@ -378,6 +397,10 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                     }
                 }
             }
+    }
+    if (probe) {
+        vm_drain();
+        stamp(4);
     }
     if (a.nsplit == 1 || !a.counters) return;
     /* last split of this (segment, kv head) to finish merges the splits */

@@ -12,6 +12,13 @@ typedef __attribute__((ext_vector_type(4))) float s2p_f32x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t s2p_u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t s2p_u32x2;
 
+/* 16-byte streaming load through a global-address-space pointer (a generic
+ * pointer would compile to flat_load, which also counts against lgkmcnt and
+ * serialises with LDS traffic) */
+S2P_DEV s2p_u32x4 gld_nt128(const void* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) s2p_u32x4*)p);
+}
+
 /* bf16 bit pattern -> float (exact) */
 S2P_DEV float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 S2P_DEV float bf2f_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -19,11 +26,9 @@ S2P_DEV float bf2f_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 /* float -> bf16 bit pattern, round to nearest even (NaN stays NaN) */
 S2P_DEV uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
-        return (uint16_t)((u >> 16) | 0x0040u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    /* v_cvt_pk_bf16_f32: round to nearest even, NaN quieted (the rule:
+     * u + 0x7FFF + lsb, NaN -> (u >> 16) | 0x40; pinned by a GPU test) */
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 /* IEEE f16 bit pattern <-> float (hardware conversions, RNE) */

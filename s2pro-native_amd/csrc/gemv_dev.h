@@ -250,12 +250,10 @@ __device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, boo
         }
         __syncthreads();
     }
-    /* zero the group sums of the padded tail (read by the correction MFMA) */
-    for (int i = tid; i < M * 3 * (wnp - wn); i += NT) {
-        const int m = i / (3 * (wnp - wn)), rem = i - m * 3 * (wnp - wn);
-        const int p = rem / (wnp - wn), g = wn + rem - p * (wnp - wn);
-        L.X3[(m * 3 + p) * L.xg + g] = 0;
-    }
+    /* zero the group sums of the padded tail (read by the correction MFMA;
+     * fewer than 32 groups per row) */
+    for (int row = tid >> 5; row < M * 3; row += NT / 32)
+        if ((tid & 31) < wnp - wn) L.X3[row * L.xg + wn + (tid & 31)] = 0;
     for (int bb = 0; bb < nb8; bb += NT) {
         const int b = bb + tid;
         const bool valid = b < nb8;
@@ -888,11 +886,8 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
          * the registers, the rest loaded here */
         const int nb8 = gn * 4;
         const int wnp = gv_round32(gn);
-        for (int i = lane; i < M * 3 * (wnp - gn); i += 64) {
-            const int m = i / (3 * (wnp - gn)), rem = i - m * 3 * (wnp - gn);
-            const int pp = rem / (wnp - gn), g = gn + rem - pp * (wnp - gn);
-            L.X3[(m * 3 + pp) * L.xg + g] = 0;
-        }
+        for (int row = lane >> 5; row < M * 3; row += 2)
+            if ((lane & 31) < wnp - gn) L.X3[row * L.xg + gn + (lane & 31)] = 0;
 #pragma unroll
         for (int m = 0; m < 8; m++)
             if (m < M) gv_stage_one<WFMT>(a, L, m, lane, lane < nb8, pre.raw[m], pre.wn4);
@@ -928,6 +923,10 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
     }
     __syncthreads();
     stamp(2);
+    if (probe) { /* diagnostics: weights arrived */
+        vm_drain();
+        stamp(6);
+    }
 
     s2p_f32x4 acc[MT], corr[MT];
 #pragma unroll
@@ -964,14 +963,13 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
             for (int s = 0; s < ks; s++) v += rf[(size_t)(jw * ks + s) * MT * 256 + src];
             return v;
         };
-        const int nitems = units * M * 16;
-        for (int base = 0; base < nitems; base += nw * 64) {
+        for (int u = 0; u < units; u++)
+        for (int base = 0; base < M * 16; base += nw * 64) {
             const int idx = base + tid;
-            const int rho = idx & 15, um = idx >> 4;
-            const int u = um / M, m = um - u * M;
+            const int rho = idx & 15, m = idx >> 4;
             const int tile = g * units + u;
             const int n = tile * 16 + rho;
-            const bool ok = u < units && tile < tiles;
+            const bool ok = m < M && tile < tiles;
             if (swiglu) {
                 if (ok) {
                     float gv = tsum(u, rho, m), uv = tsum(units + u, rho, m);

@@ -351,3 +351,16 @@ extern "C" hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t
                        n_acc, R);
     return hipGetLastError();
 }
+
+/* Test hook: the device float -> bf16 conversion every kernel uses, over n
+ * values (pinned against the rule by a GPU test). */
+__global__ void k_f2bf(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f2bf(in[i]);
+}
+
+extern "C" hipError_t s2p_test_f2bf(const float* in, uint16_t* out, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_f2bf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, out, n);
+    return hipGetLastError();
+}

@@ -123,6 +123,8 @@ EXTRA = {
     "s2p_gemv_set_slots": (None, [I]),
     "s2p_gemv_set_engine": (None, [I]),
     "s2p_gemv_set_probe": (None, [P, I]),
+    "s2p_attn_set_probe": (None, [P, I]),
+    "s2p_test_f2bf": (I, [P, P, I64, P]),
     "s2p_backbone_mk_grid": (I, [P]),
     "s2p_backbone_mk_status": (I, [P]),
     "s2p_backbone_mk_times": (I, [P, P, I]),

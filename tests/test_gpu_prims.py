@@ -99,3 +99,26 @@ def test_qkv_split_silu_add(lib):
 def test_rows_zero_is_success(lib):
     assert lib.s2pk_rms_norm(None, None, None, 0, 2560, 1e-6, S()) == 0
     assert lib.s2pk_attention(None, None, None, None, 0, 32, 8, 128, 0, 16, S()) == 0
+
+
+def test_f2bf_matches_rule(lib):
+    """The hardware float -> bf16 conversion the kernels use equals the
+    rule's rounding (or_f2bf: nearest even, NaN quieted with its payload's
+    top bits) on random bit patterns and the edge cases: ties, carries into
+    the exponent, overflow to inf, infinities, NaN payloads, subnormals."""
+    r = np.random.default_rng(77)
+    bits = r.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    edge = []
+    for sign in (0, 0x80000000):
+        for e in (0x00000000, 0x00800000, 0x3F800000, 0x7F000000, 0x7F800000):
+            for m in (0, 1, 0x7FFF, 0x8000, 0x8001, 0x18000, 0x10000, 0x7FFFFF, 0x7F8000,
+                      0x400000, 0x400001, 0x3FFFFF):
+                edge.append(sign | e | m)
+    bits = np.concatenate([bits, np.array(edge, np.uint32)])
+    x = bits.view(np.float32)
+    out = empty((x.size,))
+    s2pamd.hip_check(lib.s2p_test_f2bf(P(to_dev(x)), P(out), x.size, S()))
+    got = to_host(out, np.uint16)
+    want = po.f32_to_bf16(x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(hex(bits[i]), hex(got[i]), hex(want[i])) for i in bad[:8]]
