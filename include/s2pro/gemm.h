@@ -29,7 +29,7 @@ extern "C" {
 #endif
 
 typedef enum {
-    S2P_GEMM_BF16 = 0,   /* unquantised (not served by this build) */
+    S2P_GEMM_BF16 = 0,   /* unquantised bf16 weights (s2p_gemm_bf16) */
     S2P_GEMM_FP8  = 1,   /* out of scope */
     S2P_GEMM_INT8 = 2,   /* weight-only INT8 per channel / INT4 group-wise */
 } s2p_gemm_mode;
@@ -93,6 +93,11 @@ s2p_status s2p_linear_init_random_int4(s2p_linear* lin, int in_features,
 s2p_status s2p_linear_init_random_int8(s2p_linear* lin, int in_features,
                                        int out_features, float sigma,
                                        uint64_t seed, hipStream_t stream);
+
+/* Raw bf16 GEMM for non-quantised matmuls (reference gemm.h:93-96, cuBLAS
+ * there): y[M,N] = x[M,K] * w[N,K]^T, bf16 in/out, fp32 accumulate. */
+s2p_status s2p_gemm_bf16(const void* x, const void* w, void* y, int M, int N,
+                         int K, hipStream_t stream);
 
 /* ---- raw primitives (reference src/sched/int8_gemv.cu) ------------------ */
 

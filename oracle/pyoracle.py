@@ -65,6 +65,9 @@ _SIGS = {
     "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P]),
     "or_linear_fwd": (None, [P, P, P, I]),
     "or_layer": (None, [P, P, I, P, P, I, I, P, P]),
+    "or_gemm_bf16": (None, [P, P, P, I, I, I]),
+    "or_gemm_bf16_f64": (None, [P, P, P, I, I, I]),
+    "or_draft_step": (None, [P, P, P, I, I, P, P, P]),
 }
 
 
@@ -310,3 +313,36 @@ def layer(lw, x, rows, kc, vc, max_seq, prefix, pos, vis=None):
     va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
     lib().or_layer(ctypes.addressof(lw), ptr(x), rows, ptr(kc), ptr(vc), max_seq, prefix,
                    ptr(pa), ptr(va))
+
+
+def gemm_bf16(x, w, M, N, K):
+    y = np.empty((M, N), np.uint16)
+    lib().or_gemm_bf16(ptr(x), ptr(w), ptr(y), M, N, K)
+    return y
+
+
+def gemm_bf16_f64(x, w, M, N, K):
+    y = np.empty((M, N), np.float64)
+    lib().or_gemm_bf16_f64(ptr(x), ptr(w), ptr(y), M, N, K)
+    return y
+
+
+class OrDraft(ctypes.Structure):
+    """or_draft_w: bf16 weight pointers in the order of s2p_oracle.h."""
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("fuse", "wqkv", "wo", "w1", "w3", "w2", "q_norm", "k_norm", "attn_norm",
+                 "ffn_norm", "final_norm")]
+
+
+def make_draft(w):
+    """w: dict of contiguous uint16 arrays keyed by the OrDraft field names
+    (kept alive by the caller)."""
+    return OrDraft(*[ptr(w[n]) for n, _ in OrDraft._fields_])
+
+
+def draft_step(d, kc, vc, max_seq, pos, h, e):
+    """In place on kc, vc; returns the step's output [2560] bf16 bits."""
+    out = np.empty(2560, np.uint16)
+    lib().or_draft_step(ctypes.addressof(d), ptr(kc), ptr(vc), max_seq, pos, ptr(h), ptr(e),
+                        ptr(out))
+    return out

@@ -1020,3 +1020,66 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
     free(xn); free(qkv); free(q); free(k); free(v); free(att);
     free(proj); free(gu); free(h); free(slots);
 }
+
+/* ---- the draft model ------------------------------------------------------ */
+
+void or_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.f;
+            for (int k = 0; k < K; k++)
+                acc = fmaf(or_bf2f(w[(size_t)n * K + k]), or_bf2f(x[(size_t)m * K + k]), acc);
+            y[(size_t)m * N + n] = or_f2bf(acc);
+        }
+}
+
+void or_gemm_bf16_f64(const uint16_t* x, const uint16_t* w, double* y, int M, int N, int K) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            double acc = 0.0;
+            for (int k = 0; k < K; k++)
+                acc += (double)or_bf2f(w[(size_t)n * K + k]) * (double)or_bf2f(x[(size_t)m * K + k]);
+            y[(size_t)m * N + n] = acc;
+        }
+}
+
+/* Op order of src/draft/draft.c:167-199: fuse, RMSNorm, wqkv, qk-norm (q, k),
+ * RoPE at the state's position, KV append, causal attention over slots
+ * 0..pos, wo + residual, RMSNorm, w1 / w3, SiLU-mul, w2 + residual, final
+ * RMSNorm. */
+void or_draft_step(const or_draft_w* d, uint16_t* kc, uint16_t* vc, int max_seq, int pos,
+                   const uint16_t* h, const uint16_t* e, uint16_t* out) {
+    const int D = 2560, F = 9728, QW = 4096, KVW = 1024;
+    const float eps = 1e-6f;
+    uint16_t* xcat = (uint16_t*)malloc(2 * (size_t)2 * D);
+    uint16_t* x = (uint16_t*)malloc(2 * (size_t)D);
+    uint16_t* a = (uint16_t*)malloc(2 * (size_t)D);
+    uint16_t* qkv = (uint16_t*)malloc(2 * (size_t)(QW + 2 * KVW));
+    uint16_t* att = (uint16_t*)malloc(2 * (size_t)QW);
+    uint16_t* gu = (uint16_t*)malloc(2 * (size_t)2 * F);
+    uint16_t* ffn = (uint16_t*)malloc(2 * (size_t)F);
+    memcpy(xcat, h, 2 * (size_t)D);
+    memcpy(xcat + D, e, 2 * (size_t)D);
+    or_gemm_bf16(xcat, d->fuse, x, 1, D, 2 * D);
+    or_rms_norm(x, d->attn_norm, a, 1, D, eps);
+    or_gemm_bf16(a, d->wqkv, qkv, 1, QW + 2 * KVW, D);
+    uint16_t* q = qkv;
+    uint16_t* k = qkv + QW;
+    uint16_t* v = k + KVW;
+    or_qk_norm(q, d->q_norm, 1, 32, 128, eps);
+    or_qk_norm(k, d->k_norm, 1, 8, 128, eps);
+    or_rope(q, 1, 32, 128, pos, NULL, 1000000.0f);
+    or_rope(k, 1, 8, 128, pos, NULL, 1000000.0f);
+    or_kv_append(k, v, kc, vc, 1, 8, 128, pos, NULL, max_seq);
+    or_attention(q, kc, vc, att, 1, 32, 8, 128, pos, NULL, max_seq);
+    or_gemm_bf16(att, d->wo, a, 1, D, QW);
+    or_add(x, a, D);
+    or_rms_norm(x, d->ffn_norm, a, 1, D, eps);
+    or_gemm_bf16(a, d->w1, gu, 1, F, D);
+    or_gemm_bf16(a, d->w3, gu + F, 1, F, D);
+    or_silu_mul(gu, ffn, 1, F);
+    or_gemm_bf16(ffn, d->w2, a, 1, D, F);
+    or_add(x, a, D);
+    or_rms_norm(x, d->final_norm, out, 1, D, eps);
+    free(xcat); free(x); free(a); free(qkv); free(att); free(gu); free(ffn);
+}

@@ -172,6 +172,30 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
               uint16_t* vc, int max_seq, int prefix, const int32_t* pos,
               const uint64_t* vis);
 
+/* ---- the draft model (src/draft/draft.c:157-202) ---------------------- */
+/* y[M,N] = bf16(sum_k w[n,k] x[m,k]) with an fp32 sum in increasing k: the
+ * contract of s2p_gemm_bf16 (reference gemm.h:93-96, cuBLAS there, whose
+ * summation order is not published: pinned against the binary64 dot only). */
+void or_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int M, int N, int K);
+void or_gemm_bf16_f64(const uint16_t* x, const uint16_t* w, double* y, int M, int N, int K);
+
+typedef struct {
+    const uint16_t* fuse;   /* [2560, 5120] */
+    const uint16_t* wqkv;   /* [6144, 2560] */
+    const uint16_t* wo;     /* [2560, 4096] */
+    const uint16_t* w1;     /* [9728, 2560] */
+    const uint16_t* w3;     /* [9728, 2560] */
+    const uint16_t* w2;     /* [2560, 9728] */
+    const uint16_t* q_norm; /* [128] */
+    const uint16_t* k_norm; /* [128] */
+    const uint16_t* attn_norm, *ffn_norm, *final_norm; /* [2560] */
+} or_draft_w;
+
+/* One draft step at position pos: consumes h, e [2560], appends K/V at slot
+ * pos of kc/vc [8, max_seq, 128], writes out [2560] (final-normed). */
+void or_draft_step(const or_draft_w* d, uint16_t* kc, uint16_t* vc, int max_seq, int pos,
+                   const uint16_t* h, const uint16_t* e, uint16_t* out);
+
 #ifdef __cplusplus
 }
 #endif

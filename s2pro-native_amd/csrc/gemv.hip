@@ -102,6 +102,31 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
     }
 }
 
+/* bf16-weight fallback for K not a multiple of 128: one wave per output,
+ * lanes stride K, fp32 sums, fixed-order wave reduction. */
+__global__ __launch_bounds__(256) void k_gemv_bf16_generic(const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ x,
+                                                           uint16_t* __restrict__ y, int M, int N,
+                                                           int K) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    for (int m = 0; m < M; m++) {
+        float acc = 0.f;
+        for (int k = lane; k < K; k += 64)
+            acc = fmaf(bf2f(w[(size_t)n * K + k]), bf2f(x[(size_t)m * K + k]), acc);
+        acc = wave_sum_down(acc);
+        if (lane == 0) y[(size_t)m * N + n] = f2bf(acc);
+    }
+}
+
+extern "C" hipError_t s2p_gemv_bf16_generic_launch(const void* w, const void* x, void* y, int M,
+                                                   int N, int K, hipStream_t st) {
+    hipLaunchKernelGGL(k_gemv_bf16_generic, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st,
+                       (const uint16_t*)w, (const uint16_t*)x, (uint16_t*)y, M, N, K);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------- launchers */
 
 static int g_slots_override = 0;
@@ -221,7 +246,7 @@ extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_
     const bool swiglu = a->epi == GEMV_EPI_SWIGLU;
     const int tiles = swiglu ? (a->N >> 1) / 16 : (a->N + 15) / 16;
     const int nwmax = mt == 1 ? 16 : 8;
-    const int chg = a->wfmt == GEMV_W_INT4 ? 16 : 8;
+    const int chg = gv_chg(a->wfmt);
     int cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -319,10 +344,14 @@ extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
         if (e3 != hipSuccess) return e3;
         if (s2p_gemv3_plan(&a3, &grid, &block, &lds) == hipSuccess) {
             if (g_probe_at >= 0 && g_probe_at-- == 0) a3.probe = g_probe;
-            return a3.wfmt == GEMV_W_INT4 ? gv3_launch<GEMV_W_INT4>(a3, grid, block, lds, st)
-                                          : gv3_launch<GEMV_W_INT8>(a3, grid, block, lds, st);
+            switch (a3.wfmt) {
+                case GEMV_W_INT4: return gv3_launch<GEMV_W_INT4>(a3, grid, block, lds, st);
+                case GEMV_W_INT8: return gv3_launch<GEMV_W_INT8>(a3, grid, block, lds, st);
+                default: return gv3_launch<GEMV_W_BF16>(a3, grid, block, lds, st);
+            }
         }
     }
+    if (a.wfmt == GEMV_W_BF16) return hipErrorNotSupported; /* whole-K engine only */
     const hipError_t pe = s2p_gemv_plan(&a, s2p_gemv_slots(), &grid, &lds);
     if (pe != hipSuccess) return pe;
     const int mt = (a.M + 15) / 16;

@@ -212,6 +212,7 @@ S2P_DEV void gv_stage_one(const GemvArgs& a, const GvLds& L, int m, int b, bool 
         o = (s2p_u32x4){v[0], v[1], v[2], v[3]};
     }
     if (valid) *(LDS(s2p_u32x4)*)(L.x + m * L.xs + b * 8) = o;
+    if constexpr (WFMT == GEMV_W_BF16) return; /* no group sums: no bias term */
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
     if (valid && (b & 3) == 0) {
@@ -296,6 +297,10 @@ __device__ void gv_stage(const GemvArgs& a, const GvLds& L, int wg0, int wn, boo
  * 2 x (2 loads x 4 groups) */
 #define GV_CHG_INT4 16
 #define GV_CHG_INT8 8
+#define GV_CHG_BF16 4
+static __host__ __device__ constexpr int gv_chg(int wfmt) {
+    return wfmt == GEMV_W_INT4 ? GV_CHG_INT4 : (wfmt == GEMV_W_INT8 ? GV_CHG_INT8 : GV_CHG_BF16);
+}
 struct GvBuf {
     uint32_t w[16];
     s2p_u32x2 s;
@@ -325,6 +330,17 @@ S2P_DEV void gv_load(GvBuf& B, const GemvArgs& a, int nrow, int gabs, int gn, in
         const uint16_t* srow = (const uint16_t*)a.s + (size_t)nrow * (a.K >> 5) + gabs +
                                (sok ? 4 * q : 0);
         B.s = *(const s2p_u32x2*)srow;
+    } else if constexpr (WFMT == GEMV_W_BF16) {
+        /* lane (q, r): k 8q..8q+7 of group it of row r, the A operand as is */
+        const uint16_t* wrow = (const uint16_t*)a.w + (size_t)nrow * a.K + (size_t)gabs * 32 + 8 * q;
+#pragma unroll
+        for (int it = 0; it < GV_CHG_BF16; it++) {
+            const s2p_u32x4 v = gld_nt128(wrow + (it < gn ? it * 32 : 0));
+            B.w[it * 4 + 0] = v.x;
+            B.w[it * 4 + 1] = v.y;
+            B.w[it * 4 + 2] = v.z;
+            B.w[it * 4 + 3] = v.w;
+        }
     } else {
         const uint8_t* wrow = a.w + (size_t)nrow * a.K + (size_t)gabs * 32;
 #pragma unroll
@@ -414,6 +430,18 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
                 corr[t] = mfma16x16x16(ah, bx, corr[t]);
                 corr[t] = mfma16x16x16(al, bx, corr[t]);
             }
+    } else if constexpr (WFMT == GEMV_W_BF16) {
+#pragma unroll
+        for (int g = 0; g < GV_CHG_BF16; g++) {
+            if (g >= gn) break;
+            const s2p_u32x4 av = {B.w[g * 4 + 0], B.w[g * 4 + 1], B.w[g * 4 + 2], B.w[g * 4 + 3]};
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const s2p_u32x4 bv =
+                    *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
+                acc[t] = mfma16x16x32(av, bv, acc[t]);
+            }
+        }
     } else {
 #pragma unroll
         for (int it = 0; it < GV_CHG_INT8 / 4; it++) {
@@ -799,7 +827,7 @@ template <int WFMT, int MT, bool COH>
 __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* smem,
                           uint16_t* Y) {
 #pragma clang fp contract(off)
-    constexpr int CHG = WFMT == GEMV_W_INT4 ? GV_CHG_INT4 : GV_CHG_INT8;
+    constexpr int CHG = gv_chg(WFMT);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
     const int M = a.M, G = a.K >> 5, ks = a.ks, rt = a.rt, gps = a.gps;
@@ -943,9 +971,10 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
             s2p_f32x4 v;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                v[i] = WFMT == GEMV_W_INT4
-                           ? 16.0f * acc[t][i] - 24.0f * corr[t][i]
-                           : fmaf(-128.0f, L.xtot[min(t * 16 + r, M - 1)], acc[t][i]);
+                v[i] = WFMT == GEMV_W_INT4   ? 16.0f * acc[t][i] - 24.0f * corr[t][i]
+                       : WFMT == GEMV_W_INT8 ? fmaf(-128.0f, L.xtot[min(t * 16 + r, M - 1)],
+                                                    acc[t][i])
+                                             : acc[t][i];
             rb[(wave * MT + t) * 64 + lane] = v;
             acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
             corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};

@@ -13,7 +13,7 @@ extern "C" {
 #define GEMV_MAX_M 128         /* rows per call (8 MFMA column tiles) */
 #define GEMV_SSQ_COLS 16       /* columns per sum-of-squares block */
 
-enum { GEMV_W_INT4 = 0, GEMV_W_INT8 = 1 };            /* weight formats */
+enum { GEMV_W_INT4 = 0, GEMV_W_INT8 = 1, GEMV_W_BF16 = 2 }; /* weight formats */
 enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1 };            /* activation staging */
 /* STORE: y = bf16(W x); RESID: y = bf16(y + bf16(W x)) plus per-16-column
  * sums of squares; SWIGLU: W = [gate; up] (2F rows), y[m][F] =
@@ -21,8 +21,8 @@ enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1 };            /* activation staging */
 enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1, GEMV_EPI_SWIGLU = 2 };
 
 typedef struct {
-    const uint8_t*  w;       /* INT4: packed [N][K/2]; INT8: [N][K] */
-    const void*     s;       /* INT4: f16 [N][K/32]; INT8: f32 [N] */
+    const uint8_t*  w;       /* INT4: packed [N][K/2]; INT8: [N][K]; BF16: bf16 [N][K] */
+    const void*     s;       /* INT4: f16 [N][K/32]; INT8: f32 [N]; BF16: unused */
     const uint16_t* x;       /* bf16 activations, row stride ldx */
     int             ldx;
     uint16_t*       y;       /* bf16 output (or residual stream), stride ldy */
@@ -55,6 +55,8 @@ void s2p_gemv_set_engine(int engine);
 void s2p_gemv_set_probe(uint64_t* buf, int index);
 /* resident-workgroup target the launcher plans GEMVs for (env S2P_GEMV_TARGET_WG) */
 int s2p_gemv_slots(void);
+hipError_t s2p_gemv_bf16_generic_launch(const void* w, const void* x, void* y, int M, int N,
+                                         int K, hipStream_t st);
 hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,
                                    const void* x, void* y, int M, int N, int K,
                                    int gshift, hipStream_t st);

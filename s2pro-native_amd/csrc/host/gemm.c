@@ -118,6 +118,38 @@ static int gshift_of(int G) {
 
 /* ------------------------------------------------------------ raw GEMVs */
 
+s2p_status s2p_gemm_bf16(const void* x, const void* w, void* y, int M, int N, int K,
+                         hipStream_t stream) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0) return S2P_ERR_INVALID;
+    if (!g.inited) return S2P_ERR_STATE;
+    hipError_t e = hipSuccess;
+    if (K % 128 == 0) {
+        /* whole-K engine, in row chunks whose activations fit in LDS */
+        int mc = M < GEMV_MAX_M ? M : GEMV_MAX_M;
+        for (int m0 = 0; m0 < M;) {
+            const int rows = M - m0 < mc ? M - m0 : mc;
+            GemvArgs a;
+            s2p_gemv_args_plain(&a, GEMV_W_BF16, w, NULL, (const uint16_t*)x + (size_t)m0 * K,
+                                (uint16_t*)y + (size_t)m0 * N, rows, N, K);
+            e = s2p_gemv_launch(&a, stream);
+            if (e == hipErrorNotSupported && mc > 1) {
+                mc = (mc + 1) / 2;
+                continue;
+            }
+            if (e != hipSuccess) break;
+            m0 += rows;
+        }
+        if (e == hipSuccess) return S2P_OK;
+        if (e != hipErrorNotSupported) {
+            fprintf(stderr, "[s2pro] gemm_bf16 (M=%d,N=%d,K=%d): %s\n", M, N, K,
+                    hipGetErrorString(e));
+            return S2P_ERR_CUDA;
+        }
+    }
+    e = s2p_gemv_bf16_generic_launch(w, x, y, M, N, K, stream);
+    return e == hipSuccess ? S2P_OK : S2P_ERR_CUDA;
+}
+
 s2p_status s2p_int8_gemv(void* y_bf16, const void* x_bf16, const void* w_i8, const float* scales,
                          int M, int N, int K, hipStream_t stream) {
     if (!y_bf16 || !x_bf16 || !w_i8 || !scales || M <= 0 || N <= 0 || K <= 0)
@@ -257,7 +289,14 @@ s2p_status s2p_linear_forward(const s2p_linear* lin, const void* x_bf16, void* y
                               s2p_gemm_mode mode, hipStream_t stream) {
     if (!lin || !x_bf16 || !y_bf16 || M <= 0) return S2P_ERR_INVALID;
     if (!g.inited) return S2P_ERR_STATE;
-    if (mode != S2P_GEMM_INT8 || !lin->int8_ready) return S2P_ERR_UNSUPPORTED;
+    if (mode == S2P_GEMM_BF16 || (mode == S2P_GEMM_INT8 && !lin->int8_ready)) {
+        /* bf16 weights (reference gemm.c:493-500: also the fallback for
+         * layers without a quantised copy) */
+        if (!lin->w_bf16.data) return S2P_ERR_STATE;
+        return s2p_gemm_bf16(x_bf16, lin->w_bf16.data, y_bf16, M, lin->out_features,
+                             lin->in_features, stream);
+    }
+    if (mode != S2P_GEMM_INT8) return S2P_ERR_UNSUPPORTED;
     if (M > S2P_GEMV_MAX_M_MFMA) return S2P_ERR_INVALID;
     const int N = lin->out_features, K = lin->in_features;
     if (lin->q_packed)

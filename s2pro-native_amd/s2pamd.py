@@ -57,6 +57,18 @@ class SlowLayer(ctypes.Structure):
                 ("k_norm", Tensor)]
 
 
+class DraftModel(ctypes.Structure):
+    """s2p_draft_model (include/s2pro/draft.h)"""
+    _fields_ = [(n, Tensor) for n in
+                ("fuse", "wqkv", "wo", "w1", "w3", "w2", "q_norm", "k_norm", "attn_norm",
+                 "ffn_norm", "final_norm", "xcat", "x", "a", "qkv", "attn", "gu", "ffn")]
+
+
+class DraftState(ctypes.Structure):
+    """s2p_draft_state (include/s2pro/draft.h)"""
+    _fields_ = [("kc", Tensor), ("vc", Tensor), ("pos", I)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/s2pro/*.h
 SIGS = {
     # status.h / tensor.h
@@ -85,6 +97,13 @@ SIGS = {
     "s2p_int4p_gemv": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_int4p_gemm_tc": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_int4p_dequant": (I, [P, P, P, I, I, I, P]),
+    "s2p_gemm_bf16": (I, [P, P, P, I, I, I, P]),
+    # draft.h
+    "s2p_draft_load": (I, [P, ctypes.c_char_p]),
+    "s2p_draft_free": (None, [P]),
+    "s2p_draft_state_init": (I, [P]),
+    "s2p_draft_state_free": (None, [P]),
+    "s2p_draft_step": (I, [P, P, P, P, P, P]),
     # kernels.h
     "s2pk_rms_norm": (I, [P, P, P, I, I, F, P]),
     "s2pk_qk_norm": (I, [P, P, I, I, I, F, P]),

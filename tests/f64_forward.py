@@ -103,3 +103,13 @@ def forward(layers, final_norm, head, x_bits, kv_bits, L, parent):
         vc = bf(kv_bits[li, 8:])
         x = layer(W, x, kc, vc, L, pos, vis)
     return rms(x, final_norm) @ head.T
+
+
+def draft_step(W, h, e, kc, vc, pos):
+    """Binary64 draft step (src/draft/draft.c:157-202): x = fuse [h; e], one
+    backbone-shaped layer at RoPE position / KV slot pos (gate_up = [w1; w3]),
+    final RMSNorm.  kc, vc: (8, ctx, 128) f64, updated at slot pos."""
+    x = np.concatenate([h, e])[None, :] @ W["fuse"].T
+    Wl = dict(W, gate_up=np.vstack([W["w1"], W["w3"]]))
+    x = layer(Wl, x, kc, vc, pos, [pos], [1])
+    return rms(x, W["final_norm"])[0]
