@@ -32,10 +32,10 @@
 #include "s2pro/kernels.h"
 #include "s2pro/slowar_kernels.h"
 
-template <int MQT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnArgs a) {
+template <int MQT, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    attn_block<MQT>(a, blockIdx.x, blockIdx.y, blockIdx.z, (LDS(unsigned char)*)smem_raw);
+    attn_block<MQT, W>(a, blockIdx.x, blockIdx.y, blockIdx.z, (LDS(unsigned char)*)smem_raw);
 }
 
 /* merge split partials (one thread per output element) */
@@ -57,10 +57,26 @@ extern "C" void s2p_attn_set_probe(uint64_t* buf, int index) {
     g_attn_probe_at = buf ? index : -1;
 }
 
+static int g_attn_waves = AT_WAVES;
+/* test hook: blocks of 8 waves (the persistent kernel's shape) or 4 */
+extern "C" void s2p_attn_set_waves(int w) { g_attn_waves = w == 8 ? 8 : AT_WAVES; }
+
+template <int MQT, int W>
+static void attn_launch(const AttnArgs& a, dim3 grid, hipStream_t st) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_attn<MQT, W>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES_W(W));
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_attn<MQT, W>), grid, dim3(64 * W), AT_LDS_BYTES_W(W), st, a);
+}
+
 static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
                            int64_t part_cap, hipStream_t st) {
     if (g_attn_probe_at >= 0 && g_attn_probe_at-- == 0) a.probe = g_attn_probe;
-    const int tiles = (max_span + AT_TILE * AT_WAVES - 1) / (AT_TILE * AT_WAVES);
+    const int W = g_attn_waves;
+    const int tiles = (max_span + AT_TILE * W - 1) / (AT_TILE * W);
     int tpw = 1; /* tiles per wave per split */
     if (a.part && part_cap > 0) {
         while ((int64_t)n_seg * a.kvh_n * ((tiles + tpw - 1) / tpw) > 4096) tpw *= 2;
@@ -72,14 +88,17 @@ static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
     } else {
         tpw = tiles > 0 ? tiles : 1;
     }
-    a.split_pos = tpw * AT_TILE * AT_WAVES;
+    a.split_pos = tpw * AT_TILE * W;
     a.nsplit = (max_span + a.split_pos - 1) / a.split_pos;
     if (a.nsplit < 1) a.nsplit = 1;
     dim3 grid((unsigned)n_seg, (unsigned)a.kvh_n, (unsigned)a.nsplit);
-    if (max_nrows <= 4)
-        hipLaunchKernelGGL(k_attn<1>, grid, dim3(256), AT_LDS_BYTES, st, a);
-    else
-        hipLaunchKernelGGL(k_attn<2>, grid, dim3(256), AT_LDS_BYTES, st, a);
+    if (W == 8) {
+        if (max_nrows <= 4) attn_launch<1, 8>(a, grid, st);
+        else attn_launch<2, 8>(a, grid, st);
+    } else {
+        if (max_nrows <= 4) attn_launch<1, AT_WAVES>(a, grid, st);
+        else attn_launch<2, AT_WAVES>(a, grid, st);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,

@@ -21,11 +21,13 @@
 #define AT_VSTRIDE 136
 #define AT_PSTRIDE 40
 #define LDS(T) __attribute__((address_space(3))) T
-/* LDS carve-up of one attention block (bytes) */
-#define AT_SV_BYTES (AT_WAVES * AT_TILE * AT_VSTRIDE * 2)
-#define AT_SP_BYTES (AT_WAVES * 32 * AT_PSTRIDE * 2)
-#define AT_SML_BYTES (AT_WAVES * 32 * 2 * 4)
-#define AT_LDS_BYTES (AT_SV_BYTES + 2 * AT_SP_BYTES + AT_SML_BYTES + 16)
+/* LDS carve-up of one attention block of W waves (bytes) */
+#define AT_SV_BYTES_W(W) ((W) * AT_TILE * AT_VSTRIDE * 2)
+#define AT_SP_BYTES_W(W) ((W) * 32 * AT_PSTRIDE * 2)
+#define AT_SML_BYTES_W(W) ((W) * 32 * 2 * 4)
+#define AT_LDS_BYTES_W(W) (AT_SV_BYTES_W(W) + 2 * AT_SP_BYTES_W(W) + AT_SML_BYTES_W(W) + 16)
+#define AT_SV_BYTES AT_SV_BYTES_W(AT_WAVES)
+#define AT_LDS_BYTES AT_LDS_BYTES_W(AT_WAVES)
 
 enum { AM_CONTIG = 0, AM_PTRS = 1, AM_PLAN = 2 };
 
@@ -159,14 +161,19 @@ S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, 
 
 /* One (segment, kv head, position split) attention block; smem holds
  * AT_LDS_BYTES.  Body of k_attn, also run by the persistent verify kernel. */
-template <int MQT>
+template <int MQT, int W = AT_WAVES>
 __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
+    constexpr int SVB = AT_SV_BYTES_W(W), SPB = AT_SP_BYTES_W(W), SMLB = AT_SML_BYTES_W(W);
     LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
-    LDS(uint16_t)* s_p = (LDS(uint16_t)*)(smem + AT_SV_BYTES);
-    LDS(uint16_t)* s_pl = (LDS(uint16_t)*)(smem + AT_SV_BYTES + AT_SP_BYTES);
-    LDS(float)* s_ml = (LDS(float)*)(smem + AT_SV_BYTES + 2 * AT_SP_BYTES);
-    LDS(int)* s_flag = (LDS(int)*)(smem + AT_SV_BYTES + 2 * AT_SP_BYTES + AT_SML_BYTES);
-#define SV(w, t, d) s_v[((w) * AT_TILE + (t)) * AT_VSTRIDE + (d)]
+    LDS(uint16_t)* s_p = (LDS(uint16_t)*)(smem + SVB);
+    LDS(uint16_t)* s_pl = (LDS(uint16_t)*)(smem + SVB + SPB);
+    LDS(float)* s_ml = (LDS(float)*)(smem + SVB + 2 * SPB);
+    LDS(int)* s_flag = (LDS(int)*)(smem + SVB + 2 * SPB + SMLB);
+/* V tile of wave w: 32 positions x 16 chunks of 16 bytes, chunk (t, k)
+ * stored at slot k ^ 2 (t / 8 % 4) of row t (rows of 256 B, so the PV
+ * gather of 8 rows x 16 columns hits distinct banks) */
+#define SV(w, t, d) \
+    s_v[(w) * (AT_TILE * 128) + (t) * 128 + ((((d) >> 3) ^ (((t) >> 2) & 6)) << 3) + ((d) & 7)]
 #define SP(w, r, c) s_p[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
 #define SPL(w, r, c) s_pl[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
 #define SML(w, qv, k) s_ml[((w) * 32 + (qv)) * 2 + (k)]
@@ -179,7 +186,8 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     const float scale = 0.08838834764831845f;
     const int qrow_stride = a.qh * AT_HD;
     uint64_t* const probe =
-        a.probe ? a.probe + ((size_t)(sp * gridDim.y + kvh) * gridDim.x + seg) * 8 : nullptr;
+        a.probe ? a.probe + ((size_t)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8
+                : nullptr;
     auto stamp = [&](int i) __attribute__((always_inline)) {
         if (probe && threadIdx.x == 0) probe[i] = wall_clock64();
     };
@@ -215,7 +223,7 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int tb = p_begin + wave * AT_TILE; tb < p_end; tb += AT_WAVES * AT_TILE) {
+    for (int tb = p_begin + wave * AT_TILE; tb < p_end; tb += W * AT_TILE) {
         /* K: 2 position subtiles x 4 dim chunks, one 16-byte load each */
         s2p_u32x4 kr[2][4];
 #pragma unroll
@@ -225,21 +233,17 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             for (int ch = 0; ch < 4; ch++)
                 kr[ps][ch] = gld_nt128(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq);
         }
-        /* V tile -> LDS [pos][dim]: every load in flight, then the stores
-         * (keeps the tile out of registers during the score MFMAs) */
-        {
-            s2p_u32x4 vr[8];
+        /* V tile straight to LDS (global_load_lds: lane l of load i fills
+         * bytes 16 l of the load's 1 KB = slot l % 16 of row 4 i + l / 16),
+         * no registers held during the score MFMAs */
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int idx = i * 64 + lane;
-                const int pos = min(tb + (idx >> 4), p_end - 1);
-                vr[i] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * (idx & 15));
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int idx = i * 64 + lane;
-                *(LDS(s2p_u32x4)*)&SV(wave, idx >> 4, 8 * (idx & 15)) = vr[i];
-            }
+        for (int i = 0; i < 8; i++) {
+            const int t = 4 * i + (lane >> 4);
+            const int pos = min(tb + t, p_end - 1);
+            const int k = (lane & 15) ^ ((t >> 2) & 6);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(S.vp + (size_t)pos * AT_HD + 8 * k),
+                (LDS(void)*)(s_v + wave * (AT_TILE * 128) + i * 512), 16, 0, 0);
         }
         if (probe && tb == p_begin) {
             vm_drain();
@@ -283,6 +287,7 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 SPL(wave, 16 * qt + 4 * qq + v, 16 + c) = f2bf(p1 - bf2f(h1));
             }
         }
+        vm_drain(); /* the V tile has landed in LDS */
         wave_sync_lds();
         s2p_u32x4 pa[MQT], pl[MQT];
 #pragma unroll
@@ -327,12 +332,12 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         for (int v = 0; v < 4; v++) {
             const int qv = 16 * qt + 4 * qq + v;
             float M = -INFINITY;
-#pragma unroll
-            for (int w = 0; w < AT_WAVES; w++) M = fmaxf(M, SML(w, qv, 0));
+#pragma unroll 4
+            for (int w = 0; w < W; w++) M = fmaxf(M, SML(w, qv, 0));
             const float Ms = M == -INFINITY ? 0.f : M;
             float lt = 0.f;
-#pragma unroll
-            for (int w = 0; w < AT_WAVES; w++) lt += __expf(SML(w, qv, 0) - Ms) * SML(w, qv, 1);
+#pragma unroll 4
+            for (int w = 0; w < W; w++) lt += __expf(SML(w, qv, 0) - Ms) * SML(w, qv, 1);
             const float f = __expf(m[qt][v] - Ms);
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= f;
@@ -360,10 +365,15 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 for (int v = 0; v < 4; v++)
                     o[qt][dt][v] += s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c];
     };
-    __syncthreads();
-    if (wave >= 2) put(wave - 2);
-    __syncthreads();
-    if (wave < 2) add(wave);
+    /* pairwise tree: wave w += wave w + half for half = W/2 .. 2, then wave
+     * 0 += wave 1 below */
+#pragma unroll
+    for (int half = W / 2; half >= 2; half /= 2) {
+        __syncthreads();
+        if (wave >= half && wave < 2 * half) put(wave - half);
+        __syncthreads();
+        if (wave < half) add(wave);
+    }
     __syncthreads();
     if (wave == 1) put(0);
     __syncthreads();
@@ -413,9 +423,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         *s_flag = prev == (unsigned)(a.nsplit - 1);
     }
     __syncthreads();
-    if (*s_flag && 2 * S.nrows * 4 * a.nsplit + S.nrows * 4 > AT_SV_BYTES / 4) {
+    if (*s_flag && 2 * S.nrows * 4 * a.nsplit + S.nrows * 4 > SVB / 4) {
         /* too many splits for the LDS merge: one output at a time */
-        for (int idx = threadIdx.x; idx < S.nrows * 4 * AT_HD; idx += 256) {
+        for (int idx = threadIdx.x; idx < S.nrows * 4 * AT_HD; idx += W * 64) {
             const int rl = idx >> 9, g = (idx >> 7) & 3, d = idx & (AT_HD - 1);
             attn_merge_one(a.part, a.out, a.rows, a.qh, a.nsplit, S.row0 + rl, 4 * kvh + g, d);
         }
@@ -430,14 +440,14 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         LDS(float)* wm = (LDS(float)*)s_v;   /* [npair][ns] m, then weights */
         LDS(float)* wl = wm + npair * ns;    /* [npair][ns] l */
         LDS(float)* lt = wl + npair * ns;    /* [npair] */
-        for (int idx = threadIdx.x; idx < npair * ns; idx += 256) {
+        for (int idx = threadIdx.x; idx < npair * ns; idx += W * 64) {
             const int pr = idx / ns, sp2 = idx - pr * ns;
             const size_t pi = ((size_t)(S.row0 + (pr >> 2)) * a.qh + 4 * kvh + (pr & 3)) * ns + sp2;
             wm[idx] = coh_ldf(a.part + pi * 2);
             wl[idx] = coh_ldf(a.part + pi * 2 + 1);
         }
         __syncthreads();
-        if (threadIdx.x < npair) {
+        if ((int)threadIdx.x < npair) {
             const int pr = threadIdx.x;
             float M = -INFINITY;
             for (int k = 0; k < ns; k++) M = fmaxf(M, wm[pr * ns + k]);
@@ -452,7 +462,7 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         }
         __syncthreads();
         const float* po = a.part + (size_t)a.rows * a.qh * ns * 2;
-        for (int idx = threadIdx.x; idx < npair * AT_HD; idx += 256) {
+        for (int idx = threadIdx.x; idx < npair * AT_HD; idx += W * 64) {
             const int pr = idx >> 7, d = idx & (AT_HD - 1);
             const int row = S.row0 + (pr >> 2), h = 4 * kvh + (pr & 3);
             const size_t p0 = ((size_t)row * a.qh + h) * ns;
@@ -470,6 +480,10 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         }
         if (threadIdx.x == 0)
             __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (probe && *s_flag) {
+        vm_drain();
+        stamp(5);
     }
     __syncthreads();
 #undef SV

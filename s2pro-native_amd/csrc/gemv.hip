@@ -56,7 +56,9 @@
 template <int WFMT, int MT>
 __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void k_gemv3(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem3[];
-    gv3_block<WFMT, MT, false>(a, blockIdx.x, gridDim.x, (LDS(unsigned char)*)smem3, a.y);
+    GvBuf b0, b1;
+    gv3_block<WFMT, MT, false>(a, blockIdx.x, gridDim.x, (LDS(unsigned char)*)smem3, a.y, b0,
+                               b1);
 }
 
 template <int WFMT, int MT, bool WIN1>
@@ -253,7 +255,12 @@ extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_
         cus <= 0)
         cus = 256;
     const int kmax = swiglu ? nwmax / 2 : nwmax;
-    int gps = chg;
+    static int gps0 = -1;
+    if (gps0 < 0) {
+        const char* e = getenv("S2P_GV3_GPS0"); /* tuning: groups per K slice to start from */
+        gps0 = e && atoi(e) >= 4 ? (atoi(e) & ~3) : 0;
+    }
+    int gps = gps0 ? gps0 : chg;
     while ((G + gps - 1) / gps > kmax) gps += 4;
     int ks = (G + gps - 1) / gps;
     /* units: output tiles per group (SWIGLU: a unit is a gate + up pair) */
@@ -295,6 +302,36 @@ extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_
         units--;
     }
 }
+
+/* Whole-K plan for workgroups of exactly nw waves (the persistent kernel's
+ * shape): rt tiles x ks = nw / rt K slices with no idle wave; one tile
+ * (SWIGLU: one gate + up pair) preferred, then two. */
+extern "C" hipError_t s2p_gemv3_plan_nw(GemvArgs* a, int nw, size_t lds_cap, size_t* lds_out) {
+    const hipError_t ce = s2p_gemv_plan_check(a);
+    if (ce != hipSuccess) return ce;
+    const int G = a->K >> 5;
+    const bool swiglu = a->epi == GEMV_EPI_SWIGLU;
+    for (int rt = swiglu ? 2 : 1; rt <= 2; rt++) {
+        if (nw % rt) continue;
+        const int ks = nw / rt;
+        const int gps = (((G + ks - 1) / ks) + 3) & ~3;
+        if ((G + gps - 1) / gps != ks) continue; /* a slice would be empty */
+        const size_t lds = gv3_lds_bytes(a->M, gps, a->wfmt, ks, nw, 2);
+        if (lds > lds_cap) continue;
+        a->gps = gps;
+        a->ks = ks;
+        a->rt = rt;
+        a->splits = 1;
+        *lds_out = lds;
+        return hipSuccess;
+    }
+    return hipErrorNotSupported;
+}
+
+static int g_v3_nw = 0;
+/* test hook: plan whole-K launches for workgroups of nw waves on a grid of
+ * s2p_gemv_slots() workgroups (the persistent kernel's decomposition) */
+extern "C" void s2p_gemv_set_v3_nw(int nw) { g_v3_nw = nw > 0 ? nw : 0; }
 
 static int g_engine = 0;
 extern "C" void s2p_gemv_set_engine(int engine) { g_engine = engine; }
@@ -342,7 +379,15 @@ extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
         dim3 block;
         const hipError_t e3 = s2p_gemv_plan_check(&a3);
         if (e3 != hipSuccess) return e3;
-        if (s2p_gemv3_plan(&a3, &grid, &block, &lds) == hipSuccess) {
+        hipError_t pe3;
+        if (g_v3_nw) {
+            pe3 = s2p_gemv3_plan_nw(&a3, g_v3_nw, GV3_LDS_MAX, &lds);
+            grid = dim3((unsigned)s2p_gemv_slots());
+            block = dim3((unsigned)(64 * g_v3_nw));
+        } else {
+            pe3 = s2p_gemv3_plan(&a3, &grid, &block, &lds);
+        }
+        if (pe3 == hipSuccess) {
             if (g_probe_at >= 0 && g_probe_at-- == 0) a3.probe = g_probe;
             switch (a3.wfmt) {
                 case GEMV_W_INT4: return gv3_launch<GEMV_W_INT4>(a3, grid, block, lds, st);

@@ -823,24 +823,95 @@ S2P_DEV void st_act16(uint16_t* p, uint16_t v) {
     else *p = v;
 }
 
-template <int WFMT, int MT, bool COH>
+/* Work geometry of workgroup p of P and of one of its waves. */
+struct Gv3Geo {
+    int nw, units, tiles, niter;
+    int j, sp, gb, gn, nch, T;
+};
+
+template <int WFMT>
+S2P_DEV Gv3Geo gv3_geo(const GemvArgs& a, int p, int P, int wave) {
+    Gv3Geo g;
+    const int G = a.K >> 5, ks = a.ks, rt = a.rt;
+    const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
+    g.nw = rt * ks;
+    g.units = swiglu ? rt >> 1 : rt;                       /* output tiles per group */
+    g.tiles = swiglu ? (a.N >> 1) >> 4 : (a.N + 15) >> 4;  /* output tiles */
+    const int ngroups = (g.tiles + g.units - 1) / g.units;
+    g.niter = p < ngroups ? (ngroups - p + P - 1) / P : 0;
+    g.j = wave / ks;                                        /* tile of the group */
+    g.sp = wave - g.j * ks;                                 /* K slice */
+    g.gb = g.sp * a.gps;
+    g.gn = min(G, g.gb + a.gps) - g.gb;
+    g.nch = (g.gn + gv_chg(WFMT) - 1) / gv_chg(WFMT);
+    g.T = g.niter * g.nch;
+    return g;
+}
+
+/* weight row of lane row r of this wave in tile group tg */
+S2P_DEV int gv3_wrow(const GemvArgs& a, const Gv3Geo& g, int tg, int r) {
+    int base;
+    if (a.epi == GEMV_EPI_SWIGLU) {
+        const int h = g.units;
+        const int t = tg * h + (g.j < h ? g.j : g.j - h);
+        base = (g.j < h ? 0 : a.N >> 1) + t * 16;
+    } else {
+        base = (tg * g.units + g.j) * 16;
+    }
+    return min(base + r, a.N - 1);
+}
+
+/* chunk t of the wave's flattened (tile group, chunk) stream */
+template <int WFMT>
+S2P_DEV void gv3_load(GvBuf& B, const GemvArgs& a, const Gv3Geo& g, int p, int P, int t) {
+    constexpr int CHG = gv_chg(WFMT);
+    const int lane = threadIdx.x & 63;
+    const int it = g.nch == 1 ? t : t / g.nch, c = t - it * g.nch;
+    gv_load<WFMT>(B, a, gv3_wrow(a, g, p + it * P, lane & 15), g.gb + c * CHG,
+                  min(CHG, g.gn - c * CHG), lane >> 4);
+}
+
+/* The first weight chunk of workgroup p, issued ahead (the persistent kernel
+ * issues it before the barrier that precedes the GEMV). */
+template <int WFMT>
+S2P_DEV void gv3_prefetch(const GemvArgs& a, int p, int P, GvBuf& b0, GvBuf& b1) {
+    const Gv3Geo g = gv3_geo<WFMT>(a, p, P, threadIdx.x >> 6);
+    /* both buffers defined on every path: their old contents are dead */
+    if (g.T > 0) {
+        gv3_load<WFMT>(b0, a, g, p, P, 0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) b0.w[i] = 0u;
+        b0.s = (s2p_u32x2){0u, 0u};
+    }
+    if (g.T > 1) {
+        gv3_load<WFMT>(b1, a, g, p, P, 1);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) b1.w[i] = 0u;
+        b1.s = (s2p_u32x2){0u, 0u};
+    }
+}
+
+/* PRE: b0 and b1 already hold (or are loading) the first two chunks
+ * (gv3_prefetch). */
+/* COH: activation loads bypass the L2 (their producer ran in this launch
+ * and the L2 was not invalidated since); WT: outputs written through. */
+template <int WFMT, int MT, bool COH, bool PRE = false, bool WT = COH>
 __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* smem,
-                          uint16_t* Y) {
+                          uint16_t* Y, GvBuf& b0, GvBuf& b1) {
 #pragma clang fp contract(off)
     constexpr int CHG = gv_chg(WFMT);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
-    const int M = a.M, G = a.K >> 5, ks = a.ks, rt = a.rt, gps = a.gps;
-    const int nw = rt * ks;
+    const int M = a.M, ks = a.ks, gps = a.gps;
+    const Gv3Geo geo = gv3_geo<WFMT>(a, p, P, wave);
+    const int nw = geo.nw, units = geo.units, tiles = geo.tiles, niter = geo.niter;
+    if (niter == 0) return; /* uniform over the workgroup */
     const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
     const int F = a.N >> 1;
-    const int units = swiglu ? rt >> 1 : rt;             /* output tiles per group */
-    const int tiles = swiglu ? F >> 4 : (a.N + 15) >> 4; /* output tiles */
-    const int ngroups = (tiles + units - 1) / units;
-    const int niter = p < ngroups ? (ngroups - p + P - 1) / P : 0;
-    if (niter == 0) return; /* uniform over the workgroup */
-    const int j = wave / ks, sp = wave - j * ks; /* tile of the group, K slice */
-    const int gb = sp * gps, gn = min(G, gb + gps) - gb;
+    const int sp = geo.sp, gb = geo.gb, gn = geo.gn;
+    (void)r;
     uint64_t* const probe = a.probe ? a.probe + (size_t)blockIdx.x * 8 : nullptr;
     auto stamp = [&](int i) __attribute__((always_inline)) {
         if (probe && tid == 0) probe[i] = wall_clock64();
@@ -866,30 +937,14 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
     L.flag = nullptr;
     LDS(s2p_f32x4)* red = (LDS(s2p_f32x4)*)(smem + o2);
 
-    /* weight rows of this wave in tile group g */
-    auto wrow = [&](int g) __attribute__((always_inline)) {
-        int t, base;
-        if (swiglu) {
-            const int h = units;
-            t = g * h + (j < h ? j : j - h);
-            base = (j < h ? 0 : F) + t * 16;
-        } else {
-            t = g * units + j;
-            base = t * 16;
-        }
-        return min(base + r, a.N - 1);
-    };
-    const int nch = (gn + CHG - 1) / CHG;
-    const int T = niter * nch;
+    const int nch = geo.nch, T = geo.T;
     auto load_t = [&](GvBuf& B, int t) __attribute__((always_inline)) {
-        const int it = t / nch, c = t - it * nch;
-        gv_load<WFMT>(B, a, wrow(p + it * P), gb + c * CHG, min(CHG, gn - c * CHG), q);
+        gv3_load<WFMT>(B, a, geo, p, P, t);
     };
 
-    GvBuf b0, b1;
     Gv3Pre pre;
-    gv3_pre_issue<COH>(a, pre, j == 0, wave, lane, gb, gn);
-    load_t(b0, 0);
+    gv3_pre_issue<COH>(a, pre, geo.j == 0, wave, lane, gb, gn);
+    if constexpr (!PRE) load_t(b0, 0); /* in flight during the staging */
     if (a.xmode == GEMV_X_NORM) {
         /* inverse RMS per row: lanes take the producer's blocks, fixed-order
          * wave reduction */
@@ -909,7 +964,7 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
         __syncthreads();
     }
     stamp(1);
-    if (j == 0) {
+    if (geo.j == 0) {
         /* the slice's stager: rows < 8 of the first 64 column blocks from
          * the registers, the rest loaded here */
         const int nb8 = gn * 4;
@@ -1006,7 +1061,7 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
                         gv *= ((const float*)a.s)[n];
                         uv *= ((const float*)a.s)[F + n];
                     }
-                    st_act16<COH>(Y + (size_t)m * a.ldy + n, silu_mul_bf16(f2bf(gv), f2bf(uv)));
+                    st_act16<WT>(Y + (size_t)m * a.ldy + n, silu_mul_bf16(f2bf(gv), f2bf(uv)));
                 }
                 continue;
             }
@@ -1018,11 +1073,11 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
                 uint16_t* yp = Y + (size_t)m * a.ldy + n;
                 if (a.epi == GEMV_EPI_RESID) {
                     const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
-                    st_act16<COH>(yp, xo);
+                    st_act16<WT>(yp, xo);
                     const float xv = bf2f(xo);
                     ssq = xv * xv;
                 } else {
-                    st_act16<COH>(yp, yb);
+                    st_act16<WT>(yp, yb);
                 }
             }
             if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
@@ -1032,25 +1087,49 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
         }
     };
     auto step = [&](const GvBuf& B, int t) __attribute__((always_inline)) {
-        const int it = t / nch, c = t - it * nch;
+        const int it = nch == 1 ? t : t / nch, c = t - it * nch;
         gv_compute<WFMT, MT>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
         if (c == nch - 1) finish(it);
     };
-    /* every path into a step has the same loads outstanding, and no load is
-     * issued past the end */
     int t = 0;
-    for (; t + 2 < T; t += 2) {
-        load_t(b1, t + 1);
+    if constexpr (!PRE) {
+        /* one chunk ahead: b1 is loaded while b0 is multiplied; every path
+         * into a step has the same loads outstanding, and no load is issued
+         * past the end */
+        for (; t + 2 < T; t += 2) {
+            load_t(b1, t + 1);
+            step(b0, t);
+            load_t(b0, t + 2);
+            step(b1, t + 1);
+        }
+        if (T - t == 2) {
+            load_t(b1, t + 1);
+            step(b0, t);
+            step(b1, t + 1);
+        } else {
+            step(b0, t);
+        }
+    } else {
+    /* b0 holds chunk t and b1 chunk t + 1 (both issued before the barrier):
+     * two chunks in flight, every load in the loop unconditional, no load
+     * issued past the end */
+    for (; t + 3 < T; t += 2) {
         step(b0, t);
         load_t(b0, t + 2);
         step(b1, t + 1);
+        load_t(b1, t + 3);
     }
-    if (T - t == 2) {
-        load_t(b1, t + 1);
+    if (T - t == 3) {
+        step(b0, t);
+        load_t(b0, t + 2);
+        step(b1, t + 1);
+        step(b0, t + 2);
+    } else if (T - t == 2) {
         step(b0, t);
         step(b1, t + 1);
     } else {
         step(b0, t);
+    }
     }
     if (probe) {
         vm_drain();

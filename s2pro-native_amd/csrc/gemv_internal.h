@@ -51,6 +51,10 @@ typedef struct {
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
 /* test hook: 0 = launcher's choice, 2 = split-K engine only */
 void s2p_gemv_set_engine(int engine);
+/* test hook: whole-K launches shaped like the persistent kernel's GEMVs */
+void s2p_gemv_set_v3_nw(int nw);
+/* whole-K plan for workgroups of exactly nw waves (persistent kernel) */
+hipError_t s2p_gemv3_plan_nw(GemvArgs* a, int nw, size_t lds_cap, size_t* lds_out);
 /* diagnostics: stage clocks of the whole-K launch `index` launches from now */
 void s2p_gemv_set_probe(uint64_t* buf, int index);
 /* resident-workgroup target the launcher plans GEMVs for (env S2P_GEMV_TARGET_WG) */

@@ -510,11 +510,12 @@ static int mk_build(s2p_backbone* b) {
     A->segs = b->d_segs;
     A->n_seg = b->n_seg;
     {
-        /* the split of s2p_attn_plan_launch, so both paths agree bit for bit */
-        const int tiles = (b->max_span + 127) / 128;
+        /* the split of s2p_attn_plan_launch for blocks of 8 waves (256
+         * positions per tile round), so both paths agree bit for bit */
+        const int tiles = (b->max_span + 255) / 256;
         int tpw = 1;
         while ((int64_t)b->n_seg * 8 * ((tiles + tpw - 1) / tpw) > 4096) tpw *= 2;
-        A->split_pos = 128 * tpw;
+        A->split_pos = 256 * tpw;
         A->nsplit = (b->max_span + A->split_pos - 1) / A->split_pos;
     }
     if (s2p_attn_plan_part_floats(M, b->max_span) > b->attn_part_floats) return 0;
@@ -530,7 +531,12 @@ static int mk_build(s2p_backbone* b) {
         const char* pp = getenv("S2P_MK_PROBE_PHASE");
         A->probe = (pp && b->d_ts_wg) ? b->d_ts_wg + (size_t)(1 + 6 * b->o.n_layers) * 2 * b->mk_nwg
                                       : NULL;
-        A->probe_phase = pp ? atoi(pp) : -1;
+        A->probe_phase = pp ? (pp[0] == 'a' ? 1000 + atoi(pp + 1) : atoi(pp)) : -1;
+        /* "l,i": stage clocks of GEMV i of layer l (whole-K engine probe) */
+        int pl = -1, pi = -1;
+        if (A->probe && sscanf(pp, "%d,%d", &pl, &pi) == 2 && pl >= 0 && pl < b->o.n_layers &&
+            pi >= 0 && pi < 4)
+            Ls[pl].g[pi].a.probe = A->probe;
     }
     return 1;
 }

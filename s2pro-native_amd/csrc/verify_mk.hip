@@ -44,7 +44,8 @@
 #include "mk_internal.h"
 #include "prims_dev.h"
 
-#define MK_THREADS 256
+#define MK_WAVES 8
+#define MK_THREADS (64 * MK_WAVES)
 #define MK_GROUP 16
 #define MK_SPIN_LIMIT (1u << 20)
 
@@ -133,6 +134,10 @@ __device__ void mk_bar_sync(MkBar& b, uint64_t* ts_wg) {
             }
             if (ts_wg) ts_wg[((size_t)(b.k - 1) * 2 + 1) * gridDim.x + blockIdx.x] = wall_clock64();
         }
+        /* acquire: drop this CU's L1 and this XCD's L2 lines from before the
+         * barrier, so the next phase may read activations through the caches
+         * (every store of the phase was written through before arrival) */
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
 }
@@ -140,28 +145,17 @@ __device__ void mk_bar_sync(MkBar& b, uint64_t* ts_wg) {
 /* barriers per launch for n_layers */
 static __host__ __device__ int mk_nbar(int n_layers) { return 1 + 6 * n_layers; }
 
-/* Phase bodies: separate (non-inlined) functions so each gets its own
- * register allocation; across calls only the phase loop and the barrier
- * state stay live. */
 __device__ __forceinline__ void mk_phase_init(const MkArgs* A, const uint16_t* x_in) {
     const int lane = threadIdx.x & 63;
     const int gw = blockIdx.x * (MK_THREADS / 64) + (threadIdx.x >> 6);
     const int nw = gridDim.x * (MK_THREADS / 64);
-    /* residual stream x = x_in and its per-64-column sums of squares */
+    /* residual stream x = x_in and its sums of squares */
     for (int it = gw; it < 40 * A->rows; it += nw)
         resid_init_item(x_in, A->x, A->ssq_a, 2560, it % 40, it / 40, lane);
     /* RoPE table of the plan's positions (the same for every layer) */
     const int gt = blockIdx.x * MK_THREADS + threadIdx.x;
     for (int it = gt; it < A->rows * 64; it += gridDim.x * MK_THREADS)
         rope_tab_item(A->plan, A->rope_base, A->rope_tab, it / 64, it % 64);
-}
-
-template <int WFMT>
-__device__ __forceinline__ void mk_phase_gemv(const MkGemv* g, LDS(unsigned char)* smem,
-                                              uint16_t* y_override, uint64_t* probe) {
-    const int n = g->P * g->S;
-    for (int vb = blockIdx.x; vb < n; vb += gridDim.x)
-        gv_block<WFMT, 1, true, true>(g->a, vb % g->P, g->P, vb / g->P, smem, y_override, probe);
 }
 
 __device__ __forceinline__ void mk_phase_qkrope(const MkArgs* A, int l) {
@@ -175,7 +169,7 @@ __device__ __forceinline__ void mk_phase_qkrope(const MkArgs* A, int l) {
 }
 
 __device__ __forceinline__ void mk_phase_attn(const MkArgs* A, int l,
-                                                        LDS(unsigned char)* smem) {
+                                              LDS(unsigned char)* smem) {
     AttnArgs at = {};
     at.mode = 2; /* AM_PLAN */
     at.q = A->q;
@@ -190,14 +184,23 @@ __device__ __forceinline__ void mk_phase_attn(const MkArgs* A, int l,
     at.split_pos = A->split_pos;
     at.part = A->attn_part;
     at.counters = A->attn_counters;
+    if (A->probe && A->probe_phase == 1000 + l) at.probe = A->probe;
     const int nseg = A->n_seg;
     const int nb = nseg * 8 * A->nsplit;
     for (int vb = blockIdx.x; vb < nb; vb += gridDim.x)
-        attn_block<2>(at, vb % nseg, (vb / nseg) % 8, vb / (nseg * 8), smem);
+        attn_block<2, MK_WAVES>(at, vb % nseg, (vb / nseg) % 8, vb / (nseg * 8), smem);
 }
 
-/* Phase sequence: 0 resid init, then 6 per layer (wqkv, qkrope, attention,
- * wo, gate_up, w2), then the head. */
+/* GEMV i of a layer (0 wqkv, 1 wo, 2 gate_up, 3 w2) or the head (l == n) */
+S2P_DEV const MkGemv* mk_gemv(const MkArgs* A, int l, int i) {
+    return l == A->n_layers ? A->head : &A->layers[l].g[i];
+}
+
+/* Phase sequence: resid init | per layer: wqkv | qk-norm + RoPE + append |
+ * attention | wo | gate_up | w2 | and the head.  Every GEMV's first weight
+ * chunk is issued before the barrier that precedes it (weights do not
+ * depend on the previous phase), so the barrier wait and the weight latency
+ * overlap. */
 template <int WFMT>
 __global__ __launch_bounds__(MK_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void k_verify_mk(
     const MkArgs* __restrict__ A, const uint16_t* __restrict__ x_in, uint16_t* logits) {
@@ -205,45 +208,58 @@ __global__ __launch_bounds__(MK_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     LDS(unsigned char)* smem = (LDS(unsigned char)*)smem_raw;
     const int n_layers = A->n_layers;
     MkBar bar = mk_bar_init(A->bar, A->err, mk_nbar(n_layers));
-    const int nph = 2 + 6 * n_layers;
     uint64_t* ts = A->ts;
+    int tsi = 0;
+    auto stamp = [&]() __attribute__((always_inline)) {
+        tsi++;
+        if (ts && blockIdx.x == 0 && threadIdx.x == 0) ts[tsi] = wall_clock64();
+    };
     if (ts && blockIdx.x == 0 && threadIdx.x == 0) ts[0] = wall_clock64();
-    for (int ph = 0; ph < nph; ph++) {
-        const int l = (ph - 1) / 6, sub = (ph - 1) % 6;
-        if (ph == 0) {
-            mk_phase_init(A, x_in);
-        } else if (ph != nph - 1 && sub == 1) {
-            mk_phase_qkrope(A, l);
-        } else if (ph != nph - 1 && sub == 2) {
-            mk_phase_attn(A, l, smem);
-            if (A->dbg_attn_twice) {
-                uint64_t t0 = wall_clock64();
-                __syncthreads();
+    GvBuf pre, pre1;
+    mk_phase_init(A, x_in);
+    {
+        const GemvArgs g0 = mk_gemv(A, 0, 0)->a;
+        gv3_prefetch<WFMT>(g0, blockIdx.x, gridDim.x, pre, pre1);
+    }
+    mk_bar_sync(bar, A->ts_wg);
+    stamp();
+    for (int l = 0; l <= n_layers; l++) {
+        for (int i = 0; i < 4; i++) {
+            if (l < n_layers && i == 1) {
+                mk_phase_qkrope(A, l);
+                mk_bar_sync(bar, A->ts_wg);
+                stamp();
                 mk_phase_attn(A, l, smem);
-                vm_drain();
-                __syncthreads();
-                if (A->ts_wg && threadIdx.x == 0)
-                    A->ts_wg[((size_t)(2 + 6 * A->n_layers) * 2) * gridDim.x + blockIdx.x] =
-                        wall_clock64() - t0;
+                const GemvArgs gn = mk_gemv(A, l, 1)->a;
+                gv3_prefetch<WFMT>(gn, blockIdx.x, gridDim.x, pre, pre1);
+                mk_bar_sync(bar, A->ts_wg);
+                stamp();
             }
-        } else { /* one GEMV call site: the layer GEMVs and the head */
-            const bool head = ph == nph - 1;
-            uint64_t* probe =
-                (A->probe && ph == A->probe_phase) ? A->probe + (size_t)blockIdx.x * 8 : nullptr;
-            mk_phase_gemv<WFMT>(head ? A->head : &A->layers[l].g[sub == 0 ? 0 : sub - 2], smem,
-                                head ? logits : nullptr, probe);
+            const bool head = l == n_layers;
+            /* a copy in registers: read through a pointer, every field would
+             * be reloaded after each store the phase makes */
+            const GemvArgs ga = mk_gemv(A, l, i)->a;
+            /* activations through the L2 (invalidated at the barrier),
+             * outputs written through */
+            gv3_block<WFMT, 1, false, true, true>(ga, blockIdx.x, gridDim.x, smem,
+                                                  head ? logits : ga.y, pre, pre1);
+            if (head) break;
+            if (i != 0) { /* the next GEMV follows directly */
+                const int nl = i == 3 ? l + 1 : l, ni = i == 3 ? 0 : i + 1;
+                const GemvArgs gn = mk_gemv(A, nl, ni)->a;
+                gv3_prefetch<WFMT>(gn, blockIdx.x, gridDim.x, pre, pre1);
+            }
+            mk_bar_sync(bar, A->ts_wg);
+            stamp();
         }
-        if (ph != nph - 1) mk_bar_sync(bar, A->ts_wg);
-        if (ts && blockIdx.x == 0 && threadIdx.x == 0) ts[ph + 1] = wall_clock64();
     }
 }
 
 /* ------------------------------------------------------------------ host */
 
-static size_t mk_lds_bytes(void) {
-    size_t b = AT_LDS_BYTES;
-    return b < 64 * 1024 ? 64 * 1024 : b;
-}
+/* one workgroup per CU: the whole LDS (the whole-K GEMVs stage up to
+ * M x 9728 activations; attention needs AT_LDS_BYTES_W(8)) */
+static size_t mk_lds_bytes(void) { return 160 * 1024 - 256; /* static LDS: barrier state */ }
 
 extern "C" int s2p_mk_grid(int* nwg, size_t* lds) {
     int dev = 0, cus = 0;
@@ -251,6 +267,11 @@ extern "C" int s2p_mk_grid(int* nwg, size_t* lds) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return -1;
     const size_t sb = mk_lds_bytes();
+    (void)hipFuncSetAttribute((const void*)k_verify_mk<0>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sb);
+    (void)hipFuncSetAttribute((const void*)k_verify_mk<1>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)sb);
+    if (hipGetLastError() != hipSuccess) return -1;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_verify_mk<0>,
                                                      MK_THREADS, sb) != hipSuccess)
@@ -260,7 +281,7 @@ extern "C" int s2p_mk_grid(int* nwg, size_t* lds) {
                                                      MK_THREADS, sb) != hipSuccess)
         return -1;
     if (per_cu8 < per_cu) per_cu = per_cu8;
-    if (per_cu > 2) per_cu = 2;
+    if (per_cu > 1) per_cu = 1;
     if (per_cu < 1) return -1;
     int n = cus * per_cu;
     if (n > MK_MAX_GROUPS * MK_GROUP) n = MK_MAX_GROUPS * MK_GROUP;
@@ -272,13 +293,12 @@ extern "C" int s2p_mk_grid(int* nwg, size_t* lds) {
 extern "C" hipError_t s2p_mk_plan_gemv(const GemvArgs* ap, int nwg, size_t lds_cap, MkGemv* out) {
     MkGemv g;
     g.a = *ap;
-    dim3 grid;
     size_t lds = 0;
-    const hipError_t e = s2p_gemv_plan(&g.a, nwg, &grid, &lds);
+    if (g.a.M > 16) return hipErrorInvalidValue;
+    const hipError_t e = s2p_gemv3_plan_nw(&g.a, MK_WAVES, lds_cap, &lds);
     if (e != hipSuccess) return e;
-    if (g.a.win < g.a.gps || lds > lds_cap || g.a.M > 16) return hipErrorInvalidValue;
-    g.P = (int)grid.x;
-    g.S = (int)grid.y;
+    g.P = nwg;
+    g.S = 1;
     *out = g;
     return hipSuccess;
 }

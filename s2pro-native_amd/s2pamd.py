@@ -141,6 +141,8 @@ EXTRA = {
     "s2p_backbone_set_mk": (None, [P, I]),
     "s2p_gemv_set_slots": (None, [I]),
     "s2p_gemv_set_engine": (None, [I]),
+    "s2p_gemv_set_v3_nw": (None, [I]),
+    "s2p_attn_set_waves": (None, [I]),
     "s2p_gemv_set_probe": (None, [P, I]),
     "s2p_attn_set_probe": (None, [P, I]),
     "s2p_test_f2bf": (I, [P, P, I64, P]),

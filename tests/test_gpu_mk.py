@@ -31,7 +31,10 @@ def test_mk_matches_layerwise(lib, quant, n_layers, L):
         out = {}
         # the layer-by-layer GEMVs planned for the persistent kernel's grid
         lib.s2p_gemv_set_slots(lib.s2p_backbone_mk_grid(bb))
-        lib.s2p_gemv_set_engine(2)  # the persistent kernel runs the split-K engine
+        # the layer kernels shaped like the persistent kernel's phases:
+        # whole-K GEMVs of 8 waves on its grid, attention blocks of 8 waves
+        lib.s2p_gemv_set_v3_nw(8)
+        lib.s2p_attn_set_waves(8)
         for mode in (1, 0):
             lib.s2p_backbone_set_mk(bb, mode)
             kv.copy_(__import__("torch").from_numpy(kv0.view(np.int16)).to(kv.device))
@@ -56,5 +59,6 @@ def test_mk_matches_layerwise(lib, quant, n_layers, L):
         assert np.array_equal(to_host(logits, np.uint16), out[1][0])
     finally:
         lib.s2p_gemv_set_slots(0)
-        lib.s2p_gemv_set_engine(0)
+        lib.s2p_gemv_set_v3_nw(0)
+        lib.s2p_attn_set_waves(4)
         lib.s2p_backbone_free(bb)
