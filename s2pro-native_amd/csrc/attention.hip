@@ -100,7 +100,7 @@ static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
         else attn_launch<2, AT_WAVES>(a, grid, st);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.nsplit == 1) return e;
+    if (e != hipSuccess || a.nsplit == 1 || a.counters) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,
                        a.rows, a.qh, a.nsplit);
     return hipGetLastError();
@@ -179,6 +179,35 @@ extern "C" hipError_t s2pk_attention_decode(const s2p_bf16* q, const s2p_bf16* c
 
 extern "C" int64_t s2p_attn_plan_part_floats(int rows, int max_span) {
     return s2pk_attention_part_floats(rows, 32, max_span);
+}
+
+extern "C" hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan,
+                                                 const S2pAttnSeg* segs, int n_seg, int rows,
+                                                 int layer, int max_span, float* part,
+                                                 const void* qkv, const void* qn_w,
+                                                 const void* kn_w, const float* rope_tab,
+                                                 float eps, unsigned* counters, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!qkv || !qn_w || !kn_w || !rope_tab) return hipErrorInvalidValue;
+    AttnArgs a = {};
+    a.mode = AM_PLAN;
+    a.q = (const uint16_t*)q;
+    a.out = (uint16_t*)out;
+    a.rows = rows;
+    a.qh = 32;
+    a.kvh_n = 8;
+    a.plan = *plan;
+    a.segs = segs;
+    a.layer = layer;
+    a.part = part;
+    a.counters = counters;
+    a.qkv = (const uint16_t*)qkv;
+    a.qn_w = (const uint16_t*)qn_w;
+    a.kn_w = (const uint16_t*)kn_w;
+    a.rope_tab = rope_tab;
+    a.eps = eps;
+    return attn_run(a, n_seg, AT_SEG_ROWS, max_span, s2p_attn_plan_part_floats(rows, max_span),
+                    st);
 }
 
 extern "C" hipError_t s2p_attn_plan_launch(const void* q, void* out, const S2pRowPlan* plan,

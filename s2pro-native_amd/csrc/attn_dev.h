@@ -12,6 +12,7 @@
 
 #include "coh.h"
 #include "common.h"
+#include "prims_dev.h"
 #include "prims_internal.h"
 
 #define AT_HD 128
@@ -25,7 +26,9 @@
 #define AT_SV_BYTES_W(W) ((W) * AT_TILE * AT_VSTRIDE * 2)
 #define AT_SP_BYTES_W(W) ((W) * 32 * AT_PSTRIDE * 2)
 #define AT_SML_BYTES_W(W) ((W) * 32 * 2 * 4)
-#define AT_LDS_BYTES_W(W) (AT_SV_BYTES_W(W) + 2 * AT_SP_BYTES_W(W) + AT_SML_BYTES_W(W) + 16)
+#define AT_SQ_BYTES (32 * AT_HD * 2) /* fused path: the block's q vectors */
+#define AT_LDS_BYTES_W(W) \
+    (AT_SV_BYTES_W(W) + 2 * AT_SP_BYTES_W(W) + AT_SML_BYTES_W(W) + 16 + AT_SQ_BYTES)
 #define AT_SV_BYTES AT_SV_BYTES_W(AT_WAVES)
 #define AT_LDS_BYTES AT_LDS_BYTES_W(AT_WAVES)
 
@@ -58,6 +61,15 @@ struct AttnArgs {
      * splits itself (persistent kernel); NULL: k_attn_combine does */
     unsigned* counters;
     uint64_t* probe; /* diagnostics: [grid][8] stage clocks */
+    /* PLAN, fused qk-norm + RoPE + KV append (qkv != NULL): q is computed
+     * from the raw fused qkv rows into q (written, then read back by the
+     * same block), and the blocks whose positions cover a segment's new
+     * slots append that segment's K/V of their kv head first */
+    const uint16_t* qkv;
+    const uint16_t* qn_w;
+    const uint16_t* kn_w;
+    const float* rope_tab; /* [rows][64][cos, sin] of the plan's positions */
+    float eps;
 };
 
 struct SegInfo {
@@ -193,19 +205,129 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     };
     stamp(0);
 
+    /* one tile of K (registers) and V (straight to this wave's LDS: lane l
+     * of load i fills bytes 16 l of the load's 1 KB = slot l % 16 of row
+     * 4 i + l / 16) */
+    s2p_u32x4 kr[2][4];
+    auto issue_tile = [&](int tb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ps = 0; ps < 2; ps++) {
+            const int pos = min(tb + 16 * ps + c, p_end - 1);
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++)
+                kr[ps][ch] = gld_nt128(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int t = 4 * i + (lane >> 4);
+            const int pos = min(tb + t, p_end - 1);
+            const int k = (lane & 15) ^ ((t >> 2) & 6);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(S.vp + (size_t)pos * AT_HD + 8 * k),
+                (LDS(void)*)(s_v + wave * (AT_TILE * 128) + i * 512), 16, 0, 0);
+        }
+    };
+    const int tb0 = p_begin + wave * AT_TILE;
+    bool early = false; /* first tile issued before the fused prologue */
+
     /* Q operands: A row i = c -> query vector qv = 16 qt + c */
     s2p_u32x4 qa[MQT][4];
+    if (a.qkv) {
+        /* fused qk-norm + RoPE + K/V append, one wave per (row, head) item:
+         * the block's 4 q heads of its segment's rows (to LDS), then the k/v
+         * of every new slot of the session inside the block's positions (a
+         * tree's ancestors may sit in another segment: each block appends
+         * what it reads itself; blocks that overlap write identical values).
+         * Every load of a batch of items is issued before any is used. */
+        LDS(uint16_t)* s_q = (LDS(uint16_t)*)(smem + SVB + 2 * SPB + SMLB + 16);
+        const int first = S.row0 - (a.plan.slot[S.row0] - S.L); /* session's slot-L row */
+        const int s0 = max(p_begin, S.L), s1 = min(p_end, S.span);
+        const int nq = S.nrows * 4, nit = nq + max(0, s1 - s0);
+        early = s1 <= s0 && tb0 < p_end; /* the block appends nothing */
+        if (early) issue_tile(tb0);
+        constexpr int IB = 4;
+        for (int base = wave; base < nit; base += IB * W) {
+            float v0[IB], v1[IB], cs[IB][4];
+            uint16_t w0[IB], w1[IB], x0[IB], x1[IB];
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++) {
-        const int qv = 16 * qt + c;
-        const int rl = qv >> 2, g = qv & 3;
+            for (int j = 0; j < IB; j++) {
+                const int it = base + j * W;
+                if (it >= nit) break; /* uniform */
+                const bool isq = it < nq;
+                const int row = isq ? S.row0 + (it >> 2) : first + (s0 - S.L) + (it - nq);
+                const int head = isq ? 4 * kvh + (it & 3) : 32 + kvh;
+                const uint16_t* src = a.qkv + (size_t)row * 6144 + head * AT_HD;
+                v0[j] = bf2f(coh_ld16(src + lane));
+                v1[j] = bf2f(coh_ld16(src + lane + 64));
+                const uint16_t* nw = isq ? a.qn_w : a.kn_w;
+                w0[j] = nw[lane];
+                w1[j] = nw[lane + 64];
+                const float* tab = a.rope_tab + (size_t)row * 128;
+                cs[j][0] = coh_ldf(tab + (lane >> 1) * 2);
+                cs[j][1] = coh_ldf(tab + (lane >> 1) * 2 + 1);
+                cs[j][2] = coh_ldf(tab + ((lane + 64) >> 1) * 2);
+                cs[j][3] = coh_ldf(tab + ((lane + 64) >> 1) * 2 + 1);
+                if (!isq) { /* the v head rides along */
+                    x0[j] = coh_ld16(src + 8 * AT_HD + lane);
+                    x1[j] = coh_ld16(src + 8 * AT_HD + lane + 64);
+                }
+            }
 #pragma unroll
-        for (int ch = 0; ch < 4; ch++) {
-            if (rl < S.nrows) {
-                qa[qt][ch] = coh_ld128(a.q + (size_t)(S.row0 + rl) * qrow_stride +
-                                       (4 * kvh + g) * AT_HD + 32 * ch + 8 * qq);
-            } else {
-                qa[qt][ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
+            for (int j = 0; j < IB; j++) {
+                const int it = base + j * W;
+                if (it >= nit) break;
+                float o0, o1;
+                qkrope_math(v0[j], v1[j], w0[j], w1[j], cs[j][0], cs[j][1], cs[j][2], cs[j][3],
+                            a.eps, lane, &o0, &o1);
+                if (it < nq) {
+                    LDS(uint16_t)* dq = s_q + it * AT_HD; /* q vector (rl, g) = it */
+                    const uint16_t q0 = f2bf(o0), q1 = f2bf(o1);
+                    dq[lane] = q0;
+                    dq[lane + 64] = q1;
+                    if (sp == 0) { /* the q rows also land in q (inspection) */
+                        uint16_t* gq = (uint16_t*)a.q + (size_t)(S.row0 + (it >> 2)) * qrow_stride +
+                                       (4 * kvh + (it & 3)) * AT_HD;
+                        gq[lane] = q0;
+                        gq[lane + 64] = q1;
+                    }
+                } else {
+                    const int row = first + (s0 - S.L) + (it - nq);
+                    uint16_t* kvb =
+                        (uint16_t*)a.plan.kv[a.plan.sess[row]] + (size_t)a.layer * a.plan.layer_stride;
+                    const size_t slot = (size_t)a.plan.slot[row];
+                    uint16_t* kd = kvb + ((size_t)kvh * a.plan.max_seq + slot) * AT_HD;
+                    uint16_t* vd = kvb + ((size_t)(a.kvh_n + kvh) * a.plan.max_seq + slot) * AT_HD;
+                    coh_st16(kd + lane, f2bf(o0));
+                    coh_st16(kd + lane + 64, f2bf(o1));
+                    coh_st16(vd + lane, x0[j]);
+                    coh_st16(vd + lane + 64, x1[j]);
+                }
+            }
+        }
+        vm_drain();
+        __syncthreads();
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++) {
+            const int qv = 16 * qt + c;
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++)
+                qa[qt][ch] = (qv >> 2) < S.nrows
+                                 ? *(const LDS(s2p_u32x4)*)(s_q + qv * AT_HD + 32 * ch + 8 * qq)
+                                 : (s2p_u32x4){0u, 0u, 0u, 0u};
+        }
+    } else {
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++) {
+            const int qv = 16 * qt + c;
+            const int rl = qv >> 2, g = qv & 3;
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++) {
+                if (rl < S.nrows) {
+                    qa[qt][ch] = coh_ld128(a.q + (size_t)(S.row0 + rl) * qrow_stride +
+                                           (4 * kvh + g) * AT_HD + 32 * ch + 8 * qq);
+                } else {
+                    qa[qt][ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
+                }
             }
         }
     }
@@ -223,28 +345,8 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int tb = p_begin + wave * AT_TILE; tb < p_end; tb += W * AT_TILE) {
-        /* K: 2 position subtiles x 4 dim chunks, one 16-byte load each */
-        s2p_u32x4 kr[2][4];
-#pragma unroll
-        for (int ps = 0; ps < 2; ps++) {
-            const int pos = min(tb + 16 * ps + c, p_end - 1);
-#pragma unroll
-            for (int ch = 0; ch < 4; ch++)
-                kr[ps][ch] = gld_nt128(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq);
-        }
-        /* V tile straight to LDS (global_load_lds: lane l of load i fills
-         * bytes 16 l of the load's 1 KB = slot l % 16 of row 4 i + l / 16),
-         * no registers held during the score MFMAs */
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int t = 4 * i + (lane >> 4);
-            const int pos = min(tb + t, p_end - 1);
-            const int k = (lane & 15) ^ ((t >> 2) & 6);
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(S.vp + (size_t)pos * AT_HD + 8 * k),
-                (LDS(void)*)(s_v + wave * (AT_TILE * 128) + i * 512), 16, 0, 0);
-        }
+    for (int tb = tb0; tb < p_end; tb += W * AT_TILE) {
+        if (!(early && tb == tb0)) issue_tile(tb);
         if (probe && tb == p_begin) {
             vm_drain();
             stamp(1);
@@ -462,21 +564,33 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         }
         __syncthreads();
         const float* po = a.part + (size_t)a.rows * a.qh * ns * 2;
-        for (int idx = threadIdx.x; idx < npair * AT_HD; idx += W * 64) {
-            const int pr = idx >> 7, d = idx & (AT_HD - 1);
+        /* item = (pair, 4 dims): 16-byte partial loads, 8 splits in flight */
+        for (int idx = threadIdx.x; idx < npair * (AT_HD / 4); idx += W * 64) {
+            const int pr = idx >> 5, d = (idx & 31) * 4;
             const int row = S.row0 + (pr >> 2), h = 4 * kvh + (pr & 3);
             const size_t p0 = ((size_t)row * a.qh + h) * ns;
-            float acc = 0.f;
-            for (int k0 = 0; k0 < ns; k0 += 16) {
-                float ov[16];
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int k0 = 0; k0 < ns; k0 += 8) {
+                s2p_u32x4 ov[8];
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    ov[j] = k0 + j < ns ? coh_ldf(po + (p0 + k0 + j) * AT_HD + d) : 0.f;
+                for (int j = 0; j < 8; j++)
+                    ov[j] = k0 + j < ns ? coh_ld128(po + (p0 + k0 + j) * AT_HD + d)
+                                        : (s2p_u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-                for (int j = 0; j < 16; j++)
-                    if (k0 + j < ns) acc = fmaf(ov[j], wm[pr * ns + k0 + j], acc);
+                for (int j = 0; j < 8; j++) {
+                    if (k0 + j >= ns) break;
+                    const float w = wm[pr * ns + k0 + j];
+                    acc[0] = fmaf(__uint_as_float(ov[j].x), w, acc[0]);
+                    acc[1] = fmaf(__uint_as_float(ov[j].y), w, acc[1]);
+                    acc[2] = fmaf(__uint_as_float(ov[j].z), w, acc[2]);
+                    acc[3] = fmaf(__uint_as_float(ov[j].w), w, acc[3]);
+                }
             }
-            coh_st16(a.out + ((size_t)row * a.qh + h) * AT_HD + d, f2bf(acc / lt[pr]));
+            const float lp = lt[pr];
+            const uint64_t o4 = (uint64_t)f2bf(acc[0] / lp) | ((uint64_t)f2bf(acc[1] / lp) << 16) |
+                                ((uint64_t)f2bf(acc[2] / lp) << 32) |
+                                ((uint64_t)f2bf(acc[3] / lp) << 48);
+            coh_st64(a.out + ((size_t)row * a.qh + h) * AT_HD + d, o4);
         }
         if (threadIdx.x == 0)
             __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -331,6 +331,7 @@ int s2p_backbone_mk_status(s2p_backbone* b) {
 /* ------------------------------------------------------------------ plan */
 
 static int mk_build(s2p_backbone* b);
+static S2pRowPlan row_plan(const s2p_backbone* b);
 
 s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStream_t st) {
     if (!b || !vb || vb->n_sess <= 0 || vb->rows <= 0 || vb->rows > S2P_VERIFY_MAX_ROWS ||
@@ -396,6 +397,12 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
     /* bucketed so that a graph captured for one span serves nearby spans */
     b->max_span = ((max_span + SPAN_BUCKET - 1) / SPAN_BUCKET) * SPAN_BUCKET;
     if (b->max_span > b->o.ctx_len) b->max_span = b->o.ctx_len;
+    {
+        /* the RoPE table of the plan's positions, used by every layer */
+        const S2pRowPlan rp = row_plan(b);
+        S2P_TRY(hip_ok(s2p_rope_tab_launch(&rp, rows, ROPE_BASE, b->d_rope, st), "rope table"));
+        S2P_TRY(hip_ok(hipStreamSynchronize(st), "rope table sync"));
+    }
     b->mk_ready = mk_build(b);
     if (b->mk_ready) {
         S2P_TRY(hip_ok(hipMemsetAsync(b->d_err, 0, sizeof(int), st), "mk plan"));
@@ -557,10 +564,11 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
         const s2p_slow_layer* L = &b->layers[l];
         S2P_TRY(gemv(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
                      L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st));
-        S2P_TRY(hip_ok(s2p_qkrope_append_launch(b->qkv, b->q, L->q_norm.data, L->k_norm.data, &plan,
-                                                M, l, NORM_EPS, ROPE_BASE, st), "qkrope"));
-        S2P_TRY(hip_ok(s2p_attn_plan_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
-                                            b->max_span, b->attn_part, st), "attention"));
+        S2P_TRY(hip_ok(s2p_attn_plan_fused_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
+                                                  b->max_span, b->attn_part, b->qkv,
+                                                  L->q_norm.data, L->k_norm.data, b->d_rope,
+                                                  NORM_EPS, NULL, st),
+                       "attention"));
         S2P_TRY(gemv(&L->wo, M, b->attn, S2P_Q_HEADS * S2P_HEAD_DIM, b->x, S2P_DIM, GEMV_X_PLAIN,
                      NULL, NULL, GEMV_EPI_RESID, ssq_b, st));
         S2P_TRY(gemv(&L->gate_up, M, b->x, S2P_DIM, b->gu, S2P_FFN_DIM, GEMV_X_NORM,

@@ -320,6 +320,20 @@ extern "C" hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq
     return hipGetLastError();
 }
 
+/* RoPE table of a verify plan: (cos, sin) of every row's position and pair,
+ * the rule's values (rope_cs), computed once per plan. */
+__global__ __launch_bounds__(64) void k_rope_tab(S2pRowPlan plan, float base,
+                                                 float* __restrict__ tab) {
+    rope_tab_item(plan, base, tab, blockIdx.x, threadIdx.x);
+}
+
+extern "C" hipError_t s2p_rope_tab_launch(const S2pRowPlan* plan, int rows, float base,
+                                          float* tab, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_tab, dim3((unsigned)rows), dim3(64), 0, st, *plan, base, tab);
+    return hipGetLastError();
+}
+
 /* Tree commit: session s, layer l, plane h (16 = 8 K + 8 V heads).  Accepted
  * node path[d-1] (index >= d) moves to slot L + d in increasing d, so no
  * source is overwritten before it is read. */

@@ -25,6 +25,28 @@ S2P_DEV void rope_cs(int p, int i, int head_dim, float base, float* c, float* s)
     *s = bf2f(f2bf((float)sin((double)ang)));
 }
 
+/* qk-norm + RoPE arithmetic of one (row, head), lane = elements lane and
+ * lane + 64 (v0, v1) with norm weights w0, w1 and the (cos, sin) of their
+ * pairs; the partner of element e (e ^ 1) lives in lane ^ 1 */
+S2P_DEV void qkrope_math(float v0, float v1, uint16_t w0, uint16_t w1, float c0, float s0,
+                         float c1, float s1, float eps, int lane, float* o0, float* o1) {
+#pragma clang fp contract(off)
+    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
+    s = wave_sum_down(s);
+    s = __shfl(s, 0, 64);
+    const float inv = rsqrt_rule(s / 128.0f + eps);
+    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(w0))));
+    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(w1))));
+    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
+    if ((lane & 1) == 0) {
+        *o0 = __fsub_rn(__fmul_rn(v0, c0), __fmul_rn(pv0, s0)); /* x0' */
+        *o1 = __fsub_rn(__fmul_rn(v1, c1), __fmul_rn(pv1, s1));
+    } else {
+        *o0 = __fadd_rn(__fmul_rn(v0, c0), __fmul_rn(pv0, s0)); /* x1' */
+        *o1 = __fadd_rn(__fmul_rn(v1, c1), __fmul_rn(pv1, s1));
+    }
+}
+
 /* qk-norm + RoPE of one (row, head) of the fused qkv output, one wave:
  * q heads 0..31 go to q_out, k heads 32..39 (with the matching v head) to
  * the row's KV slot of `layer` (kernels.cu:81-109, 114-168, 172-222). */
@@ -39,31 +61,22 @@ S2P_DEV void qkrope_item_t(const uint16_t* qkv, uint16_t* q_out, const uint16_t*
     const int kh = head - QH;
     const uint16_t* src = qkv + (size_t)row * qkv_w + (is_q ? head * HD : QH * HD + kh * HD);
     const uint16_t* nw = is_q ? qn_w : kn_w;
-    float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
-    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
-    s = wave_sum_down(s);
-    s = __shfl(s, 0, 64);
-    const float inv = rsqrt_rule(s / (float)HD + eps);
-    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(nw[lane]))));
-    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(nw[lane + 64]))));
-    /* RoPE: element e = lane + 64*slot, partner e ^ 1 lives in lane ^ 1 */
-    const int p = plan.pos[row];
-    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
-    float o[2];
+    const float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
+    /* RoPE: element e = lane + 64*slot, pair e >> 1 */
+    float cs[2][2];
 #pragma unroll
     for (int slot = 0; slot < 2; slot++) {
         const int e = lane + 64 * slot;
-        const float me = slot ? v1 : v0, pa = slot ? pv1 : pv0;
-        float c, sn;
         if constexpr (TAB) { /* (cos, sin) of (row, pair), precomputed with rope_cs */
-            c = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2);
-            sn = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2 + 1);
+            cs[slot][0] = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2);
+            cs[slot][1] = coh_ldf(rope_tab + ((size_t)row * 64 + (e >> 1)) * 2 + 1);
         } else {
-            rope_cs(p, e >> 1, HD, base, &c, &sn);
+            rope_cs(plan.pos[row], e >> 1, HD, base, &cs[slot][0], &cs[slot][1]);
         }
-        if ((e & 1) == 0) o[slot] = __fsub_rn(__fmul_rn(me, c), __fmul_rn(pa, sn)); /* x0' */
-        else o[slot] = __fadd_rn(__fmul_rn(me, c), __fmul_rn(pa, sn));              /* x1' */
     }
+    float o[2];
+    qkrope_math(v0, v1, nw[lane], nw[lane + 64], cs[0][0], cs[0][1], cs[1][0], cs[1][1], eps,
+                lane, &o[0], &o[1]);
     if (is_q) {
         uint16_t* dst = q_out + (size_t)row * QH * HD + head * HD;
         coh_st16(dst + lane, f2bf(o[0]));

@@ -40,6 +40,9 @@ hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t* path,
                                 hipStream_t st);
 hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq, int rows,
                                  int width, hipStream_t st);
+/* (cos, sin) of every row's position and pair i < 64: tab [rows][64][2] */
+hipError_t s2p_rope_tab_launch(const S2pRowPlan* plan, int rows, float base, float* tab,
+                               hipStream_t st);
 
 /* Verify-plan attention over the per-layer caches of the plan's sessions.
  * segs: device [n_seg]; max_span: host bound of max(span) (grid sizing);
@@ -47,6 +50,14 @@ hipError_t s2p_resid_init_launch(const void* xin, void* x, float* ssq, int rows,
 hipError_t s2p_attn_plan_launch(const void* q, void* out, const S2pRowPlan* plan,
                                 const S2pAttnSeg* segs, int n_seg, int rows, int layer,
                                 int max_span, float* part, hipStream_t st);
+/* The same, fused with qk-norm + RoPE + KV append (q is the scratch the q
+ * rows are written to) and, with counters ([n_seg * 8], zero between calls),
+ * with the split merge done by the last split of each block. */
+hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan,
+                                      const S2pAttnSeg* segs, int n_seg, int rows, int layer,
+                                      int max_span, float* part, const void* qkv,
+                                      const void* qn_w, const void* kn_w, const float* rope_tab,
+                                      float eps, unsigned* counters, hipStream_t st);
 int64_t    s2p_attn_plan_part_floats(int rows, int max_span);
 
 #ifdef __cplusplus
