@@ -42,7 +42,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part,
                                                       uint16_t* __restrict__ out, int rows,
                                                       int qh, int nsplit) {
-    attn_merge_one(part, out, rows, qh, nsplit, blockIdx.x, blockIdx.y, threadIdx.x);
+    /* the partials come from the previous launch: plain (cached) loads */
+    attn_merge_one<false>(part, out, rows, qh, nsplit, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
 static int64_t part_floats(int rows, int qh, int nsplit) {

@@ -75,7 +75,7 @@ struct AttnArgs {
 struct SegInfo {
     const uint16_t* kp;
     const uint16_t* vp;
-    int L, row0, nrows, span;
+    int L, row0, nrows, span, first;
     const uint64_t* vis; /* NULL: causal */
 };
 
@@ -103,8 +103,8 @@ S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
         s.nrows = g.nrows;
         s.L = g.L;
         s.span = g.span;
-        const uint16_t* kv =
-            (const uint16_t*)a.plan.kv[g.sess] + (size_t)a.layer * a.plan.layer_stride;
+        s.first = g.first;
+        const uint16_t* kv = (const uint16_t*)g.kv + (size_t)a.layer * a.plan.layer_stride;
         s.kp = kv + (size_t)kvh * a.plan.max_seq * AT_HD;
         s.vp = kv + (size_t)(a.kvh_n + kvh) * a.plan.max_seq * AT_HD;
         s.vis = a.plan.vis;
@@ -143,12 +143,19 @@ S2P_DEV void wave_sync_lds() {
 
 /* merge the split partials of (row, head h, dim d):
  * out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s, in split order */
+template <bool COH>
+S2P_DEV float ld_f(const float* p) {
+    if constexpr (COH) return coh_ldf(p);
+    else return *p;
+}
+
+template <bool COH = true>
 S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, int nsplit,
                             int row, int h, int d) {
     const size_t p0 = ((size_t)row * qh + h) * nsplit;
     const float* po = part + (size_t)rows * qh * nsplit * 2;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, coh_ldf(part + (p0 + s) * 2));
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ld_f<COH>(part + (p0 + s) * 2));
     const float Ms = M == -INFINITY ? 0.f : M;
     float lt = 0.f, acc = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += 8) {
@@ -156,9 +163,9 @@ S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, 
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const bool ok = s0 + j < nsplit;
-            mv[j] = ok ? coh_ldf(part + (p0 + s0 + j) * 2) : 0.f;
-            lv[j] = ok ? coh_ldf(part + (p0 + s0 + j) * 2 + 1) : 0.f;
-            ov[j] = ok ? coh_ldf(po + (p0 + s0 + j) * AT_HD + d) : 0.f;
+            mv[j] = ok ? ld_f<COH>(part + (p0 + s0 + j) * 2) : 0.f;
+            lv[j] = ok ? ld_f<COH>(part + (p0 + s0 + j) * 2 + 1) : 0.f;
+            ov[j] = ok ? ld_f<COH>(po + (p0 + s0 + j) * AT_HD + d) : 0.f;
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -240,12 +247,12 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
          * what it reads itself; blocks that overlap write identical values).
          * Every load of a batch of items is issued before any is used. */
         LDS(uint16_t)* s_q = (LDS(uint16_t)*)(smem + SVB + 2 * SPB + SMLB + 16);
-        const int first = S.row0 - (a.plan.slot[S.row0] - S.L); /* session's slot-L row */
+        const int first = S.first; /* the session's row at slot L */
         const int s0 = max(p_begin, S.L), s1 = min(p_end, S.span);
         const int nq = S.nrows * 4, nit = nq + max(0, s1 - s0);
-        early = s1 <= s0 && tb0 < p_end; /* the block appends nothing */
-        if (early) issue_tile(tb0);
-        constexpr int IB = 4;
+        const bool appends = s1 > s0;
+        early = !appends && tb0 < p_end;
+        constexpr int IB = 8; /* every item of a 4-wave block in one batch at M <= 5 */
         for (int base = wave; base < nit; base += IB * W) {
             float v0[IB], v1[IB], cs[IB][4];
             uint16_t w0[IB], w1[IB], x0[IB], x1[IB];
@@ -272,6 +279,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                     x1[j] = coh_ld16(src + 8 * AT_HD + lane + 64);
                 }
             }
+            /* the first K/V tile goes out behind the first batch's loads, so
+             * the item arithmetic below waits for those loads only */
+            if (early && base == wave) issue_tile(tb0);
 #pragma unroll
             for (int j = 0; j < IB; j++) {
                 const int it = base + j * W;
@@ -291,12 +301,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                         gq[lane + 64] = q1;
                     }
                 } else {
-                    const int row = first + (s0 - S.L) + (it - nq);
-                    uint16_t* kvb =
-                        (uint16_t*)a.plan.kv[a.plan.sess[row]] + (size_t)a.layer * a.plan.layer_stride;
-                    const size_t slot = (size_t)a.plan.slot[row];
-                    uint16_t* kd = kvb + ((size_t)kvh * a.plan.max_seq + slot) * AT_HD;
-                    uint16_t* vd = kvb + ((size_t)(a.kvh_n + kvh) * a.plan.max_seq + slot) * AT_HD;
+                    const size_t slot = (size_t)(s0 + (it - nq)); /* row first + slot - L */
+                    uint16_t* kd = (uint16_t*)S.kp + slot * AT_HD;
+                    uint16_t* vd = (uint16_t*)S.vp + slot * AT_HD;
                     coh_st16(kd + lane, f2bf(o0));
                     coh_st16(kd + lane + 64, f2bf(o1));
                     coh_st16(vd + lane, x0[j]);
@@ -304,7 +311,8 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 }
             }
         }
-        vm_drain();
+        if (early && nit <= wave) issue_tile(tb0); /* a wave with no item */
+        if (appends) vm_drain(); /* the appended K/V before any tile load */
         __syncthreads();
 #pragma unroll
         for (int qt = 0; qt < MQT; qt++) {
@@ -480,35 +488,52 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     if (wave == 1) put(0);
     __syncthreads();
     stamp(3);
-    if (wave == 0) {
-        add(0);
-        /* ---- write ---- */
+    if (wave == 0) add(0);
+    if (a.nsplit == 1) {
+        if (wave == 0) {
 #pragma unroll
-        for (int qt = 0; qt < MQT; qt++)
+            for (int qt = 0; qt < MQT; qt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int qv = 16 * qt + 4 * qq + v;
-                const int rl = qv >> 2, g = qv & 3;
-                if (rl >= S.nrows) continue;
-                const int row = S.row0 + rl;
-                const int h = 4 * kvh + g;
-                if (a.nsplit == 1) {
+                for (int v = 0; v < 4; v++) {
+                    const int qv = 16 * qt + 4 * qq + v;
+                    const int rl = qv >> 2, g = qv & 3;
+                    if (rl >= S.nrows) continue;
+                    const int row = S.row0 + rl;
+                    const int h = 4 * kvh + g;
                     const float inv = 1.0f / ltot[qt][v];
 #pragma unroll
                     for (int dt = 0; dt < 8; dt++)
                         coh_st16(a.out + (size_t)row * qrow_stride + h * AT_HD + 16 * dt + c,
                                  f2bf(o[qt][dt][v] * inv));
-                } else {
-                    const size_t pi = ((size_t)row * a.qh + h) * a.nsplit + sp;
-                    float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
-#pragma unroll
-                    for (int dt = 0; dt < 8; dt++) coh_stf(po + 16 * dt + c, o[qt][dt][v]);
-                    if (c == 0) {
-                        coh_stf(a.part + pi * 2, mtot[qt][v]);
-                        coh_stf(a.part + pi * 2 + 1, ltot[qt][v]);
-                    }
                 }
+        }
+    } else {
+        /* partial (m, l, O) of this split: O through LDS ([q vector][dim]), then
+         * 16-byte write-through stores by the whole block */
+        LDS(float)* s_mlw = (LDS(float)*)s_p; /* [32][2], free after the tiles */
+        if (wave == 0) {
+            put(0);
+            if (c == 0) {
+#pragma unroll
+                for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        s_mlw[(16 * qt + 4 * qq + v) * 2] = mtot[qt][v];
+                        s_mlw[(16 * qt + 4 * qq + v) * 2 + 1] = ltot[qt][v];
+                    }
             }
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < S.nrows * 4 * (AT_HD / 4); idx += W * 64) {
+            const int qv = idx >> 5, d4 = (idx & 31) * 4;
+            const int row = S.row0 + (qv >> 2), h = 4 * kvh + (qv & 3);
+            const size_t pi = ((size_t)row * a.qh + h) * a.nsplit + sp;
+            float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
+            coh_st128(po + d4, *(const LDS(s2p_u32x4)*)(s_o + qv * AT_HD + d4));
+            if (d4 == 0)
+                coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(s_mlw[qv * 2]) |
+                                              ((uint64_t)__float_as_uint(s_mlw[qv * 2 + 1]) << 32));
+        }
     }
     if (probe) {
         vm_drain();

@@ -377,7 +377,8 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
             g->row0 = s * R + r0;
             g->nrows = R - r0 < 8 ? R - r0 : 8;
             g->span = L + R;
-            g->pad_ = 0;
+            g->first = s * R;
+            g->kv = vb->kv[s];
         }
         if (L + R > max_span) max_span = L + R;
     }

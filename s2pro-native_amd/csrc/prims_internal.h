@@ -28,7 +28,8 @@ typedef struct {
     int32_t row0;   /* first row */
     int32_t nrows;  /* rows in this segment (<= 8) */
     int32_t span;   /* slots [0, span) may be visible to some row */
-    int32_t pad_;
+    int32_t first;  /* the session's first row (its node 0, KV slot L) */
+    const void* kv; /* the session's KV base (plan.kv[sess]), so the kernel has it at hand */
 } S2pAttnSeg;
 
 hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,

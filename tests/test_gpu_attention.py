@@ -87,7 +87,8 @@ class RowPlan(__import__("ctypes").Structure):
 class AttnSeg(__import__("ctypes").Structure):
     import ctypes as _c
     _fields_ = [("sess", _c.c_int32), ("L", _c.c_int32), ("row0", _c.c_int32),
-                ("nrows", _c.c_int32), ("span", _c.c_int32), ("pad_", _c.c_int32)]
+                ("nrows", _c.c_int32), ("span", _c.c_int32), ("first", _c.c_int32),
+                ("kv", _c.c_void_p)]
 
 
 def _tree_masks(parent):
@@ -126,7 +127,7 @@ def test_attention_plan_mode(lib, parent, L, max_seq):
                    kvp.data_ptr(), 16 * max_seq * 128, max_seq)
     segs = []
     for r0 in range(0, R, 8):
-        segs.append(AttnSeg(0, L, r0, min(8, R - r0), L + R, 0))
+        segs.append(AttnSeg(0, L, r0, min(8, R - r0), L + R, 0, kvd.data_ptr()))
     seg_arr = (AttnSeg * len(segs))(*segs)
     segd = to_dev(np.frombuffer(bytes(seg_arr), np.uint8).copy())
     span = ((L + R + 511) // 512) * 512
