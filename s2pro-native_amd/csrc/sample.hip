@@ -170,6 +170,10 @@ struct TxShared {
     int greedy;
     float temp, topp, m, sum, t, m2, s2;
     int masked[32];
+    /* lane 0's scratch (in LDS rather than private memory) */
+    int ridx[64];
+    float rval[64];
+    int path[64];
 };
 
 /* Sampler transform of one logits row into sh.ti / sh.p2 (ranks 0..29). */
@@ -211,8 +215,8 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
         sh.temp = use_ras ? 1.0f : sp->temperature;
         sh.topp = use_ras ? 0.9f : sp->top_p;
         if (capped > 0) {
-            int ridx[64];
-            float rval[64];
+            int* ridx = sh.ridx;
+            float* rval = sh.rval;
             int rn = 0;
             for (int j = 0; j < capped; j++) {
                 const int ci = vocab_to_cand(sp->prev[j]);
@@ -435,7 +439,7 @@ __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
         /* push the drafted tokens of the root path (root excluded) */
         /* root path; parent indices are validated (parent[u] in [0, u)) so a
          * malformed tree ends the walk instead of reading out of bounds */
-        int path[64];
+        int* path = sh.path;
         int n = 0;
         for (int u = v; u > 0 && u < a.R && n < 64;) {
             path[n++] = u;
@@ -464,10 +468,59 @@ S2P_DEV float prob_of(const int32_t* ti, const float* p, int ci) {
     return 0.f;
 }
 
+/* argmax over the wave with the sequential rule's tie order: the first
+ * (lowest) index among equal maxima; NaN never wins (the sequential loop's
+ * `pert > best` is false for NaN); all -inf -> index 0 */
+S2P_DEV int wave_argmax_first(float v, int idx) {
+    if (v != v) v = -INFINITY;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    return idx;
+}
+
+/* perturbed log-probability of candidate j of a seeded draw: the loop
+ * bodies of gumbel_draw (plain sample / bonus token, residual == false)
+ * and residual_draw (residual == true), one candidate per lane */
+S2P_DEV float draw_pert(const s2ps_dev_state* sp, const float* prob, int j, bool residual) {
+    if (j >= TOP_K) return -INFINITY;
+    float u;
+    if (residual) {
+        if (!(prob[j] > 0.f)) return -INFINITY;
+        u = (float)rule_u24(sp, (uint32_t)j) / 16777216.0f;
+    } else {
+        const uint64_t step_seed = ((uint64_t)sp->seed31 * 19349663ULL) ^ (sp->count * 73856093ULL);
+        const uint64_t hashed = (step_seed * 8589934591ULL) ^ ((uint64_t)j * 479001599ULL);
+        u = (float)(uint32_t)(hashed & 0xFFFFFFULL) / 16777216.0f;
+    }
+    if (u < 1e-10f) u = 1e-10f;
+    const float g = -s2p_logf(-s2p_logf(u));
+    return s2p_logf(prob[j] + 1e-10f) + g;
+}
+
+/* One wave per session.  Control flow is uniform: every lane reads the same
+ * state (in LDS) and takes the same decisions; lane 0 alone mutates the
+ * state; the per-candidate work of the seeded draws and of the residual
+ * (two logs per candidate, the dominant cost) runs one candidate per lane,
+ * with the sequential rule's sums and tie order kept. */
 __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
-    const int s = blockIdx.x;
-    if (threadIdx.x != 0) return;
-    s2ps_dev_state st = *a.states[s];
+    __shared__ s2ps_dev_state st;
+    __shared__ float p[TOP_K], qp[TOP_K], rsd[TOP_K];
+    __shared__ int32_t pti[TOP_K], qti[TOP_K];
+    __shared__ uint32_t bcast;
+    const int s = blockIdx.x, lane = threadIdx.x;
+    {
+        const uint32_t* src = (const uint32_t*)a.states[s];
+        uint32_t* dst = (uint32_t*)&st;
+        for (int i = lane; i < (int)(sizeof(st) / 4); i += 64) dst[i] = src[i];
+    }
+    __syncthreads();
     const TxOut* work = (const TxOut*)a.work;
     const int R = a.R;
     const int64_t* tok = a.tok + (size_t)s * R;
@@ -478,42 +531,57 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
     for (;;) {
         const TxOut* tp = work + ((size_t)(s * R + v) * 2 + 0);
         const TxOut* tq = work + ((size_t)(s * R + v) * 2 + 1);
-        float p[TOP_K];
-        int32_t pti[TOP_K];
-        for (int k = 0; k < TOP_K; k++) {
-            p[k] = tp->p[k];
-            pti[k] = tp->ti[k];
+        if (lane < TOP_K) {
+            p[lane] = tp->p[lane];
+            pti[lane] = tp->ti[lane];
+            qp[lane] = tq->p[lane];
+            qti[lane] = tq->ti[lane];
         }
+        __syncthreads();
         const int greedy = tp->greedy;
         int accepted = -1, rejected_any = 0, j = 0;
         for (int c = v + 1; c < R && accepted < 0; c++) {
             if (a.parent[c] != v) continue;
             const int ci = vocab_to_cand(tok[c]);
             const float pc = ci < 0 ? 0.f : prob_of(pti, p, ci);
-            const float qc = ci < 0 ? 0.f : prob_of(tq->ti, tq->p, ci);
-            const uint32_t u = greedy ? 0u
-                                      : (st.seeded ? rule_u24(&st, 64u + (uint32_t)j)
-                                                   : (uint32_t)(xoshiro_next(st.rng) >> 40));
+            const float qc = ci < 0 ? 0.f : prob_of(qti, qp, ci);
+            uint32_t u;
+            if (greedy) {
+                u = 0u;
+            } else if (st.seeded) {
+                u = rule_u24(&st, 64u + (uint32_t)j);
+            } else {
+                if (lane == 0) bcast = (uint32_t)(xoshiro_next(st.rng) >> 40);
+                __syncthreads();
+                u = bcast;
+                __syncthreads();
+            }
             if ((double)u * (double)qc < (double)pc * 16777216.0) {
                 accepted = c;
                 break;
             }
             rejected_any = 1;
-            float rsd[TOP_K], z = 0.f;
-            for (int k = 0; k < TOP_K; k++) {
-                const float d = p[k] - prob_of(tq->ti, tq->p, pti[k]);
-                rsd[k] = d > 0.f ? d : 0.f;
-                z += rsd[k];
+            if (lane < TOP_K) {
+                const float d = p[lane] - prob_of(qti, qp, pti[lane]);
+                rsd[lane] = d > 0.f ? d : 0.f;
             }
-            if (z > 0.f)
-                for (int k = 0; k < TOP_K; k++) p[k] = rsd[k] / z;
+            __syncthreads();
+            float z = 0.f;
+            for (int k = 0; k < TOP_K; k++) z += rsd[k]; /* the rule's order */
+            if (z > 0.f && lane < TOP_K) p[lane] = rsd[lane] / z;
+            __syncthreads();
             j++;
         }
         if (accepted >= 0) {
-            path[n_acc++] = accepted;
-            emit[n_emit++] = tok[accepted];
+            if (lane == 0) {
+                path[n_acc] = accepted;
+                emit[n_emit] = tok[accepted];
+            }
+            n_acc++;
+            n_emit++;
             if (tok[accepted] == TOK_EOS) break;
-            state_push(&st, tok[accepted]);
+            if (lane == 0) state_push(&st, tok[accepted]);
+            __syncthreads();
             v = accepted;
             continue;
         }
@@ -521,19 +589,32 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
         if (greedy) {
             for (int k = 1; k < TOP_K; k++)
                 if (p[k] > p[choice]) choice = k;
-        } else if (rejected_any) {
-            choice = residual_draw(&st, p);
+        } else if (st.seeded) {
+            choice = wave_argmax_first(draw_pert(&st, p, lane, rejected_any != 0), lane);
         } else {
-            choice = st.seeded ? gumbel_draw(&st, p) : xoshiro_draw(&st, p);
+            if (lane == 0) bcast = (uint32_t)xoshiro_draw(&st, p);
+            __syncthreads();
+            choice = (int)bcast;
         }
         const int64_t t = cand_to_vocab(pti[choice]);
-        emit[n_emit++] = t;
-        state_push(&st, t);
+        if (lane == 0) {
+            emit[n_emit] = t;
+            state_push(&st, t);
+        }
+        n_emit++;
+        __syncthreads();
         break;
     }
-    a.out_n_acc[s] = n_acc;
-    a.out_n_emit[s] = n_emit;
-    *a.states[s] = st;
+    if (lane == 0) {
+        a.out_n_acc[s] = n_acc;
+        a.out_n_emit[s] = n_emit;
+    }
+    __syncthreads();
+    {
+        uint32_t* dst = (uint32_t*)a.states[s];
+        const uint32_t* src = (const uint32_t*)&st;
+        for (int i = lane; i < (int)(sizeof(st) / 4); i += 64) dst[i] = src[i];
+    }
 }
 
 extern "C" size_t s2p_accept_work_bytes(int n_sess, int rows) {
