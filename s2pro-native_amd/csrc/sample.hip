@@ -156,9 +156,8 @@ S2P_DEV uint32_t okey(float v) {
 
 struct TxShared {
     float cand[N_CAND];
-    uint32_t key[N_CAND];
     s2ps_dev_state st;
-    unsigned hist[256];
+    unsigned hist[4][256]; /* one histogram per wave (LDS atomics contend less) */
     uint32_t prefix;
     int need;       /* survivors still to take at the threshold key */
     int n_gt;       /* collected strictly above the threshold */
@@ -230,7 +229,12 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
         }
     }
     __syncthreads();
-    for (int i = tid; i < N_CAND; i += TX_THREADS) sh.key[i] = okey(sh.cand[i]);
+    /* this thread's keys (a contiguous index range) stay in registers */
+    constexpr int PER = (N_CAND + TX_THREADS - 1) / TX_THREADS; /* 17 */
+    const int i0 = tid * PER;
+    uint32_t kk[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) kk[j] = i0 + j < N_CAND ? okey(sh.cand[i0 + j]) : 0u;
     if (tid == 0) {
         sh.prefix = 0;
         sh.need = TOP_K;
@@ -240,19 +244,21 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
     for (int pass = 0; pass < 4; pass++) {
         const int shift = 24 - 8 * pass;
         const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
-        sh.hist[tid] = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) sh.hist[w][tid] = 0;
         __syncthreads();
         const uint32_t pre = sh.prefix;
-        for (int i = tid; i < N_CAND; i += TX_THREADS) {
-            const uint32_t k = sh.key[i];
-            if ((k & hmask) == pre) atomicAdd(&sh.hist[(k >> shift) & 0xFFu], 1u);
-        }
+        unsigned* hw = sh.hist[tid >> 6];
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (i0 + j < N_CAND && (kk[j] & hmask) == pre) atomicAdd(&hw[(kk[j] >> shift) & 0xFFu], 1u);
         __syncthreads();
         if (tid < 64) {
             /* lane l owns bins 255-4l .. 252-4l (descending) */
             unsigned b4[4], own = 0;
             for (int i = 0; i < 4; i++) {
-                b4[i] = sh.hist[255 - 4 * tid - i];
+                const int bin = 255 - 4 * tid - i;
+                b4[i] = sh.hist[0][bin] + sh.hist[1][bin] + sh.hist[2][bin] + sh.hist[3][bin];
                 own += b4[i];
             }
             /* exclusive prefix over lanes in descending-bin order */
@@ -283,36 +289,44 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
     const uint32_t T = sh.prefix;
     const int need = sh.need;
     if (tid == 0) sh.n_gt = 0;
-    const int per = (N_CAND + TX_THREADS - 1) / TX_THREADS; /* 17 */
-    const int i0 = tid * per, i1 = min(N_CAND, i0 + per);
     int n_eq = 0;
     __syncthreads();
-    for (int i = i0; i < i1; i++) {
-        const uint32_t k = sh.key[i];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        if (i0 + j >= N_CAND) break;
+        const uint32_t k = kk[j];
         if (k > T) {
             const int s = atomicAdd(&sh.n_gt, 1);
-            sh.ti[s] = i;
+            sh.ti[s] = i0 + j;
         } else if (k == T) {
             n_eq++;
         }
     }
-    sh.eq_base[tid] = n_eq;
-    __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int t = 0; t < TX_THREADS; t++) {
-            const int c = sh.eq_base[t];
-            sh.eq_base[t] = run;
-            run += c;
+    {
+        /* exclusive prefix of the per-thread tie counts in thread order
+         * (integers: any association gives the same result) */
+        const int lane = tid & 63, wv = tid >> 6;
+        int inc = n_eq;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(inc, off, 64);
+            if (lane >= off) inc += o;
         }
+        if (lane == 63) sh.eq_base[wv] = inc; /* wave totals, read below */
+        __syncthreads();
+        int base = 0;
+        for (int w = 0; w < wv; w++) base += sh.eq_base[w];
+        __syncthreads();
+        sh.eq_base[tid] = base + inc - n_eq;
     }
     __syncthreads();
     {
         int r = sh.eq_base[tid];
         const int ngt = TOP_K - need; /* == sh.n_gt */
-        for (int i = i0; i < i1 && r < need; i++)
-            if (sh.key[i] == T) {
-                sh.ti[ngt + r] = i;
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (i0 + j < N_CAND && r < need && kk[j] == T) {
+                sh.ti[ngt + r] = i0 + j;
                 r++;
             }
     }
@@ -380,7 +394,11 @@ __global__ __launch_bounds__(TX_THREADS) void k_sample(const uint16_t* __restric
     __shared__ TxShared sh;
     const int row = blockIdx.x;
     s2ps_dev_state* sp = states[row];
-    if (threadIdx.x == 0) sh.st = *sp;
+    {
+        const uint32_t* src = (const uint32_t*)sp;
+        uint32_t* dst = (uint32_t*)&sh.st;
+        for (int i = threadIdx.x; i < (int)(sizeof(sh.st) / 4); i += TX_THREADS) dst[i] = src[i];
+    }
     __syncthreads();
     transform_row(sh, logits + (size_t)row * vocab_stride, eos_logits ? eos_logits + row : nullptr);
     if (threadIdx.x != 0) return;
@@ -434,8 +452,13 @@ __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
         for (int c = v + 1; c < a.R; c++) has_child |= a.parent[c] == v;
         if (!has_child) return;
     }
+    {
+        const uint32_t* src = (const uint32_t*)a.states[s];
+        uint32_t* dst = (uint32_t*)&sh.st;
+        for (int i = threadIdx.x; i < (int)(sizeof(sh.st) / 4); i += TX_THREADS) dst[i] = src[i];
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        sh.st = *a.states[s];
         /* push the drafted tokens of the root path (root excluded) */
         /* root path; parent indices are validated (parent[u] in [0, u)) so a
          * malformed tree ends the walk instead of reading out of bounds */
