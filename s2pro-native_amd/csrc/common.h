@@ -56,12 +56,33 @@ S2P_DEV s2p_f32x4 mfma16x16x32(s2p_u32x4 a, s2p_u32x4 b, s2p_f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+/* lane permutation within 16-lane rows (DPP control CTRL), a VALU move */
+template <int CTRL>
+S2P_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+/* v + (v of lane ^ 1) + (... of lane ^ 2): the 4-lane butterfly of
+ * __shfl_xor 1 then 2, with quad_perm moves */
+S2P_DEV float quad_sum(float v) {
+    v += dpp_f<0xB1>(v); /* quad_perm [1,0,3,2] */
+    v += dpp_f<0x4E>(v); /* quad_perm [2,3,0,1] */
+    return v;
+}
 /* Wave-wide (64 lanes) reductions through cross-lane shuffles.  The sum
  * follows the shuffle-down tree (offsets 32,16,...,1): lane 0 ends with
  * ((x0+x32)+(x16+x48))+... */
 S2P_DEV float wave_sum_down(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+    /* the same tree in lane 0, with cross-lane moves that stay in the VALU
+     * (no LDS round trip): halves and 16-lane rows by permlane swaps, then
+     * row rotations (lane i < 16 - off reads lane i + off) */
+    v += __uint_as_float(
+        __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+    v += __uint_as_float(
+        __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+    v += dpp_f<0x128>(v); /* row_ror:8 */
+    v += dpp_f<0x124>(v); /* row_ror:4 */
+    v += dpp_f<0x122>(v); /* row_ror:2 */
+    v += dpp_f<0x121>(v); /* row_ror:1 */
     return v;
 }
 /* sum over each aligned group of 16 lanes (fixed-order butterfly; every

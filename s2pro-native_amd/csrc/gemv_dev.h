@@ -213,8 +213,7 @@ S2P_DEV void gv_stage_one(const GemvArgs& a, const GvLds& L, int m, int b, bool 
     }
     if (valid) *(LDS(s2p_u32x4)*)(L.x + m * L.xs + b * 8) = o;
     if constexpr (WFMT == GEMV_W_BF16) return; /* no group sums: no bias term */
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s = quad_sum(s);
     if (valid && (b & 3) == 0) {
         uint16_t h, md, lo;
         split3(s, h, md, lo);
@@ -303,7 +302,8 @@ static __host__ __device__ constexpr int gv_chg(int wfmt) {
 }
 struct GvBuf {
     uint32_t w[16];
-    s2p_u32x2 s;
+    s2p_u32x2 s;      /* INT4: f16 scales of row r, groups 4q..4q+3 */
+    s2p_u32x2 sa[4];  /* INT4 (whole-K engine): f16 scales of row r, all 16 groups */
 };
 
 /* Branch-free: every load is issued (out-of-range groups read a clamped,
@@ -312,7 +312,7 @@ struct GvBuf {
  * loads, or selects on the loaded data, make it wait for everything.  The
  * out-of-range data is never used: the multiply stops at gn, and the bias
  * correction pairs those groups' (finite) scales with zero-padded sums. */
-template <int WFMT>
+template <int WFMT, bool TR = false>
 S2P_DEV void gv_load(GvBuf& B, const GemvArgs& a, int nrow, int gabs, int gn, int q) {
     if constexpr (WFMT == GEMV_W_INT4) {
         const uint8_t* wrow = a.w + (size_t)nrow * (a.K >> 1) + (size_t)gabs * 16;
@@ -330,6 +330,13 @@ S2P_DEV void gv_load(GvBuf& B, const GemvArgs& a, int nrow, int gabs, int gn, in
         const uint16_t* srow = (const uint16_t*)a.s + (size_t)nrow * (a.K >> 5) + gabs +
                                (sok ? 4 * q : 0);
         B.s = *(const s2p_u32x2*)srow;
+        if constexpr (TR) {
+            /* every lane of row r takes the row's 16 scales (four lanes read
+             * the same bytes: one cache access) */
+            const uint16_t* s0 = (const uint16_t*)a.s + (size_t)nrow * (a.K >> 5) + gabs;
+#pragma unroll
+            for (int d = 0; d < 4; d++) B.sa[d] = *(const s2p_u32x2*)(s0 + (4 * d < gn ? 4 * d : 0));
+        }
     } else if constexpr (WFMT == GEMV_W_BF16) {
         /* lane (q, r): k 8q..8q+7 of group it of row r, the A operand as is */
         const uint16_t* wrow = (const uint16_t*)a.w + (size_t)nrow * a.K + (size_t)gabs * 32 + 8 * q;
@@ -367,13 +374,75 @@ S2P_DEV s2p_f32x4 mfma16x16x16(s2p_u32x2 a, s2p_u32x2 b, s2p_f32x4 c) {
 }
 
 /* multiply one chunk: cg = chunk's first group within the staged window */
-template <int WFMT, int MT>
+template <int WFMT, int MT, bool TR = false>
 S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, int wave, int q,
                         int r, s2p_f32x4 (&acc)[MT], s2p_f32x4 (&corr)[MT]) {
     int mrow[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) mrow[t] = min(t * 16 + r, M - 1);
-    if constexpr (WFMT == GEMV_W_INT4) {
+    if constexpr (WFMT == GEMV_W_INT4 && TR) {
+        /* Transposed tile: the staged activations are the A operand (row m)
+         * and the dequantised weights of row r the B operand (column n), so
+         * lane (q, r) holds D[m = 16t + 4q + i][n = r] and every element of
+         * a lane takes the same group scale: one v_fma_mix_f32 per element
+         * straight from the loaded f16, no scale staging. */
+        uint32_t kmask = 0x00780078u, kone = 0x3F803F80u;
+        asm volatile("" : "+v"(kmask), "+v"(kone));
+#pragma unroll
+        for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
+            if (it * 4 >= gn) break;
+            uint32_t d0 = B.w[it * 4 + 0], d1 = B.w[it * 4 + 1];
+            uint32_t d2 = B.w[it * 4 + 2], d3 = B.w[it * 4 + 3];
+            xpose4(d0, d1, d2, d3);
+            const uint32_t dj[4] = {d0, d1, d2, d3};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int g = it * 4 + j;
+                const s2p_u32x4 wv = deq_int4(dj[j], kmask, kone);
+                const uint32_t sw = (g & 2) ? B.sa[g >> 2].y : B.sa[g >> 2].x;
+                const _Float16 sh = __builtin_bit_cast(
+                    _Float16, (uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+                const float sf = (float)sh;
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const s2p_u32x4 xv =
+                        *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
+                    const s2p_f32x4 raw = mfma16x16x32(xv, wv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(sf, raw[i], acc[t][i]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0); /* keep LDS reads from piling up */
+        }
+        /* bias correction: corr += X (16 cols m x 16 groups) . S (16 groups x
+         * 16 rows n), the scales of row r / groups 4q..4q+3 as exact bf16
+         * hi + lo (the B operand) */
+        uint32_t shi[2], slo[2];
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            const uint32_t pair = B.s[d];
+            uint32_t hb[2], lb[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float f = h2f((uint16_t)(e ? pair >> 16 : pair & 0xFFFFu));
+                hb[e] = __float_as_uint(f) & 0xFFFF0000u;
+                lb[e] = __float_as_uint(f - __uint_as_float(hb[e])) >> 16;
+            }
+            shi[d] = (hb[0] >> 16) | hb[1];
+            slo[d] = lb[0] | (lb[1] << 16);
+        }
+        const s2p_u32x2 ah = {shi[0], shi[1]};
+        const s2p_u32x2 al = {slo[0], slo[1]};
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const s2p_u32x2 bx = *(const LDS(s2p_u32x2)*)(L.X3 + (mrow[t] * 3 + p) * L.xg +
+                                                         cg + 4 * q);
+                corr[t] = mfma16x16x16(bx, ah, corr[t]);
+                corr[t] = mfma16x16x16(bx, al, corr[t]);
+            }
+    } else if constexpr (WFMT == GEMV_W_INT4) {
         /* scales of row r, groups 4q..4q+3: f32 to this wave's LDS slice in
          * [group][row] order, and bf16 hi / lo as the correction's A operand */
         LDS(float)* sc = L.sc + wave * GV_CHG_INT4 * 16;
@@ -861,35 +930,44 @@ S2P_DEV int gv3_wrow(const GemvArgs& a, const Gv3Geo& g, int tg, int r) {
     return min(base + r, a.N - 1);
 }
 
+/* INT4 at one column tile runs the transposed tile (gv_compute TR) */
+static __host__ __device__ constexpr bool gv3_tr(int wfmt, int mt, bool) {
+    return wfmt == GEMV_W_INT4 && mt == 1;
+}
+
 /* chunk t of the wave's flattened (tile group, chunk) stream */
-template <int WFMT>
+template <int WFMT, int MT, bool PRE>
 S2P_DEV void gv3_load(GvBuf& B, const GemvArgs& a, const Gv3Geo& g, int p, int P, int t) {
     constexpr int CHG = gv_chg(WFMT);
     const int lane = threadIdx.x & 63;
     const int it = g.nch == 1 ? t : t / g.nch, c = t - it * g.nch;
-    gv_load<WFMT>(B, a, gv3_wrow(a, g, p + it * P, lane & 15), g.gb + c * CHG,
+    gv_load<WFMT, gv3_tr(WFMT, MT, PRE)>(B, a, gv3_wrow(a, g, p + it * P, lane & 15), g.gb + c * CHG,
                   min(CHG, g.gn - c * CHG), lane >> 4);
 }
 
 /* The first weight chunk of workgroup p, issued ahead (the persistent kernel
  * issues it before the barrier that precedes the GEMV). */
-template <int WFMT>
+template <int WFMT, int MT = 1>
 S2P_DEV void gv3_prefetch(const GemvArgs& a, int p, int P, GvBuf& b0, GvBuf& b1) {
-    const Gv3Geo g = gv3_geo<WFMT>(a, p, P, threadIdx.x >> 6);
+    const Gv3Geo g = gv3_geo<WFMT>(a, p, P, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
     /* both buffers defined on every path: their old contents are dead */
     if (g.T > 0) {
-        gv3_load<WFMT>(b0, a, g, p, P, 0);
+        gv3_load<WFMT, MT, true>(b0, a, g, p, P, 0);
     } else {
 #pragma unroll
         for (int i = 0; i < 16; i++) b0.w[i] = 0u;
         b0.s = (s2p_u32x2){0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 4; i++) b0.sa[i] = (s2p_u32x2){0u, 0u};
     }
     if (g.T > 1) {
-        gv3_load<WFMT>(b1, a, g, p, P, 1);
+        gv3_load<WFMT, MT, true>(b1, a, g, p, P, 1);
     } else {
 #pragma unroll
         for (int i = 0; i < 16; i++) b1.w[i] = 0u;
         b1.s = (s2p_u32x2){0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 4; i++) b1.sa[i] = (s2p_u32x2){0u, 0u};
     }
 }
 
@@ -902,7 +980,8 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
                           uint16_t* Y, GvBuf& b0, GvBuf& b1) {
 #pragma clang fp contract(off)
     constexpr int CHG = gv_chg(WFMT);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r = lane & 15;
     const int M = a.M, ks = a.ks, gps = a.gps;
     const Gv3Geo geo = gv3_geo<WFMT>(a, p, P, wave);
@@ -939,7 +1018,7 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
 
     const int nch = geo.nch, T = geo.T;
     auto load_t = [&](GvBuf& B, int t) __attribute__((always_inline)) {
-        gv3_load<WFMT>(B, a, geo, p, P, t);
+        gv3_load<WFMT, MT, PRE>(B, a, geo, p, P, t);
     };
 
     Gv3Pre pre;
@@ -1037,58 +1116,86 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
         if (it == 0) stamp(3);
         __syncthreads();
         if (it == 0) stamp(4);
-        /* output (row rho of unit u, column m): element rho % 4 of lane
-         * (rho / 4) * 16 + m % 16, column tile m / 16, of the unit's waves */
-        const LDS(float)* rf = (const LDS(float)*)rb;
-        const int g = p + it * P;
-        auto tsum = [&](int jw, int rho, int m) __attribute__((always_inline)) {
-            const int src = ((m >> 4) * 64 + (rho >> 2) * 16 + (m & 15)) * 4 + (rho & 3);
-            float v = 0.f;
-            for (int s = 0; s < ks; s++) v += rf[(size_t)(jw * ks + s) * MT * 256 + src];
-            return v;
-        };
-        for (int u = 0; u < units; u++)
-        for (int base = 0; base < M * 16; base += nw * 64) {
-            const int idx = base + tid;
-            const int rho = idx & 15, m = idx >> 4;
-            const int tile = g * units + u;
-            const int n = tile * 16 + rho;
-            const bool ok = m < M && tile < tiles;
-            if (swiglu) {
-                if (ok) {
-                    float gv = tsum(u, rho, m), uv = tsum(units + u, rho, m);
-                    if (WFMT == GEMV_W_INT8) {
-                        gv *= ((const float*)a.s)[n];
-                        uv *= ((const float*)a.s)[F + n];
+        /* Unit u (a 16-row output tile; SWIGLU: its gate and up tiles) is
+         * reduced by its own waves, lane-locally: a lane sums its elements
+         * over the ks K-slice partials in slice order (deterministic), then
+         * runs the epilogue.  Element i of lane (q, r) in column tile t is
+         * (m, n) = (16t + 4q + i, r) for the transposed INT4 tile, and
+         * (16t + r, 4q + i) otherwise.  Transposed: element i is handled by
+         * the unit's slice wave i % ks (the per-column sums of squares are
+         * per element); otherwise slice wave 0 takes all four. */
+        constexpr bool TRN = gv3_tr(WFMT, MT, PRE);
+        const int u = geo.j, sl0 = geo.sp;
+        const int tile = (p + it * P) * units + u;
+        if (u < units && tile < tiles && (TRN || sl0 == 0)) { /* uniform */
+            const int n0 = tile * 16;
+            const LDS(float)* rf = (const LDS(float)*)rb;
+#pragma unroll 1
+            for (int t = 0; t < MT; t++) {
+                float sq4 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (TRN && i % ks != sl0) continue; /* uniform */
+                    float v = 0.f, w = 0.f;
+                    for (int sl = 0; sl < ks; sl++)
+                        v += rf[(((u * ks + sl) * MT + t) * 64 + lane) * 4 + i];
+                    if (swiglu)
+                        for (int sl = 0; sl < ks; sl++)
+                            w += rf[((((units + u) * ks + sl) * MT + t) * 64 + lane) * 4 + i];
+                    const int m = TRN ? t * 16 + 4 * q + i : t * 16 + r;
+                    const int n = n0 + (TRN ? r : 4 * q + i);
+                    const bool ok = m < M;
+                    if (swiglu) {
+                        if (ok) {
+                            float gv = v, uv = w;
+                            if (WFMT == GEMV_W_INT8) {
+                                gv *= ((const float*)a.s)[n];
+                                uv *= ((const float*)a.s)[F + n];
+                            }
+                            st_act16<WT>(Y + (size_t)m * a.ldy + n,
+                                         silu_mul_bf16(f2bf(gv), f2bf(uv)));
+                        }
+                        continue;
                     }
-                    st_act16<WT>(Y + (size_t)m * a.ldy + n, silu_mul_bf16(f2bf(gv), f2bf(uv)));
+                    float sq = 0.f;
+                    if (ok && n < a.N) {
+                        if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
+                        const uint16_t yb = f2bf(v);
+                        uint16_t* yp = Y + (size_t)m * a.ldy + n;
+                        if (a.epi == GEMV_EPI_RESID) {
+                            const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
+                            st_act16<WT>(yp, xo);
+                            const float xv = bf2f(xo);
+                            sq = xv * xv;
+                        } else {
+                            st_act16<WT>(yp, yb);
+                        }
+                    }
+                    if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                        if (TRN) {
+                            /* over the tile's 16 rows n = r of column m */
+                            const float tot = sum_lanes16(sq);
+                            if (r == 0 && ok)
+                                coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+                        } else {
+                            sq4 += sq;
+                        }
+                    }
                 }
-                continue;
-            }
-            float ssq = 0.f;
-            if (ok && n < a.N) {
-                float v = tsum(u, rho, m);
-                if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
-                const uint16_t yb = f2bf(v);
-                uint16_t* yp = Y + (size_t)m * a.ldy + n;
-                if (a.epi == GEMV_EPI_RESID) {
-                    const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
-                    st_act16<WT>(yp, xo);
-                    const float xv = bf2f(xo);
-                    ssq = xv * xv;
-                } else {
-                    st_act16<WT>(yp, yb);
+                if (!TRN && !swiglu && a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                    float tot = sq4;
+                    tot += __shfl_xor(tot, 16, 64);
+                    tot += __shfl_xor(tot, 32, 64);
+                    const int m = t * 16 + r;
+                    if (q == 0 && m < M)
+                        coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
                 }
-            }
-            if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
-                const float tot = sum_lanes16(ssq); /* the 16 rows of (tile, m) */
-                if (rho == 0 && ok) coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
             }
         }
     };
     auto step = [&](const GvBuf& B, int t) __attribute__((always_inline)) {
         const int it = nch == 1 ? t : t / nch, c = t - it * nch;
-        gv_compute<WFMT, MT>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
+        gv_compute<WFMT, MT, gv3_tr(WFMT, MT, PRE)>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
         if (c == nch - 1) finish(it);
     };
     int t = 0;
