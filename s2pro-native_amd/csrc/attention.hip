@@ -35,7 +35,8 @@
 template <int MQT, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    attn_block<MQT, W>(a, blockIdx.x, blockIdx.y, blockIdx.z, (LDS(unsigned char)*)smem_raw);
+    attn_block<MQT, W, false>(a, blockIdx.x, blockIdx.y, blockIdx.z,
+                              (LDS(unsigned char)*)smem_raw);
 }
 
 /* merge split partials (one thread per output element) */

@@ -121,17 +121,21 @@ S2P_DEV bool visible(const SegInfo& s, int rl, int j) {
 }
 
 S2P_DEV float max16(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1, 16));
-    v = fmaxf(v, __shfl_xor(v, 2, 16));
-    v = fmaxf(v, __shfl_xor(v, 4, 16));
-    v = fmaxf(v, __shfl_xor(v, 8, 16));
+    /* every lane of the 16-lane row gets the max (DPP moves; max is exact,
+     * so the rotations' order is immaterial) */
+    v = fmaxf(v, dpp_f<0xB1>(v)); /* quad_perm [1,0,3,2] */
+    v = fmaxf(v, dpp_f<0x4E>(v)); /* quad_perm [2,3,0,1] */
+    v = fmaxf(v, dpp_f<0x124>(v)); /* row_ror:4 */
+    v = fmaxf(v, dpp_f<0x128>(v)); /* row_ror:8 */
     return v;
 }
 S2P_DEV float sum16(float v) {
-    v += __shfl_xor(v, 1, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 8, 16);
+    /* lane 0 of each 16-lane row gets the xor-butterfly total ((q0 + q1) +
+     * (q2 + q3)) of its quad sums q (DPP moves; the other lanes get partial
+     * rotations, unused) */
+    v = quad_sum(v);
+    v += dpp_f<0x124>(v); /* row_ror:4 */
+    v += dpp_f<0x128>(v); /* row_ror:8 */
     return v;
 }
 
@@ -180,7 +184,10 @@ S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, 
 
 /* One (segment, kv head, position split) attention block; smem holds
  * AT_LDS_BYTES.  Body of k_attn, also run by the persistent verify kernel. */
-template <int MQT, int W = AT_WAVES>
+/* COH: the q / qkv / RoPE-table reads bypass the L2 (the persistent
+ * kernel, where their producer ran in the same launch); the layer kernel
+ * reads them through the caches */
+template <int MQT, int W = AT_WAVES, bool COH = true>
 __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
     constexpr int SVB = AT_SV_BYTES_W(W), SPB = AT_SP_BYTES_W(W), SMLB = AT_SML_BYTES_W(W);
     LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
@@ -264,19 +271,21 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 const int row = isq ? S.row0 + (it >> 2) : first + (s0 - S.L) + (it - nq);
                 const int head = isq ? 4 * kvh + (it & 3) : 32 + kvh;
                 const uint16_t* src = a.qkv + (size_t)row * 6144 + head * AT_HD;
-                v0[j] = bf2f(coh_ld16(src + lane));
-                v1[j] = bf2f(coh_ld16(src + lane + 64));
+                v0[j] = bf2f(COH ? coh_ld16(src + lane) : src[lane]);
+                v1[j] = bf2f(COH ? coh_ld16(src + lane + 64) : src[lane + 64]);
                 const uint16_t* nw = isq ? a.qn_w : a.kn_w;
                 w0[j] = nw[lane];
                 w1[j] = nw[lane + 64];
                 const float* tab = a.rope_tab + (size_t)row * 128;
-                cs[j][0] = coh_ldf(tab + (lane >> 1) * 2);
-                cs[j][1] = coh_ldf(tab + (lane >> 1) * 2 + 1);
-                cs[j][2] = coh_ldf(tab + ((lane + 64) >> 1) * 2);
-                cs[j][3] = coh_ldf(tab + ((lane + 64) >> 1) * 2 + 1);
+                const float* t0 = tab + (lane >> 1) * 2;
+                const float* t1 = tab + ((lane + 64) >> 1) * 2;
+                cs[j][0] = COH ? coh_ldf(t0) : t0[0];
+                cs[j][1] = COH ? coh_ldf(t0 + 1) : t0[1];
+                cs[j][2] = COH ? coh_ldf(t1) : t1[0];
+                cs[j][3] = COH ? coh_ldf(t1 + 1) : t1[1];
                 if (!isq) { /* the v head rides along */
-                    x0[j] = coh_ld16(src + 8 * AT_HD + lane);
-                    x1[j] = coh_ld16(src + 8 * AT_HD + lane + 64);
+                    x0[j] = COH ? coh_ld16(src + 8 * AT_HD + lane) : src[8 * AT_HD + lane];
+                    x1[j] = COH ? coh_ld16(src + 8 * AT_HD + lane + 64) : src[8 * AT_HD + lane + 64];
                 }
             }
             /* the first K/V tile goes out behind the first batch's loads, so
@@ -331,8 +340,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
 #pragma unroll
             for (int ch = 0; ch < 4; ch++) {
                 if (rl < S.nrows) {
-                    qa[qt][ch] = coh_ld128(a.q + (size_t)(S.row0 + rl) * qrow_stride +
-                                           (4 * kvh + g) * AT_HD + 32 * ch + 8 * qq);
+                    const uint16_t* qp = a.q + (size_t)(S.row0 + rl) * qrow_stride +
+                                         (4 * kvh + g) * AT_HD + 32 * ch + 8 * qq;
+                    qa[qt][ch] = COH ? coh_ld128(qp) : *(const s2p_u32x4*)qp;
                 } else {
                     qa[qt][ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
                 }
@@ -475,20 +485,41 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 for (int v = 0; v < 4; v++)
                     o[qt][dt][v] += s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c];
     };
+    /* the tree's hand-offs in a lane-major layout ([slot][qt][dt][lane] of
+     * 16 bytes): one ds_write_b128 / ds_read_b128 per register quad,
+     * conflict-free */
+    static_assert((W / 2) * MQT * 8 * 64 * 16 <= SVB, "merge slots exceed the V tiles");
+    LDS(s2p_f32x4)* s_o4 = (LDS(s2p_f32x4)*)s_v;
+    auto put4 = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) s_o4[((slot * MQT + qt) * 8 + dt) * 64 + lane] = o[qt][dt];
+    };
+    auto add4 = [&](int slot) {
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const s2p_f32x4 t = s_o4[((slot * MQT + qt) * 8 + dt) * 64 + lane];
+#pragma unroll
+                for (int v = 0; v < 4; v++) o[qt][dt][v] += t[v];
+            }
+    };
     /* pairwise tree: wave w += wave w + half for half = W/2 .. 2, then wave
      * 0 += wave 1 below */
 #pragma unroll
     for (int half = W / 2; half >= 2; half /= 2) {
         __syncthreads();
-        if (wave >= half && wave < 2 * half) put(wave - half);
+        if (wave >= half && wave < 2 * half) put4(wave - half);
         __syncthreads();
-        if (wave < half) add(wave);
+        if (wave < half) add4(wave);
     }
     __syncthreads();
-    if (wave == 1) put(0);
+    if (wave == 1) put4(0);
     __syncthreads();
     stamp(3);
-    if (wave == 0) add(0);
+    if (wave == 0) add4(0);
     if (a.nsplit == 1) {
         if (wave == 0) {
 #pragma unroll

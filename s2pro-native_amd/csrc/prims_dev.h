@@ -33,11 +33,11 @@ S2P_DEV void qkrope_math(float v0, float v1, uint16_t w0, uint16_t w1, float c0,
 #pragma clang fp contract(off)
     float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
     s = wave_sum_down(s);
-    s = __shfl(s, 0, 64);
+    s = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(s), 0)); /* lane 0's total */
     const float inv = rsqrt_rule(s / 128.0f + eps);
     v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(w0))));
     v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(w1))));
-    const float pv0 = __shfl_xor(v0, 1, 64), pv1 = __shfl_xor(v1, 1, 64);
+    const float pv0 = dpp_f<0xB1>(v0), pv1 = dpp_f<0xB1>(v1); /* lane ^ 1 */
     if ((lane & 1) == 0) {
         *o0 = __fsub_rn(__fmul_rn(v0, c0), __fmul_rn(pv0, s0)); /* x0' */
         *o1 = __fsub_rn(__fmul_rn(v1, c1), __fmul_rn(pv1, s1));
