@@ -53,12 +53,12 @@
 #include "s2pro/gemm.h"
 
 /* whole-K workgroups of up to 16 waves (MT = 1) or 8 waves */
-template <int WFMT, int MT>
+template <int WFMT, int MT, bool NOTR = false>
 __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void k_gemv3(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem3[];
     GvBuf b0, b1;
-    gv3_block<WFMT, MT, false>(a, blockIdx.x, gridDim.x, (LDS(unsigned char)*)smem3, a.y, b0,
-                               b1);
+    gv3_block<WFMT, MT, false, false, false, NOTR>(a, blockIdx.x, gridDim.x,
+                                                  (LDS(unsigned char)*)smem3, a.y, b0, b1);
 }
 
 template <int WFMT, int MT, bool WIN1>
@@ -342,17 +342,27 @@ extern "C" void s2p_gemv_set_probe(uint64_t* buf, int index) {
     g_probe_at = buf ? index : -1;
 }
 
-template <int WFMT, int MT>
-static hipError_t gv3_launch_mt(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
-                                hipStream_t st) {
+template <int WFMT, int MT, bool NOTR>
+static hipError_t gv3_launch_k(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
+                               hipStream_t st) {
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_gemv3<WFMT, MT>,
+        (void)hipFuncSetAttribute((const void*)k_gemv3<WFMT, MT, NOTR>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, GV3_LDS_MAX);
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_gemv3<WFMT, MT>), grid, block, lds, st, a);
+    hipLaunchKernelGGL((k_gemv3<WFMT, MT, NOTR>), grid, block, lds, st, a);
     return hipGetLastError();
+}
+
+/* launches shaped like the persistent kernel's GEMVs (test hook) also use
+ * its untransposed INT4 tile, so the two agree bit for bit */
+template <int WFMT, int MT>
+static hipError_t gv3_launch_mt(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
+                                hipStream_t st) {
+    if constexpr (WFMT == GEMV_W_INT4 && MT == 1)
+        if (g_v3_nw) return gv3_launch_k<WFMT, MT, true>(a, grid, block, lds, st);
+    return gv3_launch_k<WFMT, MT, false>(a, grid, block, lds, st);
 }
 
 template <int WFMT>

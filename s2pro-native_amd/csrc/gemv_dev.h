@@ -386,11 +386,18 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
          * lane (q, r) holds D[m = 16t + 4q + i][n = r] and every element of
          * a lane takes the same group scale: one v_fma_mix_f32 per element
          * straight from the loaded f16, no scale staging. */
+        static_assert(MT == 1 || !TR, "the transposed tile is one column tile");
         uint32_t kmask = 0x00780078u, kone = 0x3F803F80u;
         asm volatile("" : "+v"(kmask), "+v"(kone));
+        /* a block's four activation reads are issued together, ahead of its
+         * dequantisation (one LDS latency per 4 groups) */
+        const LDS(uint16_t)* xrow = L.x + mrow[0] * L.xs + cg * 32 + q * 8;
 #pragma unroll
         for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
             if (it * 4 >= gn) break;
+            s2p_u32x4 xa[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) xa[j] = *(const LDS(s2p_u32x4)*)(xrow + (it * 4 + j) * 32);
             uint32_t d0 = B.w[it * 4 + 0], d1 = B.w[it * 4 + 1];
             uint32_t d2 = B.w[it * 4 + 2], d3 = B.w[it * 4 + 3];
             xpose4(d0, d1, d2, d3);
@@ -403,14 +410,9 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
                 const _Float16 sh = __builtin_bit_cast(
                     _Float16, (uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
                 const float sf = (float)sh;
+                const s2p_f32x4 raw = mfma16x16x32(xa[j], wv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                for (int t = 0; t < MT; t++) {
-                    const s2p_u32x4 xv =
-                        *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
-                    const s2p_f32x4 raw = mfma16x16x32(xv, wv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(sf, raw[i], acc[t][i]);
-                }
+                for (int i = 0; i < 4; i++) acc[0][i] = fmaf(sf, raw[i], acc[0][i]);
             }
             __builtin_amdgcn_sched_barrier(0); /* keep LDS reads from piling up */
         }
@@ -930,18 +932,21 @@ S2P_DEV int gv3_wrow(const GemvArgs& a, const Gv3Geo& g, int tg, int r) {
     return min(base + r, a.N - 1);
 }
 
-/* INT4 at one column tile runs the transposed tile (gv_compute TR) */
-static __host__ __device__ constexpr bool gv3_tr(int wfmt, int mt, bool) {
-    return wfmt == GEMV_W_INT4 && mt == 1;
+/* INT4 at one column tile runs the transposed tile (gv_compute TR), except
+ * in the persistent kernel (NOTR), whose register budget the untransposed
+ * tile fits, and in layer launches shaped like it (the test hook that
+ * compares the two) */
+static __host__ __device__ constexpr bool gv3_tr(int wfmt, int mt, bool notr) {
+    return wfmt == GEMV_W_INT4 && mt == 1 && !notr;
 }
 
 /* chunk t of the wave's flattened (tile group, chunk) stream */
-template <int WFMT, int MT, bool PRE>
+template <int WFMT, int MT, bool NOTR>
 S2P_DEV void gv3_load(GvBuf& B, const GemvArgs& a, const Gv3Geo& g, int p, int P, int t) {
     constexpr int CHG = gv_chg(WFMT);
     const int lane = threadIdx.x & 63;
     const int it = g.nch == 1 ? t : t / g.nch, c = t - it * g.nch;
-    gv_load<WFMT, gv3_tr(WFMT, MT, PRE)>(B, a, gv3_wrow(a, g, p + it * P, lane & 15), g.gb + c * CHG,
+    gv_load<WFMT, gv3_tr(WFMT, MT, NOTR)>(B, a, gv3_wrow(a, g, p + it * P, lane & 15), g.gb + c * CHG,
                   min(CHG, g.gn - c * CHG), lane >> 4);
 }
 
@@ -957,8 +962,6 @@ S2P_DEV void gv3_prefetch(const GemvArgs& a, int p, int P, GvBuf& b0, GvBuf& b1)
 #pragma unroll
         for (int i = 0; i < 16; i++) b0.w[i] = 0u;
         b0.s = (s2p_u32x2){0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 4; i++) b0.sa[i] = (s2p_u32x2){0u, 0u};
     }
     if (g.T > 1) {
         gv3_load<WFMT, MT, true>(b1, a, g, p, P, 1);
@@ -966,8 +969,6 @@ S2P_DEV void gv3_prefetch(const GemvArgs& a, int p, int P, GvBuf& b0, GvBuf& b1)
 #pragma unroll
         for (int i = 0; i < 16; i++) b1.w[i] = 0u;
         b1.s = (s2p_u32x2){0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 4; i++) b1.sa[i] = (s2p_u32x2){0u, 0u};
     }
 }
 
@@ -975,7 +976,7 @@ S2P_DEV void gv3_prefetch(const GemvArgs& a, int p, int P, GvBuf& b0, GvBuf& b1)
  * (gv3_prefetch). */
 /* COH: activation loads bypass the L2 (their producer ran in this launch
  * and the L2 was not invalidated since); WT: outputs written through. */
-template <int WFMT, int MT, bool COH, bool PRE = false, bool WT = COH>
+template <int WFMT, int MT, bool COH, bool PRE = false, bool WT = COH, bool NOTR = PRE>
 __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* smem,
                           uint16_t* Y, GvBuf& b0, GvBuf& b1) {
 #pragma clang fp contract(off)
@@ -1018,7 +1019,7 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
 
     const int nch = geo.nch, T = geo.T;
     auto load_t = [&](GvBuf& B, int t) __attribute__((always_inline)) {
-        gv3_load<WFMT, MT, PRE>(B, a, geo, p, P, t);
+        gv3_load<WFMT, MT, NOTR>(B, a, geo, p, P, t);
     };
 
     Gv3Pre pre;
@@ -1116,86 +1117,137 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
         if (it == 0) stamp(3);
         __syncthreads();
         if (it == 0) stamp(4);
-        /* Unit u (a 16-row output tile; SWIGLU: its gate and up tiles) is
-         * reduced by its own waves, lane-locally: a lane sums its elements
-         * over the ks K-slice partials in slice order (deterministic), then
-         * runs the epilogue.  Element i of lane (q, r) in column tile t is
-         * (m, n) = (16t + 4q + i, r) for the transposed INT4 tile, and
-         * (16t + r, 4q + i) otherwise.  Transposed: element i is handled by
-         * the unit's slice wave i % ks (the per-column sums of squares are
-         * per element); otherwise slice wave 0 takes all four. */
-        constexpr bool TRN = gv3_tr(WFMT, MT, PRE);
-        const int u = geo.j, sl0 = geo.sp;
-        const int tile = (p + it * P) * units + u;
-        if (u < units && tile < tiles && (TRN || sl0 == 0)) { /* uniform */
-            const int n0 = tile * 16;
+        if constexpr (NOTR) {
+            /* output (row rho of unit u, column m): element rho % 4 of lane
+             * (rho / 4) * 16 + m % 16, column tile m / 16, of the unit's waves */
             const LDS(float)* rf = (const LDS(float)*)rb;
-#pragma unroll 1
-            for (int t = 0; t < MT; t++) {
-                float sq4 = 0.f;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    if (TRN && i % ks != sl0) continue; /* uniform */
-                    float v = 0.f, w = 0.f;
-                    for (int sl = 0; sl < ks; sl++)
-                        v += rf[(((u * ks + sl) * MT + t) * 64 + lane) * 4 + i];
-                    if (swiglu)
-                        for (int sl = 0; sl < ks; sl++)
-                            w += rf[((((units + u) * ks + sl) * MT + t) * 64 + lane) * 4 + i];
-                    const int m = TRN ? t * 16 + 4 * q + i : t * 16 + r;
-                    const int n = n0 + (TRN ? r : 4 * q + i);
-                    const bool ok = m < M;
-                    if (swiglu) {
-                        if (ok) {
-                            float gv = v, uv = w;
-                            if (WFMT == GEMV_W_INT8) {
-                                gv *= ((const float*)a.s)[n];
-                                uv *= ((const float*)a.s)[F + n];
-                            }
-                            st_act16<WT>(Y + (size_t)m * a.ldy + n,
-                                         silu_mul_bf16(f2bf(gv), f2bf(uv)));
+            const int g = p + it * P;
+            auto tsum = [&](int jw, int rho, int m) __attribute__((always_inline)) {
+                const int src = ((m >> 4) * 64 + (rho >> 2) * 16 + (m & 15)) * 4 + (rho & 3);
+                float v = 0.f;
+                for (int s = 0; s < ks; s++) v += rf[(size_t)(jw * ks + s) * MT * 256 + src];
+                return v;
+            };
+            for (int u = 0; u < units; u++)
+            for (int base = 0; base < M * 16; base += nw * 64) {
+                const int idx = base + tid;
+                const int rho = idx & 15, m = idx >> 4;
+                const int tile = g * units + u;
+                const int n = tile * 16 + rho;
+                const bool ok = m < M && tile < tiles;
+                if (swiglu) {
+                    if (ok) {
+                        float gv = tsum(u, rho, m), uv = tsum(units + u, rho, m);
+                        if (WFMT == GEMV_W_INT8) {
+                            gv *= ((const float*)a.s)[n];
+                            uv *= ((const float*)a.s)[F + n];
                         }
-                        continue;
+                        st_act16<WT>(Y + (size_t)m * a.ldy + n, silu_mul_bf16(f2bf(gv), f2bf(uv)));
                     }
-                    float sq = 0.f;
-                    if (ok && n < a.N) {
-                        if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
-                        const uint16_t yb = f2bf(v);
-                        uint16_t* yp = Y + (size_t)m * a.ldy + n;
-                        if (a.epi == GEMV_EPI_RESID) {
-                            const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
-                            st_act16<WT>(yp, xo);
-                            const float xv = bf2f(xo);
-                            sq = xv * xv;
-                        } else {
-                            st_act16<WT>(yp, yb);
-                        }
-                    }
-                    if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
-                        if (TRN) {
-                            /* over the tile's 16 rows n = r of column m */
-                            const float tot = sum_lanes16(sq);
-                            if (r == 0 && ok)
-                                coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
-                        } else {
-                            sq4 += sq;
-                        }
+                    continue;
+                }
+                float ssq = 0.f;
+                if (ok && n < a.N) {
+                    float v = tsum(u, rho, m);
+                    if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
+                    const uint16_t yb = f2bf(v);
+                    uint16_t* yp = Y + (size_t)m * a.ldy + n;
+                    if (a.epi == GEMV_EPI_RESID) {
+                        const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
+                        st_act16<WT>(yp, xo);
+                        const float xv = bf2f(xo);
+                        ssq = xv * xv;
+                    } else {
+                        st_act16<WT>(yp, yb);
                     }
                 }
-                if (!TRN && !swiglu && a.epi == GEMV_EPI_RESID && a.ssq_out) {
-                    float tot = sq4;
-                    tot += __shfl_xor(tot, 16, 64);
-                    tot += __shfl_xor(tot, 32, 64);
-                    const int m = t * 16 + r;
-                    if (q == 0 && m < M)
-                        coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+                if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                    const float tot = sum_lanes16(ssq); /* the 16 rows of (tile, m) */
+                    if (rho == 0 && ok) coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+                }
+            }
+        } else {
+            /* Unit u (a 16-row output tile; SWIGLU: its gate and up tiles) is
+             * reduced by its own waves, lane-locally: a lane sums its elements
+             * over the ks K-slice partials in slice order (deterministic), then
+             * runs the epilogue.  Element i of lane (q, r) in column tile t is
+             * (m, n) = (16t + 4q + i, r) for the transposed INT4 tile, and
+             * (16t + r, 4q + i) otherwise.  Transposed: element i is handled by
+             * the unit's slice wave i % ks (the per-column sums of squares are
+             * per element); otherwise slice wave 0 takes all four. */
+            constexpr bool TRN = gv3_tr(WFMT, MT, NOTR);
+            const int u = geo.j, sl0 = geo.sp;
+            const int tile = (p + it * P) * units + u;
+            if (u < units && tile < tiles && (TRN || sl0 == 0)) { /* uniform */
+                const int n0 = tile * 16;
+                const LDS(float)* rf = (const LDS(float)*)rb;
+    #pragma unroll 1
+                for (int t = 0; t < MT; t++) {
+                    float sq4 = 0.f;
+    #pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (TRN && i % ks != sl0) continue; /* uniform */
+                        float v = 0.f, w = 0.f;
+                        for (int sl = 0; sl < ks; sl++)
+                            v += rf[(((u * ks + sl) * MT + t) * 64 + lane) * 4 + i];
+                        if (swiglu)
+                            for (int sl = 0; sl < ks; sl++)
+                                w += rf[((((units + u) * ks + sl) * MT + t) * 64 + lane) * 4 + i];
+                        const int m = TRN ? t * 16 + 4 * q + i : t * 16 + r;
+                        const int n = n0 + (TRN ? r : 4 * q + i);
+                        const bool ok = m < M;
+                        if (swiglu) {
+                            if (ok) {
+                                float gv = v, uv = w;
+                                if (WFMT == GEMV_W_INT8) {
+                                    gv *= ((const float*)a.s)[n];
+                                    uv *= ((const float*)a.s)[F + n];
+                                }
+                                st_act16<WT>(Y + (size_t)m * a.ldy + n,
+                                             silu_mul_bf16(f2bf(gv), f2bf(uv)));
+                            }
+                            continue;
+                        }
+                        float sq = 0.f;
+                        if (ok && n < a.N) {
+                            if (WFMT == GEMV_W_INT8) v *= ((const float*)a.s)[n];
+                            const uint16_t yb = f2bf(v);
+                            uint16_t* yp = Y + (size_t)m * a.ldy + n;
+                            if (a.epi == GEMV_EPI_RESID) {
+                                const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
+                                st_act16<WT>(yp, xo);
+                                const float xv = bf2f(xo);
+                                sq = xv * xv;
+                            } else {
+                                st_act16<WT>(yp, yb);
+                            }
+                        }
+                        if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                            if (TRN) {
+                                /* over the tile's 16 rows n = r of column m */
+                                const float tot = sum_lanes16(sq);
+                                if (r == 0 && ok)
+                                    coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+                            } else {
+                                sq4 += sq;
+                            }
+                        }
+                    }
+                    if (!TRN && !swiglu && a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                        float tot = sq4;
+                        tot += __shfl_xor(tot, 16, 64);
+                        tot += __shfl_xor(tot, 32, 64);
+                        const int m = t * 16 + r;
+                        if (q == 0 && m < M)
+                            coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, tot);
+                    }
                 }
             }
         }
     };
     auto step = [&](const GvBuf& B, int t) __attribute__((always_inline)) {
         const int it = nch == 1 ? t : t / nch, c = t - it * nch;
-        gv_compute<WFMT, MT, gv3_tr(WFMT, MT, PRE)>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
+        gv_compute<WFMT, MT, gv3_tr(WFMT, MT, NOTR)>(B, L, c * CHG, min(CHG, gn - c * CHG), M, 0, q, r, acc, corr);
         if (c == nch - 1) finish(it);
     };
     int t = 0;
