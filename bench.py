@@ -189,7 +189,7 @@ def main():
         ms = e0.elapsed_time(e1) / args.steps
 
         # dominant kernel: the GEMV engine, every weight GEMV of one step
-        # (36 x {wqkv, wo, gate_up, w2} + head at M = 5), launched eagerly on
+        # (36 x {wqkv, wo, gate_up, w2} + head at M = 5), replayed as one graph on
         # this stream and bracketed by HIP events
         lins = []
         for l in range(N_LAYERS):
@@ -205,14 +205,22 @@ def main():
                 s2pamd.check(lib.s2p_linear_forward(ctypes.byref(lin), s2pamd.dptr(xbuf),
                                                     s2pamd.dptr(ybuf), R, 2, S), "gemv")
         gemvs()
-        reps = 5
         side.synchronize()
+        # the 145 launches captured once and replayed: the events then time
+        # the kernels back to back, not the host's per-launch call overhead
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            gemvs()
+        graph.replay()
+        side.synchronize()
+        reps = 5
         g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         g0.record(side)
         for _ in range(reps):
-            gemvs()
+            graph.replay()
         g1.record(side)
         side.synchronize()
+        del graph
         n_launch = reps * len(lins)
         avg_launch_s = g0.elapsed_time(g1) / 1e3 / n_launch
         wbytes = sum(lin.w_pack.bytes + lin.w_iscale.bytes for lin in lins)

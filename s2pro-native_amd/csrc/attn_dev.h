@@ -260,9 +260,12 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         const bool appends = s1 > s0;
         early = !appends && tb0 < p_end;
         constexpr int IB = 8; /* every item of a 4-wave block in one batch at M <= 5 */
+        /* the norm weights of this lane's two elements, once per wave (q and k) */
+        const uint16_t qw0 = a.qn_w[lane], qw1 = a.qn_w[lane + 64];
+        const uint16_t kw0 = a.kn_w[lane], kw1 = a.kn_w[lane + 64];
         for (int base = wave; base < nit; base += IB * W) {
             float v0[IB], v1[IB], cs[IB][4];
-            uint16_t w0[IB], w1[IB], x0[IB], x1[IB];
+            uint16_t x0[IB], x1[IB];
 #pragma unroll
             for (int j = 0; j < IB; j++) {
                 const int it = base + j * W;
@@ -273,16 +276,22 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 const uint16_t* src = a.qkv + (size_t)row * 6144 + head * AT_HD;
                 v0[j] = bf2f(COH ? coh_ld16(src + lane) : src[lane]);
                 v1[j] = bf2f(COH ? coh_ld16(src + lane + 64) : src[lane + 64]);
-                const uint16_t* nw = isq ? a.qn_w : a.kn_w;
-                w0[j] = nw[lane];
-                w1[j] = nw[lane + 64];
+                /* (cos, sin) of the lane's two pairs, 8 bytes each */
                 const float* tab = a.rope_tab + (size_t)row * 128;
                 const float* t0 = tab + (lane >> 1) * 2;
                 const float* t1 = tab + ((lane + 64) >> 1) * 2;
-                cs[j][0] = COH ? coh_ldf(t0) : t0[0];
-                cs[j][1] = COH ? coh_ldf(t0 + 1) : t0[1];
-                cs[j][2] = COH ? coh_ldf(t1) : t1[0];
-                cs[j][3] = COH ? coh_ldf(t1 + 1) : t1[1];
+                if (COH) {
+                    cs[j][0] = coh_ldf(t0);
+                    cs[j][1] = coh_ldf(t0 + 1);
+                    cs[j][2] = coh_ldf(t1);
+                    cs[j][3] = coh_ldf(t1 + 1);
+                } else {
+                    const float2 c0 = *(const float2*)t0, c1 = *(const float2*)t1;
+                    cs[j][0] = c0.x;
+                    cs[j][1] = c0.y;
+                    cs[j][2] = c1.x;
+                    cs[j][3] = c1.y;
+                }
                 if (!isq) { /* the v head rides along */
                     x0[j] = COH ? coh_ld16(src + 8 * AT_HD + lane) : src[8 * AT_HD + lane];
                     x1[j] = COH ? coh_ld16(src + 8 * AT_HD + lane + 64) : src[8 * AT_HD + lane + 64];
@@ -296,8 +305,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 const int it = base + j * W;
                 if (it >= nit) break;
                 float o0, o1;
-                qkrope_math(v0[j], v1[j], w0[j], w1[j], cs[j][0], cs[j][1], cs[j][2], cs[j][3],
-                            a.eps, lane, &o0, &o1);
+                const bool isq = it < nq;
+                qkrope_math(v0[j], v1[j], isq ? qw0 : kw0, isq ? qw1 : kw1, cs[j][0], cs[j][1],
+                            cs[j][2], cs[j][3], a.eps, lane, &o0, &o1);
                 if (it < nq) {
                     LDS(uint16_t)* dq = s_q + it * AT_HD; /* q vector (rl, g) = it */
                     const uint16_t q0 = f2bf(o0), q1 = f2bf(o1);

@@ -56,6 +56,13 @@
 template <int WFMT, int MT, bool NOTR = false>
 __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void k_gemv3(GemvArgs a) {
     extern __shared__ __align__(16) unsigned char smem3[];
+    /* every argument in one round of scalar loads: left to itself the
+     * compiler issues them next to their first uses, three dependent
+     * kernarg round trips before the first weight load */
+    asm volatile("" ::"s"(a.w), "s"(a.s), "s"(a.x), "s"(a.y), "s"(a.norm_w), "s"(a.ssq_in),
+                 "s"(a.ssq_out), "s"(a.probe), "s"(a.ldx), "s"(a.ldy), "s"(a.M), "s"(a.N),
+                 "s"(a.K), "s"(a.gps), "s"(a.ks), "s"(a.rt), "s"(a.xmode), "s"(a.epi),
+                 "s"(a.ssq_in_blocks), "s"(a.norm_eps), "s"(gridDim.x));
     GvBuf b0, b1;
     gv3_block<WFMT, MT, false, false, false, NOTR>(a, blockIdx.x, gridDim.x,
                                                   (LDS(unsigned char)*)smem3, a.y, b0, b1);
