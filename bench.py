@@ -13,6 +13,10 @@ steps/s, plus `roofline` for the dominant kernel (the INT4 GEMV engine) timed
 with HIP events on its own stream, and `cpu_baseline` (the scalar C oracle on
 one host core over a bounded sample: one backbone layer + the head GEMV,
 extrapolated to 36 layers).
+
+`--workload config4|config5` runs the batch (8 sessions x K=4, M = 40) and tree
+(4 sessions x 16-node tree, M = 68, KV 8192) configurations the same way; their
+lines are reported beside the headline, which stays config 3.
 """
 import argparse
 import ctypes
@@ -37,10 +41,29 @@ def int4_bytes(N, Kd):
     return N * Kd // 2 + 2 * N * Kd // 32
 
 
-def step_alg_bytes():
+TREE16 = [-1, 0, 0, 1, 1, 2, 2, 3, 3, 4, 5, 6, 6, 7, 8, 10, 11]
+# sessions, per-session parent array, KV lengths, cache capacity
+WORKLOADS = {
+    "config3": dict(parent=[-1, 0, 1, 2, 3], lens=[CTX],
+                    desc="config3: 36L INT4-g32 backbone + INT4 head 2560->155776, K=4 chain "
+                         "(M=5), b=1, bf16 KV 2048, device acceptance T0.8 p0.8"),
+    "config4": dict(parent=[-1, 0, 1, 2, 3],
+                    lens=[int(v) for v in np.random.default_rng(4).integers(256, 4097, 8)],
+                    desc="config4: 8 sessions x K=4 chain (M=40), 36L INT4-g32 + INT4 head, "
+                         "KV lengths ~ U[256, 4096] (seed 4), per-session acceptance"),
+    "config5": dict(parent=TREE16, lens=[8192] * 4,
+                    desc="config5: 4 sessions x 16-node draft tree (M=68), 36L INT4-g32 + INT4 "
+                         "head, KV 8192, tree acceptance"),
+}
+
+
+def step_alg_bytes(lens=(CTX,), rows=K + 1):
+    """Weights and scales once, each cached KV token once (4,096 B per layer),
+    activations and logits per row (3,887,360 B: 17,879,040 + 1,557,760 at
+    M = 5)."""
     w = N_LAYERS * sum(int4_bytes(n, k) for n, k in W_LAYER) + int4_bytes(155776, 2560)
-    kv = N_LAYERS * 2 * 8 * 128 * 2 * CTX
-    act = 17_879_040 + 1_557_760
+    kv = N_LAYERS * 2 * 8 * 128 * 2 * sum(lens)
+    act = rows * 3_887_360
     return w, kv, w + kv + act
 
 
@@ -100,6 +123,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS),
+                    help="config3 (the headline metric) or the batch / tree configs 4, 5")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy (3 launches): the reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -127,21 +152,29 @@ def main():
     torch.cuda.synchronize()
     with torch.cuda.stream(side):
         S = s2pamd.stream_ptr()
+        wl = WORKLOADS[args.workload]
+        parent = np.array(wl["parent"], np.int32)
+        lens = wl["lens"]
+        NS, R = len(lens), len(parent)
+        M = NS * R
+        ctx = max(lens) + 64
         opts = s2pamd.BackboneOpts(N_LAYERS, s2pamd.WQ_INT4, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB,
-                                   16, 1, CTX + 64)
+                                   max(16, M), NS, ctx)
         bb = ctypes.c_void_p()
         s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(opts), 2026, S, ctypes.byref(bb)))
-        kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
-        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0, 5, S))
-        parent = np.array([-1, 0, 1, 2, 3], np.int32)
-        R = K + 1
-        kvp = (ctypes.c_void_p * 1)(kv.data_ptr())
-        ln = np.array([CTX], np.int32)
-        vb = s2pamd.VerifyBatch(1, R, parent.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
+        kvs = []
+        for s_ in range(NS):
+            kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
+            s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0,
+                                                       5 + s_, S))
+            kvs.append(kv)
+        kvp = (ctypes.c_void_p * NS)(*[k.data_ptr() for k in kvs])
+        ln = np.array(lens, np.int32)
+        vb = s2pamd.VerifyBatch(NS, R, parent.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
         s2pamd.check(lib.s2p_verify_plan(bb, ctypes.byref(vb), S))
-        x = torch.empty((R, 2560), dtype=torch.int16, device=dev)
+        x = torch.empty((M, 2560), dtype=torch.int16, device=dev)
         s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(x), x.numel(), 0.0, 1.0, 9, S))
-        logits = torch.empty((R, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
+        logits = torch.empty((M, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
         s2pamd.check(lib.s2p_verify_forward(bb, s2pamd.dptr(x), s2pamd.dptr(logits), S))
         # draft logits: target + N(0, 0.5); drafted ids by the device sampler
         noise = torch.empty_like(logits)
@@ -149,25 +182,33 @@ def main():
                                                    13, S))
         drf = (logits.view(torch.bfloat16).float() + noise.view(torch.bfloat16).float()).to(
             torch.bfloat16).view(torch.int16)
-        st = StateBytes.make(0.8, 0.8, 1.1, 16, seed=0, entropy=0)
-        d_state = torch.from_numpy(np.frombuffer(bytes(st), np.uint8).copy()).to(dev)
-        d_sptr = torch.tensor([d_state.data_ptr()], dtype=torch.int64, device=dev)
-        d_draft_state = d_state.clone()
-        d_dptr = torch.tensor([d_draft_state.data_ptr()], dtype=torch.int64, device=dev)
-        tok = torch.zeros(R, dtype=torch.int64, device=dev)
+        # per-session sampler states (seeds differ); drafted ids: the device
+        # sampler on each node's parent draft row
+        d_states, d_drafts = [], []
+        for s_ in range(NS):
+            st = StateBytes.make(0.8, 0.8, 1.1, 16, seed=s_, entropy=s_)
+            d_states.append(torch.from_numpy(np.frombuffer(bytes(st), np.uint8).copy()).to(dev))
+            d_drafts.append(d_states[-1].clone())
+        d_sptr = torch.tensor([t.data_ptr() for t in d_states], dtype=torch.int64, device=dev)
+        tok = torch.zeros(M, dtype=torch.int64, device=dev)
         sem = torch.zeros(1, dtype=torch.int32, device=dev)
         eos = torch.zeros(1, dtype=torch.uint8, device=dev)
-        for i in range(K):
-            s2pamd.hip_check(lib.s2pk_sample(s2pamd.dptr(drf[i]), s2pamd.S2P_VOCAB, None,
-                                             s2pamd.dptr(d_dptr), 1,
-                                             ctypes.c_void_p(tok.data_ptr() + 8 * (i + 1)),
-                                             s2pamd.dptr(sem), None, s2pamd.dptr(eos), S))
+        for s_ in range(NS):
+            d_dptr = torch.tensor([d_drafts[s_].data_ptr()], dtype=torch.int64, device=dev)
+            for i in range(1, R):
+                s2pamd.hip_check(lib.s2pk_sample(s2pamd.dptr(drf[s_ * R + int(parent[i])]),
+                                                 s2pamd.S2P_VOCAB, None, s2pamd.dptr(d_dptr), 1,
+                                                 ctypes.c_void_p(tok.data_ptr() +
+                                                                 8 * (s_ * R + i)),
+                                                 s2pamd.dptr(sem), None, s2pamd.dptr(eos), S))
+            side.synchronize()
         d_parent = torch.from_numpy(parent).to(dev)
-        work = torch.empty(lib.s2p_verify_accept_work_bytes(1, R), dtype=torch.uint8, device=dev)
-        path = torch.zeros(R, dtype=torch.int32, device=dev)
-        nacc = torch.zeros(1, dtype=torch.int32, device=dev)
-        emit = torch.zeros(R + 1, dtype=torch.int64, device=dev)
-        nemit = torch.zeros(1, dtype=torch.int32, device=dev)
+        work = torch.empty(lib.s2p_verify_accept_work_bytes(NS, R), dtype=torch.uint8,
+                           device=dev)
+        path = torch.zeros(M, dtype=torch.int32, device=dev)
+        nacc = torch.zeros(NS, dtype=torch.int32, device=dev)
+        emit = torch.zeros(NS * (R + 1), dtype=torch.int64, device=dev)
+        nemit = torch.zeros(NS, dtype=torch.int32, device=dev)
         io = s2pamd.StepIO(x.data_ptr(), logits.data_ptr(), drf.data_ptr(), s2pamd.S2P_VOCAB,
                            d_parent.data_ptr(), tok.data_ptr(), d_sptr.data_ptr(), path.data_ptr(),
                            nacc.data_ptr(), emit.data_ptr(), nemit.data_ptr(), work.data_ptr())
@@ -189,21 +230,21 @@ def main():
         ms = e0.elapsed_time(e1) / args.steps
 
         # dominant kernel: the GEMV engine, every weight GEMV of one step
-        # (36 x {wqkv, wo, gate_up, w2} + head at M = 5), replayed as one graph on
+        # (36 x {wqkv, wo, gate_up, w2} + head at the step's M), replayed as one graph on
         # this stream and bracketed by HIP events
         lins = []
         for l in range(N_LAYERS):
             L = lib.s2p_backbone_layer(bb, l).contents
             lins += [L.wqkv, L.wo, L.gate_up, L.w2]
         lins.append(lib.s2p_backbone_head(bb).contents)
-        ybuf = torch.empty((R, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
-        xbuf = torch.empty((R, 9728), dtype=torch.int16, device=dev)
+        ybuf = torch.empty((M, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
+        xbuf = torch.empty((M, 9728), dtype=torch.int16, device=dev)
         s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(xbuf), xbuf.numel(), 0.0, 1.0, 3, S))
 
         def gemvs():
             for lin in lins:
                 s2pamd.check(lib.s2p_linear_forward(ctypes.byref(lin), s2pamd.dptr(xbuf),
-                                                    s2pamd.dptr(ybuf), R, 2, S), "gemv")
+                                                    s2pamd.dptr(ybuf), M, 2, S), "gemv")
         gemvs()
         side.synchronize()
         # the 145 launches captured once and replayed: the events then time
@@ -224,15 +265,16 @@ def main():
         n_launch = reps * len(lins)
         avg_launch_s = g0.elapsed_time(g1) / 1e3 / n_launch
         wbytes = sum(lin.w_pack.bytes + lin.w_iscale.bytes for lin in lins)
-        abytes = sum(2 * R * (lin.in_features + lin.out_features) for lin in lins)
+        abytes = sum(2 * M * (lin.in_features + lin.out_features) for lin in lins)
         per_launch = (wbytes + abytes) / len(lins)
         gemv_gbs = per_launch / avg_launch_s / 1e9
         lib.s2p_backbone_free(bb)
 
-    w, kvb, alg = step_alg_bytes()
+    w, kvb, alg = step_alg_bytes(lens, M)
     step_gbs = alg / (ms / 1e3) / 1e9
+    headline = args.workload == "config3"
     out = {
-        "metric": METRIC,
+        "metric": METRIC if headline else f"verify steps/s ({args.workload}, 36L INT4)",
         "value": round(1e3 / ms, 3),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -244,22 +286,23 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init INT4-g32 weights, N(0,1) KV cache and inputs)",
-        "config": {"workload": "config3: 36L INT4-g32 backbone + INT4 head 2560->155776, "
-                               "K=4 chain (M=5), b=1, bf16 KV 2048, device acceptance T0.8 p0.8",
-                   "global_batch": 1, "seq_len": CTX, "parallelism": "single GPU"},
+        "config": {"workload": wl["desc"], "global_batch": NS, "seq_len": max(lens),
+                   "parallelism": "single GPU"},
         "step_alg_bytes": alg,
         "step_hbm_gbs": round(step_gbs, 1),
         "step_frac_of_peak": round(step_gbs / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
-                     "traffic": measured_traffic(),
-                     "traffic_source": "profiles/gemv_int4_config3_traffic.md",
-                     "kernel": "k_gemv3<INT4, MT=1> (all 145 weight GEMVs of a step)",
+                     "traffic": measured_traffic() if headline else None,
+                     "traffic_source": "profiles/gemv_int4_config3_traffic.md" if headline
+                     else None,
+                     "kernel": f"k_gemv3<INT4, MT={(M + 15) // 16}> (all 145 weight GEMVs of "
+                               f"a step)",
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "alg_bytes_per_launch": int(per_launch)},
     }
-    if not args.no_cpu:
+    if headline and not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
 

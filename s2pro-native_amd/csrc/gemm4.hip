@@ -1,0 +1,305 @@
+/* s2pro MI355X — INT4-g32 weight GEMM for the batched / tree verify rows
+ * (16 < M <= 96: configs 4 and 5 of the verify path).
+ *
+ * Replaces the reference's M > 16 path (dequant + cuBLAS, gemm.c:467-490, or
+ * the WMMA kernel int8_gemv.cu:535-618) for packed INT4 weights.
+ *
+ * The whole-K GEMV engine stages all M x K activations of a workgroup in LDS,
+ * which stops fitting past M ~ 16 (M = 68 x K = 2560 is 348 KB).  Here the
+ * waves of a workgroup split ROWS, not K, and share one activation window:
+ *   - a workgroup of 4 waves owns 4 row tiles of 16 (SWIGLU: 2 gate tiles and
+ *     the 2 matching up tiles), every wave one tile, over the whole of K;
+ *   - K advances in windows of 16 groups (512 k): the workgroup stages the
+ *     window's M x 512 activations in LDS (RMSNorm with the rule's roundings,
+ *     the INT4 k-slot order and the group sums of the bias correction, as the
+ *     GEMV staging does), then every wave multiplies its tile's 16-group chunk
+ *     of weights against it (MT = ceil(M / 16) MFMA column tiles, the GEMV
+ *     engine's untransposed INT4 tile), accumulating over the windows;
+ *   - the next chunk's weights are in flight while a window is staged and
+ *     multiplied; two workgroups per CU overlap one's staging with the other's
+ *     multiply.
+ * Per group the dequantisation (9 VALU per 8 weights) is shared by the MT
+ * column tiles, so at M = 68 the MFMA work, not the weight stream, sets the
+ * pace.  Accumulation order per output is fixed (window by window, group by
+ * group): deterministic.  The epilogues are the GEMV engine's: bf16 store,
+ * residual add with per-16-column sums of squares, SwiGLU. */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemv_dev.h"
+
+#define G4_WAVES 4
+#define G4_WIN 16 /* groups per window = one weight chunk (GV_CHG_INT4) */
+#define G4_MAX_M 96
+
+static __host__ __device__ size_t g4_xs() { return (size_t)G4_WIN * 32 + GV_XPAD; }
+static __host__ __device__ size_t g4_xg() { return (size_t)gv_round32(G4_WIN) + 8; }
+/* x [M][xs] bf16 | X3 [M][3][xg] bf16 | scale staging [waves][16][16] f32 |
+ * inverse RMS [GEMV_MAX_M] f32 */
+static __host__ __device__ size_t g4_lds_bytes(int M) {
+    const size_t x = ((size_t)M * g4_xs() * 2 + 15) & ~(size_t)15;
+    const size_t x3 = ((size_t)M * 3 * g4_xg() * 2 + 15) & ~(size_t)15;
+    return x + x3 + G4_WAVES * 1024 + GEMV_MAX_M * 4 + 16;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_gemm4(GemvArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) unsigned char smem4[];
+    LDS(unsigned char)* smem = (LDS(unsigned char)*)smem4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, r = lane & 15;
+    const int M = a.M, G = a.K >> 5;
+    const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
+    const int F = a.N >> 1;
+
+    /* this wave's tile: rows wbase .. wbase + 15 of W */
+    int tile, wbase, tiles;
+    if (swiglu) {
+        tiles = F >> 4;
+        tile = blockIdx.x * 2 + (wave & 1);
+        wbase = (wave < 2 ? 0 : F) + tile * 16;
+    } else {
+        tiles = (a.N + 15) >> 4;
+        tile = blockIdx.x * G4_WAVES + wave;
+        wbase = tile * 16;
+    }
+    const bool active = tile < tiles; /* uniform; idle waves still stage */
+    const int nrow = min(wbase + r, a.N - 1);
+
+    GvLds L;
+    L.xs = (int)g4_xs();
+    L.xg = (int)g4_xg();
+    L.x = (LDS(uint16_t)*)smem;
+    size_t off = ((size_t)M * L.xs * 2 + 15) & ~(size_t)15;
+    L.X3 = (LDS(uint16_t)*)(smem + off);
+    off += ((size_t)M * 3 * L.xg * 2 + 15) & ~(size_t)15;
+    L.sc = (LDS(float)*)(smem + off + (size_t)wave * 1024);
+    off += G4_WAVES * 1024;
+    L.inv = (LDS(float)*)(smem + off);
+    off += GEMV_MAX_M * 4;
+    L.xtot = nullptr;
+    L.flag = (LDS(int)*)(smem + off);
+
+    GvBuf b0, b1;
+    const int nch_all = (G + G4_WIN - 1) / G4_WIN;
+    /* K split sp of a.splits: chunks [c0, c0 + nch) (a.win chunks a split) */
+    const int sp = blockIdx.y;
+    const int c0 = sp * a.win;
+    const int nch = min(a.win, nch_all - c0);
+    auto load_c = [&](GvBuf& B, int c) __attribute__((always_inline)) {
+        gv_load<GEMV_W_INT4, false>(B, a, nrow, c * G4_WIN, min(G4_WIN, G - c * G4_WIN), q);
+    };
+    load_c(b0, c0); /* in flight during the inverse RMS and the first staging */
+
+    if (a.xmode == GEMV_X_NORM) {
+        for (int m = wave; m < M; m += G4_WAVES) {
+            float s = 0.f;
+            for (int b = lane; b < a.ssq_in_blocks; b += 64) s += a.ssq_in[(size_t)b * GEMV_MAX_M + m];
+            s = wave_sum_down(s);
+            if (lane == 0) L.inv[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
+        }
+    }
+
+    /* window c of the activations into LDS: the raw rows go straight to
+     * their slots (16-byte direct-to-LDS loads, one per row and wave, all in
+     * flight together), then every lane transforms its 8-element block b =
+     * lane of the rows in place (RMSNorm, k-slot order, group sums: a group's
+     * 4 blocks sit in adjacent lanes) */
+    auto stage = [&](int c) __attribute__((always_inline)) {
+        const int gn = min(G4_WIN, G - c * G4_WIN);
+        const int nb = gn * 4;
+        const size_t k0 = (size_t)c * G4_WIN * 32;
+        __syncthreads(); /* the previous window is no longer read */
+        for (int m = wave; m < M; m += G4_WAVES)
+            if (lane < nb)
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(a.x + (size_t)m * a.ldx + k0 + lane * 8),
+                    (LDS(void)*)(L.x + m * L.xs), 16, 0, 0);
+        s2p_u32x4 wn4 = {0u, 0u, 0u, 0u};
+        if (a.xmode == GEMV_X_NORM && lane < nb) wn4 = *(const s2p_u32x4*)(a.norm_w + k0 + lane * 8);
+        if (gn < G4_WIN)
+            for (int i = tid; i < M * 3 * (G4_WIN - gn); i += 256) {
+                const int row = i / (G4_WIN - gn), g = gn + i % (G4_WIN - gn);
+                L.X3[row * L.xg + g] = 0;
+            }
+        vm_drain(); /* this wave's rows (and the weights issued before) landed */
+        __syncthreads();
+        for (int m = wave; m < M; m += G4_WAVES) {
+            const bool ok = lane < nb;
+            const s2p_u32x4 raw = ok ? *(const LDS(s2p_u32x4)*)(L.x + m * L.xs + lane * 8)
+                                     : (s2p_u32x4){0u, 0u, 0u, 0u};
+            gv_stage_one<GEMV_W_INT4>(a, L, m, lane, ok, raw, wn4);
+        }
+        __syncthreads();
+    };
+
+    s2p_f32x4 acc[MT], corr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        acc[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+        corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    auto mult = [&](const GvBuf& B, int c) __attribute__((always_inline)) {
+        gv_compute<GEMV_W_INT4, MT, false>(B, L, 0, min(G4_WIN, G - c * G4_WIN), M, 0, q, r, acc,
+                                           corr);
+    };
+    const int ce = c0 + nch;
+    for (int c = c0; c < ce; c += 2) {
+        stage(c);
+        if (c + 1 < ce) load_c(b1, c + 1);
+        mult(b0, c);
+        if (c + 1 >= ce) break;
+        stage(c + 1);
+        if (c + 2 < ce) load_c(b0, c + 2);
+        mult(b1, c + 1);
+    }
+
+    /* epilogue: element i of lane (q, r) in column tile t is
+     * (n, m) = (wbase + 4q + i, 16t + r) */
+    s2p_f32x4 v[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[t][i] = 16.0f * acc[t][i] - 24.0f * corr[t][i];
+    uint16_t* Y = a.y;
+    if (a.splits > 1) {
+        /* K-split handoff as in the GEMV engine's split-K path: this
+         * split's partial rows (the 64-row block layout: wave w holds rows
+         * 16w..16w+15, SWIGLU gate rows then up rows) written through to
+         * memory, arrival counted once the stores completed, and the last
+         * split to arrive sums the splits in order and runs the epilogue */
+        const int rb = blockIdx.x;
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int m = t * 16 + r;
+            if (m >= M) continue;
+            float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + wave * 16 + q * 4];
+            coh_st128(dst, __builtin_bit_cast(s2p_u32x4, v[t]));
+        }
+        vm_drain();
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            *L.flag = prev == (unsigned)(a.splits - 1);
+        }
+        __syncthreads();
+        if (*L.flag) {
+            gv_fixup<GEMV_W_INT4, false>(a, rb, Y);
+            vm_drain();
+            if (tid == 0)
+                __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    if (swiglu) {
+        __syncthreads(); /* the last window is no longer read: reuse x for the up tiles */
+        LDS(s2p_f32x4)* ex = (LDS(s2p_f32x4)*)smem;
+        if (wave >= 2) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) ex[((wave - 2) * MT + t) * 64 + lane] = v[t];
+        }
+        __syncthreads();
+        if (wave < 2 && active) {
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const s2p_f32x4 u = ex[(wave * MT + t) * 64 + lane];
+                const int m = t * 16 + r;
+                if (m >= M) continue;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = tile * 16 + 4 * q + i;
+                    Y[(size_t)m * a.ldy + n] = silu_mul_bf16(f2bf(v[t][i]), f2bf(u[i]));
+                }
+            }
+        }
+        return;
+    }
+    if (!active) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int m = t * 16 + r;
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = wbase + 4 * q + i;
+            if (m >= M || n >= a.N) continue;
+            const uint16_t yb = f2bf(v[t][i]);
+            uint16_t* yp = Y + (size_t)m * a.ldy + n;
+            if (a.epi == GEMV_EPI_RESID) {
+                const uint16_t xo = f2bf(__fadd_rn(bf2f(*yp), bf2f(yb)));
+                *yp = xo;
+                const float xv = bf2f(xo);
+                sq += xv * xv;
+            } else {
+                *yp = yb;
+            }
+        }
+        if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+            /* the tile's 16 rows of column m: 4 per lane, then across q */
+            sq += __shfl_xor(sq, 16, 64);
+            sq += __shfl_xor(sq, 32, 64);
+            if (q == 0 && m < M) coh_stf(a.ssq_out + (size_t)tile * GEMV_MAX_M + m, sq);
+        }
+    }
+}
+
+template <int MT>
+static hipError_t g4_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)k_gemm4<MT>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((k_gemm4<MT>), grid, dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+/* INT4 weights, 16 < M <= 96, any epilogue; hipErrorNotSupported otherwise
+ * (the caller falls back to the split-K GEMV engine). */
+extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
+    const GemvArgs& a = *ap;
+    if (a.wfmt != GEMV_W_INT4 || a.M <= 16 || a.M > G4_MAX_M || (a.K & 127) || a.N <= 0)
+        return hipErrorNotSupported;
+    if (a.epi == GEMV_EPI_SWIGLU && ((a.N & 1) || ((a.N >> 1) & 31))) return hipErrorInvalidValue;
+    if (a.xmode == GEMV_X_NORM && (!a.norm_w || !a.ssq_in || a.ssq_in_blocks <= 0))
+        return hipErrorInvalidValue;
+    const size_t lds = g4_lds_bytes(a.M);
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    GemvArgs b = a;
+    const unsigned nblk = a.epi == GEMV_EPI_SWIGLU
+                              ? (unsigned)(((a.N >> 1) / 16 + 1) / 2)
+                              : (unsigned)(((a.N + 15) / 16 + G4_WAVES - 1) / G4_WAVES);
+    /* too few row blocks to fill the chip: split K over about 2 workgroups
+     * per CU (needs the caller's split-K scratch: partials and counters) */
+    const int nch = ((a.K >> 5) + G4_WIN - 1) / G4_WIN;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    int ks = (int)((2u * (unsigned)cus + nblk - 1) / nblk);
+    if (ks > nch) ks = nch;
+    if (ks < 1) ks = 1;
+    int cps = (nch + ks - 1) / ks;
+    ks = (nch + cps - 1) / cps;
+    b.nrb = (int)nblk;
+    if (ks > 1 && (!a.part || !a.counters || (int)nblk > GV_COUNTERS ||
+                   (int64_t)ks * a.M * nblk * 64 > a.part_cap)) {
+        ks = 1;
+        cps = nch;
+    }
+    b.splits = ks;
+    b.win = cps;
+    const dim3 grid(nblk, (unsigned)ks);
+    switch ((a.M + 15) / 16) {
+        case 2: return g4_launch_mt<2>(b, grid, lds, st);
+        case 3: return g4_launch_mt<3>(b, grid, lds, st);
+        case 4: return g4_launch_mt<4>(b, grid, lds, st);
+        case 5: return g4_launch_mt<5>(b, grid, lds, st);
+        default: return g4_launch_mt<6>(b, grid, lds, st);
+    }
+}

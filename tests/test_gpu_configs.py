@@ -10,9 +10,10 @@ column tiles), KV context 8192, acceptance along the longest accepted root
 path with residual resampling.
 
 Logits follow the tolerance of test_gpu_verify (north star: 1e-2 relative
-to the oracle's reference-order forward, no less accurate than it against
-binary64); acceptance decisions, emitted ids and sampler states are
-bit-exact against the host rule applied to the logits the GPU produced."""
+to the oracle's reference-order forward per row; over all sessions' rows no
+less accurate than it against binary64); acceptance decisions, emitted ids
+and sampler states are bit-exact against the host rule applied to the logits
+the GPU produced."""
 import numpy as np
 import pytest
 
@@ -21,8 +22,8 @@ import pyoracle as po
 import s2pamd
 from gpu_util import P, S, bf16_bits, bf16_vals, empty, to_dev, to_host
 from test_gpu_sample import draft_tokens, run_accept
-from test_gpu_verify import (TREE16, check_logits, f64_weights, make_backbone, new_kv,
-                             oracle_forward, plan)
+from test_gpu_verify import (TREE16, check_logits, check_rms, f64_weights, make_backbone,
+                             new_kv, oracle_forward, plan)
 
 pytestmark = pytest.mark.gpu
 
@@ -54,13 +55,19 @@ def run_config(lib, parent, lens, ctx, seed):
         got_bits = to_host(logits, np.uint16)
         got = bf16_vals(got_bits)
         W, fn, head = f64_weights(lib, bb, N_LAYERS)
+        wants, truths = [], []
         for s in range(n):
             rows = slice(s * R, (s + 1) * R)
             want, _ = oracle_forward(lib, bb, N_LAYERS, x[rows], hosts[s], ctx, int(lens[s]),
                                      parent, head_rows)
             truth = f64.forward(W, fn, head, x[rows],
                                 hosts[s].reshape(N_LAYERS, 16, ctx, 128), int(lens[s]), parent)
-            check_logits(got[rows], want, truth, f"session {s} (L={lens[s]})")
+            check_logits(got[rows], want, truth, f"session {s} (L={lens[s]})", rms=False)
+            wants.append(bf16_vals(want))
+            truths.append(truth)
+        # the accuracy criterion over all sessions' rows (5 rows alone are too
+        # few for an rms comparison of two rounding orders)
+        check_rms(got, np.concatenate(wants), np.concatenate(truths), "all sessions")
     finally:
         lib.s2p_backbone_free(bb)
 

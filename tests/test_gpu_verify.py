@@ -130,7 +130,10 @@ def f64_weights(lib, bb, n_layers):
     return layers, fnorm, f64.dequant(w, s, hl.out_features, hl.in_features)
 
 
-def check_logits(got, want_bits, truth, what):
+def check_logits(got, want_bits, truth, what, rms=True):
+    """Per-row tolerance against the oracle and (rms=True) the accuracy
+    criterion over these rows; callers pooling several sessions pass
+    rms=False and apply check_rms to all rows at once."""
     want = bf16_vals(want_bits)
     tn = np.linalg.norm(truth, axis=1)
     rows = [f"{r}: gpu {np.linalg.norm(got[r] - truth[r]) / tn[r]:.2e} "
@@ -139,6 +142,13 @@ def check_logits(got, want_bits, truth, what):
     print(what, "per-row L2 rel err vs binary64:\n  " + "\n  ".join(rows))
     e_ref_row = np.linalg.norm(want - truth, axis=1) / tn
     assert_close_norm(got, want, rel=np.maximum(1e-2, 0.5 * e_ref_row), what=what)
+    if rms:
+        check_rms(got, want, truth, what)
+
+
+def check_rms(got, want, truth, what):
+    """Over all rows the GPU is no less accurate than the reference order:
+    rms error against binary64 at most 1.25x the oracle's."""
     e_gpu = np.sqrt(np.mean((got - truth) ** 2))
     e_ref = np.sqrt(np.mean((want - truth) ** 2))
     assert e_gpu <= 1.25 * e_ref, f"{what}: GPU rms err {e_gpu:.4g} vs oracle {e_ref:.4g}"
