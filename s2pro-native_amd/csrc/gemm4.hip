@@ -1,5 +1,5 @@
 /* s2pro MI355X — INT4-g32 weight GEMM for the batched / tree verify rows
- * (16 < M <= 96: configs 4 and 5 of the verify path).
+ * (16 < M <= 80: configs 4 and 5 of the verify path).
  *
  * Replaces the reference's M > 16 path (dequant + cuBLAS, gemm.c:467-490, or
  * the WMMA kernel int8_gemv.cu:535-618) for packed INT4 weights.
@@ -7,8 +7,8 @@
  * The whole-K GEMV engine stages all M x K activations of a workgroup in LDS,
  * which stops fitting past M ~ 16 (M = 68 x K = 2560 is 348 KB).  Here the
  * waves of a workgroup split ROWS, not K, and share one activation window:
- *   - a workgroup of 4 waves owns 4 row tiles of 16 (SWIGLU: 2 gate tiles and
- *     the 2 matching up tiles), every wave one tile, over the whole of K;
+ *   - a workgroup of 8 waves owns 8 row tiles of 16 (SWIGLU: 4 gate tiles and
+ *     the 4 matching up tiles), every wave one tile, over the whole of K;
  *   - K advances in windows of 16 groups (512 k): the workgroup stages the
  *     window's M x 512 activations in LDS (RMSNorm with the rule's roundings,
  *     the INT4 k-slot order and the group sums of the bias correction, as the
@@ -16,8 +16,10 @@
  *     of weights against it (MT = ceil(M / 16) MFMA column tiles, the GEMV
  *     engine's untransposed INT4 tile), accumulating over the windows;
  *   - the next chunk's weights are in flight while a window is staged and
- *     multiplied; two workgroups per CU overlap one's staging with the other's
- *     multiply.
+ *     multiplied; two waves per SIMD hide each other's latencies;
+ *   - when the row blocks are too few to fill the chip, K is split over
+ *     workgroups and the last split to arrive at a 64-row block sums the
+ *     splits in order and runs the epilogue (the GEMV engine's handoff).
  * Per group the dequantisation (9 VALU per 8 weights) is shared by the MT
  * column tiles, so at M = 68 the MFMA work, not the weight stream, sets the
  * pace.  Accumulation order per output is fixed (window by window, group by
@@ -28,9 +30,12 @@
 
 #include "gemv_dev.h"
 
-#define G4_WAVES 4
+#define G4_WAVES 8
 #define G4_WIN 16 /* groups per window = one weight chunk (GV_CHG_INT4) */
-#define G4_MAX_M 96
+/* M <= 80 (five column tiles).  At six tiles (M = 81..96) rows 76-79 came out
+ * wrong now and then in the GPU tests (not deterministic); that shape is left
+ * to the split-K GEMV engine until the cause is found. */
+#define G4_MAX_M 80
 
 static __host__ __device__ size_t g4_xs() { return (size_t)G4_WIN * 32 + GV_XPAD; }
 static __host__ __device__ size_t g4_xg() { return (size_t)gv_round32(G4_WIN) + 8; }
@@ -43,7 +48,7 @@ static __host__ __device__ size_t g4_lds_bytes(int M) {
 }
 
 template <int MT>
-__global__ __launch_bounds__(256) void k_gemm4(GemvArgs a) {
+__global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) unsigned char smem4[];
     LDS(unsigned char)* smem = (LDS(unsigned char)*)smem4;
@@ -58,8 +63,8 @@ __global__ __launch_bounds__(256) void k_gemm4(GemvArgs a) {
     int tile, wbase, tiles;
     if (swiglu) {
         tiles = F >> 4;
-        tile = blockIdx.x * 2 + (wave & 1);
-        wbase = (wave < 2 ? 0 : F) + tile * 16;
+        tile = blockIdx.x * 4 + (wave & 3);
+        wbase = (wave < 4 ? 0 : F) + tile * 16;
     } else {
         tiles = (a.N + 15) >> 4;
         tile = blockIdx.x * G4_WAVES + wave;
@@ -120,7 +125,7 @@ __global__ __launch_bounds__(256) void k_gemm4(GemvArgs a) {
         s2p_u32x4 wn4 = {0u, 0u, 0u, 0u};
         if (a.xmode == GEMV_X_NORM && lane < nb) wn4 = *(const s2p_u32x4*)(a.norm_w + k0 + lane * 8);
         if (gn < G4_WIN)
-            for (int i = tid; i < M * 3 * (G4_WIN - gn); i += 256) {
+            for (int i = tid; i < M * 3 * (G4_WIN - gn); i += 64 * G4_WAVES) {
                 const int row = i / (G4_WIN - gn), g = gn + i % (G4_WIN - gn);
                 L.X3[row * L.xg + g] = 0;
             }
@@ -170,39 +175,47 @@ __global__ __launch_bounds__(256) void k_gemm4(GemvArgs a) {
          * 16w..16w+15, SWIGLU gate rows then up rows) written through to
          * memory, arrival counted once the stores completed, and the last
          * split to arrive sums the splits in order and runs the epilogue */
-        const int rb = blockIdx.x;
+        /* the workgroup's 128 rows are two 64-row fixup blocks: block h
+         * holds tiles 4h..4h+3, or (SWIGLU) gate tiles 2h, 2h+1 then the
+         * matching up tiles */
+        const int h = swiglu ? (wave & 3) >> 1 : wave >> 2;
+        const int row = swiglu ? (wave >= 4 ? 32 : 0) + (wave & 1) * 16 : (wave & 3) * 16;
+        const int rb = blockIdx.x * 2 + h;
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const int m = t * 16 + r;
-            if (m >= M) continue;
-            float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + wave * 16 + q * 4];
+            if (m >= M || rb >= a.nrb) continue;
+            float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + row + q * 4];
             coh_st128(dst, __builtin_bit_cast(s2p_u32x4, v[t]));
         }
         vm_drain();
         __syncthreads();
         if (tid == 0) {
-            const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned prev = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1u,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *L.flag = prev == (unsigned)(a.splits - 1);
         }
         __syncthreads();
         if (*L.flag) {
-            gv_fixup<GEMV_W_INT4, false>(a, rb, Y);
+            /* threads 0..255 take block 2x, 256..511 block 2x + 1 */
+            const int fb = blockIdx.x * 2 + (tid >> 8);
+            if (fb < a.nrb) gv_fixup<GEMV_W_INT4, false>(a, fb, Y, tid & 255);
             vm_drain();
             if (tid == 0)
-                __hip_atomic_store(&a.counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
     if (swiglu) {
         __syncthreads(); /* the last window is no longer read: reuse x for the up tiles */
         LDS(s2p_f32x4)* ex = (LDS(s2p_f32x4)*)smem;
-        if (wave >= 2) {
+        if (wave >= 4) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) ex[((wave - 2) * MT + t) * 64 + lane] = v[t];
+            for (int t = 0; t < MT; t++) ex[((wave - 4) * MT + t) * 64 + lane] = v[t];
         }
         __syncthreads();
-        if (wave < 2 && active) {
+        if (wave < 4 && active) {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
                 const s2p_f32x4 u = ex[(wave * MT + t) * 64 + lane];
@@ -254,11 +267,11 @@ static hipError_t g4_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStre
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_gemm4<MT>), grid, dim3(256), lds, st, a);
+    hipLaunchKernelGGL((k_gemm4<MT>), grid, dim3(64 * G4_WAVES), lds, st, a);
     return hipGetLastError();
 }
 
-/* INT4 weights, 16 < M <= 96, any epilogue; hipErrorNotSupported otherwise
+/* INT4 weights, 16 < M <= 80, any epilogue; hipErrorNotSupported otherwise
  * (the caller falls back to the split-K GEMV engine). */
 extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const GemvArgs& a = *ap;
@@ -270,10 +283,13 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const size_t lds = g4_lds_bytes(a.M);
     if (lds > 160 * 1024) return hipErrorNotSupported;
     GemvArgs b = a;
+    /* workgroups of 8 row tiles (SWIGLU: 4 gate + 4 up tiles) */
     const unsigned nblk = a.epi == GEMV_EPI_SWIGLU
-                              ? (unsigned)(((a.N >> 1) / 16 + 1) / 2)
+                              ? (unsigned)(((a.N >> 1) / 16 + 3) / 4)
                               : (unsigned)(((a.N + 15) / 16 + G4_WAVES - 1) / G4_WAVES);
-    /* too few row blocks to fill the chip: split K over about 2 workgroups
+    /* 64-row fixup blocks of the split handoff (SWIGLU: 32 gate + 32 up) */
+    const int nrb = a.epi == GEMV_EPI_SWIGLU ? (a.N >> 1) / 32 : (a.N + 63) / 64;
+    /* too few row blocks to fill the chip: split K over about one workgroup
      * per CU (needs the caller's split-K scratch: partials and counters) */
     const int nch = ((a.K >> 5) + G4_WIN - 1) / G4_WIN;
     int cus = 256, dev = 0;
@@ -281,14 +297,14 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
         cus = 256;
-    int ks = (int)((2u * (unsigned)cus + nblk - 1) / nblk);
+    int ks = (int)(((unsigned)cus + nblk - 1) / nblk);
     if (ks > nch) ks = nch;
     if (ks < 1) ks = 1;
     int cps = (nch + ks - 1) / ks;
     ks = (nch + cps - 1) / cps;
-    b.nrb = (int)nblk;
+    b.nrb = nrb;
     if (ks > 1 && (!a.part || !a.counters || (int)nblk > GV_COUNTERS ||
-                   (int64_t)ks * a.M * nblk * 64 > a.part_cap)) {
+                   (int64_t)ks * a.M * nrb * 64 > a.part_cap)) {
         ks = 1;
         cps = nch;
     }
@@ -299,7 +315,6 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         case 2: return g4_launch_mt<2>(b, grid, lds, st);
         case 3: return g4_launch_mt<3>(b, grid, lds, st);
         case 4: return g4_launch_mt<4>(b, grid, lds, st);
-        case 5: return g4_launch_mt<5>(b, grid, lds, st);
-        default: return g4_launch_mt<6>(b, grid, lds, st);
+        default: return g4_launch_mt<5>(b, grid, lds, st);
     }
 }

@@ -391,7 +391,7 @@ extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
     GemvArgs a = *ap;
     dim3 grid;
     size_t lds = 0;
-    /* INT4 at 16 < M <= 96: the row-split GEMM with streamed activation
+    /* INT4 at 16 < M <= 80: the row-split GEMM with streamed activation
      * windows (gemm4.hip) */
     if (g_engine == 0 && a.gps == 0 && !g_v3_nw && a.wfmt == GEMV_W_INT4 && a.M > 16) {
         const hipError_t e4 = s2p_gemm4_launch(&a, st);

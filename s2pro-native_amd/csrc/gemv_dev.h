@@ -561,11 +561,12 @@ S2P_DEV float gv_sum_splits(const float* p, size_t stride, int S) {
     return s;
 }
 
-/* last arrival at row block rb: sum the splits and run the epilogue */
+/* last arrival at row block rb: sum the splits and run the epilogue (on
+ * 256 threads: thread tid of them) */
 template <int WFMT, bool COH>
-__device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y) {
+__device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y, int tid = threadIdx.x) {
 #pragma clang fp contract(off)
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int lane = tid & 63;
     const int M = a.M, S = a.splits;
     const size_t stride = (size_t)M * a.nrb * 64;
     const float* part = a.part;

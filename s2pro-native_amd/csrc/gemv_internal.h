@@ -49,7 +49,7 @@ typedef struct {
 } GemvArgs;
 
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
-/* INT4, 16 < M <= 96 (gemm4.hip); hipErrorNotSupported outside that range */
+/* INT4, 16 < M <= 80 (gemm4.hip); hipErrorNotSupported outside that range */
 hipError_t s2p_gemm4_launch(const GemvArgs* a, hipStream_t st);
 /* test hook: 0 = launcher's choice, 2 = split-K engine only */
 void s2p_gemv_set_engine(int engine);
