@@ -54,6 +54,37 @@ hipError_t s2pk_attention_decode(const s2p_bf16* q,
 /* scratch size (floats) required by s2pk_attention_decode */
 int64_t s2pk_attention_part_floats(int rows, int q_heads, int max_len);
 
+/* INT8 / INT4 KV cache (reference slowar_kernels.h:76-120, kernels.cu:510-946).
+ * Payload [kv_heads][max_seq][bw == 8 ? head_dim : head_dim / 2] bytes
+ * (bw 4: element 2b in the low nibble), scales f16 [kv_heads][max_seq]
+ * [head_dim / 32]; head_dim 128, bw 8 or 4.  Quantise-on-append: per
+ * 32-group scale f16(absmax / QMAX), values rint(x / scale) clamped to
+ * +-QMAX (127 or 7).  Scale pointers cross the ABI as void* (f16). */
+/* rows at positions pos..pos+rows-1 of one cache (kernels.cu:583-600) */
+hipError_t s2pk_kv_append8(const s2p_bf16* k, const s2p_bf16* v, int8_t* k_cache,
+                           int8_t* v_cache, void* k_scale, void* v_scale, int rows,
+                           int kv_heads, int head_dim, int pos, int max_seq, int bw,
+                           hipStream_t st);
+/* row r at position pos[r] of its own caches (kernels.cu:602-620) */
+hipError_t s2pk_kv_append8_ptrs(const s2p_bf16* k, const s2p_bf16* v,
+                                int8_t* const* k_caches, int8_t* const* v_caches,
+                                void* const* k_scales, void* const* v_scales, int rows,
+                                int kv_heads, int head_dim, const int32_t* pos, int max_seq,
+                                int bw, hipStream_t st);
+/* causal single pass over one quantised cache, rows at pos.. (kernels.cu:724-746) */
+hipError_t s2pk_attention8(const s2p_bf16* q, const int8_t* k_cache, const int8_t* v_cache,
+                           const void* k_scale, const void* v_scale, s2p_bf16* out, int rows,
+                           int q_heads, int kv_heads, int head_dim, int pos, int max_seq, int bw,
+                           hipStream_t st);
+/* split decode, row r attends its caches [0..pos[r]]; part holds
+ * s2pk_attention_part_floats(rows, q_heads, max_len) floats (kernels.cu:751-946) */
+hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* const* k_caches,
+                                  const int8_t* const* v_caches, const void* const* k_scales,
+                                  const void* const* v_scales, s2p_bf16* out, int rows,
+                                  int q_heads, int kv_heads, int head_dim, const int32_t* pos,
+                                  int max_seq, int max_len, float* part, int bw,
+                                  hipStream_t st);
+
 /* Per-session sampler state, device resident; byte layout of the reference
  * s2ps_dev_state (slowar_kernels.h:132-142). */
 typedef struct {

@@ -57,6 +57,9 @@ _SIGS = {
     "or_attention": (None, [P, P, P, P, I, I, I, I, I, P, I]),
     "or_attention_split": (None, [P, P, P, P, I, I, I, I, I, I]),
     "or_attention_f64": (None, [P, P, P, P, I, I, I, I, I, P, I]),
+    "or_kv_append8": (None, [P, P, P, P, P, P, I, I, I, P, I, I]),
+    "or_attention8": (None, [P, P, P, P, P, P, I, I, I, I, I, I]),
+    "or_attention8_f64": (None, [P, P, P, P, P, P, I, I, I, P, I, I]),
     "or_state_init": (None, [P, F, F, F, I, U64, U64]),
     "or_set_libm": (None, [I]),
     "or_transform": (I, [P, P, P, P, P, P]),
@@ -223,6 +226,34 @@ def attention_f64(q, kc, vc, rows, qh, kvh, hd, prefix, max_seq, vis=None):
     va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
     lib().or_attention_f64(ptr(q), ptr(kc), ptr(vc), ptr(out), rows, qh, kvh, hd, prefix,
                            ptr(va), max_seq)
+    return out
+
+
+# ------------------------------------------------------ INT8 / INT4 KV cache
+def _parr(arrs):
+    return (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+
+
+def kv_append8(k, v, kcs, vcs, kss, vss, rows, kvh, pos0, slots, max_seq, bw):
+    """In place on the host caches (lists of numpy arrays: int8 payloads,
+    uint16 f16 scales); slots None: rows at pos0.. of cache 0."""
+    sa = None if slots is None else np.ascontiguousarray(slots, np.int32)
+    lib().or_kv_append8(ptr(k), ptr(v), _parr(kcs), _parr(vcs), _parr(kss), _parr(vss), rows,
+                        kvh, pos0, ptr(sa), max_seq, bw)
+
+
+def attention8(q, kc, vc, ks, vs, rows, qh, kvh, pos0, max_seq, bw):
+    out = np.empty((rows, qh * 128), np.uint16)
+    lib().or_attention8(ptr(q), ptr(kc), ptr(vc), ptr(ks), ptr(vs), ptr(out), rows, qh, kvh,
+                        pos0, max_seq, bw)
+    return out
+
+
+def attention8_f64(q, kcs, vcs, kss, vss, rows, qh, kvh, pos, max_seq, bw):
+    out = np.empty((rows, qh * 128), np.float64)
+    pa = np.ascontiguousarray(pos, np.int32)
+    lib().or_attention8_f64(ptr(q), _parr(kcs), _parr(vcs), _parr(kss), _parr(vss), ptr(out),
+                            rows, qh, kvh, ptr(pa), max_seq, bw)
     return out
 
 

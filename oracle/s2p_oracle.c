@@ -621,6 +621,168 @@ void or_attention_f64(const uint16_t* q, const uint16_t* kc,
     free(s);
 }
 
+/* ---- INT8 / INT4 KV cache (kernels.cu:510-946) ---------------------------
+ * Cache: payload [kv_heads][max_seq][bw == 8 ? 128 : 64] bytes, scales f16
+ * [kv_heads][max_seq][4] (one per 32-element group). */
+
+/* k_kv_append8 (kernels.cu:516-581): per 32-group absmax / QMAX rounded
+ * through f16, values x / scale rounded to nearest even and clamped to
+ * +-QMAX (QMAX 127 for bw 8, 7 for bw 4; bw 4 packs element 2b in the low
+ * nibble).  slot_arr == NULL: row r goes to slot pos0 + r of one cache;
+ * else to slot slot_arr[r] of cache r (caches given as a pointer array). */
+void or_kv_append8(const uint16_t* k, const uint16_t* v, int8_t* const* kcs,
+                   int8_t* const* vcs, uint16_t* const* kss, uint16_t* const* vss,
+                   int rows, int kv_heads, int pos0, const int32_t* slot_arr,
+                   int max_seq, int bw) {
+    const int hd = 128, el = bw == 8 ? 128 : 64, qmax = bw == 8 ? 127 : 7;
+    for (int r = 0; r < rows; r++) {
+        const int c = slot_arr ? r : 0;
+        const int p = slot_arr ? slot_arr[r] : pos0 + r;
+        for (int h = 0; h < kv_heads; h++)
+            for (int kv = 0; kv < 2; kv++) {
+                const uint16_t* src = (kv ? v : k) + ((size_t)r * kv_heads + h) * hd;
+                int8_t* pay = (kv ? vcs : kcs)[c] + ((size_t)h * max_seq + p) * el;
+                uint16_t* sc = (kv ? vss : kss)[c] + ((size_t)h * max_seq + p) * 4;
+                for (int g = 0; g < 4; g++) {
+                    float a = 0.f;
+                    for (int e = 0; e < 32; e++) a = fmaxf(a, fabsf(or_bf2f(src[g * 32 + e])));
+                    const uint16_t hs = or_f2h(a / (float)qmax);
+                    const float s = or_h2f(hs);
+                    int qv[32];
+                    for (int e = 0; e < 32; e++) {
+                        int q = s > 0.f ? (int)rintf(or_bf2f(src[g * 32 + e]) / s) : 0;
+                        qv[e] = q < -qmax ? -qmax : (q > qmax ? qmax : q);
+                    }
+                    if (bw == 8) {
+                        for (int e = 0; e < 32; e++) pay[g * 32 + e] = (int8_t)qv[e];
+                    } else {
+                        for (int e = 0; e < 32; e += 2)
+                            pay[(g * 32 + e) / 2] = (int8_t)((qv[e] & 0xF) | ((qv[e + 1] & 0xF) << 4));
+                    }
+                    sc[g] = hs;
+                }
+            }
+    }
+}
+
+/* element e of a cached row.  bw 4: the two's complement nibble the append
+ * wrote (element 2b low).  The reference's decode expression
+ * (int8_t)((nib << 4) >> 4) (kernels.cu:675, 717, 845, 906) sign-extends
+ * only high nibbles: a negative low nibble reads back as 9..15.  The rule
+ * here, and the GPU kernels, decode both nibbles as written. */
+static float kv8_val(const int8_t* row, int e, int bw) {
+    if (bw == 8) return (float)row[e];
+    const uint8_t b = (uint8_t)row[e >> 1];
+    const int nib = (e & 1) ? (b >> 4) : (b & 0xF);
+    return (float)(nib >= 8 ? nib - 16 : nib);
+}
+
+/* k_attention8 (kernels.cu:614-722): causal single pass, row r attends
+ * slots 0..pos0+r; per 128-slot tile the scores are sum_g fma(pp_g, ks_g)
+ * with pp_g the in-order fma dot of the group, the tile max and sum are the
+ * 128-lane trees, and V is dequantised as (p * vs_g) * v.  The rule's
+ * s2p_expf replaces expf; l * corr + sum as one fma (nvcc contracts it). */
+void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                   const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
+                   int q_heads, int kv_heads, int pos0, int max_seq, int bw) {
+    const int hd = 128, el = bw == 8 ? 128 : 64, group = q_heads / kv_heads;
+    float sq[128], sp[128], red[128], acc[128];
+    for (int r = 0; r < rows; r++) {
+        const int len = pos0 + r + 1;
+        for (int h = 0; h < q_heads; h++) {
+            const int kvh = h / group;
+            const int8_t* kb = kc + (size_t)kvh * max_seq * el;
+            const int8_t* vb = vc + (size_t)kvh * max_seq * el;
+            const uint16_t* ksb = ks + (size_t)kvh * max_seq * 4;
+            const uint16_t* vsb = vs + (size_t)kvh * max_seq * 4;
+            for (int e = 0; e < hd; e++)
+                sq[e] = or_bf2f(q[((size_t)r * q_heads + h) * hd + e]) * ATTN_SCALE_128;
+            float m = -INFINITY, l = 0.f;
+            for (int d = 0; d < hd; d++) acc[d] = 0.f;
+            for (int t0 = 0; t0 < len; t0 += 128) {
+                float s[128];
+                for (int t = 0; t < 128; t++) {
+                    const int j = t0 + t;
+                    s[t] = -INFINITY;
+                    if (j < len) {
+                        float d = 0.f;
+                        for (int g = 0; g < 4; g++) {
+                            float pp = 0.f;
+                            for (int e = 0; e < 32; e++)
+                                pp = fmaf(sq[g * 32 + e], kv8_val(kb + (size_t)j * el, g * 32 + e, bw), pp);
+                            d = fmaf(pp, or_h2f(ksb[(size_t)j * 4 + g]), d);
+                        }
+                        s[t] = d;
+                    }
+                }
+                float tmax = -INFINITY;
+                for (int t = 0; t < 128; t++) tmax = fmaxf(tmax, s[t]);
+                const float m_new = fmaxf(m, tmax);
+                const float corr = (m == -INFINITY) ? 0.f : s2p_expf(m - m_new);
+                for (int t = 0; t < 128; t++) {
+                    sp[t] = (s[t] == -INFINITY) ? 0.f : s2p_expf(s[t] - m_new);
+                    red[t] = sp[t];
+                }
+                for (int off = 64; off > 0; off >>= 1)
+                    for (int t = 0; t < off; t++) red[t] += red[t + off];
+                l = fmaf(l, corr, red[0]);
+                const int lim = len - t0 < 128 ? len - t0 : 128;
+                for (int d = 0; d < hd; d++) {
+                    float a = acc[d] * corr;
+                    for (int j2 = 0; j2 < lim; j2++) {
+                        const size_t j = (size_t)(t0 + j2);
+                        a = fmaf(sp[j2] * or_h2f(vsb[j * 4 + (d >> 5)]), kv8_val(vb + j * el, d, bw), a);
+                    }
+                    acc[d] = a;
+                }
+                m = m_new;
+            }
+            for (int d = 0; d < hd; d++)
+                out[((size_t)r * q_heads + h) * hd + d] = or_f2bf(acc[d] / l);
+        }
+    }
+}
+
+/* Binary64 attention over the dequantised INT8 / INT4 cache (ground truth
+ * for both the single-pass and the split decode kernels): row r of cache c
+ * attends slots 0..len_c - 1, len_c = pos[r] + 1. */
+void or_attention8_f64(const uint16_t* q, const int8_t* const* kcs, const int8_t* const* vcs,
+                       const uint16_t* const* kss, const uint16_t* const* vss, double* out,
+                       int rows, int q_heads, int kv_heads, const int32_t* pos, int max_seq,
+                       int bw) {
+    const int hd = 128, el = bw == 8 ? 128 : 64, group = q_heads / kv_heads;
+    for (int r = 0; r < rows; r++) {
+        const int len = pos[r] + 1;
+        double* s = (double*)malloc((size_t)len * sizeof(double));
+        for (int h = 0; h < q_heads; h++) {
+            const int kvh = h / group;
+            const int8_t* kb = kcs[r] + (size_t)kvh * max_seq * el;
+            const int8_t* vb = vcs[r] + (size_t)kvh * max_seq * el;
+            const uint16_t* ksb = kss[r] + (size_t)kvh * max_seq * 4;
+            const uint16_t* vsb = vss[r] + (size_t)kvh * max_seq * 4;
+            double mx = -INFINITY;
+            for (int j = 0; j < len; j++) {
+                double d = 0.0;
+                for (int e = 0; e < hd; e++)
+                    d += (double)or_bf2f(q[((size_t)r * q_heads + h) * hd + e]) *
+                         kv8_val(kb + (size_t)j * el, e, bw) * or_h2f(ksb[(size_t)j * 4 + (e >> 5)]);
+                s[j] = d / sqrt(128.0);
+                if (s[j] > mx) mx = s[j];
+            }
+            double l = 0.0;
+            for (int j = 0; j < len; j++) { s[j] = exp(s[j] - mx); l += s[j]; }
+            for (int d = 0; d < hd; d++) {
+                double a = 0.0;
+                for (int j = 0; j < len; j++)
+                    a += s[j] * kv8_val(vb + (size_t)j * el, d, bw) * or_h2f(vsb[(size_t)j * 4 + (d >> 5)]);
+                out[((size_t)r * q_heads + h) * hd + d] = a / l;
+            }
+        }
+        free(s);
+    }
+}
+
+
 /* ------------------------------------------------------------- sampler */
 
 #define N_SEM 4096

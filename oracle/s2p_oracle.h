@@ -94,6 +94,22 @@ void or_attention_f64(const uint16_t* q, const uint16_t* kc,
                       int kv_heads, int head_dim, int prefix,
                       const uint64_t* vis, int max_seq);
 
+/* INT8 / INT4 KV cache (kernels.cu:510-946): payload [kv_heads][max_seq]
+ * [bw == 8 ? 128 : 64] bytes, f16 scales [kv_heads][max_seq][4].  Caches are
+ * passed as pointer arrays: slot_arr == NULL appends rows at pos0.. of cache
+ * 0, else row r at slot slot_arr[r] of cache r. */
+void or_kv_append8(const uint16_t* k, const uint16_t* v, int8_t* const* kcs,
+                   int8_t* const* vcs, uint16_t* const* kss, uint16_t* const* vss,
+                   int rows, int kv_heads, int pos0, const int32_t* slot_arr,
+                   int max_seq, int bw);
+void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                   const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
+                   int q_heads, int kv_heads, int pos0, int max_seq, int bw);
+void or_attention8_f64(const uint16_t* q, const int8_t* const* kcs, const int8_t* const* vcs,
+                       const uint16_t* const* kss, const uint16_t* const* vss, double* out,
+                       int rows, int q_heads, int kv_heads, const int32_t* pos, int max_seq,
+                       int bw);
+
 /* ---- sampler (src/slowar/sampling.c) ------------------------------------ */
 /* Device sampler state, byte layout of src/slowar/slowar_kernels.h:132-142. */
 typedef struct {

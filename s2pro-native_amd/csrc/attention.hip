@@ -47,6 +47,15 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
     attn_merge_one<false>(part, out, rows, qh, nsplit, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
+/* the split merge for other attention kernels with the same partial layout
+ * (the INT8 / INT4 KV decode) */
+extern "C" hipError_t s2p_attn_combine_launch(const float* part, uint16_t* out, int rows, int qh,
+                                              int nsplit, hipStream_t st) {
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)rows, (unsigned)qh), dim3(AT_HD), 0, st,
+                       part, out, rows, qh, nsplit);
+    return hipGetLastError();
+}
+
 static int64_t part_floats(int rows, int qh, int nsplit) {
     return (int64_t)rows * qh * nsplit * (AT_HD + 2);
 }

@@ -1,0 +1,311 @@
+/* s2pro MI355X — INT8 / INT4 KV cache: quantise-on-append and attention
+ * over the quantised cache (reference kernels.cu:510-946, launchers
+ * slowar_kernels.h:84-120).
+ *
+ * Cache layout (the reference's, so sessions and prefix caches are
+ * interchangeable): payload [kv_heads][max_seq][bw == 8 ? 128 : 64] bytes,
+ * scales f16 [kv_heads][max_seq][4], one per 32-element group.
+ *
+ * Append: one workgroup per (row, kv head), thread d = element d; the group
+ * absmax is a max over the 32 lanes of a half wave (exact in any order); the
+ * scale is f16(absmax / QMAX) and the values rint(x / scale) clamped to
+ * +-QMAX, with IEEE division, as the reference (kernels.cu:541-579).
+ *
+ * Attention: one workgroup of 128 threads per (row, query head) and 128-slot
+ * tiles, in the reference's arithmetic order (kernels.cu:614-722), so the
+ * result equals the oracle restatement bit for bit: per slot the score is
+ * sum_g fma(pp_g, ks_g) of in-order group dots; the tile max and sum follow
+ * the 128-lane trees (the sum's first level through LDS, the rest as the
+ * shuffle-down tree); V enters as (p * vs_g) * v.  Exponentials are the
+ * rule's s2p_expf.  The decode variant gives each 128-slot tile its own
+ * workgroup (a split), writes the (m, l, O) partial and merges the splits
+ * with the bf16 path's combine.
+ *
+ * bw 4 decodes both nibbles as the two's complement the append writes (the
+ * reference's decode expression sign-extends only the high nibble). */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "common.h"
+#include "s2pro/s2p_fmath.h"
+#include "s2pro/slowar_kernels.h"
+
+#define KV8_HD 128
+#define KV8_TILE 128
+
+static __device__ __forceinline__ float kv8_val(const int8_t* row, int e, int bw) {
+    if (bw == 8) return (float)row[e];
+    const uint8_t b = (uint8_t)row[e >> 1];
+    const int nib = (e & 1) ? (b >> 4) : (b & 0xF);
+    return (float)(nib >= 8 ? nib - 16 : nib);
+}
+
+/* max over the 32 lanes of a half wave (the lanes of one 32-element group) */
+static __device__ __forceinline__ float max32(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int BW>
+__global__ __launch_bounds__(KV8_HD) void k_kv_append8(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int8_t* kc0, int8_t* vc0,
+    uint16_t* ks0, uint16_t* vs0, int8_t* const* kcs, int8_t* const* vcs, uint16_t* const* kss,
+    uint16_t* const* vss, int kv_heads, int pos0, const int32_t* pos_arr, int max_seq) {
+#pragma clang fp contract(off)
+    constexpr int QMAX = BW == 8 ? 127 : 7;
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    const int r = blockIdx.x / kv_heads, h = blockIdx.x % kv_heads;
+    const int d = threadIdx.x;
+    const int p = pos_arr ? pos_arr[r] : pos0 + r;
+    if (p < 0 || p >= max_seq) return; /* never written outside the cache */
+    for (int kv = 0; kv < 2; kv++) {
+        int8_t* pay = kv ? (vcs ? vcs[r] : vc0) : (kcs ? kcs[r] : kc0);
+        uint16_t* sc = kv ? (vss ? vss[r] : vs0) : (kss ? kss[r] : ks0);
+        const float x = bf2f((kv ? v : k)[((size_t)r * kv_heads + h) * KV8_HD + d]);
+        const float a = max32(fabsf(x));
+        const uint16_t hs = f2h(__fdiv_rn(a, (float)QMAX));
+        const float s = h2f(hs);
+        int q = s > 0.f ? (int)rintf(__fdiv_rn(x, s)) : 0;
+        q = max(-QMAX, min(QMAX, q));
+        const size_t row = (size_t)h * max_seq + p;
+        if (BW == 8) {
+            pay[row * EL + d] = (int8_t)q;
+        } else {
+            const int hi = __shfl_down(q, 1, 64);
+            if ((d & 1) == 0) pay[row * EL + (d >> 1)] = (int8_t)((q & 0xF) | ((hi & 0xF) << 4));
+        }
+        if ((d & 31) == 0) sc[row * 4 + (d >> 5)] = hs;
+    }
+}
+
+/* Scores, max, exponentials and sum of one 128-slot tile [t0, t0 + 128) of
+ * a row attending slots [0, len); sp[] (LDS) gets the tile's p.  Returns the
+ * tile's sum (all threads) and updates m (all threads). */
+struct Kv8Lds {
+    float sq[KV8_HD];
+    float sp[KV8_TILE];
+    float red[KV8_TILE];
+    float bc[2];
+};
+
+template <int BW>
+static __device__ __forceinline__ float kv8_tile(const int8_t* kb, const uint16_t* ksb, int t0,
+                                                 int len, float& m, float& corr, Kv8Lds& L,
+                                                 bool split) {
+#pragma clang fp contract(off)
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int j = t0 + t;
+    float s = -INFINITY;
+    if (j < len) {
+        const int8_t* kr = kb + (size_t)j * EL;
+        float dsum = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float pp = 0.f;
+#pragma unroll 8
+            for (int e = 0; e < 32; e++) pp = fmaf(L.sq[g * 32 + e], kv8_val(kr, g * 32 + e, BW), pp);
+            dsum = fmaf(pp, h2f(ksb[(size_t)j * 4 + g]), dsum);
+        }
+        s = dsum;
+    }
+    /* tile max: exact in any order */
+    float mx = s;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) L.bc[wave] = mx;
+    __syncthreads();
+    const float tmax = fmaxf(L.bc[0], L.bc[1]);
+    const float m_new = split ? tmax : fmaxf(m, tmax);
+    corr = (m == -INFINITY) ? 0.f : s2p_expf(m - m_new);
+    const float p = (s == -INFINITY) ? 0.f : s2p_expf(s - m_new);
+    L.sp[t] = p;
+    L.red[t] = p;
+    __syncthreads();
+    /* the 128-lane tree: red[t] += red[t + 64], then the shuffle-down tree
+     * over the first 64 (lane 0 holds the total) */
+    float tot = 0.f;
+    if (wave == 0) {
+        tot = wave_sum_down(L.red[t] + L.red[t + 64]);
+        if (lane == 0) L.bc[0] = tot;
+    }
+    __syncthreads();
+    tot = L.bc[0];
+    m = m_new;
+    return tot;
+}
+
+template <int BW>
+__global__ __launch_bounds__(KV8_TILE) void k_attention8(
+    const uint16_t* __restrict__ q, const int8_t* kc, const int8_t* vc, const uint16_t* ks,
+    const uint16_t* vs, uint16_t* out, int q_heads, int kv_heads, int pos0, int max_seq) {
+#pragma clang fp contract(off)
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    __shared__ Kv8Lds L;
+    const int row = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    const int len = pos0 + row + 1;
+    const int kvh = h / (q_heads / kv_heads);
+    const int8_t* kb = kc + (size_t)kvh * max_seq * EL;
+    const int8_t* vb = vc + (size_t)kvh * max_seq * EL;
+    const uint16_t* ksb = ks + (size_t)kvh * max_seq * 4;
+    const uint16_t* vsb = vs + (size_t)kvh * max_seq * 4;
+    L.sq[t] = bf2f(q[((size_t)row * q_heads + h) * KV8_HD + t]) * 0.08838834764831845f;
+    __syncthreads();
+    float m = -INFINITY, l = 0.f, acc = 0.f;
+    for (int t0 = 0; t0 < len; t0 += KV8_TILE) {
+        float corr;
+        const float tsum = kv8_tile<BW>(kb, ksb, t0, len, m, corr, L, false);
+        l = fmaf(l, corr, tsum);
+        const int lim = min(KV8_TILE, len - t0);
+        float a = acc * corr;
+        for (int j2 = 0; j2 < lim; j2++) {
+            const size_t j = (size_t)(t0 + j2);
+            a = fmaf(L.sp[j2] * h2f(vsb[j * 4 + (t >> 5)]), kv8_val(vb + j * EL, t, BW), a);
+        }
+        acc = a;
+        __syncthreads(); /* sp / red are rewritten by the next tile */
+    }
+    out[((size_t)row * q_heads + h) * KV8_HD + t] = f2bf(__fdiv_rn(acc, l));
+}
+
+/* one 128-slot split of a decode row: (m, l, O) partial in the bf16 path's
+ * layout (m, l pairs, then the O rows) */
+template <int BW>
+__global__ __launch_bounds__(KV8_TILE) void k_attention8_split(
+    const uint16_t* __restrict__ q, const int8_t* const* kcs, const int8_t* const* vcs,
+    const uint16_t* const* kss, const uint16_t* const* vss, int rows, int q_heads, int kv_heads,
+    const int32_t* pos, int max_seq, int nsplit, float* part) {
+#pragma clang fp contract(off)
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    __shared__ Kv8Lds L;
+    const int row = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, t = threadIdx.x;
+    const int p = pos[row];
+    const int len = (p >= 0 && p < max_seq) ? p + 1 : 0;
+    const size_t pi = ((size_t)row * q_heads + h) * nsplit + sp;
+    float* po = part + (size_t)rows * q_heads * nsplit * 2 + pi * KV8_HD;
+    const int t0 = sp * KV8_TILE;
+    if (t0 >= len) { /* uniform: an empty split */
+        po[t] = 0.f;
+        if (t == 0) {
+            part[pi * 2] = -INFINITY;
+            part[pi * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    const int kvh = h / (q_heads / kv_heads);
+    const int8_t* kb = kcs[row] + (size_t)kvh * max_seq * EL;
+    const int8_t* vb = vcs[row] + (size_t)kvh * max_seq * EL;
+    const uint16_t* ksb = kss[row] + (size_t)kvh * max_seq * 4;
+    const uint16_t* vsb = vss[row] + (size_t)kvh * max_seq * 4;
+    L.sq[t] = bf2f(q[((size_t)row * q_heads + h) * KV8_HD + t]) * 0.08838834764831845f;
+    __syncthreads();
+    float m = -INFINITY, corr;
+    const float l = kv8_tile<BW>(kb, ksb, t0, len, m, corr, L, true);
+    const int lim = min(KV8_TILE, len - t0);
+    float a = 0.f;
+    for (int j2 = 0; j2 < lim; j2++) {
+        const size_t j = (size_t)(t0 + j2);
+        a = fmaf(L.sp[j2] * h2f(vsb[j * 4 + (t >> 5)]), kv8_val(vb + j * EL, t, BW), a);
+    }
+    po[t] = a;
+    if (t == 0) {
+        part[pi * 2] = m;
+        part[pi * 2 + 1] = l;
+    }
+}
+
+extern "C" hipError_t s2p_attn_combine_launch(const float* part, uint16_t* out, int rows, int qh,
+                                              int nsplit, hipStream_t st);
+
+extern "C" hipError_t s2pk_kv_append8(const s2p_bf16* k, const s2p_bf16* v, int8_t* k_cache,
+                                      int8_t* v_cache, void* k_scale, void* v_scale, int rows,
+                                      int kv_heads, int head_dim, int pos, int max_seq, int bw,
+                                      hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim != KV8_HD || (bw != 8 && bw != 4) || kv_heads <= 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(rows * kv_heads));
+    if (bw == 8)
+        hipLaunchKernelGGL(k_kv_append8<8>, grid, dim3(KV8_HD), 0, st, (const uint16_t*)k,
+                           (const uint16_t*)v, k_cache, v_cache, (uint16_t*)k_scale,
+                           (uint16_t*)v_scale, nullptr, nullptr, nullptr, nullptr, kv_heads, pos,
+                           nullptr, max_seq);
+    else
+        hipLaunchKernelGGL(k_kv_append8<4>, grid, dim3(KV8_HD), 0, st, (const uint16_t*)k,
+                           (const uint16_t*)v, k_cache, v_cache, (uint16_t*)k_scale,
+                           (uint16_t*)v_scale, nullptr, nullptr, nullptr, nullptr, kv_heads, pos,
+                           nullptr, max_seq);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2pk_kv_append8_ptrs(const s2p_bf16* k, const s2p_bf16* v,
+                                           int8_t* const* k_caches, int8_t* const* v_caches,
+                                           void* const* k_scales, void* const* v_scales, int rows,
+                                           int kv_heads, int head_dim, const int32_t* pos,
+                                           int max_seq, int bw, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim != KV8_HD || (bw != 8 && bw != 4) || kv_heads <= 0 || !pos)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(rows * kv_heads));
+    if (bw == 8)
+        hipLaunchKernelGGL(k_kv_append8<8>, grid, dim3(KV8_HD), 0, st, (const uint16_t*)k,
+                           (const uint16_t*)v, nullptr, nullptr, nullptr, nullptr, k_caches,
+                           v_caches, (uint16_t* const*)k_scales, (uint16_t* const*)v_scales,
+                           kv_heads, 0, pos, max_seq);
+    else
+        hipLaunchKernelGGL(k_kv_append8<4>, grid, dim3(KV8_HD), 0, st, (const uint16_t*)k,
+                           (const uint16_t*)v, nullptr, nullptr, nullptr, nullptr, k_caches,
+                           v_caches, (uint16_t* const*)k_scales, (uint16_t* const*)v_scales,
+                           kv_heads, 0, pos, max_seq);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2pk_attention8(const s2p_bf16* q, const int8_t* k_cache,
+                                      const int8_t* v_cache, const void* k_scale,
+                                      const void* v_scale, s2p_bf16* out, int rows, int q_heads,
+                                      int kv_heads, int head_dim, int pos, int max_seq, int bw,
+                                      hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim != KV8_HD || (bw != 8 && bw != 4) || kv_heads <= 0 || q_heads % kv_heads ||
+        pos < 0 || pos + rows > max_seq)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)rows, (unsigned)q_heads);
+    if (bw == 8)
+        hipLaunchKernelGGL(k_attention8<8>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           k_cache, v_cache, (const uint16_t*)k_scale, (const uint16_t*)v_scale,
+                           (uint16_t*)out, q_heads, kv_heads, pos, max_seq);
+    else
+        hipLaunchKernelGGL(k_attention8<4>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           k_cache, v_cache, (const uint16_t*)k_scale, (const uint16_t*)v_scale,
+                           (uint16_t*)out, q_heads, kv_heads, pos, max_seq);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* const* k_caches,
+                                             const int8_t* const* v_caches,
+                                             const void* const* k_scales,
+                                             const void* const* v_scales, s2p_bf16* out, int rows,
+                                             int q_heads, int kv_heads, int head_dim,
+                                             const int32_t* pos, int max_seq, int max_len,
+                                             float* part, int bw, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (head_dim != KV8_HD || (bw != 8 && bw != 4) || kv_heads <= 0 || q_heads % kv_heads ||
+        !part || max_len <= 0 || !pos)
+        return hipErrorInvalidValue;
+    const int nsplit = (max_len + KV8_TILE - 1) / KV8_TILE;
+    const dim3 grid((unsigned)rows, (unsigned)q_heads, (unsigned)nsplit);
+    if (bw == 8)
+        hipLaunchKernelGGL(k_attention8_split<8>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           k_caches, v_caches, (const uint16_t* const*)k_scales,
+                           (const uint16_t* const*)v_scales, rows, q_heads, kv_heads, pos,
+                           max_seq, nsplit, part);
+    else
+        hipLaunchKernelGGL(k_attention8_split<4>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           k_caches, v_caches, (const uint16_t* const*)k_scales,
+                           (const uint16_t* const*)v_scales, rows, q_heads, kv_heads, pos,
+                           max_seq, nsplit, part);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return s2p_attn_combine_launch(part, (uint16_t*)out, rows, q_heads, nsplit, st);
+}

@@ -119,6 +119,10 @@ SIGS = {
     "s2pk_attention_ptrs": (I, [P, P, P, P, I, I, I, I, P, I, P]),
     "s2pk_attention_decode": (I, [P, P, P, P, I, I, I, I, P, I, I, P, P]),
     "s2pk_attention_part_floats": (I64, [I, I, I]),
+    "s2pk_kv_append8": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P]),
+    "s2pk_kv_append8_ptrs": (I, [P, P, P, P, P, P, I, I, I, P, I, I, P]),
+    "s2pk_attention8": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
+    "s2pk_attention8_decode": (I, [P, P, P, P, P, P, I, I, I, I, P, I, I, P, I, P]),
     "s2pk_sample": (I, [P, I64, P, P, I, P, P, P, P, P]),
     # verify.h
     "s2p_backbone_create_random": (I, [P, U64, P, P]),
