@@ -65,6 +65,8 @@ typedef struct {
     int          max_rows;      /* rows per verify call: sessions x R (<= 128) */
     int          max_sessions;
     int          ctx_len;       /* per-session KV capacity (slots) */
+    int          kv_bits;       /* KV cache: 0 or 16 = bf16; 8 / 4 = INT8 / INT4 with
+                                 * f16 scales per 32 dims (kernels.cu:510-946) */
 } s2p_backbone_opts;
 
 typedef struct s2p_backbone s2p_backbone;
@@ -80,7 +82,9 @@ void       s2p_backbone_free(s2p_backbone* b);
 s2p_slow_layer* s2p_backbone_layer(s2p_backbone* b, int layer);
 s2p_linear*     s2p_backbone_head(s2p_backbone* b);
 void*           s2p_backbone_final_norm(s2p_backbone* b);
-/* bytes of one session's KV: [n_layers][2 * 8][ctx_len][128] bf16 */
+/* bytes of one session's KV: [n_layers][2 * 8][ctx_len][128] bf16, or with
+ * kv_bits 8 / 4 per layer the payload [2 * 8][ctx_len][128 or 64] int8 and
+ * then its f16 scales [2 * 8][ctx_len][4] */
 size_t          s2p_backbone_kv_bytes(const s2p_backbone* b);
 /* weight bytes streamed by one verify step (backbone + head) */
 size_t          s2p_backbone_weight_bytes(const s2p_backbone* b);

@@ -60,6 +60,7 @@ _SIGS = {
     "or_kv_append8": (None, [P, P, P, P, P, P, I, I, I, P, I, I]),
     "or_attention8": (None, [P, P, P, P, P, P, I, I, I, I, I, I]),
     "or_attention8_f64": (None, [P, P, P, P, P, P, I, I, I, P, I, I]),
+    "or_attention8_vis": (None, [P, P, P, P, P, P, I, I, I, I, P, I, I]),
     "or_state_init": (None, [P, F, F, F, I, U64, U64]),
     "or_set_libm": (None, [I]),
     "or_transform": (I, [P, P, P, P, P, P]),
@@ -68,6 +69,7 @@ _SIGS = {
     "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P]),
     "or_linear_fwd": (None, [P, P, P, I]),
     "or_layer": (None, [P, P, I, P, P, I, I, P, P]),
+    "or_layer8": (None, [P, P, I, P, P, P, P, I, I, P, P, I]),
     "or_gemm_bf16": (None, [P, P, P, I, I, I]),
     "or_gemm_bf16_f64": (None, [P, P, P, I, I, I]),
     "or_draft_step": (None, [P, P, P, I, I, P, P, P]),
@@ -249,6 +251,14 @@ def attention8(q, kc, vc, ks, vs, rows, qh, kvh, pos0, max_seq, bw):
     return out
 
 
+def attention8_vis(q, kc, vc, ks, vs, rows, qh, kvh, prefix, vis, max_seq, bw):
+    out = np.empty((rows, qh * 128), np.uint16)
+    va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
+    lib().or_attention8_vis(ptr(q), ptr(kc), ptr(vc), ptr(ks), ptr(vs), ptr(out), rows, qh, kvh,
+                            prefix, ptr(va), max_seq, bw)
+    return out
+
+
 def attention8_f64(q, kcs, vcs, kss, vss, rows, qh, kvh, pos, max_seq, bw):
     out = np.empty((rows, qh * 128), np.float64)
     pa = np.ascontiguousarray(pos, np.int32)
@@ -344,6 +354,14 @@ def layer(lw, x, rows, kc, vc, max_seq, prefix, pos, vis=None):
     va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
     lib().or_layer(ctypes.addressof(lw), ptr(x), rows, ptr(kc), ptr(vc), max_seq, prefix,
                    ptr(pa), ptr(va))
+
+
+def layer8(lw, x, rows, kc, vc, ks, vs, max_seq, prefix, pos, vis, bw):
+    """In place on x and the quantised caches (kc, vc int8; ks, vs uint16)."""
+    pa = np.ascontiguousarray(pos, np.int32)
+    va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
+    lib().or_layer8(ctypes.addressof(lw), ptr(x), rows, ptr(kc), ptr(vc), ptr(ks), ptr(vs),
+                    max_seq, prefix, ptr(pa), ptr(va), bw)
 
 
 def gemm_bf16(x, w, M, N, K):

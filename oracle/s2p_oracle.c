@@ -682,13 +682,19 @@ static float kv8_val(const int8_t* row, int e, int bw) {
  * with pp_g the in-order fma dot of the group, the tile max and sum are the
  * 128-lane trees, and V is dequantised as (p * vs_g) * v.  The rule's
  * s2p_expf replaces expf; l * corr + sum as one fma (nvcc contracts it). */
-void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
-                   const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
-                   int q_heads, int kv_heads, int pos0, int max_seq, int bw) {
+/* Slots visible to row r: [0, prefix) and the node slots of vis[r] (bit b =
+ * slot prefix + b; its highest bit is the row itself), or, with vis NULL,
+ * causal rows at prefix.. (kernels.cu:724-746).  The arithmetic of every
+ * visible slot is the reference's; an invisible slot scores -inf, as one
+ * beyond the length does. */
+void or_attention8_vis(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                       const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
+                       int q_heads, int kv_heads, int prefix, const uint64_t* vis, int max_seq,
+                       int bw) {
     const int hd = 128, el = bw == 8 ? 128 : 64, group = q_heads / kv_heads;
     float sq[128], sp[128], red[128], acc[128];
     for (int r = 0; r < rows; r++) {
-        const int len = pos0 + r + 1;
+        const int len = !vis ? prefix + r + 1 : (vis[r] ? prefix + 64 - __builtin_clzll(vis[r]) : prefix);
         for (int h = 0; h < q_heads; h++) {
             const int kvh = h / group;
             const int8_t* kb = kc + (size_t)kvh * max_seq * el;
@@ -704,7 +710,7 @@ void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
                 for (int t = 0; t < 128; t++) {
                     const int j = t0 + t;
                     s[t] = -INFINITY;
-                    if (j < len) {
+                    if (j < len && visible(prefix, vis, r, j)) {
                         float d = 0.f;
                         for (int g = 0; g < 4; g++) {
                             float pp = 0.f;
@@ -741,6 +747,13 @@ void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
                 out[((size_t)r * q_heads + h) * hd + d] = or_f2bf(acc[d] / l);
         }
     }
+}
+
+/* k_attention8 (kernels.cu:625-728): causal rows at pos0.. of one cache */
+void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                   const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
+                   int q_heads, int kv_heads, int pos0, int max_seq, int bw) {
+    or_attention8_vis(q, kc, vc, ks, vs, out, rows, q_heads, kv_heads, pos0, NULL, max_seq, bw);
 }
 
 /* Binary64 attention over the dequantised INT8 / INT4 cache (ground truth
@@ -1181,6 +1194,47 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
 
     free(xn); free(qkv); free(q); free(k); free(v); free(att);
     free(proj); free(gu); free(h); free(slots);
+}
+
+/* run_layer with the INT8 / INT4 KV cache (slowar.c:156-260 with the
+ * quantised-cache kernels of kernels.cu:510-946): K (after qk-norm and RoPE,
+ * rounded to bf16) and V are quantised on append at slots prefix + r, and
+ * the attention reads the quantised cache with the rows' visibility. */
+void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* vc,
+               uint16_t* ks, uint16_t* vs, int max_seq, int prefix, const int32_t* pos,
+               const uint64_t* vis, int bw) {
+    const int dim = lw->wqkv.K;
+    const int qw = 4096, kvw = 1024, ffn = lw->w2.K;
+    const float eps = 1e-6f;
+    uint16_t* xn = (uint16_t*)malloc(2 * (size_t)rows * dim);
+    uint16_t* qkv = (uint16_t*)malloc(2 * (size_t)rows * (qw + 2 * kvw));
+    uint16_t* q = (uint16_t*)malloc(2 * (size_t)rows * qw);
+    uint16_t* k = (uint16_t*)malloc(2 * (size_t)rows * kvw);
+    uint16_t* v = (uint16_t*)malloc(2 * (size_t)rows * kvw);
+    uint16_t* att = (uint16_t*)malloc(2 * (size_t)rows * qw);
+    uint16_t* proj = (uint16_t*)malloc(2 * (size_t)rows * dim);
+    uint16_t* gu = (uint16_t*)malloc(2 * (size_t)rows * 2 * ffn);
+    uint16_t* h = (uint16_t*)malloc(2 * (size_t)rows * ffn);
+
+    or_rms_norm(x, lw->attn_norm, xn, rows, dim, eps);
+    or_linear_fwd(&lw->wqkv, xn, qkv, rows);
+    or_qkv_split(qkv, q, k, v, rows, qw, kvw);
+    or_qk_norm(q, lw->q_norm, rows, 32, 128, eps);
+    or_qk_norm(k, lw->k_norm, rows, 8, 128, eps);
+    or_rope(q, rows, 32, 128, 0, pos, 1000000.0f);
+    or_rope(k, rows, 8, 128, 0, pos, 1000000.0f);
+    or_kv_append8(k, v, &kc, &vc, &ks, &vs, rows, 8, prefix, NULL, max_seq, bw);
+    or_attention8_vis(q, kc, vc, ks, vs, att, rows, 32, 8, prefix, vis, max_seq, bw);
+    or_linear_fwd(&lw->wo, att, proj, rows);
+    or_add(x, proj, (int64_t)rows * dim);
+    or_rms_norm(x, lw->ffn_norm, xn, rows, dim, eps);
+    or_linear_fwd(&lw->gate_up, xn, gu, rows);
+    or_silu_mul(gu, h, rows, ffn);
+    or_linear_fwd(&lw->w2, h, proj, rows);
+    or_add(x, proj, (int64_t)rows * dim);
+
+    free(xn); free(qkv); free(q); free(k); free(v); free(att);
+    free(proj); free(gu); free(h);
 }
 
 /* ---- the draft model ------------------------------------------------------ */

@@ -105,6 +105,12 @@ void or_kv_append8(const uint16_t* k, const uint16_t* v, int8_t* const* kcs,
 void or_attention8(const uint16_t* q, const int8_t* kc, const int8_t* vc,
                    const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
                    int q_heads, int kv_heads, int pos0, int max_seq, int bw);
+/* the same with the verify visibility (vis[r] bit b: slot prefix + b), or
+ * causal rows at prefix.. when vis is NULL */
+void or_attention8_vis(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                       const uint16_t* ks, const uint16_t* vs, uint16_t* out, int rows,
+                       int q_heads, int kv_heads, int prefix, const uint64_t* vis, int max_seq,
+                       int bw);
 void or_attention8_f64(const uint16_t* q, const int8_t* const* kcs, const int8_t* const* vcs,
                        const uint16_t* const* kss, const uint16_t* const* vss, double* out,
                        int rows, int q_heads, int kv_heads, const int32_t* pos, int max_seq,
@@ -187,6 +193,11 @@ void or_linear_fwd(const or_linear* L, const uint16_t* x, uint16_t* y, int M);
 void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
               uint16_t* vc, int max_seq, int prefix, const int32_t* pos,
               const uint64_t* vis);
+/* the same over one layer's INT8 / INT4 KV cache (payload [8][max_seq][128
+ * or 64], f16 scales [8][max_seq][4]); rows append at slots prefix + r */
+void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* vc,
+               uint16_t* ks, uint16_t* vs, int max_seq, int prefix, const int32_t* pos,
+               const uint64_t* vis, int bw);
 
 /* ---- the draft model (src/draft/draft.c:157-202) ---------------------- */
 /* y[M,N] = bf16(sum_k w[n,k] x[m,k]) with an fp32 sum in increasing k: the

@@ -59,6 +59,7 @@ struct s2p_backbone {
     void* h_stage;
     size_t stage_bytes;
     int planned, rows, n_sess, R, n_seg, max_span;
+    int kvb;               /* KV cache bits: 16 (bf16), 8 or 4 */
     int seg_rows_max;
     /* persistent verify kernel (one launch per forward) */
     /* launch descriptor block: MkArgs, MkLayer[n_layers], head MkGemv */
@@ -131,12 +132,14 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
                                       hipStream_t st, s2p_backbone** out) {
     if (!opts || !out || opts->n_layers <= 0 || opts->max_rows <= 0 ||
         opts->max_rows > GEMV_MAX_M || opts->max_sessions <= 0 || opts->ctx_len <= 0 ||
-        opts->head_rows <= 0)
+        opts->head_rows <= 0 ||
+        (opts->kv_bits != 0 && opts->kv_bits != 16 && opts->kv_bits != 8 && opts->kv_bits != 4))
         return S2P_ERR_INVALID;
     S2P_TRY(s2p_gemm_init(opts->max_rows));
     s2p_backbone* b = (s2p_backbone*)calloc(1, sizeof(*b));
     if (!b) return S2P_ERR_OOM;
     b->o = *opts;
+    b->kvb = opts->kv_bits == 0 ? 16 : opts->kv_bits;
     b->layers = (s2p_slow_layer*)calloc((size_t)opts->n_layers, sizeof(s2p_slow_layer));
     s2p_status rc = b->layers ? S2P_OK : S2P_ERR_OOM;
     for (int l = 0; l < opts->n_layers && rc == S2P_OK; l++) {
@@ -167,6 +170,10 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc(&b->gu, R * 2 * S2P_FFN_DIM * 2);
     if (rc == S2P_OK) rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M);
     b->attn_part_floats = s2p_attn_plan_part_floats((int)R, opts->ctx_len);
+    if (b->kvb != 16) {
+        const int64_t p8 = s2p_attn8_plan_part_floats((int)R, opts->ctx_len);
+        if (p8 > b->attn_part_floats) b->attn_part_floats = p8;
+    }
     if (rc == S2P_OK) rc = dalloc((void**)&b->attn_part, sizeof(float) * b->attn_part_floats);
     const int S = opts->max_sessions;
     const int nseg_max = (int)R + S; /* segments of <= 8 rows per session */
@@ -254,6 +261,7 @@ s2p_linear* s2p_backbone_head(s2p_backbone* b) { return b ? &b->head : NULL; }
 void* s2p_backbone_final_norm(s2p_backbone* b) { return b ? b->final_norm.data : NULL; }
 
 size_t s2p_backbone_kv_bytes(const s2p_backbone* b) {
+    if (b->kvb != 16) return (size_t)b->o.n_layers * s2p_kv8_layer_bytes(b->o.ctx_len, b->kvb);
     return (size_t)b->o.n_layers * 2 * S2P_KV_HEADS * (size_t)b->o.ctx_len * S2P_HEAD_DIM * 2;
 }
 
@@ -404,7 +412,7 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
         S2P_TRY(hip_ok(s2p_rope_tab_launch(&rp, rows, ROPE_BASE, b->d_rope, st), "rope table"));
         S2P_TRY(hip_ok(hipStreamSynchronize(st), "rope table sync"));
     }
-    b->mk_ready = mk_build(b);
+    b->mk_ready = b->kvb == 16 && mk_build(b); /* the persistent kernel reads bf16 caches */
     if (b->mk_ready) {
         S2P_TRY(hip_ok(hipMemsetAsync(b->d_err, 0, sizeof(int), st), "mk plan"));
         S2P_TRY(hip_ok(hipMemcpyAsync(b->d_mk, b->h_mk, b->mk_bytes, hipMemcpyHostToDevice, st),
@@ -565,6 +573,17 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
         const s2p_slow_layer* L = &b->layers[l];
         S2P_TRY(gemv(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
                      L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st));
+        if (b->kvb != 16) {
+            /* quantised caches: prologue + quantise-on-append, then the
+             * split attention and its combine */
+            S2P_TRY(hip_ok(s2p_qkrope_append8_launch(b->qkv, b->q, L->q_norm.data,
+                                                     L->k_norm.data, &plan, M, l, NORM_EPS,
+                                                     b->d_rope, b->kvb, st),
+                           "qk-norm / rope / append8"));
+            S2P_TRY(hip_ok(s2p_attn8_plan_launch(b->q, b->attn, &plan, M, l, b->max_span,
+                                                 b->attn_part, b->kvb, st),
+                           "attention8"));
+        } else
         S2P_TRY(hip_ok(s2p_attn_plan_fused_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
                                                   b->max_span, b->attn_part, b->qkv,
                                                   L->q_norm.data, L->k_norm.data, b->d_rope,
@@ -637,6 +656,10 @@ s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,
     if (!b || !out_path || !out_n_acc) return S2P_ERR_INVALID;
     if (!b->planned) return S2P_ERR_STATE;
     const S2pRowPlan plan = row_plan(b);
+    if (b->kvb != 16)
+        return hip_ok(s2p_kv_commit8_launch(&plan, out_path, out_n_acc, b->n_sess, b->R,
+                                            b->o.n_layers, b->kvb, st),
+                      "kv commit");
     return hip_ok(s2p_kv_commit_launch(&plan, out_path, out_n_acc, b->n_sess, b->R,
                                        b->o.n_layers, st), "kv commit");
 }

@@ -90,16 +90,17 @@ struct Kv8Lds {
     float bc[2];
 };
 
-template <int BW>
+template <int BW, bool VIS = false>
 static __device__ __forceinline__ float kv8_tile(const int8_t* kb, const uint16_t* ksb, int t0,
                                                  int len, float& m, float& corr, Kv8Lds& L,
-                                                 bool split) {
+                                                 bool split, int prefix = 0, uint64_t vis = 0) {
 #pragma clang fp contract(off)
     constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int j = t0 + t;
     float s = -INFINITY;
-    if (j < len) {
+    /* VIS: slots [0, prefix) and the node slots prefix + b of vis's bits */
+    if (j < len && (!VIS || j < prefix || ((vis >> (j - prefix)) & 1ull))) {
         const int8_t* kr = kb + (size_t)j * EL;
         float dsum = 0.f;
 #pragma unroll
@@ -308,4 +309,233 @@ extern "C" hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* co
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return s2p_attn_combine_launch(part, (uint16_t*)out, rows, q_heads, nsplit, st);
+}
+
+/* ------------------------------------------------------------------------
+ * The verify plan over quantised session caches.  A session's KV base holds,
+ * per layer, the payload planes [16][max_seq][EL] (K heads 0..7, then V
+ * heads) followed by their f16 scales [16][max_seq][4]: kv8_layer_bytes per
+ * layer.  Rows are planned as for the bf16 cache (S2pRowPlan): row r writes
+ * slot plan.slot[r], has RoPE position plan.pos[r] and sees [0, L) plus the
+ * node slots of plan.vis[r], whose highest bit is the row's own node. */
+#include "prims_dev.h"
+
+static __host__ __device__ inline size_t kv8_layer_bytes(int max_seq, int bw) {
+    return (size_t)16 * max_seq * ((bw == 8 ? KV8_HD : KV8_HD / 2) + 8);
+}
+
+struct Kv8Plane {
+    int8_t* pay;    /* [max_seq][EL] */
+    uint16_t* sc;   /* [max_seq][4] */
+};
+
+template <int BW>
+static __device__ __forceinline__ Kv8Plane kv8_plane(const S2pRowPlan& plan, int sess, int layer,
+                                                     int plane) {
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    int8_t* lb = (int8_t*)plan.kv[sess] + (size_t)layer * kv8_layer_bytes(plan.max_seq, BW);
+    Kv8Plane p;
+    p.pay = lb + (size_t)plane * plan.max_seq * EL;
+    p.sc = (uint16_t*)(lb + (size_t)16 * plan.max_seq * EL) + (size_t)plane * plan.max_seq * 4;
+    return p;
+}
+
+/* quantise element pair (x0 = element lane, x1 = element lane + 64) of one
+ * 128-wide row into payload row `pay` and scale row `sc` (kernels.cu:541-579) */
+template <int BW>
+static __device__ __forceinline__ void kv8_put(float x0, float x1, int8_t* pay, uint16_t* sc,
+                                               int lane) {
+#pragma clang fp contract(off)
+    constexpr int QMAX = BW == 8 ? 127 : 7;
+    const float xs[2] = {x0, x1};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int e = lane + 64 * h;
+        const float a = max32(fabsf(xs[h]));
+        const uint16_t hs = f2h(__fdiv_rn(a, (float)QMAX));
+        const float s = h2f(hs);
+        int q = s > 0.f ? (int)rintf(__fdiv_rn(xs[h], s)) : 0;
+        q = max(-QMAX, min(QMAX, q));
+        if (BW == 8) {
+            pay[e] = (int8_t)q;
+        } else {
+            const int hi = __shfl_down(q, 1, 64);
+            if ((e & 1) == 0) pay[e >> 1] = (int8_t)((q & 0xF) | ((hi & 0xF) << 4));
+        }
+        if ((lane & 31) == 0) sc[e >> 5] = hs;
+    }
+}
+
+/* qk-norm + RoPE of one (row, head) of the fused qkv output (the rounding
+ * points of the bf16 plan's prologue); q heads to q_out, K (rounded to bf16)
+ * and V quantised into the row's slot. */
+template <int BW>
+__global__ __launch_bounds__(64) void k_qkrope_append8(const uint16_t* __restrict__ qkv,
+                                                       uint16_t* __restrict__ q_out,
+                                                       const uint16_t* __restrict__ qn_w,
+                                                       const uint16_t* __restrict__ kn_w,
+                                                       S2pRowPlan plan, int layer, float eps,
+                                                       const float* __restrict__ rope_tab) {
+#pragma clang fp contract(off)
+    const int QH = 32, KVH = 8, HD = 128, W = (QH + 2 * KVH) * HD;
+    const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+    const bool is_q = head < QH;
+    const int kh = head - QH;
+    const uint16_t* src = qkv + (size_t)row * W + (is_q ? head * HD : QH * HD + kh * HD);
+    const uint16_t* nw = is_q ? qn_w : kn_w;
+    const float v0 = bf2f(src[lane]), v1 = bf2f(src[lane + 64]);
+    const float* cs = rope_tab + (size_t)row * 128;
+    float o[2];
+    qkrope_math(v0, v1, nw[lane], nw[lane + 64], cs[(lane >> 1) * 2], cs[(lane >> 1) * 2 + 1],
+                cs[((lane + 64) >> 1) * 2], cs[((lane + 64) >> 1) * 2 + 1], eps, lane, &o[0],
+                &o[1]);
+    if (is_q) {
+        uint16_t* dst = q_out + (size_t)row * QH * HD + head * HD;
+        dst[lane] = f2bf(o[0]);
+        dst[lane + 64] = f2bf(o[1]);
+        return;
+    }
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    const int sess = plan.sess[row];
+    const size_t slot = (size_t)plan.slot[row];
+    const Kv8Plane kp = kv8_plane<BW>(plan, sess, layer, kh);
+    const Kv8Plane vp = kv8_plane<BW>(plan, sess, layer, KVH + kh);
+    kv8_put<BW>(bf2f(f2bf(o[0])), bf2f(f2bf(o[1])), kp.pay + slot * EL, kp.sc + slot * 4, lane);
+    const uint16_t* vs = qkv + (size_t)row * W + (QH + KVH) * HD + kh * HD;
+    kv8_put<BW>(bf2f(vs[lane]), bf2f(vs[lane + 64]), vp.pay + slot * EL, vp.sc + slot * 4, lane);
+}
+
+/* One 128-slot split of a planned row over its session's quantised cache:
+ * the (m, l, O) partial of k_attention8_split with the row's visibility. */
+template <int BW>
+__global__ __launch_bounds__(KV8_TILE) void k_attention8_plan(const uint16_t* __restrict__ q,
+                                                              S2pRowPlan plan, int layer,
+                                                              int rows, int nsplit,
+                                                              float* __restrict__ part) {
+#pragma clang fp contract(off)
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    const int QH = 32, KVH = 8;
+    __shared__ Kv8Lds L;
+    const int row = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, t = threadIdx.x;
+    const uint64_t vis = plan.vis[row];
+    const int slot = plan.slot[row];
+    const int node = 63 - __builtin_clzll(vis); /* vis always holds the row's own bit */
+    const int prefix = slot - node, len = slot + 1;
+    const size_t pi = ((size_t)row * QH + h) * nsplit + sp;
+    float* po = part + (size_t)rows * QH * nsplit * 2 + pi * KV8_HD;
+    const int t0 = sp * KV8_TILE;
+    if (t0 >= len) { /* uniform: an empty split */
+        po[t] = 0.f;
+        if (t == 0) {
+            part[pi * 2] = -INFINITY;
+            part[pi * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    const int kvh = h / (QH / KVH);
+    const int sess = plan.sess[row];
+    const Kv8Plane kp = kv8_plane<BW>(plan, sess, layer, kvh);
+    const Kv8Plane vp = kv8_plane<BW>(plan, sess, layer, KVH + kvh);
+    L.sq[t] = bf2f(q[((size_t)row * QH + h) * KV8_HD + t]) * 0.08838834764831845f;
+    __syncthreads();
+    float m = -INFINITY, corr;
+    const float l = kv8_tile<BW, true>(kp.pay, kp.sc, t0, len, m, corr, L, true, prefix, vis);
+    const int lim = min(KV8_TILE, len - t0);
+    float a = 0.f;
+    for (int j2 = 0; j2 < lim; j2++) {
+        const size_t j = (size_t)(t0 + j2);
+        a = fmaf(L.sp[j2] * h2f(vp.sc[j * 4 + (t >> 5)]), kv8_val(vp.pay + j * EL, t, BW), a);
+    }
+    po[t] = a;
+    if (t == 0) {
+        part[pi * 2] = m;
+        part[pi * 2 + 1] = l;
+    }
+}
+
+/* Tree commit over quantised caches: accepted node path[d-1] moves to slot
+ * L + d in increasing d (payload row and its four scales), one wave per
+ * (session, layer, plane). */
+template <int BW>
+__global__ __launch_bounds__(64) void k_kv_commit8(S2pRowPlan plan,
+                                                   const int32_t* __restrict__ path,
+                                                   const int32_t* __restrict__ n_acc, int R) {
+    constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
+    const int s = blockIdx.x, layer = blockIdx.y, plane = blockIdx.z, lane = threadIdx.x;
+    int n = n_acc[s];
+    n = n < 0 ? 0 : (n > R - 1 ? R - 1 : n);
+    const int L = plan.slot[s * R];
+    const Kv8Plane p = kv8_plane<BW>(plan, s, layer, plane);
+    for (int d = 1; d <= n; d++) {
+        const int node = path[(size_t)s * R + d - 1];
+        if (node == d || node < d || node >= R) continue; /* chain slot, or invalid */
+        const int8_t* src = p.pay + (size_t)(L + node) * EL;
+        int8_t* dst = p.pay + (size_t)(L + d) * EL;
+        if (BW == 8) {
+            ((uint16_t*)dst)[lane] = ((const uint16_t*)src)[lane];
+        } else {
+            dst[lane] = src[lane];
+        }
+        if (lane < 4) p.sc[(size_t)(L + d) * 4 + lane] = p.sc[(size_t)(L + node) * 4 + lane];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+extern "C" size_t s2p_kv8_layer_bytes(int max_seq, int bw) { return kv8_layer_bytes(max_seq, bw); }
+
+extern "C" int64_t s2p_attn8_plan_part_floats(int rows, int max_span) {
+    const int64_t nsplit = (max_span + KV8_TILE - 1) / KV8_TILE;
+    return (int64_t)rows * 32 * nsplit * (2 + KV8_HD);
+}
+
+extern "C" hipError_t s2p_qkrope_append8_launch(const void* qkv, void* q_out, const void* qn_w,
+                                                const void* kn_w, const S2pRowPlan* plan,
+                                                int rows, int layer, float eps,
+                                                const float* rope_tab, int bw, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (bw != 8 && bw != 4) return hipErrorInvalidValue;
+    if (bw == 8)
+        hipLaunchKernelGGL(k_qkrope_append8<8>, dim3(rows, 40), dim3(64), 0, st,
+                           (const uint16_t*)qkv, (uint16_t*)q_out, (const uint16_t*)qn_w,
+                           (const uint16_t*)kn_w, *plan, layer, eps, rope_tab);
+    else
+        hipLaunchKernelGGL(k_qkrope_append8<4>, dim3(rows, 40), dim3(64), 0, st,
+                           (const uint16_t*)qkv, (uint16_t*)q_out, (const uint16_t*)qn_w,
+                           (const uint16_t*)kn_w, *plan, layer, eps, rope_tab);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pRowPlan* plan,
+                                            int rows, int layer, int max_span, float* part,
+                                            int bw, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if ((bw != 8 && bw != 4) || max_span <= 0 || max_span > plan->max_seq)
+        return hipErrorInvalidValue;
+    const int nsplit = (max_span + KV8_TILE - 1) / KV8_TILE;
+    const dim3 grid((unsigned)rows, 32u, (unsigned)nsplit);
+    if (bw == 8)
+        hipLaunchKernelGGL(k_attention8_plan<8>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           *plan, layer, rows, nsplit, part);
+    else
+        hipLaunchKernelGGL(k_attention8_plan<4>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
+                           *plan, layer, rows, nsplit, part);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return s2p_attn_combine_launch(part, (uint16_t*)out, rows, 32, nsplit, st);
+}
+
+extern "C" hipError_t s2p_kv_commit8_launch(const S2pRowPlan* plan, const int32_t* path,
+                                            const int32_t* n_acc, int n_sess, int R,
+                                            int n_layers, int bw, hipStream_t st) {
+    if (n_sess <= 0) return hipSuccess;
+    if (bw != 8 && bw != 4) return hipErrorInvalidValue;
+    if (bw == 8)
+        hipLaunchKernelGGL(k_kv_commit8<8>, dim3(n_sess, n_layers, 16), dim3(64), 0, st, *plan,
+                           path, n_acc, R);
+    else
+        hipLaunchKernelGGL(k_kv_commit8<4>, dim3(n_sess, n_layers, 16), dim3(64), 0, st, *plan,
+                           path, n_acc, R);
+    return hipGetLastError();
 }

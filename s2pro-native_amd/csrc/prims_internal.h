@@ -61,6 +61,23 @@ hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan
                                       float eps, unsigned* counters, hipStream_t st);
 int64_t    s2p_attn_plan_part_floats(int rows, int max_span);
 
+/* The verify plan over INT8 / INT4 (bw 8 / 4) session caches (kv8.hip): per
+ * layer, payload planes [16][max_seq][bw == 8 ? 128 : 64] (K heads, then V)
+ * and their f16 scales [16][max_seq][4]. */
+size_t     s2p_kv8_layer_bytes(int max_seq, int bw);
+int64_t    s2p_attn8_plan_part_floats(int rows, int max_span);
+/* qk-norm + RoPE (positions from rope_tab) + quantise-on-append */
+hipError_t s2p_qkrope_append8_launch(const void* qkv, void* q_out, const void* qn_w,
+                                     const void* kn_w, const S2pRowPlan* plan, int rows,
+                                     int layer, float eps, const float* rope_tab, int bw,
+                                     hipStream_t st);
+/* split attention over 128-slot tiles + the combine into out */
+hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pRowPlan* plan, int rows,
+                                 int layer, int max_span, float* part, int bw, hipStream_t st);
+hipError_t s2p_kv_commit8_launch(const S2pRowPlan* plan, const int32_t* path,
+                                 const int32_t* n_acc, int n_sess, int R, int n_layers, int bw,
+                                 hipStream_t st);
+
 #ifdef __cplusplus
 }
 #endif

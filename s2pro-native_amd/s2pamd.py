@@ -27,7 +27,7 @@ WQ_INT8 = 1
 
 class BackboneOpts(ctypes.Structure):
     _fields_ = [("n_layers", I), ("quant", I), ("head_quant", I), ("head_rows", I),
-                ("max_rows", I), ("max_sessions", I), ("ctx_len", I)]
+                ("max_rows", I), ("max_sessions", I), ("ctx_len", I), ("kv_bits", I)]
 
 
 class VerifyBatch(ctypes.Structure):

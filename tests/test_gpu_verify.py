@@ -31,8 +31,8 @@ def lib():
     return s2pamd.load()
 
 
-def make_backbone(lib, n_layers, quant, head_rows, max_rows, max_sessions, ctx, seed):
-    o = s2pamd.BackboneOpts(n_layers, quant, quant, head_rows, max_rows, max_sessions, ctx)
+def make_backbone(lib, n_layers, quant, head_rows, max_rows, max_sessions, ctx, seed, kv_bits=0):
+    o = s2pamd.BackboneOpts(n_layers, quant, quant, head_rows, max_rows, max_sessions, ctx, kv_bits)
     bb = ctypes.c_void_p()
     s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(o), seed, S(), ctypes.byref(bb)),
                  "backbone")

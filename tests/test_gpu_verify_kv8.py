@@ -1,0 +1,190 @@
+"""Verify forward over INT8 / INT4 session caches (backbone kv_bits 8 / 4):
+the reference's quantised-cache serving mode (model.c:201-215, kernels.cu:
+510-946) inside the verify plan, vs the oracle's layer composition over the
+same quantised caches (or_layer8), and the tree commit of quantised slots.
+
+Logits: within 1e-2 relative of the oracle per row (L2 and max norm), as the
+bf16-cache path.  The appended K / V: the dequantised rows within one
+quantisation step plus 2e-2 of the oracle's (a code can round the other way
+where the GEMV rounding of an element differs) and within 2e-2 (INT4: 6e-2)
+in rms; every
+other slot untouched.  Commit: the moved
+payload rows and scales equal the accepted nodes' rows bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+import s2pamd
+from gpu_util import (P, S, assert_close_norm, bf16_bits, bf16_vals, d2h,
+                      empty, to_dev, to_host)
+from test_gpu_verify import TREE16, host_layer, host_linear, make_backbone, plan
+from test_oracle_kv8 import decode
+
+pytestmark = pytest.mark.gpu
+
+HD, KVH = 128, 8
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return s2pamd.load()
+
+
+def layout(n_layers, ctx, bw):
+    el = HD if bw == 8 else HD // 2
+    pay = 16 * ctx * el
+    return el, pay, pay + 16 * ctx * 8
+
+
+def new_kv8(lib, bb, n_layers, ctx, L, bw, seed):
+    """A session cache whose slots [0, L) hold quantised N(0,1) rows (the
+    oracle's append), the rest zero; returns (device tensor, host bytes)."""
+    el, pay, lb = layout(n_layers, ctx, bw)
+    assert lib.s2p_backbone_kv_bytes(bb) == n_layers * lb
+    host = np.zeros(n_layers * lb, np.uint8)
+    r = np.random.default_rng(seed)
+    for l in range(n_layers):
+        kc, vc, ks, vs = planes(host, l, ctx, bw)
+        k = po.f32_to_bf16(r.standard_normal((L, KVH * HD)).astype(np.float32))
+        v = po.f32_to_bf16(r.standard_normal((L, KVH * HD)).astype(np.float32))
+        kcc, vcc = [np.ascontiguousarray(kc)], [np.ascontiguousarray(vc)]
+        kss, vss = [np.ascontiguousarray(ks)], [np.ascontiguousarray(vs)]
+        po.kv_append8(k, v, kcc, vcc, kss, vss, L, KVH, 0, None, ctx, bw)
+        kc[...], vc[...], ks[...], vs[...] = kcc[0], vcc[0], kss[0], vss[0]
+    return to_dev(host), host
+
+
+def planes(buf, l, ctx, bw):
+    """Views (kc, vc, ks, vs) of layer l of a session cache held as bytes."""
+    el, pay, lb = layout(0, ctx, bw)
+    base = buf[l * lb:(l + 1) * lb]
+    p = base[:pay].view(np.int8).reshape(16, ctx, el)
+    s = base[pay:].view(np.uint16).reshape(16, ctx, 4)
+    return p[:8], p[8:], s[:8], s[8:]
+
+
+def oracle_forward8(lib, bb, n_layers, x, host, ctx, L, parent, bw):
+    R = len(parent)
+    depth, vis = [0] * R, np.zeros(R, np.uint64)
+    for i in range(R):
+        if i:
+            depth[i] = depth[parent[i]] + 1
+        m, j = 0, i
+        while j >= 0:
+            m |= 1 << j
+            j = parent[j]
+        vis[i] = m
+    pos = np.array([L + d for d in depth], np.int32)
+    x = np.array(x, np.uint16, copy=True)
+    host = host.copy()
+    for l in range(n_layers):
+        lw, keep = host_layer(lib, bb, l)
+        kc, vc, ks, vs = [np.ascontiguousarray(a) for a in planes(host, l, ctx, bw)]
+        po.layer8(lw, x, R, kc, vc, ks, vs, ctx, L, pos, vis, bw)
+        dst = planes(host, l, ctx, bw)
+        for d, a in zip(dst, (kc, vc, ks, vs)):
+            d[...] = a
+    fnorm = d2h(lib.s2p_backbone_final_norm(bb), 2560 * 2, np.uint16)
+    xn = po.rms_norm(x, fnorm, R, 2560)
+    head, keep = host_linear(lib.s2p_backbone_head(bb).contents)
+    return po.linear_fwd(head, xn, R), host
+
+
+def step(ks):
+    """the quantisation step (the group scale) of every element"""
+    return ks.view(np.float16).astype(np.float64).repeat(32, axis=-1)
+
+
+def check_appended(got, want, st, what, bw):
+    """Dequantised appended rows: every element within one quantisation step
+    (a code that rounded the other way) plus 2e-2 relative of the oracle's,
+    and the rms difference within 2e-2 (INT4, whose steps are 18x larger:
+    6e-2) of the rows' rms."""
+    err = np.abs(got - want)
+    assert np.all(err <= 1.01 * st + 2e-2 * np.abs(want)), f"{what}: beyond one step"
+    rel = np.sqrt(np.mean(err ** 2) / np.mean(want ** 2))
+    assert rel <= (2e-2 if bw == 8 else 6e-2), f"{what}: rms difference {rel:.3g}"
+
+
+def deq(kc, ks, bw):
+    return decode(kc, bw) * ks.view(np.float16).astype(np.float64).repeat(32, axis=-1)
+
+
+@pytest.mark.parametrize("bw,parent,lens", [(8, [-1, 0, 1, 2, 3], [300]),
+                                            (4, [-1, 0, 1, 2, 3], [129]),
+                                            (8, TREE16, [130, 301])])
+def test_verify_forward_kv8_vs_oracle(lib, bw, parent, lens):
+    n_layers, ctx = 2, 384
+    R, n = len(parent), len(lens)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, n * R, n, ctx,
+                       321 + bw, kv_bits=bw)
+    try:
+        kvs, hosts = zip(*[new_kv8(lib, bb, n_layers, ctx, lens[s], bw, 40 + s)
+                           for s in range(n)])
+        print(f"kv{bw}: {n} sessions x {R} rows, lens {lens}", flush=True)
+        plan(lib, bb, parent, list(kvs), lens)
+        x = bf16_bits(np.random.default_rng(9).standard_normal((n * R, 2560)).astype(np.float32))
+        logits = empty((n * R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
+        got = bf16_vals(to_host(logits, np.uint16))
+        for s in range(n):
+            rows = slice(s * R, (s + 1) * R)
+            want, ref = oracle_forward8(lib, bb, n_layers, x[rows], hosts[s], ctx, lens[s],
+                                        parent, bw)
+            assert_close_norm(got[rows], bf16_vals(want), rel=1e-2, what=f"session {s} logits")
+            dev = to_host(kvs[s], np.uint8)
+            L = lens[s]
+            for l in range(n_layers):
+                gp, rp = planes(dev, l, ctx, bw), planes(ref, l, ctx, bw)
+                for a, b in zip(gp, rp):  # prefix and free slots untouched
+                    assert np.array_equal(a[:, :L], b[:, :L])
+                    assert np.array_equal(a[:, L + R:], b[:, L + R:])
+                for c, sc in ((0, 2), (1, 3)):
+                    check_appended(deq(gp[c][:, L:L + R], gp[sc][:, L:L + R], bw),
+                                   deq(rp[c][:, L:L + R], rp[sc][:, L:L + R], bw),
+                                   np.maximum(step(gp[sc][:, L:L + R]), step(rp[sc][:, L:L + R])),
+                                   f"layer {l} appended {'KV'[c]}", bw)
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+@pytest.mark.parametrize("bw", [8, 4])
+def test_kv_commit8_moves_accepted_nodes(lib, bw):
+    """Tree commit over quantised caches: after a forward, accepted path
+    (2, 5, 10, 15) of TREE16 moves to slots L+1..L+4 of every layer and plane,
+    payload and scales, and nothing else changes."""
+    n_layers, ctx, L = 2, 256, 77
+    R = len(TREE16)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, R, 1, ctx, 55,
+                       kv_bits=bw)
+    try:
+        kv, _ = new_kv8(lib, bb, n_layers, ctx, L, bw, 7)
+        plan(lib, bb, TREE16, [kv], [L])
+        x = bf16_bits(np.random.default_rng(3).standard_normal((R, 2560)).astype(np.float32))
+        logits = empty((R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
+        before = to_host(kv, np.uint8).copy()
+        path = np.zeros(R, np.int32)
+        path[:4] = [2, 5, 10, 15]
+        nacc = np.array([4], np.int32)
+        s2pamd.check(lib.s2p_verify_kv_commit(bb, P(to_dev(path)), P(to_dev(nacc)), S()),
+                     "commit")
+        after = to_host(kv, np.uint8)
+        for l in range(n_layers):
+            b, a = planes(before, l, ctx, bw), planes(after, l, ctx, bw)
+            for pb, pa in zip(b, a):
+                want = pb.copy()
+                for d, node in enumerate([2, 5, 10, 15], start=1):
+                    want[:, L + d] = pb[:, L + node]
+                assert np.array_equal(pa, want)
+                assert np.any(pa[:, L + 1:L + 5] != pb[:, L + 1:L + 5])
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+def test_kv_bits_rejected(lib):
+    o = s2pamd.BackboneOpts(1, s2pamd.WQ_INT4, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 8, 1, 64, 6)
+    bb = ctypes.c_void_p()
+    assert lib.s2p_backbone_create_random(ctypes.byref(o), 1, S(), ctypes.byref(bb)) != 0
