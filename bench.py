@@ -57,12 +57,21 @@ WORKLOADS = {
 }
 
 
-def step_alg_bytes(lens=(CTX,), rows=K + 1):
-    """Weights and scales once, each cached KV token once (4,096 B per layer),
-    activations and logits per row (3,887,360 B: 17,879,040 + 1,557,760 at
-    M = 5)."""
+def kv_token_bytes(kv_bits=16):
+    """Bytes of one cached token of one layer: K and V of 8 heads x 128 dims,
+    bf16 (4,096 B), or INT8 / INT4 codes plus four f16 group scales per head
+    (2,176 / 1,152 B)."""
+    if kv_bits == 16:
+        return 2 * 8 * 128 * 2
+    return 2 * 8 * (128 * kv_bits // 8 + 8)
+
+
+def step_alg_bytes(lens=(CTX,), rows=K + 1, kv_bits=16):
+    """Weights and scales once, each cached KV token once (4,096 B per layer
+    for bf16), activations and logits per row (3,887,360 B: 17,879,040 +
+    1,557,760 at M = 5)."""
     w = N_LAYERS * sum(int4_bytes(n, k) for n, k in W_LAYER) + int4_bytes(155776, 2560)
-    kv = N_LAYERS * 2 * 8 * 128 * 2 * sum(lens)
+    kv = N_LAYERS * kv_token_bytes(kv_bits) * sum(lens)
     act = rows * 3_887_360
     return w, kv, w + kv + act
 
@@ -125,6 +134,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS),
                     help="config3 (the headline metric) or the batch / tree configs 4, 5")
+    ap.add_argument("--kv-bits", type=int, default=16, choices=[16, 8, 4],
+                    help="session KV cache: bf16 (16) or the INT8 / INT4 quantised cache")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a plain 256 MiB device copy (3 launches): the reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -159,7 +170,7 @@ def main():
         M = NS * R
         ctx = max(lens) + 64
         opts = s2pamd.BackboneOpts(N_LAYERS, s2pamd.WQ_INT4, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB,
-                                   max(16, M), NS, ctx)
+                                   max(16, M), NS, ctx, args.kv_bits)
         bb = ctypes.c_void_p()
         s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(opts), 2026, S, ctypes.byref(bb)))
         kvs = []
@@ -167,6 +178,11 @@ def main():
             kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
             s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0,
                                                        5 + s_, S))
+            if args.kv_bits != 16:
+                # quantised cache: random codes, every group scale f16 0.01
+                pay = 16 * ctx * 128 * args.kv_bits // 8
+                lb = pay + 16 * ctx * 8
+                kv.view(torch.uint8).view(N_LAYERS, lb)[:, pay:].view(torch.int16).fill_(0x211F)
             kvs.append(kv)
         kvp = (ctypes.c_void_p * NS)(*[k.data_ptr() for k in kvs])
         ln = np.array(lens, np.int32)
@@ -270,11 +286,12 @@ def main():
         gemv_gbs = per_launch / avg_launch_s / 1e9
         lib.s2p_backbone_free(bb)
 
-    w, kvb, alg = step_alg_bytes(lens, M)
+    w, kvb, alg = step_alg_bytes(lens, M, args.kv_bits)
     step_gbs = alg / (ms / 1e3) / 1e9
-    headline = args.workload == "config3"
+    headline = args.workload == "config3" and args.kv_bits == 16
+    kvname = "" if args.kv_bits == 16 else f", INT{args.kv_bits} KV"
     out = {
-        "metric": METRIC if headline else f"verify steps/s ({args.workload}, 36L INT4)",
+        "metric": METRIC if headline else f"verify steps/s ({args.workload}, 36L INT4{kvname})",
         "value": round(1e3 / ms, 3),
         "unit": "steps/s",
         "n_gpus": 1,
@@ -286,7 +303,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init INT4-g32 weights, N(0,1) KV cache and inputs)",
-        "config": {"workload": wl["desc"], "global_batch": NS, "seq_len": max(lens),
+        "config": {"workload": wl["desc"] + kvname, "global_batch": NS, "seq_len": max(lens),
                    "parallelism": "single GPU"},
         "step_alg_bytes": alg,
         "step_hbm_gbs": round(step_gbs, 1),

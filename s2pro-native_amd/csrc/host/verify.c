@@ -580,8 +580,8 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
                                                      L->k_norm.data, &plan, M, l, NORM_EPS,
                                                      b->d_rope, b->kvb, st),
                            "qk-norm / rope / append8"));
-            S2P_TRY(hip_ok(s2p_attn8_plan_launch(b->q, b->attn, &plan, M, l, b->max_span,
-                                                 b->attn_part, b->kvb, st),
+            S2P_TRY(hip_ok(s2p_attn8_plan_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
+                                                 b->max_span, b->attn_part, b->kvb, st),
                            "attention8"));
         } else
         S2P_TRY(hip_ok(s2p_attn_plan_fused_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,

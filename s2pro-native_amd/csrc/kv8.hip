@@ -90,17 +90,16 @@ struct Kv8Lds {
     float bc[2];
 };
 
-template <int BW, bool VIS = false>
+template <int BW>
 static __device__ __forceinline__ float kv8_tile(const int8_t* kb, const uint16_t* ksb, int t0,
                                                  int len, float& m, float& corr, Kv8Lds& L,
-                                                 bool split, int prefix = 0, uint64_t vis = 0) {
+                                                 bool split) {
 #pragma clang fp contract(off)
     constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int j = t0 + t;
     float s = -INFINITY;
-    /* VIS: slots [0, prefix) and the node slots prefix + b of vis's bits */
-    if (j < len && (!VIS || j < prefix || ((vis >> (j - prefix)) & 1ull))) {
+    if (j < len) {
         const int8_t* kr = kb + (size_t)j * EL;
         float dsum = 0.f;
 #pragma unroll
@@ -318,6 +317,7 @@ extern "C" hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* co
  * layer.  Rows are planned as for the bf16 cache (S2pRowPlan): row r writes
  * slot plan.slot[r], has RoPE position plan.pos[r] and sees [0, L) plus the
  * node slots of plan.vis[r], whose highest bit is the row's own node. */
+#include "attn_dev.h"
 #include "prims_dev.h"
 
 static __host__ __device__ inline size_t kv8_layer_bytes(int max_seq, int bw) {
@@ -405,51 +405,230 @@ __global__ __launch_bounds__(64) void k_qkrope_append8(const uint16_t* __restric
     kv8_put<BW>(bf2f(vs[lane]), bf2f(vs[lane + 64]), vp.pay + slot * EL, vp.sc + slot * 4, lane);
 }
 
-/* One 128-slot split of a planned row over its session's quantised cache:
- * the (m, l, O) partial of k_attention8_split with the row's visibility. */
+/* Verify-plan attention over quantised caches on the matrix cores: one wave
+ * per (segment of <= 8 rows of a session, kv head, position split); its 32
+ * query vectors (8 rows x the 4 query heads of the kv head) are two 16-row
+ * MFMA tiles, as in the bf16 kernel.  Per 32-slot tile:
+ *   scores: the int8 (int4) codes are exact in bf16, so each 32-dim group g
+ *     is one 16x16x32 MFMA of q against the codes, scaled by the slot's
+ *     group scale: s = sum_g ks[slot][g] * (q_g . k_g);
+ *   PV: the codes of V (exact in bf16) are the B operand and the group scale
+ *     rides in P: the A operand of output dims in group g is p * vs[slot][g],
+ *     split hi + lo in bf16 (16 significant bits, as the bf16 kernel's P).
+ * Each split writes the (m, l, O) partial of every (row, head) it serves;
+ * s2p_attn_combine_launch merges them.  Arithmetic is fp32 throughout, in an
+ * order of its own (tolerance-checked against the reference-order oracle). */
+#define A8_TILE 32
+#define A8_PS 40 /* P row stride in bf16 (32 slots + 8 pad) */
+
+static __device__ __forceinline__ uint32_t bf_pair(float lo, float hi) {
+    /* small integers and their products with f16 scales: callers pass values
+     * exact in bf16 or round first */
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
 template <int BW>
-__global__ __launch_bounds__(KV8_TILE) void k_attention8_plan(const uint16_t* __restrict__ q,
-                                                              S2pRowPlan plan, int layer,
-                                                              int rows, int nsplit,
-                                                              float* __restrict__ part) {
-#pragma clang fp contract(off)
+static __device__ __forceinline__ float a8_code(uint32_t word, int k) {
+    /* element k (0..3 for BW 8, 0..7 for BW 4) of a little-endian word */
+    if (BW == 8) return (float)(int8_t)(word >> (8 * k));
+    const int nib = (word >> (4 * k)) & 0xF;
+    return (float)(nib >= 8 ? nib - 16 : nib);
+}
+
+template <int BW>
+__global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ q,
+                                                   S2pRowPlan plan,
+                                                   const S2pAttnSeg* __restrict__ segs,
+                                                   int layer, int rows, int nsplit,
+                                                   int split_pos, float* __restrict__ part) {
     constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
-    const int QH = 32, KVH = 8;
-    __shared__ Kv8Lds L;
-    const int row = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, t = threadIdx.x;
-    const uint64_t vis = plan.vis[row];
-    const int slot = plan.slot[row];
-    const int node = 63 - __builtin_clzll(vis); /* vis always holds the row's own bit */
-    const int prefix = slot - node, len = slot + 1;
-    const size_t pi = ((size_t)row * QH + h) * nsplit + sp;
-    float* po = part + (size_t)rows * QH * nsplit * 2 + pi * KV8_HD;
-    const int t0 = sp * KV8_TILE;
-    if (t0 >= len) { /* uniform: an empty split */
-        po[t] = 0.f;
-        if (t == 0) {
-            part[pi * 2] = -INFINITY;
-            part[pi * 2 + 1] = 0.f;
+    constexpr int QH = 32, KVH = 8;
+    __shared__ __attribute__((aligned(16))) uint8_t s_v[A8_TILE * EL];
+    /* [hi / lo][group][q tile][query][slot] */
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[2][4][2][16][A8_PS];
+    const int lane = threadIdx.x, qq = lane >> 4, c = lane & 15;
+    const S2pAttnSeg sg = segs[blockIdx.x];
+    const int kvh = blockIdx.y, sp = blockIdx.z;
+    const int span = min(sg.span, plan.max_seq);
+    const int p_begin = sp * split_pos;
+    const int p_end = min(p_begin + split_pos, span);
+    const Kv8Plane kp = kv8_plane<BW>(plan, sg.sess, layer, kvh);
+    const Kv8Plane vp = kv8_plane<BW>(plan, sg.sess, layer, KVH + kvh);
+    const float scale = 0.08838834764831845f;
+
+    /* visibility of this lane's score rows rl = 4 qt + qq */
+    uint64_t vis[2];
+    int len[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int rl = 4 * qt + qq;
+        vis[qt] = rl < sg.nrows ? plan.vis[sg.row0 + rl] : 0ull;
+        len[qt] = vis[qt] ? sg.L + 64 - __builtin_clzll(vis[qt]) : 0;
+    }
+    /* Q operands: A row c of tile qt = query vector 16 qt + c = (row rl, head g) */
+    s2p_u32x4 qa[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int qv = 16 * qt + c, rl = qv >> 2, g = qv & 3;
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++)
+            qa[qt][ch] = rl < sg.nrows
+                             ? *(const s2p_u32x4*)(q + (size_t)(sg.row0 + rl) * QH * KV8_HD +
+                                                   (4 * kvh + g) * KV8_HD + 32 * ch + 8 * qq)
+                             : (s2p_u32x4){0u, 0u, 0u, 0u};
+    }
+    float m[2][4], l[2][4];
+    s2p_f32x4 o[2][8];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            m[qt][v] = -INFINITY;
+            l[qt][v] = 0.f;
         }
-        return;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
-    const int kvh = h / (QH / KVH);
-    const int sess = plan.sess[row];
-    const Kv8Plane kp = kv8_plane<BW>(plan, sess, layer, kvh);
-    const Kv8Plane vp = kv8_plane<BW>(plan, sess, layer, KVH + kvh);
-    L.sq[t] = bf2f(q[((size_t)row * QH + h) * KV8_HD + t]) * 0.08838834764831845f;
-    __syncthreads();
-    float m = -INFINITY, corr;
-    const float l = kv8_tile<BW, true>(kp.pay, kp.sc, t0, len, m, corr, L, true, prefix, vis);
-    const int lim = min(KV8_TILE, len - t0);
-    float a = 0.f;
-    for (int j2 = 0; j2 < lim; j2++) {
-        const size_t j = (size_t)(t0 + j2);
-        a = fmaf(L.sp[j2] * h2f(vp.sc[j * 4 + (t >> 5)]), kv8_val(vp.pay + j * EL, t, BW), a);
+
+    for (int tb = p_begin; tb < p_end; tb += A8_TILE) {
+        /* V codes of the tile to LDS (16 B per lane per load; rows past the
+         * split read the last row, never used) */
+#pragma unroll
+        for (int i = 0; i < A8_TILE * EL / 1024; i++) {
+            const int off = (i * 64 + lane) * 16, t = off / EL;
+            const int pos = min(tb + t, p_end - 1);
+            *(s2p_u32x4*)(s_v + off) = *(const s2p_u32x4*)(vp.pay + (size_t)pos * EL + off % EL);
+        }
+        /* K operands: B column c = slot tb + 16 ps + c, dims 32 ch + 8 qq .. + 8 */
+        s2p_u32x4 kr[2][4];
+        s2p_u32x2 ksc[2], vsc[2];
+#pragma unroll
+        for (int ps = 0; ps < 2; ps++) {
+            const int pos = min(tb + 16 * ps + c, p_end - 1);
+            const int8_t* kr0 = kp.pay + (size_t)pos * EL;
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++) {
+                uint32_t w[2];
+                if (BW == 8) {
+                    const s2p_u32x2 t = *(const s2p_u32x2*)(kr0 + 32 * ch + 8 * qq);
+                    w[0] = t[0];
+                    w[1] = t[1];
+                } else {
+                    w[0] = *(const uint32_t*)(kr0 + 16 * ch + 4 * qq);
+                }
+                uint32_t b[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t wd = BW == 8 ? w[e >> 1] : w[0];
+                    const int k0 = BW == 8 ? 2 * (e & 1) : 2 * e;
+                    b[e] = bf_pair(a8_code<BW>(wd, k0), a8_code<BW>(wd, k0 + 1));
+                }
+                kr[ps][ch] = (s2p_u32x4){b[0], b[1], b[2], b[3]};
+            }
+            ksc[ps] = *(const s2p_u32x2*)(kp.sc + (size_t)pos * 4);
+            vsc[ps] = *(const s2p_u32x2*)(vp.sc + (size_t)pos * 4);
+        }
+        /* scores and the online softmax; lane (qq, c) element v = row 4 qt + qq,
+         * head v, slot tb + 16 ps + c */
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            s2p_f32x4 sc[2];
+#pragma unroll
+            for (int ps = 0; ps < 2; ps++) {
+                sc[ps] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ch = 0; ch < 4; ch++) {
+                    const s2p_f32x4 d = mfma16x16x32(qa[qt][ch], kr[ps][ch],
+                                                     (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+                    const uint32_t sw = ksc[ps][ch >> 1];
+                    const float ks = h2f((uint16_t)(ch & 1 ? sw >> 16 : sw & 0xFFFF));
+#pragma unroll
+                    for (int v = 0; v < 4; v++) sc[ps][v] = fmaf(ks, d[v], sc[ps][v]);
+                }
+            }
+            const int L = sg.L;
+            bool vs_ok[2];
+#pragma unroll
+            for (int ps = 0; ps < 2; ps++) {
+                const int j = tb + 16 * ps + c;
+                vs_ok[ps] = j < len[qt] && (j < L || ((vis[qt] >> (j - L)) & 1ull));
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float t0 = vs_ok[0] ? sc[0][v] * scale : -INFINITY;
+                const float t1 = vs_ok[1] ? sc[1][v] * scale : -INFINITY;
+                const float tm = max16(fmaxf(t0, t1));
+                const float mn = fmaxf(m[qt][v], tm);
+                const float ms = mn == -INFINITY ? 0.f : mn;
+                const float corr = __expf(m[qt][v] - ms);
+                const float p[2] = {__expf(t0 - ms), __expf(t1 - ms)};
+                l[qt][v] = l[qt][v] * corr + p[0] + p[1];
+                m[qt][v] = mn;
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
+#pragma unroll
+                for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t vw = vsc[ps][g >> 1];
+                        const float pv =
+                            p[ps] * h2f((uint16_t)(g & 1 ? vw >> 16 : vw & 0xFFFF));
+                        const uint16_t hi = f2bf(pv);
+                        s_p[0][g][qt][4 * qq + v][16 * ps + c] = hi;
+                        s_p[1][g][qt][4 * qq + v][16 * ps + c] = f2bf(pv - bf2f(hi));
+                    }
+            }
+        }
+        wave_sync_lds();
+        /* PV: B column c = dim 16 dt + c, rows = slots 8 qq .. 8 qq + 7 */
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const int d = 16 * dt + c, g = dt >> 1;
+            uint32_t b[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float x[2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint8_t* row = s_v + (8 * qq + 2 * e + h) * EL;
+                    if (BW == 8) {
+                        x[h] = (float)(int8_t)row[d];
+                    } else {
+                        const int nib = (d & 1) ? (row[d >> 1] >> 4) : (row[d >> 1] & 0xF);
+                        x[h] = (float)(nib >= 8 ? nib - 16 : nib);
+                    }
+                }
+                b[e] = bf_pair(x[0], x[1]);
+            }
+            const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                const s2p_u32x4 pa = *(const s2p_u32x4*)&s_p[0][g][qt][c][8 * qq];
+                const s2p_u32x4 pl = *(const s2p_u32x4*)&s_p[1][g][qt][c][8 * qq];
+                o[qt][dt] = mfma16x16x32(pl, bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(pa, bv, o[qt][dt]);
+            }
+        }
+        wave_sync_lds(); /* s_v and s_p are rewritten by the next tile */
     }
-    po[t] = a;
-    if (t == 0) {
-        part[pi * 2] = m;
-        part[pi * 2 + 1] = l;
+
+    /* partials of the served (row, head) pairs */
+    const size_t obase = (size_t)rows * QH * nsplit * 2;
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int rl = 4 * qt + qq;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float lt = sum16(l[qt][v]);
+            if (rl >= sg.nrows) continue;
+            const size_t pi = ((size_t)(sg.row0 + rl) * QH + 4 * kvh + v) * nsplit + sp;
+            if (c == 0) {
+                part[pi * 2] = m[qt][v];
+                part[pi * 2 + 1] = lt;
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) part[obase + pi * KV8_HD + 16 * dt + c] = o[qt][dt][v];
+        }
     }
 }
 
@@ -508,19 +687,24 @@ extern "C" hipError_t s2p_qkrope_append8_launch(const void* qkv, void* q_out, co
 }
 
 extern "C" hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pRowPlan* plan,
-                                            int rows, int layer, int max_span, float* part,
-                                            int bw, hipStream_t st) {
-    if (rows <= 0) return hipSuccess;
+                                            const S2pAttnSeg* segs, int n_seg, int rows,
+                                            int layer, int max_span, float* part, int bw,
+                                            hipStream_t st) {
+    if (rows <= 0 || n_seg <= 0) return hipSuccess;
     if ((bw != 8 && bw != 4) || max_span <= 0 || max_span > plan->max_seq)
         return hipErrorInvalidValue;
-    const int nsplit = (max_span + KV8_TILE - 1) / KV8_TILE;
-    const dim3 grid((unsigned)rows, 32u, (unsigned)nsplit);
+    /* 128-slot splits, longer while the grid exceeds 4096 waves (the part
+     * scratch is sized for 128) */
+    int split_pos = KV8_TILE;
+    while ((int64_t)n_seg * 8 * ((max_span + split_pos - 1) / split_pos) > 4096) split_pos *= 2;
+    const int nsplit = (max_span + split_pos - 1) / split_pos;
+    const dim3 grid((unsigned)n_seg, 8u, (unsigned)nsplit);
     if (bw == 8)
-        hipLaunchKernelGGL(k_attention8_plan<8>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
-                           *plan, layer, rows, nsplit, part);
+        hipLaunchKernelGGL(k_attn8_mfma<8>, grid, dim3(64), 0, st, (const uint16_t*)q, *plan,
+                           segs, layer, rows, nsplit, split_pos, part);
     else
-        hipLaunchKernelGGL(k_attention8_plan<4>, grid, dim3(KV8_TILE), 0, st, (const uint16_t*)q,
-                           *plan, layer, rows, nsplit, part);
+        hipLaunchKernelGGL(k_attn8_mfma<4>, grid, dim3(64), 0, st, (const uint16_t*)q, *plan,
+                           segs, layer, rows, nsplit, split_pos, part);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return s2p_attn_combine_launch(part, (uint16_t*)out, rows, 32, nsplit, st);

@@ -71,9 +71,11 @@ hipError_t s2p_qkrope_append8_launch(const void* qkv, void* q_out, const void* q
                                      const void* kn_w, const S2pRowPlan* plan, int rows,
                                      int layer, float eps, const float* rope_tab, int bw,
                                      hipStream_t st);
-/* split attention over 128-slot tiles + the combine into out */
-hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pRowPlan* plan, int rows,
-                                 int layer, int max_span, float* part, int bw, hipStream_t st);
+/* split attention over the plan's segments (matrix cores) + the combine
+ * into out; part holds s2p_attn8_plan_part_floats(rows, max_span) floats */
+hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pRowPlan* plan,
+                                 const S2pAttnSeg* segs, int n_seg, int rows, int layer,
+                                 int max_span, float* part, int bw, hipStream_t st);
 hipError_t s2p_kv_commit8_launch(const S2pRowPlan* plan, const int32_t* path,
                                  const int32_t* n_acc, int n_sess, int R, int n_layers, int bw,
                                  hipStream_t st);
