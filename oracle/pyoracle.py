@@ -69,7 +69,7 @@ _SIGS = {
     "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P]),
     "or_linear_fwd": (None, [P, P, P, I]),
     "or_layer": (None, [P, P, I, P, P, I, I, P, P]),
-    "or_layer8": (None, [P, P, I, P, P, P, P, I, I, P, P, I]),
+    "or_layer8": (None, [P, P, I, P, P, P, P, I, I, P, P, I, I]),
     "or_gemm_bf16": (None, [P, P, P, I, I, I]),
     "or_gemm_bf16_f64": (None, [P, P, P, I, I, I]),
     "or_draft_step": (None, [P, P, P, I, I, P, P, P]),
@@ -356,12 +356,13 @@ def layer(lw, x, rows, kc, vc, max_seq, prefix, pos, vis=None):
                    ptr(pa), ptr(va))
 
 
-def layer8(lw, x, rows, kc, vc, ks, vs, max_seq, prefix, pos, vis, bw):
-    """In place on x and the quantised caches (kc, vc int8; ks, vs uint16)."""
+def layer8(lw, x, rows, kc, vc, ks, vs, max_seq, prefix, pos, vis, bw, append=True):
+    """In place on x and the quantised caches (kc, vc int8; ks, vs uint16);
+    append=False reads the rows' codes from the cache instead of writing them."""
     pa = np.ascontiguousarray(pos, np.int32)
     va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
     lib().or_layer8(ctypes.addressof(lw), ptr(x), rows, ptr(kc), ptr(vc), ptr(ks), ptr(vs),
-                    max_seq, prefix, ptr(pa), ptr(va), bw)
+                    max_seq, prefix, ptr(pa), ptr(va), bw, 1 if append else 0)
 
 
 def gemm_bf16(x, w, M, N, K):

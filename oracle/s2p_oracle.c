@@ -1199,10 +1199,14 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
 /* run_layer with the INT8 / INT4 KV cache (slowar.c:156-260 with the
  * quantised-cache kernels of kernels.cu:510-946): K (after qk-norm and RoPE,
  * rounded to bf16) and V are quantised on append at slots prefix + r, and
- * the attention reads the quantised cache with the rows' visibility. */
+ * the attention reads the quantised cache with the rows' visibility.
+ * append == 0 keeps the cache as given (slots prefix + r already hold codes
+ * made elsewhere, e.g. by the GPU, so that a forward can be checked on the
+ * same cache contents: a code that rounds the other way moves the result by
+ * a whole quantisation step). */
 void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* vc,
                uint16_t* ks, uint16_t* vs, int max_seq, int prefix, const int32_t* pos,
-               const uint64_t* vis, int bw) {
+               const uint64_t* vis, int bw, int append) {
     const int dim = lw->wqkv.K;
     const int qw = 4096, kvw = 1024, ffn = lw->w2.K;
     const float eps = 1e-6f;
@@ -1223,7 +1227,7 @@ void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* 
     or_qk_norm(k, lw->k_norm, rows, 8, 128, eps);
     or_rope(q, rows, 32, 128, 0, pos, 1000000.0f);
     or_rope(k, rows, 8, 128, 0, pos, 1000000.0f);
-    or_kv_append8(k, v, &kc, &vc, &ks, &vs, rows, 8, prefix, NULL, max_seq, bw);
+    if (append) or_kv_append8(k, v, &kc, &vc, &ks, &vs, rows, 8, prefix, NULL, max_seq, bw);
     or_attention8_vis(q, kc, vc, ks, vs, att, rows, 32, 8, prefix, vis, max_seq, bw);
     or_linear_fwd(&lw->wo, att, proj, rows);
     or_add(x, proj, (int64_t)rows * dim);

@@ -194,10 +194,11 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
               uint16_t* vc, int max_seq, int prefix, const int32_t* pos,
               const uint64_t* vis);
 /* the same over one layer's INT8 / INT4 KV cache (payload [8][max_seq][128
- * or 64], f16 scales [8][max_seq][4]); rows append at slots prefix + r */
+ * or 64], f16 scales [8][max_seq][4]); rows append at slots prefix + r
+ * (append != 0) or find their codes there already (append == 0) */
 void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* vc,
                uint16_t* ks, uint16_t* vs, int max_seq, int prefix, const int32_t* pos,
-               const uint64_t* vis, int bw);
+               const uint64_t* vis, int bw, int append);
 
 /* ---- the draft model (src/draft/draft.c:157-202) ---------------------- */
 /* y[M,N] = bf16(sum_k w[n,k] x[m,k]) with an fp32 sum in increasing k: the

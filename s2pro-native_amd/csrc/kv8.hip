@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64) void k_qkrope_append8(const uint16_t* __restric
  *     group scale: s = sum_g ks[slot][g] * (q_g . k_g);
  *   PV: the codes of V (exact in bf16) are the B operand and the group scale
  *     rides in P: the A operand of output dims in group g is p * vs[slot][g],
- *     split hi + lo in bf16 (16 significant bits, as the bf16 kernel's P).
+ *     split hi + lo in bf16 by truncation (16 significant bits).
  * Each split writes the (m, l, O) partial of every (row, head) it serves;
  * s2p_attn_combine_launch merges them.  Arithmetic is fp32 throughout, in an
  * order of its own (tolerance-checked against the reference-order oracle). */
@@ -422,9 +422,9 @@ __global__ __launch_bounds__(64) void k_qkrope_append8(const uint16_t* __restric
 #define A8_PS 40 /* P row stride in bf16 (32 slots + 8 pad) */
 
 static __device__ __forceinline__ uint32_t bf_pair(float lo, float hi) {
-    /* small integers and their products with f16 scales: callers pass values
-     * exact in bf16 or round first */
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    /* two values exact in bf16 (the codes, |x| <= 127): their upper halves,
+     * packed with one byte permute */
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
 template <int BW>
@@ -490,44 +490,61 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int tb = p_begin; tb < p_end; tb += A8_TILE) {
-        /* V codes of the tile to LDS (16 B per lane per load; rows past the
-         * split read the last row, never used) */
+    /* raw codes and scales of one tile, loaded a tile ahead of their use:
+     * V rows (16 B per lane per load; rows past the split read the last
+     * row, never used), this lane's K words of slots tb + 16 ps + c (dims
+     * 32 ch + 8 qq .. + 8) and those slots' K / V group scales */
+    constexpr int NV = A8_TILE * EL / 1024, NKW = BW == 8 ? 2 : 1;
+    s2p_u32x4 rv[NV];
+    uint32_t rk[2][4][NKW];
+    s2p_u32x2 rks[2], rvs[2];
+    auto load_tile = [&](int tb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < A8_TILE * EL / 1024; i++) {
+        for (int i = 0; i < NV; i++) {
             const int off = (i * 64 + lane) * 16, t = off / EL;
             const int pos = min(tb + t, p_end - 1);
-            *(s2p_u32x4*)(s_v + off) = *(const s2p_u32x4*)(vp.pay + (size_t)pos * EL + off % EL);
+            rv[i] = *(const s2p_u32x4*)(vp.pay + (size_t)pos * EL + off % EL);
         }
-        /* K operands: B column c = slot tb + 16 ps + c, dims 32 ch + 8 qq .. + 8 */
-        s2p_u32x4 kr[2][4];
-        s2p_u32x2 ksc[2], vsc[2];
 #pragma unroll
         for (int ps = 0; ps < 2; ps++) {
             const int pos = min(tb + 16 * ps + c, p_end - 1);
             const int8_t* kr0 = kp.pay + (size_t)pos * EL;
 #pragma unroll
             for (int ch = 0; ch < 4; ch++) {
-                uint32_t w[2];
                 if (BW == 8) {
                     const s2p_u32x2 t = *(const s2p_u32x2*)(kr0 + 32 * ch + 8 * qq);
-                    w[0] = t[0];
-                    w[1] = t[1];
+                    rk[ps][ch][0] = t[0];
+                    rk[ps][ch][NKW - 1] = t[1];
                 } else {
-                    w[0] = *(const uint32_t*)(kr0 + 16 * ch + 4 * qq);
+                    rk[ps][ch][0] = *(const uint32_t*)(kr0 + 16 * ch + 4 * qq);
                 }
+            }
+            rks[ps] = *(const s2p_u32x2*)(kp.sc + (size_t)pos * 4);
+            rvs[ps] = *(const s2p_u32x2*)(vp.sc + (size_t)pos * 4);
+        }
+    };
+    if (p_begin < p_end) load_tile(p_begin);
+
+    for (int tb = p_begin; tb < p_end; tb += A8_TILE) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) *(s2p_u32x4*)(s_v + (i * 64 + lane) * 16) = rv[i];
+        /* K operands: B column c = slot tb + 16 ps + c */
+        s2p_u32x4 kr[2][4];
+        const s2p_u32x2 ksc[2] = {rks[0], rks[1]}, vsc[2] = {rvs[0], rvs[1]};
+#pragma unroll
+        for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++) {
                 uint32_t b[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint32_t wd = BW == 8 ? w[e >> 1] : w[0];
+                    const uint32_t wd = BW == 8 ? rk[ps][ch][e >> 1] : rk[ps][ch][0];
                     const int k0 = BW == 8 ? 2 * (e & 1) : 2 * e;
                     b[e] = bf_pair(a8_code<BW>(wd, k0), a8_code<BW>(wd, k0 + 1));
                 }
                 kr[ps][ch] = (s2p_u32x4){b[0], b[1], b[2], b[3]};
             }
-            ksc[ps] = *(const s2p_u32x2*)(kp.sc + (size_t)pos * 4);
-            vsc[ps] = *(const s2p_u32x2*)(vp.sc + (size_t)pos * 4);
-        }
+        if (tb + A8_TILE < p_end) load_tile(tb + A8_TILE);
         /* scores and the online softmax; lane (qq, c) element v = row 4 qt + qq,
          * head v, slot tb + 16 ps + c */
 #pragma unroll
@@ -564,8 +581,11 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
                 const float p[2] = {__expf(t0 - ms), __expf(t1 - ms)};
                 l[qt][v] = l[qt][v] * corr + p[0] + p[1];
                 m[qt][v] = mn;
+                /* rescale O only when some running max of the wave moved */
+                if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
 #pragma unroll
-                for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
+                    for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
+                }
 #pragma unroll
                 for (int ps = 0; ps < 2; ps++)
 #pragma unroll
@@ -573,9 +593,13 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
                         const uint32_t vw = vsc[ps][g >> 1];
                         const float pv =
                             p[ps] * h2f((uint16_t)(g & 1 ? vw >> 16 : vw & 0xFFFF));
-                        const uint16_t hi = f2bf(pv);
-                        s_p[0][g][qt][4 * qq + v][16 * ps + c] = hi;
-                        s_p[1][g][qt][4 * qq + v][16 * ps + c] = f2bf(pv - bf2f(hi));
+                        /* pv >= 0 = hi + lo, both truncated to bf16: 16
+                         * significant bits */
+                        const uint32_t hb = __float_as_uint(pv) & 0xFFFF0000u;
+                        const float lo = pv - __uint_as_float(hb);
+                        s_p[0][g][qt][4 * qq + v][16 * ps + c] = (uint16_t)(hb >> 16);
+                        s_p[1][g][qt][4 * qq + v][16 * ps + c] =
+                            (uint16_t)(__float_as_uint(lo) >> 16);
                     }
             }
         }

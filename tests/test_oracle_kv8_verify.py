@@ -107,6 +107,7 @@ def test_layer8_tracks_bf16_layer(bw, parent):
     pos = (L + depth).astype(np.int32)
     x = po.f32_to_bf16(r.standard_normal((R, dim)).astype(np.float32))
     x8, xb = x.copy(), x.copy()
+    kc8_0, vc8_0, ks8_0, vs8_0 = kc8.copy(), vc8.copy(), ks8.copy(), vs8.copy()
     po.layer8(lw, x8, R, kc8, vc8, ks8, vs8, ctx, L, pos, None if chain else vis, bw)
     po.layer(lw, xb, R, kc, vc, ctx, L, pos, None if chain else vis)
     # the appended slots are the quantisation of the bf16 layer's appended K / V
@@ -123,3 +124,11 @@ def test_layer8_tracks_bf16_layer(bw, parent):
     rel = np.sqrt(np.mean((a - b) ** 2) / np.mean(b ** 2))
     assert rel < (2e-2 if bw == 8 else 6e-2), rel
     assert not np.array_equal(a, b)
+    # append=False over the appended cache reproduces the forward exactly;
+    # over the cache before the append it does not (the new slots are read)
+    for kc_, vc_, ks_, vs_, same in ((kc8, vc8, ks8, vs8, True),
+                                     (kc8_0, vc8_0, ks8_0, vs8_0, False)):
+        x2 = x.copy()
+        po.layer8(lw, x2, R, kc_.copy(), vc_.copy(), ks_.copy(), vs_.copy(), ctx, L, pos,
+                  None if chain else vis, bw, append=False)
+        assert np.array_equal(x2, x8) == same
