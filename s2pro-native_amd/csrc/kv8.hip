@@ -436,7 +436,7 @@ static __device__ __forceinline__ float a8_code(uint32_t word, int k) {
 }
 
 template <int BW>
-__global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ q,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_attn8_mfma(const uint16_t* __restrict__ q,
                                                    S2pRowPlan plan,
                                                    const S2pAttnSeg* __restrict__ segs,
                                                    int layer, int rows, int nsplit,
@@ -444,8 +444,9 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
     constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
     constexpr int QH = 32, KVH = 8;
     __shared__ __attribute__((aligned(16))) uint8_t s_v[A8_TILE * EL];
-    /* [hi / lo][group][q tile][query][slot] */
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[2][4][2][16][A8_PS];
+    /* P of one scale group: [hi / lo][q tile][query][slot] */
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[2][2][16][A8_PS];
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[32][KV8_HD + 8];
     const int lane = threadIdx.x, qq = lane >> 4, c = lane & 15;
     const S2pAttnSeg sg = segs[blockIdx.x];
     const int kvh = blockIdx.y, sp = blockIdx.z;
@@ -465,18 +466,20 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
         vis[qt] = rl < sg.nrows ? plan.vis[sg.row0 + rl] : 0ull;
         len[qt] = vis[qt] ? sg.L + 64 - __builtin_clzll(vis[qt]) : 0;
     }
-    /* Q operands: A row c of tile qt = query vector 16 qt + c = (row rl, head g) */
-    s2p_u32x4 qa[2][4];
+    /* Q operands (A row c of tile qt = query vector 16 qt + c = (row rl, head
+     * g)) staged in LDS once and read per use, which keeps registers for
+     * two waves per SIMD */
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
         const int qv = 16 * qt + c, rl = qv >> 2, g = qv & 3;
 #pragma unroll
         for (int ch = 0; ch < 4; ch++)
-            qa[qt][ch] = rl < sg.nrows
-                             ? *(const s2p_u32x4*)(q + (size_t)(sg.row0 + rl) * QH * KV8_HD +
-                                                   (4 * kvh + g) * KV8_HD + 32 * ch + 8 * qq)
-                             : (s2p_u32x4){0u, 0u, 0u, 0u};
+            *(s2p_u32x4*)&s_q[qv][32 * ch + 8 * qq] =
+                rl < sg.nrows ? *(const s2p_u32x4*)(q + (size_t)(sg.row0 + rl) * QH * KV8_HD +
+                                                    (4 * kvh + g) * KV8_HD + 32 * ch + 8 * qq)
+                              : (s2p_u32x4){0u, 0u, 0u, 0u};
     }
+    wave_sync_lds();
     float m[2][4], l[2][4];
     s2p_f32x4 o[2][8];
 #pragma unroll
@@ -528,11 +531,13 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
     for (int tb = p_begin; tb < p_end; tb += A8_TILE) {
 #pragma unroll
         for (int i = 0; i < NV; i++) *(s2p_u32x4*)(s_v + (i * 64 + lane) * 16) = rv[i];
-        /* K operands: B column c = slot tb + 16 ps + c */
-        s2p_u32x4 kr[2][4];
+        /* scores: B column c = slot tb + 16 ps + c; the codes converted as
+         * they are used.  lane (qq, c) element v = row 4 qt + qq, head v */
         const s2p_u32x2 ksc[2] = {rks[0], rks[1]}, vsc[2] = {rvs[0], rvs[1]};
+        s2p_f32x4 scs[2][2];
 #pragma unroll
-        for (int ps = 0; ps < 2; ps++)
+        for (int ps = 0; ps < 2; ps++) {
+            scs[0][ps] = scs[1][ps] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ch = 0; ch < 4; ch++) {
                 uint32_t b[4];
@@ -542,27 +547,24 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
                     const int k0 = BW == 8 ? 2 * (e & 1) : 2 * e;
                     b[e] = bf_pair(a8_code<BW>(wd, k0), a8_code<BW>(wd, k0 + 1));
                 }
-                kr[ps][ch] = (s2p_u32x4){b[0], b[1], b[2], b[3]};
-            }
-        if (tb + A8_TILE < p_end) load_tile(tb + A8_TILE);
-        /* scores and the online softmax; lane (qq, c) element v = row 4 qt + qq,
-         * head v, slot tb + 16 ps + c */
+                const s2p_u32x4 kb = {b[0], b[1], b[2], b[3]};
+                const uint32_t sw = ksc[ps][ch >> 1];
+                const float ks = h2f((uint16_t)(ch & 1 ? sw >> 16 : sw & 0xFFFF));
 #pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
-            s2p_f32x4 sc[2];
+                for (int qt = 0; qt < 2; qt++) {
+                    const s2p_u32x4 qa = *(const s2p_u32x4*)&s_q[16 * qt + c][32 * ch + 8 * qq];
+                    const s2p_f32x4 d = mfma16x16x32(qa, kb, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int ps = 0; ps < 2; ps++) {
-                sc[ps] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ch = 0; ch < 4; ch++) {
-                    const s2p_f32x4 d = mfma16x16x32(qa[qt][ch], kr[ps][ch],
-                                                     (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
-                    const uint32_t sw = ksc[ps][ch >> 1];
-                    const float ks = h2f((uint16_t)(ch & 1 ? sw >> 16 : sw & 0xFFFF));
-#pragma unroll
-                    for (int v = 0; v < 4; v++) sc[ps][v] = fmaf(ks, d[v], sc[ps][v]);
+                    for (int v = 0; v < 4; v++) scs[qt][ps][v] = fmaf(ks, d[v], scs[qt][ps][v]);
                 }
             }
+        }
+        if (tb + A8_TILE < p_end) load_tile(tb + A8_TILE);
+        /* online softmax: p of (row 4 qt + qq, head v) at slots tb + 16 ps + c */
+        float pr[2][4][2];
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const s2p_f32x4* sc = scs[qt];
             const int L = sg.L;
             bool vs_ok[2];
 #pragma unroll
@@ -578,62 +580,70 @@ __global__ __launch_bounds__(64) void k_attn8_mfma(const uint16_t* __restrict__ 
                 const float mn = fmaxf(m[qt][v], tm);
                 const float ms = mn == -INFINITY ? 0.f : mn;
                 const float corr = __expf(m[qt][v] - ms);
-                const float p[2] = {__expf(t0 - ms), __expf(t1 - ms)};
-                l[qt][v] = l[qt][v] * corr + p[0] + p[1];
+                pr[qt][v][0] = __expf(t0 - ms);
+                pr[qt][v][1] = __expf(t1 - ms);
+                l[qt][v] = l[qt][v] * corr + pr[qt][v][0] + pr[qt][v][1];
                 m[qt][v] = mn;
                 /* rescale O only when some running max of the wave moved */
                 if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
 #pragma unroll
                     for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
                 }
+            }
+        }
+        /* PV one scale group at a time (dims 32 g .. 32 g + 31): A = p * vs[slot][g]
+         * through LDS, B = the V codes (column c = dim 16 dt + c, rows = slots
+         * 8 qq .. 8 qq + 7) */
 #pragma unroll
-                for (int ps = 0; ps < 2; ps++)
+        for (int g = 0; g < 4; g++) {
 #pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const uint32_t vw = vsc[ps][g >> 1];
-                        const float pv =
-                            p[ps] * h2f((uint16_t)(g & 1 ? vw >> 16 : vw & 0xFFFF));
+            for (int ps = 0; ps < 2; ps++) {
+                const uint32_t vw = vsc[ps][g >> 1];
+                const float vs = h2f((uint16_t)(g & 1 ? vw >> 16 : vw & 0xFFFF));
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
                         /* pv >= 0 = hi + lo, both truncated to bf16: 16
                          * significant bits */
+                        const float pv = pr[qt][v][ps] * vs;
                         const uint32_t hb = __float_as_uint(pv) & 0xFFFF0000u;
                         const float lo = pv - __uint_as_float(hb);
-                        s_p[0][g][qt][4 * qq + v][16 * ps + c] = (uint16_t)(hb >> 16);
-                        s_p[1][g][qt][4 * qq + v][16 * ps + c] =
-                            (uint16_t)(__float_as_uint(lo) >> 16);
+                        s_p[0][qt][4 * qq + v][16 * ps + c] = (uint16_t)(hb >> 16);
+                        s_p[1][qt][4 * qq + v][16 * ps + c] = (uint16_t)(__float_as_uint(lo) >> 16);
                     }
             }
-        }
-        wave_sync_lds();
-        /* PV: B column c = dim 16 dt + c, rows = slots 8 qq .. 8 qq + 7 */
+            wave_sync_lds();
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            const int d = 16 * dt + c, g = dt >> 1;
-            uint32_t b[4];
+            for (int dh = 0; dh < 2; dh++) {
+                const int dt = 2 * g + dh, d = 16 * dt + c;
+                uint32_t b[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float x[2];
+                for (int e = 0; e < 4; e++) {
+                    float x[2];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const uint8_t* row = s_v + (8 * qq + 2 * e + h) * EL;
-                    if (BW == 8) {
-                        x[h] = (float)(int8_t)row[d];
-                    } else {
-                        const int nib = (d & 1) ? (row[d >> 1] >> 4) : (row[d >> 1] & 0xF);
-                        x[h] = (float)(nib >= 8 ? nib - 16 : nib);
+                    for (int h = 0; h < 2; h++) {
+                        const uint8_t* row = s_v + (8 * qq + 2 * e + h) * EL;
+                        if (BW == 8) {
+                            x[h] = (float)(int8_t)row[d];
+                        } else {
+                            const int nib = (d & 1) ? (row[d >> 1] >> 4) : (row[d >> 1] & 0xF);
+                            x[h] = (float)(nib >= 8 ? nib - 16 : nib);
+                        }
                     }
+                    b[e] = bf_pair(x[0], x[1]);
                 }
-                b[e] = bf_pair(x[0], x[1]);
-            }
-            const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+                const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
 #pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
-                const s2p_u32x4 pa = *(const s2p_u32x4*)&s_p[0][g][qt][c][8 * qq];
-                const s2p_u32x4 pl = *(const s2p_u32x4*)&s_p[1][g][qt][c][8 * qq];
-                o[qt][dt] = mfma16x16x32(pl, bv, o[qt][dt]);
-                o[qt][dt] = mfma16x16x32(pa, bv, o[qt][dt]);
+                for (int qt = 0; qt < 2; qt++) {
+                    const s2p_u32x4 pa = *(const s2p_u32x4*)&s_p[0][qt][c][8 * qq];
+                    const s2p_u32x4 pl = *(const s2p_u32x4*)&s_p[1][qt][c][8 * qq];
+                    o[qt][dt] = mfma16x16x32(pl, bv, o[qt][dt]);
+                    o[qt][dt] = mfma16x16x32(pa, bv, o[qt][dt]);
+                }
             }
+            wave_sync_lds(); /* s_p is rewritten by the next group */
         }
-        wave_sync_lds(); /* s_v and s_p are rewritten by the next tile */
     }
 
     /* partials of the served (row, head) pairs */
