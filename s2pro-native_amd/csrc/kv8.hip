@@ -406,7 +406,8 @@ __global__ __launch_bounds__(64) void k_qkrope_append8(const uint16_t* __restric
 }
 
 /* Verify-plan attention over quantised caches on the matrix cores: one wave
- * per (segment of <= 8 rows of a session, kv head, position split); its 32
+ * per (segment of <= 8 rows of a session, kv head, position split: splits
+ * sized so the grid is one resident round); its 32
  * query vectors (8 rows x the 4 query heads of the kv head) are two 16-row
  * MFMA tiles, as in the bf16 kernel.  Per 32-slot tile:
  *   scores: the int8 (int4) codes are exact in bf16, so each 32-dim group g
@@ -727,10 +728,22 @@ extern "C" hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pR
     if (rows <= 0 || n_seg <= 0) return hipSuccess;
     if ((bw != 8 && bw != 4) || max_span <= 0 || max_span > plan->max_seq)
         return hipErrorInvalidValue;
-    /* 128-slot splits, longer while the grid exceeds 4096 waves (the part
-     * scratch is sized for 128) */
-    int split_pos = KV8_TILE;
-    while ((int64_t)n_seg * 8 * ((max_span + split_pos - 1) / split_pos) > 4096) split_pos *= 2;
+    /* splits of >= 128 slots (the part scratch is sized for 128), as short
+     * as one resident round of waves allows (two per SIMD: 8 per CU) */
+    static int cus = 0;
+    if (cus <= 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+    }
+    const int64_t per_split = (int64_t)n_seg * 8;
+    int64_t ns_max = (int64_t)cus * 8 / per_split;
+    if (ns_max < 1) ns_max = 1;
+    int split_pos = (int)((max_span + ns_max - 1) / ns_max);
+    split_pos = (split_pos + A8_TILE - 1) / A8_TILE * A8_TILE;
+    if (split_pos < KV8_TILE) split_pos = KV8_TILE;
     const int nsplit = (max_span + split_pos - 1) / split_pos;
     const dim3 grid((unsigned)n_seg, 8u, (unsigned)nsplit);
     if (bw == 8)
