@@ -91,6 +91,17 @@ def measured_traffic():
     return None
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(budget_s=20.0):
     """Scalar C oracle (one core): one layer (4 GEMVs in the reference lane
     order, norms, RoPE, attention over 2048 slots, SwiGLU) plus the head GEMV,
@@ -121,6 +132,7 @@ def cpu_baseline(budget_s=20.0):
     t_head = (time.perf_counter() - t0) * 8
     step = N_LAYERS * t_layer + t_head
     return {"value": round(1.0 / step, 6), "unit": "steps/s", "cores": 1, "kind": "port",
+            "host_cpus_online": os.sysconf("SC_NPROCESSORS_ONLN"), "host_cpu_model": _cpu_model(),
             "sample": f"1 of 36 layers ({t_layer:.2f} s) + 1/8 of the head GEMV, scalar C "
                       f"oracle at -O2, extrapolated to 36 layers + full head "
                       f"({step:.1f} s per step)"}
@@ -173,20 +185,22 @@ def main():
                                    max(16, M), NS, ctx, args.kv_bits)
         bb = ctypes.c_void_p()
         s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(opts), 2026, S, ctypes.byref(bb)))
-        kvs = []
+        kvs, scs = [], []
         for s_ in range(NS):
             kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
             s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0,
                                                        5 + s_, S))
+            kvs.append(kv)
             if args.kv_bits != 16:
                 # quantised cache: random codes, every group scale f16 0.01
-                pay = 16 * ctx * 128 * args.kv_bits // 8
-                lb = pay + 16 * ctx * 8
-                kv.view(torch.uint8).view(N_LAYERS, lb)[:, pay:].view(torch.int16).fill_(0x211F)
-            kvs.append(kv)
+                sc = torch.full((lib.s2p_backbone_kv_scale_bytes(bb) // 2,), 0x211F,
+                                dtype=torch.int16, device=dev)
+                scs.append(sc)
         kvp = (ctypes.c_void_p * NS)(*[k.data_ptr() for k in kvs])
+        scp = (ctypes.c_void_p * NS)(*[c.data_ptr() for c in scs]) if scs else None
         ln = np.array(lens, np.int32)
-        vb = s2pamd.VerifyBatch(NS, R, parent.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
+        vb = s2pamd.VerifyBatch(NS, R, parent.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data,
+                                ctypes.addressof(scp) if scp is not None else None)
         s2pamd.check(lib.s2p_verify_plan(bb, ctypes.byref(vb), S))
         x = torch.empty((M, 2560), dtype=torch.int16, device=dev)
         s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(x), x.numel(), 0.0, 1.0, 9, S))

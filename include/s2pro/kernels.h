@@ -55,6 +55,11 @@ hipError_t s2pk_silu_mul(const s2p_bf16* gu, s2p_bf16* h, int rows, int ffn,
 /* y = bf16(y + x) over n elements (kernels.cu:1242-1254) */
 hipError_t s2pk_add(s2p_bf16* y, const s2p_bf16* x, int64_t n, hipStream_t st);
 
+/* logits bf16 [vocab] -> fp32 scratch [vocab], exact widening: the sampler
+ * contract's device staging (kernels.h:65-66, kernels.cu:1315-1322) */
+hipError_t s2pk_sample_prepare(const s2p_bf16* logits, float* scratch, int vocab,
+                               hipStream_t st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,9 +83,11 @@ s2p_slow_layer* s2p_backbone_layer(s2p_backbone* b, int layer);
 s2p_linear*     s2p_backbone_head(s2p_backbone* b);
 void*           s2p_backbone_final_norm(s2p_backbone* b);
 /* bytes of one session's KV: [n_layers][2 * 8][ctx_len][128] bf16, or with
- * kv_bits 8 / 4 per layer the payload [2 * 8][ctx_len][128 or 64] int8 and
- * then its f16 scales [2 * 8][ctx_len][4] */
+ * kv_bits 8 / 4 the codes [n_layers][2 * 8][ctx_len][128 or 64] int8 */
 size_t          s2p_backbone_kv_bytes(const s2p_backbone* b);
+/* bytes of one session's f16 group scales [n_layers][2 * 8][ctx_len][4]
+ * (kv_bits 8 / 4; 0 for a bf16 cache) */
+size_t          s2p_backbone_kv_scale_bytes(const s2p_backbone* b);
 /* weight bytes streamed by one verify step (backbone + head) */
 size_t          s2p_backbone_weight_bytes(const s2p_backbone* b);
 
@@ -93,8 +95,13 @@ typedef struct {
     int            n_sess;
     int            rows;     /* R */
     const int32_t* parent;   /* host [R]; parent[0] = -1 */
-    void* const*   kv;       /* host [n_sess] device KV bases */
+    void* const*   kv;       /* host [n_sess] device KV bases: bf16 [layers][16][ctx][128];
+                              * INT8 / INT4 codes [layers][16][ctx][128 | 64] */
     const int32_t* kv_len;   /* host [n_sess] */
+    void* const*   kv_scales;/* host [n_sess] device bases of the INT8 / INT4 caches' f16
+                              * group scales [layers][16][ctx][4] (the reference session's
+                              * separate kvs tensor, slowar_internal.h:177-179, 208-225);
+                              * NULL for a bf16 cache */
 } s2p_verify_batch;
 
 /* Upload the per-row plan (positions, slots, visibility) and per-session KV

@@ -66,6 +66,11 @@ _SIGS = {
     "or_transform": (I, [P, P, P, P, P, P]),
     "or_sample": (ctypes.c_int64, [P, P, P, P, P]),
     "or_state_push": (None, [P, ctypes.c_int64]),
+    "or_splitmix64_next": (U64, [P]),
+    "or_xoshiro_next": (U64, [P]),
+    "or_gumbel_draw": (I, [P, P]),
+    "or_xoshiro_draw": (I, [P, P]),
+    "or_rule_u24": (ctypes.c_uint32, [P, ctypes.c_uint32]),
     "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P]),
     "or_linear_fwd": (None, [P, P, P, I]),
     "or_layer": (None, [P, P, I, P, P, I, I, P, P]),

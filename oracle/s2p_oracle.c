@@ -1004,6 +1004,13 @@ void or_state_push(or_state* sp, int64_t tok) {
     sp->count++;
 }
 
+/* Test hooks: the draw primitives and both draws, exposed so that the tests
+ * pin them against published vectors and hand-derived values. */
+uint64_t or_splitmix64_next(uint64_t* s) { return splitmix64(s); }
+uint64_t or_xoshiro_next(uint64_t s[4]) { return xoshiro_next(s); }
+int or_gumbel_draw(const or_state* sp, const float* prob) { return gumbel_draw(sp, prob); }
+int or_xoshiro_draw(or_state* sp, const float* prob) { return xoshiro_draw(sp, prob); }
+
 int64_t or_sample(or_state* sp, const uint16_t* row_bf16,
                   const uint16_t* eos_bf16, int32_t* out_sem, int* out_eos) {
     int ti[TOP_K];
@@ -1040,6 +1047,8 @@ static uint32_t rule_u24(const or_state* sp, uint32_t slot) {
     z ^= z >> 31;
     return (uint32_t)(z >> 40);
 }
+
+uint32_t or_rule_u24(const or_state* sp, uint32_t slot) { return rule_u24(sp, slot); }
 
 /* accept-test uniform: seeded -> rule_u24(slot 64 + j); unseeded -> top 24
  * bits of the next xoshiro output; greedy -> 0 */

@@ -149,6 +149,16 @@ int or_transform(const or_state* st, const uint16_t* row_bf16,
  * Returns the raw vocab id. */
 int64_t or_sample(or_state* st, const uint16_t* row_bf16,
                   const uint16_t* eos_bf16, int32_t* out_sem, int* out_eos);
+/* Test hooks: splitmix64 step (sampling.c:54-59), xoshiro256** step
+ * (sampling.c:65-75), the seeded hash-Gumbel draw (sampling.c:221-243) and the
+ * unseeded inverse-CDF draw (sampling.c:244-262) over prob[0..29] with the
+ * state as is (no history update), and the acceptance rule's counter-based
+ * 24-bit uniform. */
+uint64_t or_splitmix64_next(uint64_t* s);
+uint64_t or_xoshiro_next(uint64_t s[4]);
+int or_gumbel_draw(const or_state* st, const float* prob);
+int or_xoshiro_draw(or_state* st, const float* prob);
+uint32_t or_rule_u24(const or_state* st, uint32_t slot);
 /* history update of sampling.c:269-281 for an emitted vocab id */
 void or_state_push(or_state* st, int64_t tok);
 

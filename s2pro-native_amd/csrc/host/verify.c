@@ -55,6 +55,7 @@ struct s2p_backbone {
     int32_t* d_sess;
     uint64_t* d_vis;
     void** d_kv;
+    void** d_kvs;          /* [max_sessions] scale bases (INT8 / INT4 caches) */
     S2pAttnSeg* d_segs;
     void* h_stage;
     size_t stage_bytes;
@@ -182,8 +183,9 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_sess, R * 4);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_vis, R * 8);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_kv, (size_t)S * sizeof(void*));
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_kvs, (size_t)S * sizeof(void*));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_segs, (size_t)nseg_max * sizeof(S2pAttnSeg));
-    b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)S * sizeof(void*) +
+    b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)2 * S * sizeof(void*) +
                      (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
     b->mk_bytes = mk_off_head(opts->n_layers) + sizeof(MkGemv);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk, b->mk_bytes);
@@ -243,7 +245,7 @@ void s2p_backbone_free(s2p_backbone* b) {
     s2p_linear_free(&b->head);
     void* bufs[] = {b->x,        b->qkv,       b->q,           b->attn,          b->gu,
                     b->ssq,      b->attn_part, b->d_pos,       b->d_slot,        b->d_sess,
-                    b->d_vis,    (void*)b->d_kv, (void*)b->d_segs, (void*)b->d_mk,
+                    b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_mk,
                     (void*)b->d_bar, (void*)b->d_err, (void*)b->d_attn_ctr, (void*)b->d_ts, (void*)b->d_rope,
                     (void*)b->d_ts_wg};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
@@ -261,8 +263,15 @@ s2p_linear* s2p_backbone_head(s2p_backbone* b) { return b ? &b->head : NULL; }
 void* s2p_backbone_final_norm(s2p_backbone* b) { return b ? b->final_norm.data : NULL; }
 
 size_t s2p_backbone_kv_bytes(const s2p_backbone* b) {
-    if (b->kvb != 16) return (size_t)b->o.n_layers * s2p_kv8_layer_bytes(b->o.ctx_len, b->kvb);
+    if (b->kvb != 16)
+        return (size_t)b->o.n_layers * 2 * S2P_KV_HEADS * (size_t)b->o.ctx_len *
+               (b->kvb == 8 ? S2P_HEAD_DIM : S2P_HEAD_DIM / 2);
     return (size_t)b->o.n_layers * 2 * S2P_KV_HEADS * (size_t)b->o.ctx_len * S2P_HEAD_DIM * 2;
+}
+
+size_t s2p_backbone_kv_scale_bytes(const s2p_backbone* b) {
+    if (b->kvb == 16) return 0;
+    return (size_t)b->o.n_layers * 2 * S2P_KV_HEADS * (size_t)b->o.ctx_len * 4 * 2;
 }
 
 static size_t lin_bytes(const s2p_linear* l) {
@@ -364,13 +373,17 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
     int32_t* sess = slot + rows;
     uint64_t* vis = (uint64_t*)(((uintptr_t)(sess + rows) + 7) & ~(uintptr_t)7);
     void** kv = (void**)(vis + rows);
-    S2pAttnSeg* segs = (S2pAttnSeg*)(kv + n);
+    void** kvs = kv + n;
+    S2pAttnSeg* segs = (S2pAttnSeg*)(kvs + n);
+    if (b->kvb != 16 && !vb->kv_scales) return S2P_ERR_INVALID;
     int nseg = 0, max_span = 0;
     for (int s = 0; s < n; s++) {
         const int L = vb->kv_len[s];
         if (L < 0 || !vb->kv[s]) return S2P_ERR_INVALID;
+        if (b->kvb != 16 && !vb->kv_scales[s]) return S2P_ERR_INVALID;
         if (L + R > b->o.ctx_len) return S2P_ERR_FULL;
         kv[s] = vb->kv[s];
+        kvs[s] = b->kvb != 16 ? vb->kv_scales[s] : NULL;
         for (int i = 0; i < R; i++) {
             const int r = s * R + i;
             pos[r] = L + depth[i];
@@ -395,6 +408,7 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_sess, sess, (size_t)rows * 4, hipMemcpyHostToDevice, st), "plan"));
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_vis, vis, (size_t)rows * 8, hipMemcpyHostToDevice, st), "plan"));
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_kv, kv, (size_t)n * sizeof(void*), hipMemcpyHostToDevice, st), "plan"));
+    S2P_TRY(hip_ok(hipMemcpyAsync(b->d_kvs, kvs, (size_t)n * sizeof(void*), hipMemcpyHostToDevice, st), "plan"));
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_segs, segs, (size_t)nseg * sizeof(S2pAttnSeg),
                                   hipMemcpyHostToDevice, st), "plan"));
     S2P_TRY(hip_ok(hipStreamSynchronize(st), "plan sync"));
@@ -429,6 +443,7 @@ static S2pRowPlan row_plan(const s2p_backbone* b) {
     p.sess = b->d_sess;
     p.vis = b->d_vis;
     p.kv = b->d_kv;
+    p.kvs = b->d_kvs;
     p.layer_stride = (int64_t)2 * S2P_KV_HEADS * b->o.ctx_len * S2P_HEAD_DIM;
     p.max_seq = b->o.ctx_len;
     return p;

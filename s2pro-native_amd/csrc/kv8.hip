@@ -311,18 +311,15 @@ extern "C" hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* co
 }
 
 /* ------------------------------------------------------------------------
- * The verify plan over quantised session caches.  A session's KV base holds,
- * per layer, the payload planes [16][max_seq][EL] (K heads 0..7, then V
- * heads) followed by their f16 scales [16][max_seq][4]: kv8_layer_bytes per
- * layer.  Rows are planned as for the bf16 cache (S2pRowPlan): row r writes
+ * The verify plan over quantised session caches, in the reference session's
+ * layout (slowar_internal.h:177-179, 208-225): a session's code tensor
+ * kv [layers][16][max_seq][EL] (per layer K heads 0..7, then V heads) and its
+ * separate f16 scale tensor kvs [layers][16][max_seq][4].  Rows are planned as for the bf16 cache (S2pRowPlan): row r writes
  * slot plan.slot[r], has RoPE position plan.pos[r] and sees [0, L) plus the
  * node slots of plan.vis[r], whose highest bit is the row's own node. */
 #include "attn_dev.h"
 #include "prims_dev.h"
 
-static __host__ __device__ inline size_t kv8_layer_bytes(int max_seq, int bw) {
-    return (size_t)16 * max_seq * ((bw == 8 ? KV8_HD : KV8_HD / 2) + 8);
-}
 
 struct Kv8Plane {
     int8_t* pay;    /* [max_seq][EL] */
@@ -333,10 +330,10 @@ template <int BW>
 static __device__ __forceinline__ Kv8Plane kv8_plane(const S2pRowPlan& plan, int sess, int layer,
                                                      int plane) {
     constexpr int EL = BW == 8 ? KV8_HD : KV8_HD / 2;
-    int8_t* lb = (int8_t*)plan.kv[sess] + (size_t)layer * kv8_layer_bytes(plan.max_seq, BW);
+    const size_t pl = (size_t)layer * 16 + plane;
     Kv8Plane p;
-    p.pay = lb + (size_t)plane * plan.max_seq * EL;
-    p.sc = (uint16_t*)(lb + (size_t)16 * plan.max_seq * EL) + (size_t)plane * plan.max_seq * 4;
+    p.pay = (int8_t*)plan.kv[sess] + pl * plan.max_seq * EL;
+    p.sc = (uint16_t*)plan.kvs[sess] + pl * plan.max_seq * 4;
     return p;
 }
 
@@ -697,7 +694,6 @@ __global__ __launch_bounds__(64) void k_kv_commit8(S2pRowPlan plan,
     }
 }
 
-extern "C" size_t s2p_kv8_layer_bytes(int max_seq, int bw) { return kv8_layer_bytes(max_seq, bw); }
 
 extern "C" int64_t s2p_attn8_plan_part_floats(int rows, int max_span) {
     const int64_t nsplit = (max_span + KV8_TILE - 1) / KV8_TILE;

@@ -26,6 +26,8 @@
 #include "s2pro/kernels.h"
 #include "s2pro/s2p_fmath.h"
 #include "s2pro/slowar_kernels.h"
+#include "s2pro/verify.h"
+#include "s2pro/draft.h"
 
 #define PR_THREADS 256
 #define PR_MAX_GRID 4096
@@ -274,6 +276,40 @@ extern "C" hipError_t s2pk_add(s2p_bf16* y, const s2p_bf16* x, int64_t n, hipStr
     return hipGetLastError();
 }
 
+/* logits bf16 [vocab] -> f32 scratch [vocab] (exact widening): the device
+ * staging step of the reference sampler contract (kernels.cu:1300-1322).
+ * Eight logits per thread: one 16-byte load, two 16-byte stores, when both
+ * pointers are 16-byte aligned; element by element otherwise. */
+__global__ __launch_bounds__(256) void k_widen(const uint16_t* __restrict__ x,
+                                               float* __restrict__ y, int64_t n, int vec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        const int64_t n8 = n >> 3;
+        for (int64_t j = i; j < n8; j += stride) {
+            const s2p_u32x4 v = *(const s2p_u32x4*)(x + j * 8);
+            s2p_f32x4 lo = {bf2f_lo(v.x), bf2f_hi(v.x), bf2f_lo(v.y), bf2f_hi(v.y)};
+            s2p_f32x4 hi = {bf2f_lo(v.z), bf2f_hi(v.z), bf2f_lo(v.w), bf2f_hi(v.w)};
+            *(s2p_f32x4*)(y + j * 8) = lo;
+            *(s2p_f32x4*)(y + j * 8 + 4) = hi;
+        }
+        i += n8 * 8;
+        for (; i < n; i += stride) y[i] = bf2f(x[i]);
+        return;
+    }
+    for (; i < n; i += stride) y[i] = bf2f(x[i]);
+}
+
+extern "C" hipError_t s2pk_sample_prepare(const s2p_bf16* logits, float* scratch, int vocab,
+                                          hipStream_t st) {
+    if (vocab <= 0) return hipSuccess;
+    const int vec = ((((uintptr_t)logits) | ((uintptr_t)scratch)) & 15) == 0;
+    const int64_t work = vec ? ((int64_t)vocab + 7) / 8 : vocab;
+    hipLaunchKernelGGL(k_widen, dim3(pr_blocks(work, PR_THREADS)), dim3(PR_THREADS), 0, st,
+                       (const uint16_t*)logits, scratch, (int64_t)vocab, vec);
+    return hipGetLastError();
+}
+
 /* ----------------------------------------------- fused verify-layer kernels */
 
 /* One wave per (row, head), heads 0..q_heads-1 are query heads, then the
@@ -371,6 +407,26 @@ extern "C" hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t
 __global__ void k_f2bf(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = f2bf(in[i]);
+}
+
+/* Test hook: sizes of the internal launch descriptors that tests build
+ * through ctypes (0 S2pRowPlan, 1 S2pAttnSeg, then the public structs the
+ * Python binding mirrors), so that a stale mirror fails
+ * on the CPU instead of handing a kernel a misread descriptor. */
+extern "C" size_t s2p_test_desc_bytes(int which) {
+    switch (which) {
+        case 0: return sizeof(S2pRowPlan);
+        case 1: return sizeof(S2pAttnSeg);
+        case 2: return sizeof(s2p_backbone_opts);
+        case 3: return sizeof(s2p_verify_batch);
+        case 4: return sizeof(s2p_verify_step_io);
+        case 5: return sizeof(s2p_tensor);
+        case 6: return sizeof(s2p_linear);
+        case 7: return sizeof(s2p_slow_layer);
+        case 8: return sizeof(s2p_draft_model);
+        case 9: return sizeof(s2p_draft_state);
+        default: return 0;
+    }
 }
 
 extern "C" hipError_t s2p_test_f2bf(const float* in, uint16_t* out, int64_t n, hipStream_t st) {

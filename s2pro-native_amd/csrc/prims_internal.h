@@ -16,7 +16,10 @@ typedef struct {
     const int32_t*  slot;         /* [rows] KV cache slot written by the row */
     const int32_t*  sess;         /* [rows] session index */
     const uint64_t* vis;          /* [rows] visible node slots relative to L */
-    void* const*    kv;           /* [n_sess] KV base, [layers][2*8][max_seq][128] */
+    void* const*    kv;           /* [n_sess] KV base, [layers][2*8][max_seq][128] (bf16),
+                                   * or the INT8 / INT4 codes [layers][2*8][max_seq][128 | 64] */
+    void* const*    kvs;          /* [n_sess] INT8 / INT4 caches: f16 group scales
+                                   * [layers][2*8][max_seq][4] */
     int64_t         layer_stride; /* elements per layer in a session KV */
     int             max_seq;
 } S2pRowPlan;
@@ -61,10 +64,9 @@ hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan
                                       float eps, unsigned* counters, hipStream_t st);
 int64_t    s2p_attn_plan_part_floats(int rows, int max_span);
 
-/* The verify plan over INT8 / INT4 (bw 8 / 4) session caches (kv8.hip): per
- * layer, payload planes [16][max_seq][bw == 8 ? 128 : 64] (K heads, then V)
- * and their f16 scales [16][max_seq][4]. */
-size_t     s2p_kv8_layer_bytes(int max_seq, int bw);
+/* The verify plan over INT8 / INT4 (bw 8 / 4) session caches (kv8.hip): codes
+ * plan.kv[s] [layers][16][max_seq][bw == 8 ? 128 : 64] (K heads, then V) and
+ * f16 scales plan.kvs[s] [layers][16][max_seq][4]. */
 int64_t    s2p_attn8_plan_part_floats(int rows, int max_span);
 /* qk-norm + RoPE (positions from rope_tab) + quantise-on-append */
 hipError_t s2p_qkrope_append8_launch(const void* qkv, void* q_out, const void* qn_w,

@@ -30,8 +30,23 @@ class BackboneOpts(ctypes.Structure):
                 ("max_rows", I), ("max_sessions", I), ("ctx_len", I), ("kv_bits", I)]
 
 
+class RowPlan(ctypes.Structure):
+    """Internal S2pRowPlan (csrc/prims_internal.h), used by stage-level tests;
+    its size is checked against the library (s2p_test_desc_bytes)."""
+    _fields_ = [("pos", P), ("slot", P), ("sess", P), ("vis", P), ("kv", P), ("kvs", P),
+                ("layer_stride", I64), ("max_seq", I)]
+
+
+class AttnSeg(ctypes.Structure):
+    """Internal S2pAttnSeg (csrc/prims_internal.h)."""
+    _fields_ = [("sess", ctypes.c_int32), ("L", ctypes.c_int32), ("row0", ctypes.c_int32),
+                ("nrows", ctypes.c_int32), ("span", ctypes.c_int32), ("first", ctypes.c_int32),
+                ("kv", P)]
+
+
 class VerifyBatch(ctypes.Structure):
-    _fields_ = [("n_sess", I), ("rows", I), ("parent", P), ("kv", P), ("kv_len", P)]
+    _fields_ = [("n_sess", I), ("rows", I), ("parent", P), ("kv", P), ("kv_len", P),
+                ("kv_scales", P)]
 
 
 class StepIO(ctypes.Structure):
@@ -112,6 +127,7 @@ SIGS = {
     "s2pk_attention": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "s2pk_silu_mul": (I, [P, P, I, I, P]),
     "s2pk_add": (I, [P, P, I64, P]),
+    "s2pk_sample_prepare": (I, [P, P, I, P]),
     # slowar_kernels.h
     "s2pk_qkv_split": (I, [P, P, P, P, I, I, I, P]),
     "s2pk_rope_pos": (I, [P, P, I, I, I, I, P, F, P]),
@@ -131,6 +147,7 @@ SIGS = {
     "s2p_backbone_head": (ctypes.POINTER(Linear), [P]),
     "s2p_backbone_final_norm": (P, [P]),
     "s2p_backbone_kv_bytes": (SZ, [P]),
+    "s2p_backbone_kv_scale_bytes": (SZ, [P]),
     "s2p_backbone_weight_bytes": (SZ, [P]),
     "s2p_verify_plan": (I, [P, P, P]),
     "s2p_verify_forward": (I, [P, P, P, P]),
@@ -150,6 +167,7 @@ EXTRA = {
     "s2p_gemv_set_probe": (None, [P, I]),
     "s2p_attn_set_probe": (None, [P, I]),
     "s2p_test_f2bf": (I, [P, P, I64, P]),
+    "s2p_test_desc_bytes": (SZ, [I]),
     "s2p_backbone_mk_grid": (I, [P]),
     "s2p_backbone_mk_status": (I, [P]),
     "s2p_backbone_mk_times": (I, [P, P, I]),

@@ -73,3 +73,15 @@ def test_partial_sizes(lib):
     n2 = lib.s2pk_attention_part_floats(5, 32, 4096)
     assert n1 == 5 * 32 * 1 * 130
     assert n2 > n1 and n2 % (5 * 32 * 130) == 0
+
+
+def test_internal_descriptor_mirrors_match(lib):
+    """The ctypes mirrors of internal launch descriptors used by stage-level
+    GPU tests have the library's sizes (a stale mirror would hand a kernel
+    misread pointers)."""
+    assert ctypes.sizeof(s2pamd.RowPlan) == lib.s2p_test_desc_bytes(0)
+    assert ctypes.sizeof(s2pamd.AttnSeg) == lib.s2p_test_desc_bytes(1)
+    names = ["BackboneOpts", "VerifyBatch", "StepIO", "Tensor", "Linear", "SlowLayer",
+             "DraftModel", "DraftState"]
+    for i, n in enumerate(names, start=2):
+        assert ctypes.sizeof(getattr(s2pamd, n)) == lib.s2p_test_desc_bytes(i), n

@@ -77,18 +77,7 @@ def test_attention_single_key_returns_v(lib):
     assert np.array_equal(got, np.repeat(vc[:, 0, :], 4, axis=0))
 
 
-class RowPlan(__import__("ctypes").Structure):
-    import ctypes as _c
-    _fields_ = [("pos", _c.c_void_p), ("slot", _c.c_void_p), ("sess", _c.c_void_p),
-                ("vis", _c.c_void_p), ("kv", _c.c_void_p), ("layer_stride", _c.c_int64),
-                ("max_seq", _c.c_int)]
-
-
-class AttnSeg(__import__("ctypes").Structure):
-    import ctypes as _c
-    _fields_ = [("sess", _c.c_int32), ("L", _c.c_int32), ("row0", _c.c_int32),
-                ("nrows", _c.c_int32), ("span", _c.c_int32), ("first", _c.c_int32),
-                ("kv", _c.c_void_p)]
+from s2pamd import AttnSeg, RowPlan  # noqa: E402  (layouts checked against the library)
 
 
 def _tree_masks(parent):
@@ -124,7 +113,7 @@ def test_attention_plan_mode(lib, parent, L, max_seq):
     sessd = to_dev(np.zeros(R, np.int32))
     visd = to_dev(vis)
     plan = RowPlan(posd.data_ptr(), slotd.data_ptr(), sessd.data_ptr(), visd.data_ptr(),
-                   kvp.data_ptr(), 16 * max_seq * 128, max_seq)
+                   kvp.data_ptr(), None, 16 * max_seq * 128, max_seq)
     segs = []
     for r0 in range(0, R, 8):
         segs.append(AttnSeg(0, L, r0, min(8, R - r0), L + R, 0, kvd.data_ptr()))

@@ -122,3 +122,24 @@ def test_f2bf_matches_rule(lib):
     want = po.f32_to_bf16(x)
     bad = np.nonzero(got != want)[0]
     assert bad.size == 0, [(hex(bits[i]), hex(got[i]), hex(want[i])) for i in bad[:8]]
+
+
+@pytest.mark.parametrize("vocab,off", [(155776, 0), (4097, 0), (4097, 3), (1, 0)])
+def test_sample_prepare_widens_exactly(lib, vocab, off):
+    """s2pk_sample_prepare (kernels.h:65-66): f32 scratch = the bf16 logits,
+    exactly, on aligned and misaligned buffers and ragged lengths; nothing
+    past vocab is written."""
+    r = np.random.default_rng(vocab + off)
+    x = bf16_bits(r.standard_normal(vocab + 8).astype(np.float32) * 4.0)
+    x[:4] = bf16_bits(np.array([np.inf, -np.inf, 0.0, -0.0], np.float32))[: min(4, vocab + 8)]
+    tx = to_dev(x)
+    out = torch.full((vocab + 16,), 7.0, dtype=torch.float32, device="cuda")
+    xp = tx.data_ptr() + 2 * off
+    yp = out.data_ptr() + 4 * off
+    s2pamd.hip_check(lib.s2pk_sample_prepare(ctypes.c_void_p(xp), ctypes.c_void_p(yp), vocab, S()))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = po.bf16_to_f32(x[off:off + vocab])
+    assert np.array_equal(got[off:off + vocab].view(np.uint32), want.view(np.uint32))
+    assert np.all(got[:off] == 7.0) and np.all(got[off + vocab:] == 7.0)
+    assert lib.s2pk_sample_prepare(None, None, 0, S()) == 0

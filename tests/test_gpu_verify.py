@@ -72,12 +72,16 @@ def new_kv(lib, bb, seed):
     return kv
 
 
-def plan(lib, bb, parent, kvs, lens):
+def plan(lib, bb, parent, kvs, lens, scales=None):
+    """kvs: device tensors (the caches' codes for INT8 / INT4); scales: the
+    device addresses of the INT8 / INT4 caches' scale tensors, or None"""
     n = len(kvs)
     par = np.asarray(parent, np.int32)
     kvp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in kvs])
     ln = np.asarray(lens, np.int32)
-    vb = s2pamd.VerifyBatch(n, len(parent), par.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data)
+    scp = (ctypes.c_void_p * n)(*scales) if scales is not None else None
+    vb = s2pamd.VerifyBatch(n, len(parent), par.ctypes.data, ctypes.addressof(kvp), ln.ctypes.data,
+                            ctypes.addressof(scp) if scp is not None else None)
     s2pamd.check(lib.s2p_verify_plan(bb, ctypes.byref(vb), S()), "plan")
 
 
@@ -130,6 +134,10 @@ def f64_weights(lib, bb, n_layers):
     return layers, fnorm, f64.dequant(w, s, hl.out_features, hl.in_features)
 
 
+LOGITS_REL = 1e-2  # logits within 1e-2 of the reference
+LOGITS_CAP = 2e-2  # hard cap for a named exception row (see check_logits)
+
+
 def check_logits(got, want_bits, truth, what, rms=True):
     """Per-row tolerance against the oracle and (rms=True) the accuracy
     criterion over these rows; callers pooling several sessions pass
@@ -140,8 +148,22 @@ def check_logits(got, want_bits, truth, what, rms=True):
             f"oracle {np.linalg.norm(want[r] - truth[r]) / tn[r]:.2e} "
             f"gpu-oracle {np.linalg.norm(got[r] - want[r]) / tn[r]:.2e}" for r in range(len(got))]
     print(what, "per-row L2 rel err vs binary64:\n  " + "\n  ".join(rows))
-    e_ref_row = np.linalg.norm(want - truth, axis=1) / tn
-    assert_close_norm(got, want, rel=np.maximum(1e-2, 0.5 * e_ref_row), what=what)
+    # The bar is 1e-2 L2-relative per row against the reference order.  A row
+    # may exceed it only when the GPU row is at least as close to binary64 as
+    # the reference order is (the distance is then the reference order's own
+    # rounding error), and never beyond LOGITS_CAP; such rows are printed
+    # with their numbers as named exceptions.
+    e_ref = np.linalg.norm(want - truth, axis=1) / tn
+    e_gpu = np.linalg.norm(got - truth, axis=1) / tn
+    d = np.linalg.norm(got - want, axis=1) / np.maximum(np.linalg.norm(want, axis=1), 1e-30)
+    exc = (d > LOGITS_REL) & (e_gpu <= e_ref)
+    tol = np.where(exc, LOGITS_CAP, LOGITS_REL)
+    for r in np.nonzero(exc)[0]:
+        print(f"{what}: EXCEPTION row {r}: gpu-oracle {d[r]:.3e} > {LOGITS_REL:g}, gpu vs "
+              f"binary64 {e_gpu[r]:.3e} <= oracle vs binary64 {e_ref[r]:.3e}")
+    print(f"{what}: largest per-row tolerance applied {tol.max():g} "
+          f"(largest gpu-oracle {d.max():.3e}, {int(exc.sum())} exception rows)")
+    assert_close_norm(got, want, rel=tol, what=what)
     if rms:
         check_rms(got, want, truth, what)
 

@@ -36,35 +36,42 @@ def lib():
 
 
 def layout(n_layers, ctx, bw):
+    """A session cache as held here: the code tensor kv [layers][16][ctx][el]
+    followed by the scale tensor kvs [layers][16][ctx][4] f16 in one buffer
+    (the reference's two tensors of s2p_session, slowar_internal.h:177-179);
+    returns (el, code bytes per layer, offset of kvs, total bytes)."""
     el = HD if bw == 8 else HD // 2
     pay = 16 * ctx * el
-    return el, pay, pay + 16 * ctx * 8
+    return el, pay, n_layers * pay, n_layers * (pay + 16 * ctx * 8)
 
 
 def new_kv8(lib, bb, n_layers, ctx, L, bw, seed):
     """A session cache whose slots [0, L) hold quantised N(0,1) rows (the
-    oracle's append), the rest zero; returns (device tensor, host bytes)."""
-    el, pay, lb = layout(n_layers, ctx, bw)
-    assert lib.s2p_backbone_kv_bytes(bb) == n_layers * lb
-    host = np.zeros(n_layers * lb, np.uint8)
+    oracle's append), the rest zero; returns (device tensor, host bytes,
+    device address of its scale tensor)."""
+    el, pay, soff, total = layout(n_layers, ctx, bw)
+    assert lib.s2p_backbone_kv_bytes(bb) == soff
+    assert lib.s2p_backbone_kv_scale_bytes(bb) == total - soff
+    host = np.zeros(total, np.uint8)
     r = np.random.default_rng(seed)
     for l in range(n_layers):
-        kc, vc, ks, vs = planes(host, l, ctx, bw)
+        kc, vc, ks, vs = planes(host, l, ctx, bw, n_layers)
         k = po.f32_to_bf16(r.standard_normal((L, KVH * HD)).astype(np.float32))
         v = po.f32_to_bf16(r.standard_normal((L, KVH * HD)).astype(np.float32))
         kcc, vcc = [np.ascontiguousarray(kc)], [np.ascontiguousarray(vc)]
         kss, vss = [np.ascontiguousarray(ks)], [np.ascontiguousarray(vs)]
         po.kv_append8(k, v, kcc, vcc, kss, vss, L, KVH, 0, None, ctx, bw)
         kc[...], vc[...], ks[...], vs[...] = kcc[0], vcc[0], kss[0], vss[0]
-    return to_dev(host), host
+    dev = to_dev(host)
+    return dev, host, dev.data_ptr() + soff
 
 
-def planes(buf, l, ctx, bw):
+def planes(buf, l, ctx, bw, n_layers):
     """Views (kc, vc, ks, vs) of layer l of a session cache held as bytes."""
-    el, pay, lb = layout(0, ctx, bw)
-    base = buf[l * lb:(l + 1) * lb]
-    p = base[:pay].view(np.int8).reshape(16, ctx, el)
-    s = base[pay:].view(np.uint16).reshape(16, ctx, 4)
+    el, pay, soff, total = layout(n_layers, ctx, bw)
+    p = buf[l * pay:(l + 1) * pay].view(np.int8).reshape(16, ctx, el)
+    sb = 16 * ctx * 8
+    s = buf[soff + l * sb:soff + (l + 1) * sb].view(np.uint16).reshape(16, ctx, 4)
     return p[:8], p[8:], s[:8], s[8:]
 
 
@@ -84,9 +91,9 @@ def oracle_forward8(lib, bb, n_layers, x, host, ctx, L, parent, bw, append=True)
     host = host.copy()
     for l in range(n_layers):
         lw, keep = host_layer(lib, bb, l)
-        kc, vc, ks, vs = [np.ascontiguousarray(a) for a in planes(host, l, ctx, bw)]
+        kc, vc, ks, vs = [np.ascontiguousarray(a) for a in planes(host, l, ctx, bw, n_layers)]
         po.layer8(lw, x, R, kc, vc, ks, vs, ctx, L, pos, vis, bw, append)
-        dst = planes(host, l, ctx, bw)
+        dst = planes(host, l, ctx, bw, n_layers)
         for d, a in zip(dst, (kc, vc, ks, vs)):
             d[...] = a
     fnorm = d2h(lib.s2p_backbone_final_norm(bb), 2560 * 2, np.uint16)
@@ -115,19 +122,23 @@ def deq(kc, ks, bw):
     return decode(kc, bw) * ks.view(np.float16).astype(np.float64).repeat(32, axis=-1)
 
 
-@pytest.mark.parametrize("bw,parent,lens", [(8, [-1, 0, 1, 2, 3], [300]),
-                                            (4, [-1, 0, 1, 2, 3], [129]),
-                                            (8, TREE16, [130, 301])])
-def test_verify_forward_kv8_vs_oracle(lib, bw, parent, lens):
-    n_layers, ctx = 2, 384
+@pytest.mark.parametrize("bw,parent,lens,ctx", [(8, [-1, 0, 1, 2, 3], [300], 384),
+                                                (4, [-1, 0, 1, 2, 3], [129], 384),
+                                                (8, TREE16, [130, 301], 384),
+                                                # 8 segments over a 4608-slot span: the
+                                                # one-round split sizing gives 160-slot
+                                                # splits (not a multiple of 128)
+                                                (4, TREE16, [4500, 4321, 4402, 4570], 4608)])
+def test_verify_forward_kv8_vs_oracle(lib, bw, parent, lens, ctx):
+    n_layers = 2
     R, n = len(parent), len(lens)
     bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, n * R, n, ctx,
                        321 + bw, kv_bits=bw)
     try:
-        kvs, hosts = zip(*[new_kv8(lib, bb, n_layers, ctx, lens[s], bw, 40 + s)
-                           for s in range(n)])
+        kvs, hosts, scs = zip(*[new_kv8(lib, bb, n_layers, ctx, lens[s], bw, 40 + s)
+                                for s in range(n)])
         print(f"kv{bw}: {n} sessions x {R} rows, lens {lens}", flush=True)
-        plan(lib, bb, parent, list(kvs), lens)
+        plan(lib, bb, parent, list(kvs), lens, list(scs))
         x = bf16_bits(np.random.default_rng(9).standard_normal((n * R, 2560)).astype(np.float32))
         logits = empty((n * R, s2pamd.S2P_HEAD_SLICE))
         s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
@@ -143,7 +154,7 @@ def test_verify_forward_kv8_vs_oracle(lib, bw, parent, lens):
             assert_close_norm(got[rows], bf16_vals(want), rel=1e-2, what=f"session {s} logits")
             L = lens[s]
             for l in range(n_layers):
-                gp, rp = planes(dev, l, ctx, bw), planes(ref, l, ctx, bw)
+                gp, rp = planes(dev, l, ctx, bw, n_layers), planes(ref, l, ctx, bw, n_layers)
                 for a, b in zip(gp, rp):  # prefix and free slots untouched
                     assert np.array_equal(a[:, :L], b[:, :L])
                     assert np.array_equal(a[:, L + R:], b[:, L + R:])
@@ -166,8 +177,8 @@ def test_kv_commit8_moves_accepted_nodes(lib, bw):
     bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, R, 1, ctx, 55,
                        kv_bits=bw)
     try:
-        kv, _ = new_kv8(lib, bb, n_layers, ctx, L, bw, 7)
-        plan(lib, bb, TREE16, [kv], [L])
+        kv, _, sc = new_kv8(lib, bb, n_layers, ctx, L, bw, 7)
+        plan(lib, bb, TREE16, [kv], [L], [sc])
         x = bf16_bits(np.random.default_rng(3).standard_normal((R, 2560)).astype(np.float32))
         logits = empty((R, s2pamd.S2P_HEAD_SLICE))
         s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
@@ -179,7 +190,7 @@ def test_kv_commit8_moves_accepted_nodes(lib, bw):
                      "commit")
         after = to_host(kv, np.uint8)
         for l in range(n_layers):
-            b, a = planes(before, l, ctx, bw), planes(after, l, ctx, bw)
+            b, a = planes(before, l, ctx, bw, n_layers), planes(after, l, ctx, bw, n_layers)
             for pb, pa in zip(b, a):
                 want = pb.copy()
                 for d, node in enumerate([2, 5, 10, 15], start=1):

@@ -7,6 +7,7 @@ RoPE identity at position 0, causal independence, split-K == single pass,
 chain tree mask == causal), and the statistics of Leviathan's theorem for the
 acceptance rule.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -522,3 +523,214 @@ def test_accept_tree_first_child_rule():
     path, emitted = po.accept_tree(st, tgt, drf, parent, tok, z, z)
     assert path[0] == 1
     assert len(emitted) == len(path) + 1
+
+
+# ------------------------------------------------------------- draw pins
+# The draw primitives of sampling.c:50-78, 95-112 and 221-262, checked against
+# published vectors and values worked out by hand from their definitions, so
+# that a wrong constant, shift, rotation or step count fails here (the GPU
+# sampler is compared bit for bit with these same oracle draws).
+M64 = (1 << 64) - 1
+
+
+def _u64p(v):
+    return ctypes.pointer(ctypes.c_uint64(v))
+
+
+def test_splitmix64_published_vectors():
+    """splitmix64 (sampling.c:54-59) against its published output streams:
+    seed 1234567 (Rosetta Code "Pseudo-random numbers/Splitmix64") and seed 0
+    (the reference implementation's first outputs)."""
+    lib = po.lib()
+    s = _u64p(1234567)
+    got = [lib.or_splitmix64_next(s) for _ in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+    s = _u64p(0)
+    got = [lib.or_splitmix64_next(s) for _ in range(4)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F,
+                   0xF88BB8A8724C81EC]
+    assert s.contents.value == (4 * 0x9E3779B97F4A7C15) & M64
+
+
+def test_xoshiro256ss_hand_vectors():
+    """xoshiro256** (sampling.c:65-75) from state {1, 2, 3, 4}.  By hand: the
+    first output is rotl(2*5, 7)*9 = 1280*9 = 11520; then s2 ^= s0 -> 2,
+    s3 ^= s1 -> 6, s1 ^= s2 -> 0, s0 ^= s3 -> 7, s2 ^= 2<<17 -> 262146,
+    s3 = rotl(6, 45) = 6<<45.  The second output is rotl(0*5, 7)*9 = 0; the
+    third is rotl(262149*5, 7)*9 = 1310745*1152 = 1509978240."""
+    lib = po.lib()
+    s = (ctypes.c_uint64 * 4)(1, 2, 3, 4)
+    assert lib.or_xoshiro_next(s) == 11520
+    assert list(s) == [7, 0, 262146, 6 << 45]
+    assert lib.or_xoshiro_next(s) == 0
+    assert lib.or_xoshiro_next(s) == 1509978240
+    assert lib.or_xoshiro_next(s) == 1215971899390074240
+
+
+def test_state_init_seeds_rng_by_splitmix():
+    """s2ps_sampler_init (sampling.c:95-112): rng[i] = splitmix64 outputs from
+    entropy ^ 0xD1B54A32D192ED03, seed31 = seed & 0x7FFFFFFF."""
+    st = po.state(seed=0, entropy=0xD1B54A32D192ED03)
+    assert list(st.rng) == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F,
+                            0xF88BB8A8724C81EC]
+    st = po.state(seed=(1 << 40) | 5, entropy=0xD1B54A32D192ED03 ^ 1234567)
+    assert list(st.rng) == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                            4593380528125082431]
+    assert st.seeded == 1 and st.seed31 == 5
+    assert po.state(seed=0).seeded == 0
+
+
+def test_xoshiro_draw_inverse_cdf():
+    """Unseeded draw (sampling.c:244-262): r = (next >> 11) * 2^-53 from the
+    hand-derived stream above, first j with r < cumsum(p) over nonzero p
+    (binary64), else the last nonzero index."""
+    lib = po.lib()
+    p = np.zeros(30, np.float32)
+    p[1:] = np.float32(1.0 / 29.0)
+    p[7] = 0.0
+    outs = [11520, 0, 1509978240, 1215971899390074240]
+    st = po.state(seed=0)
+    st.rng[:] = [1, 2, 3, 4]
+    cum = np.cumsum(p.astype(np.float64))
+    for o in outs:
+        r = (o >> 11) * 2.0 ** -53
+        want = int(np.nonzero((r < cum) & (p > 0))[0][0])
+        assert lib.or_xoshiro_draw(po.ptr(st), po.ptr(p)) == want
+    assert want == 2  # r = 0.0659 falls in the second nonzero bin
+    # r beyond the total mass: the last nonzero index
+    q = np.zeros(30, np.float32)
+    q[3] = 1e-30
+    q[5] = 1e-30
+    st.rng[:] = [0, 1 << 50, 0, 0]  # output rotl(5 << 50, 7) * 9 = 45 << 57: r = 45/128
+    assert lib.or_xoshiro_draw(po.ptr(st), po.ptr(q)) == 5
+
+
+def _gumbel_u(step_seed, j):
+    h = ((step_seed * 8589934591) & M64) ^ (j * 479001599)
+    return h & 0xFFFFFF
+
+
+def _gumbel_want(step_seed, p):
+    """binary64 Gumbel-max with the clamp u >= 1e-10; returns (argmax, margin)"""
+    u = np.array([max(_gumbel_u(step_seed, j) / 16777216.0, 1e-10) for j in range(30)])
+    pert = np.log(p.astype(np.float64) + 1e-10) - np.log(-np.log(u))
+    o = np.argsort(-pert)
+    return int(o[0]), float(pert[o[0]] - pert[o[1]])
+
+
+def test_gumbel_draw_seed0_count0():
+    """Seeded draw (sampling.c:221-243) at seed31 = 0, count = 0: step_seed =
+    0, so u_j = (j * 479001599 mod 2^24) / 2^24 (u_1 = 9239551 / 2^24 by hand:
+    479001599 - 28 * 2^24).  Uniform p: the draw is the argmax of u_j; wide
+    margins: the binary64 argmax of log p_j - log(-log u_j)."""
+    lib = po.lib()
+    assert _gumbel_u(0, 1) == 9239551
+    st = po.state(seed=1)
+    st.seed31 = 0
+    st.count = 0
+    p = np.full(30, 1.0 / 30.0, np.float32)
+    u = [_gumbel_u(0, j) for j in range(30)]
+    assert lib.or_gumbel_draw(po.ptr(st), po.ptr(p)) == int(np.argmax(u))
+    r = RNG(71)
+    checked = 0
+    for _ in range(200):
+        p = r.dirichlet(np.full(30, 0.5)).astype(np.float32)
+        want, margin = _gumbel_want(0, p)
+        if margin < 1e-3:
+            continue
+        assert lib.or_gumbel_draw(po.ptr(st), po.ptr(p)) == want
+        checked += 1
+    assert checked > 150
+
+
+def test_gumbel_draw_seed_and_count():
+    """seed31 = 12345, count = 7: step_seed = 12345*19349663 ^ 7*73856093 =
+    238421777900 (worked out once, written as a literal).  The draw follows it
+    and not the step_seed of count 8 (the pre-draw count is used)."""
+    lib = po.lib()
+    ss7 = 238421777900
+    ss8 = (12345 * 19349663) ^ (8 * 73856093)
+    st = po.state(seed=12345)
+    st.count = 7
+    p = np.full(30, 1.0 / 30.0, np.float32)
+    w7 = int(np.argmax([_gumbel_u(ss7, j) for j in range(30)]))
+    w8 = int(np.argmax([_gumbel_u(ss8, j) for j in range(30)]))
+    assert w7 != w8
+    assert lib.or_gumbel_draw(po.ptr(st), po.ptr(p)) == w7
+    r = RNG(72)
+    checked = 0
+    for _ in range(200):
+        p = r.dirichlet(np.full(30, 0.5)).astype(np.float32)
+        want, margin = _gumbel_want(ss7, p)
+        if margin < 1e-3:
+            continue
+        assert lib.or_gumbel_draw(po.ptr(st), po.ptr(p)) == want
+        checked += 1
+    assert checked > 150
+
+
+def test_seeded_sample_uses_pre_draw_count():
+    """Through s2ps_sample: 30 tied top logits, top_p 1, seed 12345, seven
+    distinct earlier tokens outside the top set (count 7, no RAS).  p2 is
+    uniform, so the sample is candidate ti[argmax_j u_j(step_seed of count 7)],
+    ties ordered by ascending index."""
+    r = RNG(73)
+    row = bf16_bits(r.standard_normal(4096).astype(np.float32) - 20.0)
+    top = np.sort(r.choice(np.arange(100, 4096), 30, replace=False))
+    row[top] = bf16_bits(np.array([5.0], np.float32))[0]
+    eos = int(bf16_bits(np.array([-30.0], np.float32))[0])
+    st = po.state(temperature=0.8, top_p=1.0, seed=12345, window=16)
+    for t in range(7):
+        po.state_push(st, SEM0 + 10 + t)
+    ti, tv, p2, g = po.transform(st, row, eos)
+    # top_p = 1: the float cumsum may pass 1.0 before the last tie, which
+    # the reference then masks; the survivors are equally likely
+    nz = p2 > 0
+    assert np.array_equal(ti, top) and nz.sum() >= 29 and np.all(p2[nz] == p2[0])
+    u = np.array([_gumbel_u(238421777900, j) for j in range(30)], np.int64)
+    w7 = int(np.argmax(np.where(nz, u, -1)))
+    tok, sem, e = po.sample(st, row, eos)
+    assert sem == top[w7] and tok == SEM0 + top[w7] and st.count == 8
+
+
+def test_reference_seeded_draw_is_biased():
+    """The reference's seeded draw derives all 30 uniforms of a step from one
+    hashed value (XORs of j * 479001599), so over seeds its choice is far from
+    the target distribution: with uniform p the chi^2 of 30,000 draws against
+    uniform is in the thousands (29 dof; 58 would be p ~ 1e-3).  The rule
+    therefore keeps this draw only where it reproduces a reference sample."""
+    lib = po.lib()
+    p = np.full(30, 1.0 / 30.0, np.float32)
+    st = po.state(seed=1)
+    cnt = np.zeros(30)
+    for s in range(1, 30001):
+        st.seed31 = s
+        st.count = 0
+        cnt[lib.or_gumbel_draw(po.ptr(st), po.ptr(p))] += 1
+    chi2 = float(((cnt - 1000.0) ** 2 / 1000.0).sum())
+    assert chi2 > 1000.0
+
+
+def test_rule_u24_literal_and_uniformity():
+    """The acceptance rule's counter-based uniform: splitmix64's finaliser of
+    seed31*golden ^ count*c1 ^ (slot+1)*c2, top 24 bits.  At seed31 = count =
+    0, slot 0 the key is 0x94D049BB133111EB; uniform over 30 bins on 30,000
+    (seed, count, slot) keys (chi^2 below 58.3, p = 1e-3 at 29 dof)."""
+    lib = po.lib()
+    z = 0x94D049BB133111EB
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+    z ^= z >> 31
+    st = po.state(seed=1)
+    st.seed31 = 0
+    st.count = 0
+    assert lib.or_rule_u24(po.ptr(st), 0) == z >> 40
+    cnt = np.zeros(30)
+    for s in range(1, 101):
+        st.seed31 = s
+        for c in range(10):
+            st.count = c
+            for sl in range(30):
+                cnt[(lib.or_rule_u24(po.ptr(st), sl) * 30) >> 24] += 1
+    assert float(((cnt - 1000.0) ** 2 / 1000.0).sum()) < 58.3
