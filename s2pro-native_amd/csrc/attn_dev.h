@@ -183,12 +183,14 @@ S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, 
 }
 
 /* One (segment, kv head, position split) attention block; smem holds
- * AT_LDS_BYTES.  Body of k_attn, also run by the persistent verify kernel. */
+ * AT_LDS_BYTES.  Body of k_attn, also run by the persistent verify kernel.
+ * Returns true (uniformly) when this block wrote final outputs: a single
+ * split, or the last split to arrive, which merged all of them. */
 /* COH: the q / qkv / RoPE-table reads bypass the L2 (the persistent
  * kernel, where their producer ran in the same launch); the layer kernel
  * reads them through the caches */
 template <int MQT, int W = AT_WAVES, bool COH = true>
-__device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
+__device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
     constexpr int SVB = AT_SV_BYTES_W(W), SPB = AT_SP_BYTES_W(W), SMLB = AT_SML_BYTES_W(W);
     LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
     LDS(uint16_t)* s_p = (LDS(uint16_t)*)(smem + SVB);
@@ -580,7 +582,8 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         vm_drain();
         stamp(4);
     }
-    if (a.nsplit == 1 || !a.counters) return;
+    if (a.nsplit == 1) return true;
+    if (!a.counters) return false;
     /* last split of this (segment, kv head) to finish merges the splits */
     vm_drain();
     __syncthreads();
@@ -665,7 +668,9 @@ __device__ void attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         vm_drain();
         stamp(5);
     }
+    const bool merged = *s_flag != 0;
     __syncthreads();
+    return merged;
 #undef SV
 #undef SP
 #undef SPL

@@ -22,7 +22,7 @@
 
 #include "s2pro/verify.h"
 #include "../gemv_internal.h"
-#include "../mk_internal.h"
+#include "../mk2_internal.h"
 #include "../prims_internal.h"
 #include "../sample_internal.h"
 #include "../synth_internal.h"
@@ -62,21 +62,15 @@ struct s2p_backbone {
     int planned, rows, n_sess, R, n_seg, max_span;
     int kvb;               /* KV cache bits: 16 (bf16), 8 or 4 */
     int seg_rows_max;
-    /* persistent verify kernel (one launch per forward) */
-    /* launch descriptor block: MkArgs, MkLayer[n_layers], head MkGemv */
-    unsigned char* d_mk;
-    unsigned char* h_mk;   /* pinned host staging */
-    size_t mk_bytes;
-    uint64_t* d_bar;
-    int* d_err;
-    unsigned* d_attn_ctr;
     float* d_rope;         /* [max_rows][64][2] RoPE table of the plan */
-    uint64_t* d_ts;        /* phase timestamps (diagnostics), NULL = off */
-    uint64_t* d_ts_wg;     /* per-workgroup barrier timestamps (diagnostics) */
-    int mk_nwg;
-    size_t mk_lds;
-    int mk_ready;          /* the current plan runs on the persistent kernel */
-    int mk_enabled;        /* off: layer-by-layer launches (S2P_VERIFY_MK=0) */
+    /* persistent verify kernel (mk2.hip): one launch per forward */
+    uint8_t* d_wpack;      /* tile-packed layer weights (packed at the first eligible plan) */
+    uint8_t* d_hpack;      /* tile-packed head */
+    uint16_t* d_norms;     /* [n_layers][MK2_NORM_STRIDE] norm weights */
+    uint32_t* d_mk2;       /* flags, launch state, error flag, attention counters */
+    Mk2Args mk2;           /* launch arguments of the current plan */
+    int mk2_enabled;       /* off: layer-by-layer launches (env S2P_VERIFY_MK2=0) */
+    int mk2_ready;         /* the current plan runs on the persistent kernel */
     /* graph of one verify step */
     hipGraphExec_t gexec;
     int g_rows, g_nseg, g_span, g_valid;
@@ -121,12 +115,6 @@ static s2p_status dalloc(void** p, size_t bytes) {
         return S2P_ERR_OOM;
     }
     return S2P_OK;
-}
-
-/* layout of the persistent kernel's descriptor block */
-static size_t mk_off_layers(void) { return (sizeof(MkArgs) + 255) & ~(size_t)255; }
-static size_t mk_off_head(int n_layers) {
-    return mk_off_layers() + (((size_t)n_layers * sizeof(MkLayer) + 255) & ~(size_t)255);
 }
 
 s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t seed,
@@ -187,28 +175,13 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_segs, (size_t)nseg_max * sizeof(S2pAttnSeg));
     b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)2 * S * sizeof(void*) +
                      (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
-    b->mk_bytes = mk_off_head(opts->n_layers) + sizeof(MkGemv);
-    if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk, b->mk_bytes);
-    if (rc == S2P_OK && hipHostMalloc((void**)&b->h_mk, b->mk_bytes, 0) != hipSuccess) {
-        b->h_mk = NULL;
-        rc = S2P_ERR_OOM;
-    }
-    if (rc == S2P_OK) rc = dalloc((void**)&b->d_bar, MK_BAR_WORDS * sizeof(uint64_t));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_rope, R * 64 * 2 * sizeof(float));
-    if (rc == S2P_OK) rc = dalloc((void**)&b->d_err, sizeof(int));
-    if (rc == S2P_OK) rc = dalloc((void**)&b->d_attn_ctr, (size_t)nseg_max * 8 * sizeof(unsigned));
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_STATE_WORDS * sizeof(uint32_t));
+    if (rc == S2P_OK) /* flags, epoch and counters start at zero once; the kernel keeps them */
+        rc = hip_ok(hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st), "mk2 init");
     if (rc == S2P_OK) {
-        /* counters start at zero once; the kernels keep them consistent */
-        rc = hip_ok(hipMemsetAsync(b->d_bar, 0, MK_BAR_WORDS * sizeof(uint64_t), st), "mk init");
-        if (rc == S2P_OK) rc = hip_ok(hipMemsetAsync(b->d_err, 0, sizeof(int), st), "mk init");
-        if (rc == S2P_OK)
-            rc = hip_ok(hipMemsetAsync(b->d_attn_ctr, 0, (size_t)nseg_max * 8 * sizeof(unsigned), st),
-                        "mk init");
-    }
-    if (rc == S2P_OK) {
-        const char* e = getenv("S2P_VERIFY_MK");
-        b->mk_enabled = e && e[0] == '1'; /* opt-in until it beats the layer path */
-        if (s2p_mk_grid(&b->mk_nwg, &b->mk_lds) != 0) b->mk_enabled = 0;
+        const char* e = getenv("S2P_VERIFY_MK2");
+        b->mk2_enabled = !(e && e[0] == '0') && s2p_mk2_supported() == 0;
     }
     if (rc == S2P_OK && hipHostMalloc(&b->h_stage, b->stage_bytes, 0) != hipSuccess) {
         b->h_stage = NULL;
@@ -245,13 +218,11 @@ void s2p_backbone_free(s2p_backbone* b) {
     s2p_linear_free(&b->head);
     void* bufs[] = {b->x,        b->qkv,       b->q,           b->attn,          b->gu,
                     b->ssq,      b->attn_part, b->d_pos,       b->d_slot,        b->d_sess,
-                    b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_mk,
-                    (void*)b->d_bar, (void*)b->d_err, (void*)b->d_attn_ctr, (void*)b->d_ts, (void*)b->d_rope,
-                    (void*)b->d_ts_wg};
+                    b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_rope,
+                    (void*)b->d_wpack, (void*)b->d_hpack, (void*)b->d_norms, (void*)b->d_mk2};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
     if (b->h_stage) (void)hipHostFree(b->h_stage);
-    if (b->h_mk) (void)hipHostFree(b->h_mk);
     free(b);
 }
 
@@ -298,48 +269,22 @@ void s2p_backbone_debug_ptrs(s2p_backbone* b, void** x, void** qkv, void** q, vo
     if (gu) *gu = b->gu;
 }
 
-/* Persistent-kernel controls for tests and diagnostics (not in the public
- * header): enable / disable it for later plans; report whether the current
- * plan runs on it (1), on the layer-by-layer kernels (0), or whether a
- * barrier wait of the last launches timed out (-1, synchronises and clears
- * the flag). */
-void s2p_backbone_set_mk(s2p_backbone* b, int on) { b->mk_enabled = on && b->mk_nwg > 0; }
-int s2p_backbone_mk_grid(s2p_backbone* b) { return b->mk_nwg; }
-/* Phase timestamps of the persistent kernel (wall clock, 100 MHz on this
- * part): enable with n > 0 before planning; read back after a forward. */
-int s2p_backbone_mk_times(s2p_backbone* b, uint64_t* out, int n) {
-    if (n <= 0) return 0;
-    const int need = 3 + 6 * b->o.n_layers;
-    if (!b->d_ts) {
-        const size_t wgb = ((size_t)(need - 2 + 2) * 2 + 8) * b->mk_nwg * 8;
-        if (hipMalloc((void**)&b->d_ts, (size_t)need * 8) != hipSuccess) return -1;
-        if (hipMalloc((void**)&b->d_ts_wg, wgb) != hipSuccess) return -1;
-        (void)hipMemset(b->d_ts, 0, (size_t)need * 8);
-        (void)hipMemset(b->d_ts_wg, 0, wgb);
-        return 0;
-    }
-    if (!out) return need;
-    if (hipDeviceSynchronize() != hipSuccess) return -1;
-    const int k = n < need ? n : need;
-    return hipMemcpy(out, b->d_ts, (size_t)k * 8, hipMemcpyDeviceToHost) == hipSuccess ? k : -1;
-}
-
-/* per-workgroup barrier timestamps: [barriers][arrive, depart][nwg] */
-int s2p_backbone_mk_times_wg(s2p_backbone* b, uint64_t* out, size_t n) {
-    const size_t need = ((size_t)(1 + 6 * b->o.n_layers + 2) * 2 + 8) * b->mk_nwg;
-    if (!out) return (int)need;
-    if (!b->d_ts_wg || n < need || hipDeviceSynchronize() != hipSuccess) return -1;
-    return hipMemcpy(out, b->d_ts_wg, need * 8, hipMemcpyDeviceToHost) == hipSuccess ? b->mk_nwg : -1;
+/* Persistent-kernel controls for tests (not in the public header): enable /
+ * disable it for later plans; report whether the current plan runs on it
+ * (1), on the layer-by-layer kernels (0), or whether a flag wait of the last
+ * launches timed out (-1, synchronises and clears the flag). */
+void s2p_backbone_set_mk(s2p_backbone* b, int on) {
+    b->mk2_enabled = on && s2p_mk2_supported() == 0;
 }
 
 int s2p_backbone_mk_status(s2p_backbone* b) {
-    if (!b->mk_ready) return 0;
+    if (!b->mk2_ready) return 0;
     int err = 0;
     if (hipDeviceSynchronize() != hipSuccess ||
-        hipMemcpy(&err, b->d_err, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        hipMemcpy(&err, b->d_mk2 + MK2_ERR_WORD, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
         return -1;
     if (err) {
-        (void)hipMemset(b->d_err, 0, sizeof(int));
+        (void)hipMemset(b->d_mk2 + MK2_ERR_WORD, 0, sizeof(int));
         return -1;
     }
     return 1;
@@ -347,7 +292,7 @@ int s2p_backbone_mk_status(s2p_backbone* b) {
 
 /* ------------------------------------------------------------------ plan */
 
-static int mk_build(s2p_backbone* b);
+static int mk2_build(s2p_backbone* b, hipStream_t st);
 static S2pRowPlan row_plan(const s2p_backbone* b);
 
 s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStream_t st) {
@@ -426,13 +371,7 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
         S2P_TRY(hip_ok(s2p_rope_tab_launch(&rp, rows, ROPE_BASE, b->d_rope, st), "rope table"));
         S2P_TRY(hip_ok(hipStreamSynchronize(st), "rope table sync"));
     }
-    b->mk_ready = b->kvb == 16 && mk_build(b); /* the persistent kernel reads bf16 caches */
-    if (b->mk_ready) {
-        S2P_TRY(hip_ok(hipMemsetAsync(b->d_err, 0, sizeof(int), st), "mk plan"));
-        S2P_TRY(hip_ok(hipMemcpyAsync(b->d_mk, b->h_mk, b->mk_bytes, hipMemcpyHostToDevice, st),
-                       "mk plan"));
-        S2P_TRY(hip_ok(hipStreamSynchronize(st), "mk plan sync"));
-    }
+    b->mk2_ready = mk2_build(b, st);
     return S2P_OK;
 }
 
@@ -488,97 +427,100 @@ static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, voi
     return hip_ok(s2p_gemv_launch(&a, st), "verify gemv");
 }
 
-/* Build the persistent kernel's descriptors for the current plan (host
- * mirror); returns 0 if the plan is not served by it (the layer-by-layer
- * path runs instead). */
-static int mk_build(s2p_backbone* b) {
-    if (!b->mk_enabled || b->rows > 16 || b->o.quant != b->o.head_quant) return 0;
-    const int M = b->rows;
-    const int wfmt = b->o.quant == S2P_WQ_INT4_G32 ? GEMV_W_INT4 : GEMV_W_INT8;
-    MkArgs* A = (MkArgs*)b->h_mk;
-    MkLayer* Ls = (MkLayer*)(b->h_mk + mk_off_layers());
-    MkGemv* head = (MkGemv*)(b->h_mk + mk_off_head(b->o.n_layers));
-    memset(b->h_mk, 0, b->mk_bytes);
-    float* ssq_a = b->ssq;
-    float* ssq_b = b->ssq + (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M;
-    /* GEMVs planned for the kernel's own grid (one work unit per workgroup) */
-    const int slots = b->mk_nwg;
-    for (int l = 0; l < b->o.n_layers; l++) {
+/* Pack the weights into the persistent kernel's tile layout (once per
+ * backbone): every layer's four GEMVs, the norm weights and the head. */
+static s2p_status mk2_pack_all(s2p_backbone* b, hipStream_t st) {
+    const int NL = b->o.n_layers;
+    const size_t lb = (size_t)MK2_LAYER_BLKS * MK2_BLK;
+    const int ht = (b->head.out_features + 15) / 16;
+    S2P_TRY(dalloc((void**)&b->d_wpack, lb * NL));
+    S2P_TRY(dalloc((void**)&b->d_hpack, (size_t)ht * 20 * MK2_BLK));
+    S2P_TRY(dalloc((void**)&b->d_norms, (size_t)NL * MK2_NORM_STRIDE * 2));
+    for (int l = 0; l < NL; l++) {
         const s2p_slow_layer* L = &b->layers[l];
-        GemvArgs g[4];
-        gemv_args(&g[0], &L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
-                  L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL);
-        gemv_args(&g[1], &L->wo, M, b->attn, S2P_Q_HEADS * S2P_HEAD_DIM, b->x, S2P_DIM,
-                  GEMV_X_PLAIN, NULL, NULL, GEMV_EPI_RESID, ssq_b);
-        gemv_args(&g[2], &L->gate_up, M, b->x, S2P_DIM, b->gu, S2P_FFN_DIM, GEMV_X_NORM,
-                  L->ffn_norm.data, ssq_b, GEMV_EPI_SWIGLU, NULL);
-        gemv_args(&g[3], &L->w2, M, b->gu, S2P_FFN_DIM, b->x, S2P_DIM, GEMV_X_PLAIN, NULL, NULL,
-                  GEMV_EPI_RESID, ssq_a);
+        uint8_t* base = b->d_wpack + lb * l;
+        const struct {
+            const s2p_linear* lin;
+            size_t off;
+            int pairs;
+        } g[4] = {{&L->wqkv, 0, 0},
+                  {&L->wo, (size_t)MK2_BLK_Q * MK2_BLK, 0},
+                  {&L->gate_up, (size_t)(MK2_BLK_Q + MK2_BLK_O) * MK2_BLK, 1},
+                  {&L->w2, (size_t)(MK2_BLK_Q + MK2_BLK_O + MK2_BLK_G) * MK2_BLK, 0}};
         for (int i = 0; i < 4; i++)
-            if (s2p_mk_plan_gemv(&g[i], slots, b->mk_lds, &Ls[l].g[i]) != hipSuccess) return 0;
-        Ls[l].q_norm = (const uint16_t*)L->q_norm.data;
-        Ls[l].k_norm = (const uint16_t*)L->k_norm.data;
+            S2P_TRY(hip_ok(s2p_mk2_pack(g[i].lin->w_pack.data, g[i].lin->w_iscale.data,
+                                        g[i].lin->out_features, g[i].lin->in_features, g[i].pairs,
+                                        base + g[i].off, st),
+                           "mk2 pack"));
+        uint16_t* nd = b->d_norms + (size_t)l * MK2_NORM_STRIDE;
+        S2P_TRY(hip_ok(hipMemcpyAsync(nd + MK2_NORM_ATTN, L->attn_norm.data, S2P_DIM * 2,
+                                      hipMemcpyDeviceToDevice, st), "mk2 norms"));
+        S2P_TRY(hip_ok(hipMemcpyAsync(nd + MK2_NORM_FFN, L->ffn_norm.data, S2P_DIM * 2,
+                                      hipMemcpyDeviceToDevice, st), "mk2 norms"));
+        S2P_TRY(hip_ok(hipMemcpyAsync(nd + MK2_NORM_Q, L->q_norm.data, S2P_HEAD_DIM * 2,
+                                      hipMemcpyDeviceToDevice, st), "mk2 norms"));
+        S2P_TRY(hip_ok(hipMemcpyAsync(nd + MK2_NORM_K, L->k_norm.data, S2P_HEAD_DIM * 2,
+                                      hipMemcpyDeviceToDevice, st), "mk2 norms"));
     }
-    GemvArgs hg;
-    gemv_args(&hg, &b->head, M, b->x, S2P_DIM, NULL, b->head.out_features, GEMV_X_NORM,
-              b->final_norm.data, ssq_a, GEMV_EPI_STORE, NULL);
-    if (s2p_mk_plan_gemv(&hg, slots, b->mk_lds, head) != hipSuccess) return 0;
-    A->layers = (const MkLayer*)(b->d_mk + mk_off_layers());
+    S2P_TRY(hip_ok(s2p_mk2_pack(b->head.w_pack.data, b->head.w_iscale.data, b->head.out_features,
+                                b->head.in_features, 0, b->d_hpack, st),
+                   "mk2 pack head"));
+    return hip_ok(hipStreamSynchronize(st), "mk2 pack sync");
+}
+
+/* Set up the persistent kernel for the current plan; returns 0 if the plan
+ * is not served by it (the layer-by-layer path runs instead): more than
+ * MK2_MAX_ROWS rows, quantised caches, INT8 weights. */
+static int mk2_build(s2p_backbone* b, hipStream_t st) {
+    if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS || b->kvb != 16 ||
+        b->o.quant != S2P_WQ_INT4_G32 || b->o.head_quant != S2P_WQ_INT4_G32 ||
+        b->head.out_features > 39 * 16 * MK2_NWG || b->n_seg * 8 > MK2_F_STRIDE)
+        return 0;
+    const int split_pos = 128;
+    const int nsplit = (b->max_span + split_pos - 1) / split_pos;
+    if ((int64_t)b->rows * 32 * nsplit * (2 + S2P_HEAD_DIM) > b->attn_part_floats || nsplit > 64)
+        return 0;
+    if (!b->d_wpack && mk2_pack_all(b, st) != S2P_OK) return 0;
+    Mk2Args* A = &b->mk2;
+    memset(A, 0, sizeof(*A));
+    A->wpack = b->d_wpack;
+    A->hpack = b->d_hpack;
+    A->head_tiles = (b->head.out_features + 15) / 16;
+    A->head_n = b->head.out_features;
+    A->norms = b->d_norms;
+    A->final_norm = (const uint16_t*)b->final_norm.data;
     A->n_layers = b->o.n_layers;
-    A->head = (const MkGemv*)(b->d_mk + mk_off_head(b->o.n_layers));
-    A->wfmt = wfmt;
+    A->rows = b->rows;
     A->x = (uint16_t*)b->x;
-    A->ssq_a = ssq_a;
-    A->ssq_b = ssq_b;
     A->qkv = (uint16_t*)b->qkv;
     A->q = (uint16_t*)b->q;
     A->attn = (uint16_t*)b->attn;
-    A->rope_tab = b->d_rope;
-    A->rows = M;
-    A->eps = NORM_EPS;
-    A->rope_base = ROPE_BASE;
+    A->h = (uint16_t*)b->gu;
+    A->ssq = b->ssq;
+    A->flags = b->d_mk2;
+    A->state = b->d_mk2 + MK2_STATE_WORD;
+    A->err = (int*)(b->d_mk2 + MK2_ERR_WORD);
+    A->attn_ctr = b->d_mk2 + MK2_CTR_WORD;
     A->plan = row_plan(b);
     A->segs = b->d_segs;
     A->n_seg = b->n_seg;
-    {
-        /* the split of s2p_attn_plan_launch for blocks of 8 waves (256
-         * positions per tile round), so both paths agree bit for bit */
-        const int tiles = (b->max_span + 255) / 256;
-        int tpw = 1;
-        while ((int64_t)b->n_seg * 8 * ((tiles + tpw - 1) / tpw) > 4096) tpw *= 2;
-        A->split_pos = 256 * tpw;
-        A->nsplit = (b->max_span + A->split_pos - 1) / A->split_pos;
-    }
-    if (s2p_attn_plan_part_floats(M, b->max_span) > b->attn_part_floats) return 0;
-    A->attn_mqt2 = 1;
+    A->nsplit = nsplit;
+    A->split_pos = split_pos;
     A->attn_part = b->attn_part;
-    A->attn_counters = b->d_attn_ctr;
-    A->bar = b->d_bar;
-    A->err = b->d_err;
-    A->ts = b->d_ts;
-    A->ts_wg = b->d_ts_wg;
-    A->dbg_attn_twice = getenv("S2P_MK_DBG_ATTN2") != NULL;
-    {
-        const char* pp = getenv("S2P_MK_PROBE_PHASE");
-        A->probe = (pp && b->d_ts_wg) ? b->d_ts_wg + (size_t)(1 + 6 * b->o.n_layers) * 2 * b->mk_nwg
-                                      : NULL;
-        A->probe_phase = pp ? (pp[0] == 'a' ? 1000 + atoi(pp + 1) : atoi(pp)) : -1;
-        /* "l,i": stage clocks of GEMV i of layer l (whole-K engine probe) */
-        int pl = -1, pi = -1;
-        if (A->probe && sscanf(pp, "%d,%d", &pl, &pi) == 2 && pl >= 0 && pl < b->o.n_layers &&
-            pi >= 0 && pi < 4)
-            Ls[pl].g[pi].a.probe = A->probe;
-    }
+    A->rope_tab = b->d_rope;
+    A->eps = NORM_EPS;
     return 1;
 }
 
 s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, hipStream_t st) {
     if (!b || !x_in || !logits) return S2P_ERR_INVALID;
     if (!b->planned) return S2P_ERR_STATE;
-    if (b->mk_ready)
-        return hip_ok(s2p_mk_launch((const MkArgs*)b->d_mk, ((const MkArgs*)b->h_mk)->wfmt, x_in,
-                                    logits, b->mk_nwg, b->mk_lds, st),
-                      "verify kernel");
+    if (b->mk2_ready) {
+        Mk2Args A = b->mk2;
+        A.x_in = (const uint16_t*)x_in;
+        A.logits = (uint16_t*)logits;
+        return hip_ok(s2p_mk2_launch(&A, st), "verify kernel");
+    }
     const int M = b->rows;
     const S2pRowPlan plan = row_plan(b);
     float* ssq_a = b->ssq;

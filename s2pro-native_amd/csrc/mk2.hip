@@ -1,0 +1,1061 @@
+/* s2pro MI355X — persistent verify kernel: the K-token verify forward of the
+ * 36-layer slow-AR backbone and the lm head in ONE launch (reference
+ * run_layer, src/slowar/slowar.c:156-260, and the head projection
+ * slowar.c:503-565, restated per row), for plans of at most MK2_MAX_ROWS
+ * rows over bf16 session caches with INT4-g32 weights.
+ *
+ * Why one launch: on this part every dependent kernel costs a few
+ * microseconds of dispatch, ramp and drain, and the weight stream of a
+ * kernel cannot start before its predecessor ends.  Here the weights do not
+ * wait for the activations at all:
+ *
+ *   - one workgroup per CU (MK2_NWG = 256, co-resident), 8 waves: waves 0..6
+ *     compute, wave 7 ("IO wave") moves activations and synchronises;
+ *   - the compute waves stream every weight byte through a ring of NSLOT
+ *     register slots over the fixed per-layer sequence of their work units
+ *     (wqkv | wo | gate_up | w2, then the head): consuming unit k issues the
+ *     load of unit k + NSLOT.  The loads are issued from inline asm, so the
+ *     compiler does not serialise them behind the activations; every wait is
+ *     an explicit vmcnt(2 * (NSLOT - 1)) (the schedule is static: NSLOT - 1
+ *     refills of two loads each lie between a unit's load and its use).
+ *     Nothing else on those waves issues vector memory loads between
+ *     prefetches except the attention phase, whose own (compiler-counted)
+ *     waits can only wait longer, never shorter;
+ *   - phases depend on each other through per-tile flags (one 32-bit word
+ *     per producing tile, holding a per-launch epoch): a consumer polls
+ *     exactly the tiles it reads (attention: its kv head's 48 qkv tiles),
+ *     no grid-wide barrier.  Outputs are written through (sc1) and read
+ *     back with sc1 loads, so no cache maintenance is needed (the 8 XCD L2s
+ *     are not coherent with each other inside a kernel);
+ *   - every wait is bounded: a timeout sets a sticky error flag and every
+ *     later wait returns at once, so the grid always drains.
+ *
+ * Per unit (one 16-row tile x 4 groups of 32 k, 1152 B): the packed nibbles
+ * become bf16 128 + n = 136 + w with one v_and_or_b32 per two weights (the
+ * +8 bias is applied at pack time); activations are the MFMA A operand
+ * (row m), the weights B (column n), so each lane's four outputs share one
+ * group scale, applied by v_fma_mix straight from the f16.  The 136 x (sum
+ * of the group's activations) bias is removed exactly inside the MFMA: its
+ * C operand is MFMA(x, -136).  Units are tile-major and every wave owns a
+ * contiguous unit range, so a wave touches at most two tiles; the waves'
+ * per-tile partials meet in LDS and are summed in wave order
+ * (deterministic).
+ *
+ * The RMSNorm (rule roundings, kernels.cu:46-80) is applied to the staged
+ * rows in LDS with the inverse RMS from the producer's per-16-column sums of
+ * squares; SwiGLU and the residual adds are fused into the reductions. */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <utility>
+
+#include "coh.h"
+#include "common.h"
+#include "attn_dev.h"
+#include "gemv_dev.h"
+#include "mk2_internal.h"
+#include "prims_dev.h"
+
+#define NWAVE 8
+#define CW 7 /* compute waves */
+#define NTH (64 * NWAVE)
+#define NSLOT 10
+#define SPIN_LIMIT (1u << 22)
+#define LDSP(T) __attribute__((address_space(3))) T
+
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+typedef const __attribute__((address_space(1))) s2p_u32x4 G4;
+
+enum { PQ = 0, PO = 1, PG = 2, PD = 3 };
+
+/* ---- static geometry of the four layer GEMVs ---- */
+constexpr int phT(int P) { return P == PQ ? 384 : P == PO ? 160 : P == PG ? 608 : 160; } /* tiles / pairs */
+constexpr int phNB(int P) { return P == PQ ? 20 : P == PO ? 32 : P == PG ? 20 : 76; }    /* 4-group blocks */
+constexpr size_t phOFF(int P) {
+    return P == PQ ? 0 : P == PO ? (size_t)MK2_BLK_Q * MK2_BLK
+                                 : P == PG ? (size_t)(MK2_BLK_Q + MK2_BLK_O) * MK2_BLK
+                                           : (size_t)(MK2_BLK_Q + MK2_BLK_O + MK2_BLK_G) * MK2_BLK;
+}
+constexpr size_t LAYER_BYTES = (size_t)MK2_LAYER_BLKS * MK2_BLK;
+/* units per compute wave at most, and the per-layer unit sequence */
+constexpr int maxu(int P) { return P == PQ ? 6 : P == PO ? 5 : P == PG ? 18 : 11; }
+constexpr int LSEQ = 40;
+constexpr int seq_base(int P) { return P == PQ ? 0 : P == PO ? 6 : P == PG ? 11 : 29; }
+constexpr int seq_phase(int k) { return k < 6 ? PQ : k < 11 ? PO : k < 29 ? PG : PD; }
+constexpr int WAITN = 2 * (NSLOT - 1);
+static_assert(LSEQ % NSLOT == 0, "the ring must tile the layer sequence");
+static_assert(maxu(PQ) + maxu(PO) + maxu(PG) + maxu(PD) == LSEQ, "sequence length");
+
+/* opaque copy: keeps per-unit address arithmetic inside the layer loop
+ * (hoisted, it would pin dozens of SGPRs for the whole kernel) */
+S2P_DEV int opq(int v) {
+    v = __builtin_amdgcn_readfirstlane(v); /* wave-uniform by construction */
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+template <typename F, int... I>
+S2P_DEV void sfor_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+S2P_DEV void sfor(F&& f) {
+    sfor_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+/* workgroup wg's tiles (pairs for gate_up) and compute wave cw's units */
+struct Geo {
+    int t0, np, nt, u0, nu;
+};
+S2P_DEV Geo geo_of(int T, int nb, bool pairs, int wg, int cw) {
+    Geo g;
+    g.t0 = wg * T / MK2_NWG;
+    g.np = (wg + 1) * T / MK2_NWG - g.t0;
+    g.nt = pairs ? 2 * g.np : g.np;
+    const int U = g.nt * nb;
+    g.u0 = cw * U / CW;
+    g.nu = (cw + 1) * U / CW - g.u0;
+    return g;
+}
+template <int P>
+S2P_DEV Geo geoP(int wg, int cw) {
+    return geo_of(phT(P), phNB(P), P == PG, opq(wg), cw);
+}
+/* a compute wave's packed units: start .. last (contiguous in the packed
+ * layout), nu of them; units j >= jb lie in its second local tile */
+struct WG {
+    int start, last, nu, jb, lt0;
+};
+S2P_DEV WG wg_of(const Geo& g, int nb, bool pairs) {
+    WG w;
+    const int tp0 = pairs ? 2 * g.t0 : g.t0;
+    w.nu = g.nu;
+    w.start = g.nu > 0 ? tp0 * nb + g.u0 : 0;
+    w.last = g.nu > 0 ? w.start + g.nu - 1 : 0;
+    w.lt0 = g.u0 / nb;
+    w.jb = nb - (g.u0 - w.lt0 * nb);
+    return w;
+}
+
+/* ---- register slots ---- */
+struct Slot {
+    s2p_u32x4 w;
+    u32x2 s;
+};
+S2P_DEV void slot_issue(Slot& S, const uint8_t* p, uint32_t vw, uint32_t vs) {
+    asm volatile("global_load_dwordx4 %0, %1, %2 nt ; SLOTLOAD" : "=a"(S.w) : "v"(vw), "s"(p) : "memory");
+    asm volatile("global_load_dwordx2 %0, %1, %2 nt ; SLOTLOAD" : "=a"(S.s) : "v"(vs), "s"(p) : "memory");
+}
+template <int N>
+S2P_DEV void slot_wait(Slot& S) {
+    asm volatile("s_waitcnt vmcnt(%2) ; SLOTWAIT %0 %1" : "+a"(S.w), "+a"(S.s) : "n"(N) : "memory");
+}
+S2P_DEV void unit_issue(Slot& S, const uint8_t* blk, int start, int last, int u) {
+    const uint8_t* p = blk + (size_t)min(opq(start) + u, opq(last)) * MK2_BLK;
+    const uint32_t lane = threadIdx.x & 63;
+    slot_issue(S, p, 16 * lane, 1024 + 8 * (lane & 15));
+}
+
+struct Ctx {
+    WG w[4];      /* per layer phase */
+    WG hw;        /* head */
+    int head_t0, head_nt;
+};
+
+/* refill the slot of sequence position K (layer l) with position K + NSLOT:
+ * a unit of the same or the next layer, or past the last layer a head unit */
+template <int K>
+S2P_DEV void refill(Slot (&S)[NSLOT], const Mk2Args& A, int l, const Ctx& C) {
+    constexpr int k2 = K + NSLOT;
+    constexpr int kk = k2 % LSEQ;
+    constexpr int tp = seq_phase(kk);
+    constexpr int tu = kk - seq_base(tp);
+    const int tl = l + k2 / LSEQ;
+    /* one issue point (a branch would merge the asm outputs through copies
+     * of registers whose loads are still in flight): selects only.  Past the
+     * last layer the position is head unit kk. */
+    const bool hd = tl >= A.n_layers;
+    const uint8_t* b = hd ? A.hpack : A.wpack + (size_t)tl * LAYER_BYTES + phOFF(tp);
+    const int st = hd ? C.hw.start : C.w[tp].start;
+    const int la = hd ? C.hw.last : C.w[tp].last;
+    unit_issue(S[K % NSLOT], b, st, la, hd ? kk : tu);
+}
+
+S2P_DEV s2p_f32x4 mfma32(s2p_u32x4 a, s2p_u32x4 b, s2p_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(s2p_bf16x8, a),
+                                                   __builtin_bit_cast(s2p_bf16x8, b), c, 0, 0, 0);
+}
+
+/* one unit: 4 groups of the slot against the staged rows at xa (lane (q, r)
+ * reads row min(r, M - 1); rows >= M of the MFMA output are never used) */
+S2P_DEV s2p_f32x4 unit_mul(const Slot& S, const LDSP(uint16_t)* xa, uint32_t mask, uint32_t one,
+                           s2p_u32x4 NEG) {
+#pragma clang fp contract(off)
+    const uint32_t wd[4] = {S.w.x, S.w.y, S.w.z, S.w.w};
+    s2p_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+        const s2p_u32x4 ag = *(const LDSP(s2p_u32x4)*)(xa + gg * 32);
+        const s2p_f32x4 nb = mfma32(ag, NEG, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+        const uint32_t d = wd[gg];
+        s2p_u32x4 wv;
+        wv.x = (d & mask) | one;
+        wv.y = ((d >> 4) & mask) | one;
+        wv.z = ((d >> 8) & mask) | one;
+        wv.w = ((d >> 12) & mask) | one;
+        const s2p_f32x4 D = mfma32(ag, wv, nb);
+        const uint32_t sw = gg < 2 ? S.s.x : S.s.y;
+        const _Float16 sh =
+            __builtin_bit_cast(_Float16, (uint16_t)((gg & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+        const float sf = (float)sh;
+#pragma unroll
+        for (int i = 0; i < 4; i++) t[i] = fmaf(sf, D[i], t[i]);
+    }
+    return t;
+}
+
+/* ---- LDS carve-up (bytes) ----
+ * layer GEMVs: staged rows [M][K + 8] bf16 at 0 (w2 at M = 6: 116.8 KB),
+ *              partials [tile][cw][M][16] f32 at L_PART (6 tiles: 16 KB);
+ * head:        staged rows at 0 (30.8 KB), partials at L_HPART (39 tiles:
+ *              105 KB);
+ * attention:   its own carve-up from 0 (< 100 KB);
+ * small state from L_INV up (all phases). */
+#define L_XS 0
+#define L_PART (117 * 1024)
+#define L_HPART (32 * 1024)
+#define L_INV (140 * 1024)       /* [M] inverse RMS */
+#define L_OUTB (L_INV + 256)     /* [M][96] bf16 outputs of the workgroup's tiles */
+#define L_XOLD (L_OUTB + 1280)   /* [M][16] bf16 residual before the add */
+#define L_SSQO (L_XOLD + 256)    /* [M][16] f32 sums of squares of the new residual */
+#define L_FLAG (L_SSQO + 512)    /* [16] int broadcast words */
+#define L_NW (L_FLAG + 64)       /* [2560] bf16 norm weights */
+#define L_TOTAL (L_NW + 5120)
+
+/* ---- shared (all waves) pieces of a GEMV phase ---- */
+/* RMSNorm of the staged rows in place: xn = bf16(bf16?(x * inv) * w) with
+ * the rule's two multiplies and one rounding (kernels.cu:46-80) */
+template <int K>
+S2P_DEV void norm_rows(LDSP(unsigned char)* smem, int M) {
+#pragma clang fp contract(off)
+    constexpr int KC = K / 8, RS = K + 8;
+    LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
+    const LDSP(uint16_t)* nw = (const LDSP(uint16_t)*)(smem + L_NW);
+    const LDSP(float)* inv = (const LDSP(float)*)(smem + L_INV);
+    for (int i = threadIdx.x; i < M * KC; i += NTH) {
+        const int m = i / KC, c = i - m * KC;
+        const float iv = inv[m];
+        LDSP(s2p_u32x4)* p = (LDSP(s2p_u32x4)*)(xs + m * RS + c * 8);
+        const s2p_u32x4 v = *p;
+        const s2p_u32x4 w4 = *(const LDSP(s2p_u32x4)*)(nw + c * 8);
+        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t lo = f2bf(__fmul_rn(__fmul_rn(bf2f_lo(vv[d]), iv), bf2f_lo(ww[d])));
+            const uint32_t hi = f2bf(__fmul_rn(__fmul_rn(bf2f_hi(vv[d]), iv), bf2f_hi(ww[d])));
+            vv[d] = lo | (hi << 16);
+        }
+        *p = (s2p_u32x4){vv[0], vv[1], vv[2], vv[3]};
+    }
+    __syncthreads();
+}
+
+/* sum of the waves' partials of local tile lt, element (m, n) */
+S2P_DEV float tile_sum(const LDSP(float)* part, int lt, int m, int n, int M) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < CW; w++) s += part[((lt * CW + w) * M + m) * 16 + n];
+    return s;
+}
+
+/* reduce + epilogue into the LDS output rows (all waves) */
+template <int P>
+S2P_DEV void reduce_phase(LDSP(unsigned char)* smem, int M, int wg) {
+#pragma clang fp contract(off)
+    const LDSP(float)* part = (const LDSP(float)*)(smem + L_PART);
+    const LDSP(uint16_t)* xold = (const LDSP(uint16_t)*)(smem + L_XOLD);
+    LDSP(uint16_t)* outb = (LDSP(uint16_t)*)(smem + L_OUTB);
+    LDSP(float)* ssqo = (LDSP(float)*)(smem + L_SSQO);
+    const Geo g0 = geoP<P>(wg, 0);
+    const int ncol = g0.np * 16;
+    for (int i = threadIdx.x; i < ncol * M; i += NTH) {
+        const int n = i & 15, rest = i >> 4;
+        const int m = rest % M, k = rest / M;
+        const int c = k * 16 + n;
+        uint16_t o;
+        if (P == PG) {
+            o = silu_mul_bf16(f2bf(tile_sum(part, 2 * k, m, n, M)),
+                              f2bf(tile_sum(part, 2 * k + 1, m, n, M)));
+        } else if (P == PO || P == PD) {
+            o = f2bf(__fadd_rn(bf2f(xold[m * 16 + c]), bf2f(f2bf(tile_sum(part, k, m, n, M)))));
+        } else {
+            o = f2bf(tile_sum(part, k, m, n, M));
+        }
+        outb[m * 96 + c] = o;
+        if (P == PO || P == PD) { /* the tile's sum of squares of the new residual row */
+            const float v = bf2f(o);
+            const float t = sum_lanes16(v * v);
+            if (n == 0) ssqo[m * 16 + k] = t;
+        }
+    }
+    __syncthreads();
+}
+
+/* compute waves: one GEMV phase over the ring */
+template <int P>
+S2P_DEV void c_gemv(Slot (&S)[NSLOT], const Mk2Args& A, int l, int cw, const Ctx& C,
+                    LDSP(unsigned char)* smem, int M) {
+    constexpr int NU = maxu(P), NB = phNB(P), RS = NB * 128 + 8;
+    const WG& w = C.w[P];
+    const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
+    const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS) + min(r, M - 1) * RS + q * 8;
+    uint32_t mask = 0x000F000Fu, one = 0x43004300u, neg = 0xC308C308u;
+    asm volatile("" : "+v"(mask), "+v"(one), "+v"(neg));
+    const s2p_u32x4 NEG = {neg, neg, neg, neg};
+    s2p_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    sfor<NU>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int K = seq_base(P) + j;
+        slot_wait<WAITN>(S[K % NSLOT]);
+        if (j < w.nu) {
+            const int b = (w.start + j) % NB;
+            const s2p_f32x4 t = unit_mul(S[K % NSLOT], xs + b * 128, mask, one, NEG);
+            if (j >= w.jb) acc1 += t;
+            else acc0 += t;
+        }
+        refill<K>(S, A, l, C);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    /* partials [lt][cw][m][16]; zeros for the workgroup's tiles this wave
+     * did not touch */
+    LDSP(float)* part = (LDSP(float)*)(smem + L_PART);
+    const Geo g = geoP<P>(blockIdx.x, cw);
+    const int ntouch = w.nu == 0 ? 0 : (w.nu > w.jb ? 2 : 1);
+    for (int lt = 0; lt < g.nt; lt++) {
+        const int k = lt - w.lt0;
+        s2p_f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k == 0 && ntouch > 0) v = acc0;
+        if (k == 1 && ntouch > 1) v = acc1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * q + i;
+            if (m < M) part[((lt * CW + cw) * M + m) * 16 + r] = v[i];
+        }
+    }
+}
+
+/* ---- flags ---- */
+/* distinct per (launch, layer, kind) and never 0 (the flags' initial value) */
+S2P_DEV uint32_t flag_val(uint32_t epoch, int l, int kind) {
+    return epoch * 2048u + (uint32_t)((l + 2) * 8 + kind);
+}
+/* one wave: wait until flags f[i0 .. i0 + n) all read want (n <= 1024) */
+S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t* f = A.flags + kind * MK2_F_STRIDE + i0;
+    if (coh_ld32(A.err)) return;
+    unsigned spins = 0;
+    while (true) {
+        bool ok = true;
+        for (int i = lane; i < n; i += 64) ok = ok && coh_ld32(f + i) == want;
+        if (__all(ok)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > SPIN_LIMIT || ((spins & 1023) == 0 && coh_ld32(A.err))) {
+            if (lane == 0) __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+}
+/* one wave: publish flags f[i0 .. i0 + n) = val once this wave's stores completed */
+S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) {
+    vm_drain();
+    const int lane = threadIdx.x & 63;
+    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind * MK2_F_STRIDE + i0 + i, val);
+}
+
+/* ---- IO wave pieces of a GEMV phase ---- */
+/* stage M rows of K activations (sc1 loads straight to LDS), the layer's
+ * norm weights and the rows' inverse RMS (NORM), the residual's old values
+ * of this workgroup's tiles (RESID) */
+template <int K, bool NORM, bool RESID>
+S2P_DEV void io_stage(const Mk2Args& A, const uint16_t* src, const uint16_t* nw, int M,
+                      LDSP(unsigned char)* smem, int t0, int np) {
+    const int lane = threadIdx.x & 63;
+    constexpr int RS = K + 8;
+    LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
+    for (int m = 0; m < M; m++)
+#pragma unroll 4
+        for (int c = 0; c < K / 512; c++)
+            __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)m * K + c * 512 + lane * 8),
+                                             (LDSP(void)*)(xs + m * RS + c * 512), 16, 0, 16);
+    if (NORM) {
+#pragma unroll
+        for (int c = 0; c < 5; c++)
+            __builtin_amdgcn_global_load_lds((const void*)(nw + c * 512 + lane * 8),
+                                             (LDSP(void)*)(smem + L_NW + c * 1024), 16, 0, 0);
+        /* inverse RMS from the [M][160] per-16-column sums of squares */
+        s2p_u32x4 v[MK2_MAX_ROWS];
+#pragma unroll
+        for (int m = 0; m < MK2_MAX_ROWS; m++)
+            v[m] = (m < M && lane < 40) ? coh_ld128(A.ssq + m * 160 + lane * 4)
+                                        : (s2p_u32x4){0u, 0u, 0u, 0u};
+        LDSP(float)* inv = (LDSP(float)*)(smem + L_INV);
+#pragma unroll
+        for (int m = 0; m < MK2_MAX_ROWS; m++) {
+            if (m >= M) break;
+            float s = (__uint_as_float(v[m].x) + __uint_as_float(v[m].y)) +
+                      (__uint_as_float(v[m].z) + __uint_as_float(v[m].w));
+            s = wave_sum_down(s);
+            if (lane == 0) inv[m] = rsqrt_rule(s / 2560.0f + A.eps);
+        }
+    }
+    if (RESID) {
+        LDSP(uint16_t)* xold = (LDSP(uint16_t)*)(smem + L_XOLD);
+        for (int i = lane; i < M * 16 * np; i += 64) {
+            const int m = i / (16 * np), c = i - m * 16 * np;
+            xold[m * 16 + c] = coh_ld16(A.x + (size_t)m * 2560 + t0 * 16 + c);
+        }
+    }
+    vm_drain();
+}
+
+/* write the workgroup's output columns [t0 * 16, (t0 + np) * 16) of M rows
+ * (and, for the residual, the tiles' sums of squares), then the flags */
+S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst, int ldd,
+                      int t0, int np, int M, bool resid, int kind, uint32_t val) {
+    const int lane = threadIdx.x & 63;
+    const LDSP(uint16_t)* outb = (const LDSP(uint16_t)*)(smem + L_OUTB);
+    const int nch = np * 2; /* 16-byte chunks per row */
+    for (int i = lane; i < M * nch; i += 64) {
+        const int m = i / nch, c = i - m * nch;
+        coh_st128(dst + (size_t)m * ldd + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outb + m * 96 + c * 8));
+    }
+    if (resid && np > 0 && lane < M)
+        coh_stf(A.ssq + lane * 160 + t0, ((const LDSP(float)*)(smem + L_SSQO))[lane * 16]);
+    flags_set(A, kind, t0, np, val);
+}
+
+/* ---- attention: one (segment, kv head, 128-position split) unit per
+ * workgroup, all 8 waves; qk-norm + RoPE of the unit's q vectors and new K
+ * rows fused in (prims_dev.h rule arithmetic), new K/V rows appended to the
+ * cache by the split that holds them.  Wave w owns positions 16w..16w+15 of
+ * the split for the scores and dims 16w..16w+15 of the output for PV; the
+ * last split of a (segment, kv head) to finish merges the splits. */
+#define A_SQ 0                     /* [32][128] bf16 q vectors */
+#define A_SV (8 * 1024)            /* [128][128] bf16 V, 16-byte chunks swizzled */
+#define A_SP (40 * 1024)           /* P hi [32][136] bf16 */
+#define A_SPL (49 * 1024)          /* P lo [32][136] bf16 */
+#define A_SKN (58 * 1024)          /* new K rows [8][128] bf16 */
+#define A_SM (60 * 1024)           /* [32 q][8 waves] f32 row maxima */
+#define A_SL (61 * 1024)           /* [32 q][8 waves] f32 row sums */
+#define A_SO (62 * 1024)           /* [32][128] f32 O (merge input / final) */
+#define A_SW (78 * 1024)           /* merge: [32][nsplit] weights, [32] denominators */
+#define A_PST 136
+#define SVX(t, d) ((t) * 128 + ((((d) >> 3) ^ (((t) >> 2) & 6)) << 3) + ((d) & 7))
+
+S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32_t epoch,
+                       LDSP(unsigned char)* smem) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int qq = lane >> 4, c = lane & 15;
+    const bool io = wave == CW;
+    const S2pAttnSeg g = A.segs[seg];
+    const uint16_t* kvb = (const uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
+    uint16_t* kp = (uint16_t*)kvb + (size_t)kvh * A.plan.max_seq * 128;
+    uint16_t* vp = (uint16_t*)kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
+    const int L = g.L, span = g.span, nrows = g.nrows;
+    const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, span);
+    const int oend = min(p1, L);     /* old positions [p0, oend) */
+    const int s0 = max(p0, L);       /* new positions [s0, p1) */
+    const int nq = nrows * 4, nnew = max(0, p1 - s0);
+    LDSP(uint16_t)* s_q = (LDSP(uint16_t)*)(smem + A_SQ);
+    LDSP(uint16_t)* s_v = (LDSP(uint16_t)*)(smem + A_SV);
+    LDSP(uint16_t)* s_p = (LDSP(uint16_t)*)(smem + A_SP);
+    LDSP(uint16_t)* s_pl = (LDSP(uint16_t)*)(smem + A_SPL);
+    LDSP(uint16_t)* s_kn = (LDSP(uint16_t)*)(smem + A_SKN);
+    LDSP(float)* s_m = (LDSP(float)*)(smem + A_SM);
+    LDSP(float)* s_l = (LDSP(float)*)(smem + A_SL);
+    LDSP(float)* s_o = (LDSP(float)*)(smem + A_SO);
+    LDSP(int)* s_flag = (LDSP(int)*)(smem + L_FLAG);
+
+    /* 1. old K rows of this wave's 16 positions into registers, old V rows
+     * of the split into LDS (independent of this step's outputs) */
+    const int pos = p0 + 16 * wave + c;
+    s2p_u32x4 kr[4];
+#pragma unroll
+    for (int ch = 0; ch < 4; ch++) kr[ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
+    if (p0 + 16 * wave < oend) {
+        const int pk = min(pos, oend - 1);
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) kr[ch] = gld_nt128(kp + (size_t)pk * 128 + 32 * ch + 8 * qq);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 16 * wave + 4 * i + (lane >> 4);
+            const int pv = min(p0 + t, oend - 1);
+            const int k = (lane & 15) ^ ((t >> 2) & 6);
+            __builtin_amdgcn_global_load_lds((const void*)(vp + (size_t)pv * 128 + 8 * k),
+                                             (LDSP(void)*)(s_v + (16 * wave + 4 * i) * 128), 16, 0, 0);
+        }
+    }
+    /* 2. the unit's qkv tiles (q heads 4 kvh..4 kvh + 3, k and v head kvh) */
+    if (io) {
+        const uint32_t want = flag_val(epoch, l, MK2_F_Q);
+        flags_wait(A, MK2_F_Q, 32 * kvh, 32, want);
+        flags_wait(A, MK2_F_Q, 256 + 8 * kvh, 8, want);
+        flags_wait(A, MK2_F_Q, 320 + 8 * kvh, 8, want);
+    }
+    vm_drain(); /* this wave's V rows are in LDS */
+    __syncthreads();
+    /* 3. qk-norm + RoPE: item it < nq is q vector (row it / 4, head 4 kvh +
+     * it % 4); item nq + j is the new slot s0 + j (K normed and roped, V as
+     * is), kept in LDS and appended to the cache */
+    const uint16_t* qn = A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_Q;
+    const uint16_t* kn = A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_K;
+    for (int it = wave; it < nq + nnew; it += NWAVE) {
+        const bool isq = it < nq;
+        const int row = isq ? g.row0 + (it >> 2) : g.first + (s0 + (it - nq) - L);
+        const int head = isq ? 4 * kvh + (it & 3) : 32 + kvh;
+        const uint16_t* src = A.qkv + (size_t)row * 6144 + head * 128;
+        const float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
+        const float* tab = A.rope_tab + (size_t)row * 128;
+        const float c0 = tab[(lane >> 1) * 2], sn0 = tab[(lane >> 1) * 2 + 1];
+        const float c1 = tab[((lane + 64) >> 1) * 2], sn1 = tab[((lane + 64) >> 1) * 2 + 1];
+        const uint16_t* nw = isq ? qn : kn;
+        float o0, o1;
+        qkrope_math(v0, v1, nw[lane], nw[lane + 64], c0, sn0, c1, sn1, A.eps, lane, &o0, &o1);
+        const uint16_t b0 = f2bf(o0), b1 = f2bf(o1);
+        if (isq) {
+            s_q[it * 128 + lane] = b0;
+            s_q[it * 128 + lane + 64] = b1;
+            if (sp == 0) { /* inspection copy of the roped q rows */
+                uint16_t* gq = A.q + (size_t)row * 4096 + head * 128;
+                gq[lane] = b0;
+                gq[lane + 64] = b1;
+            }
+        } else {
+            const int j = it - nq, slot = s0 + j, t = slot - p0;
+            s_kn[j * 128 + lane] = b0;
+            s_kn[j * 128 + lane + 64] = b1;
+            const uint16_t* vs = src + 8 * 128;
+            const uint16_t x0 = coh_ld16(vs + lane), x1 = coh_ld16(vs + lane + 64);
+            s_v[SVX(t, lane)] = x0;
+            s_v[SVX(t, lane + 64)] = x1;
+            coh_st16(kp + (size_t)slot * 128 + lane, b0);
+            coh_st16(kp + (size_t)slot * 128 + lane + 64, b1);
+            coh_st16(vp + (size_t)slot * 128 + lane, x0);
+            coh_st16(vp + (size_t)slot * 128 + lane + 64, x1);
+        }
+    }
+    /* rows past the split's end hold zeros (their P is 0; stale LDS could be
+     * Inf / NaN) */
+    for (int i = threadIdx.x; i < (p0 + 128 - max(p1, p0)) * 128; i += NTH) {
+        const int t = max(p1, p0) - p0 + (i >> 7), d = i & 127;
+        s_v[SVX(t, d)] = 0;
+    }
+    __syncthreads();
+    /* 4. scores of this wave's 16 positions for the 32 q vectors */
+    if (pos >= s0 && pos < p1) {
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++)
+            kr[ch] = *(const LDSP(s2p_u32x4)*)(s_kn + (pos - s0) * 128 + 32 * ch + 8 * qq);
+    }
+    const float scale = 0.08838834764831845f;
+    s2p_f32x4 sc[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+            const s2p_u32x4 qa = *(const LDSP(s2p_u32x4)*)(s_q + (16 * qt + c) * 128 + 32 * ch + 8 * qq);
+            acc = mfma16x16x32(qa, kr[ch], acc);
+        }
+        sc[qt] = acc;
+    }
+    /* visibility: lane (qq, c) element i is q vector 16 qt + 4 qq + i
+     * (row (16 qt + 4 qq + i) / 4 = 4 qt + qq), position pos */
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int rl = 4 * qt + qq;
+        bool vis = rl < nrows && pos < p1;
+        if (vis && pos >= L) {
+            const int b = pos - L;
+            vis = b < 64 && ((A.plan.vis[g.row0 + rl] >> b) & 1ull);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float t = vis ? sc[qt][i] * scale : -INFINITY;
+            sc[qt][i] = t;
+            const float mx = max16(t);
+            if (c == 0) s_m[(16 * qt + 4 * qq + i) * 8 + wave] = mx;
+        }
+    }
+    __syncthreads();
+    /* 5. P = e^(s - M) (M over the split), row sums, P as bf16 hi + lo */
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qv = 16 * qt + 4 * qq + i;
+            const s2p_f32x4 ma = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8);
+            const s2p_f32x4 mb = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8 + 4);
+            const float M = fmaxf(fmaxf(fmaxf(ma[0], ma[1]), fmaxf(ma[2], ma[3])),
+                                  fmaxf(fmaxf(mb[0], mb[1]), fmaxf(mb[2], mb[3])));
+            const float Ms = M == -INFINITY ? 0.f : M;
+            const float p = __expf(sc[qt][i] - Ms);
+            const float ps = sum16(p);
+            if (c == 0) s_l[qv * 8 + wave] = ps;
+            const uint16_t h = f2bf(p);
+            s_p[qv * A_PST + 16 * wave + c] = h;
+            s_pl[qv * A_PST + 16 * wave + c] = f2bf(p - bf2f(h));
+        }
+    __syncthreads();
+    /* 6. O[:, 16 wave .. 16 wave + 15] = P V */
+    s2p_f32x4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ch = 0; ch < 4; ch++) {
+        uint32_t b[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = 32 * ch + 8 * qq + 2 * e;
+            b[e] = (uint32_t)s_v[SVX(t, 16 * wave + c)] | ((uint32_t)s_v[SVX(t + 1, 16 * wave + c)] << 16);
+        }
+        const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const s2p_u32x4 pa = *(const LDSP(s2p_u32x4)*)(s_p + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
+            const s2p_u32x4 pl = *(const LDSP(s2p_u32x4)*)(s_pl + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
+            o[qt] = mfma16x16x32(pl, bv, o[qt]);
+            o[qt] = mfma16x16x32(pa, bv, o[qt]);
+        }
+    }
+    /* O and the split's (m, l) per q vector into LDS */
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_o[(16 * qt + 4 * qq + i) * 128 + 16 * wave + c] = o[qt][i];
+    __syncthreads();
+    const int ns = A.nsplit;
+    const int nrow_all = A.rows;
+    float* part = A.attn_part;
+    float* po = part + (size_t)nrow_all * 32 * ns * 2;
+    bool fin = ns == 1;
+    if (!fin) {
+        /* partial of this split: written by the IO wave, then the arrival */
+        if (io) {
+            for (int idx = lane; idx < nq * 32; idx += 64) {
+                const int qv = idx >> 5, d4 = (idx & 31) * 4;
+                const size_t pi = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns + sp;
+                coh_st128(po + pi * 128 + d4, *(const LDSP(s2p_u32x4)*)(s_o + qv * 128 + d4));
+                if (d4 == 0) {
+                    const s2p_f32x4 ma = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8);
+                    const s2p_f32x4 mb = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8 + 4);
+                    const s2p_f32x4 la = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8);
+                    const s2p_f32x4 lb = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8 + 4);
+                    const float M = fmaxf(fmaxf(fmaxf(ma[0], ma[1]), fmaxf(ma[2], ma[3])),
+                                          fmaxf(fmaxf(mb[0], mb[1]), fmaxf(mb[2], mb[3])));
+                    const float ls = ((la[0] + la[1]) + (la[2] + la[3])) + ((lb[0] + lb[1]) + (lb[2] + lb[3]));
+                    coh_st64(part + pi * 2, (uint64_t)__float_as_uint(M) | ((uint64_t)__float_as_uint(ls) << 32));
+                }
+            }
+            vm_drain();
+            if (lane == 0) {
+                const unsigned prev = __hip_atomic_fetch_add(A.attn_ctr + seg * 8 + kvh, 1u,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *s_flag = prev == (unsigned)(ns - 1);
+            }
+        }
+        __syncthreads();
+        fin = *s_flag != 0;
+        if (fin) {
+            /* merge: split weights e^(m_s - M) and denominators per q vector,
+             * then every output with all of its split loads in flight */
+            LDSP(float)* wm = (LDSP(float)*)(smem + A_SW);
+            LDSP(float)* lt = wm + 32 * ns;
+            LDSP(float)* wl = lt + 32;
+            for (int idx = threadIdx.x; idx < nq * ns; idx += NTH) {
+                const int qv = idx / ns, s2 = idx - qv * ns;
+                const size_t pi = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns + s2;
+                const uint64_t ml = coh_ld64(part + pi * 2);
+                wm[idx] = __uint_as_float((uint32_t)ml);
+                wl[idx] = __uint_as_float((uint32_t)(ml >> 32));
+            }
+            __syncthreads();
+            if ((int)threadIdx.x < nq) {
+                const int qv = threadIdx.x;
+                float M = -INFINITY;
+                for (int k = 0; k < ns; k++) M = fmaxf(M, wm[qv * ns + k]);
+                const float Ms = M == -INFINITY ? 0.f : M;
+                float lsum = 0.f;
+                for (int k = 0; k < ns; k++) {
+                    const float w = __expf(wm[qv * ns + k] - Ms);
+                    lsum = fmaf(wl[qv * ns + k], w, lsum);
+                    wm[qv * ns + k] = w;
+                }
+                lt[qv] = lsum;
+            }
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < nq * 32; idx += NTH) {
+                const int qv = idx >> 5, d = (idx & 31) * 4;
+                const size_t p0i = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns;
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int k0 = 0; k0 < ns; k0 += 8) {
+                    s2p_u32x4 ov[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        ov[j] = k0 + j < ns ? coh_ld128(po + (p0i + k0 + j) * 128 + d) : (s2p_u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        if (k0 + j >= ns) break;
+                        const float w = wm[qv * ns + k0 + j];
+                        acc[0] = fmaf(__uint_as_float(ov[j].x), w, acc[0]);
+                        acc[1] = fmaf(__uint_as_float(ov[j].y), w, acc[1]);
+                        acc[2] = fmaf(__uint_as_float(ov[j].z), w, acc[2]);
+                        acc[3] = fmaf(__uint_as_float(ov[j].w), w, acc[3]);
+                    }
+                }
+                const float lp = lt[qv];
+#pragma unroll
+                for (int k = 0; k < 4; k++) s_o[qv * 128 + d + k] = acc[k] / lp;
+            }
+            __syncthreads();
+        }
+    } else {
+        /* one split: normalise in place */
+        for (int idx = threadIdx.x; idx < nq * 128; idx += NTH) {
+            const int qv = idx >> 7;
+            const s2p_f32x4 la = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8);
+            const s2p_f32x4 lb = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8 + 4);
+            const float ls = ((la[0] + la[1]) + (la[2] + la[3])) + ((lb[0] + lb[1]) + (lb[2] + lb[3]));
+            s_o[idx] = s_o[idx] / ls;
+        }
+        __syncthreads();
+    }
+    if (fin && io) {
+        /* final rows: attn[row][(4 kvh + g) * 128 + d] as bf16, then the flag */
+        for (int idx = lane; idx < nq * 16; idx += 64) {
+            const int qv = idx >> 4, d = (idx & 15) * 8;
+            const LDSP(float)* sv = s_o + qv * 128 + d;
+            s2p_u32x4 ob;
+            ob.x = (uint32_t)f2bf(sv[0]) | ((uint32_t)f2bf(sv[1]) << 16);
+            ob.y = (uint32_t)f2bf(sv[2]) | ((uint32_t)f2bf(sv[3]) << 16);
+            ob.z = (uint32_t)f2bf(sv[4]) | ((uint32_t)f2bf(sv[5]) << 16);
+            ob.w = (uint32_t)f2bf(sv[6]) | ((uint32_t)f2bf(sv[7]) << 16);
+            coh_st128(A.attn + (size_t)(g.row0 + (qv >> 2)) * 4096 + (4 * kvh + (qv & 3)) * 128 + d, ob);
+        }
+        if (ns > 1 && lane == 0)
+            __hip_atomic_store(A.attn_ctr + seg * 8 + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flags_set(A, MK2_F_ATT, seg * 8 + kvh, 1, flag_val(epoch, l, MK2_F_ATT));
+    }
+    __syncthreads();
+}
+
+/* attention phase of layer l: this workgroup's units */
+S2P_DEV void attn_phase(const Mk2Args& A, int l, uint32_t epoch, LDSP(unsigned char)* smem) {
+    const int nu = A.n_seg * 8 * A.nsplit;
+    for (int u = blockIdx.x; u < nu; u += gridDim.x) {
+        const int seg = u % A.n_seg, kvh = (u / A.n_seg) % 8, sp = u / (A.n_seg * 8);
+        attn_unit(A, l, seg, kvh, sp, epoch, smem);
+    }
+}
+
+/* ---- head: the ring continues over this wave's head units ---- */
+S2P_DEV void c_head(Slot (&S)[NSLOT], const Mk2Args& A, int cw, const Ctx& C,
+                    LDSP(unsigned char)* smem, int M) {
+    constexpr int RS = 2560 + 8;
+    const WG& w = C.hw;
+    const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
+    const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS) + min(r, M - 1) * RS + q * 8;
+    LDSP(float)* part = (LDSP(float)*)(smem + L_HPART);
+    uint32_t mask = 0x000F000Fu, one = 0x43004300u, neg = 0xC308C308u;
+    asm volatile("" : "+v"(mask), "+v"(one), "+v"(neg));
+    const s2p_u32x4 NEG = {neg, neg, neg, neg};
+    /* the wave's units are tiles (start / 20) .. (last / 20) of the packed
+     * head, local tile = tile - head_t0 */
+    s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int cur = w.start / 20;
+    auto flush = [&]() __attribute__((always_inline)) {
+        const int lt = cur - C.head_t0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * q + i;
+            if (m < M) part[((lt * CW + cw) * M + m) * 16 + r] = acc[i];
+        }
+        acc = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    for (int r0 = 0; r0 < w.nu; r0 += NSLOT) {
+        sfor<NSLOT>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            slot_wait<WAITN>(S[j]);
+            const int u = r0 + j;
+            if (u < w.nu) {
+                const int pu = w.start + u;
+                const int tile = pu / 20, b = pu - tile * 20;
+                if (tile != cur) {
+                    flush();
+                    cur = tile;
+                }
+                acc += unit_mul(S[j], xs + b * 128, mask, one, NEG);
+            }
+            unit_issue(S[j], A.hpack, w.start, w.last, u + NSLOT);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    if (w.nu > 0) flush();
+}
+
+/* head reduction: logits[m][n] of this workgroup's tiles (all waves); a
+ * tile's partials come from the waves whose unit range meets it, summed in
+ * wave order */
+S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* smem, int M) {
+    const LDSP(float)* part = (const LDSP(float)*)(smem + L_HPART);
+    const int nout = C.head_nt * 16 * M;
+    const int U = C.head_nt * 20;
+    for (int i = threadIdx.x; i < nout; i += NTH) {
+        const int n = i & 15, rest = i >> 4;
+        const int m = rest % M, lt = rest / M;
+        const int row = (C.head_t0 + lt) * 16 + n;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < CW; w++) {
+            const int u0 = w * U / CW, u1 = (w + 1) * U / CW;
+            if (u0 < (lt + 1) * 20 && u1 > lt * 20) s += part[((lt * CW + w) * M + m) * 16 + n];
+        }
+        if (row < A.head_n) A.logits[(size_t)m * A.head_n + row] = f2bf(s);
+    }
+}
+
+/* ---- the kernel ---- */
+__global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LDSP(unsigned char)* smem = (LDSP(unsigned char)*)smem_raw;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int M = A.rows, NL = A.n_layers;
+    const int wg = blockIdx.x;
+    const uint32_t epoch = coh_ld32(A.state);
+
+    if (wave < CW) {
+        /* ================= compute waves ================= */
+        asm volatile("; CPATH_BEGIN");
+        const int cw = wave;
+        Ctx C;
+        C.w[PQ] = wg_of(geoP<PQ>(wg, cw), phNB(PQ), false);
+        C.w[PO] = wg_of(geoP<PO>(wg, cw), phNB(PO), false);
+        C.w[PG] = wg_of(geoP<PG>(wg, cw), phNB(PG), true);
+        C.w[PD] = wg_of(geoP<PD>(wg, cw), phNB(PD), false);
+        {
+            const Geo gh = geo_of(A.head_tiles, 20, false, wg, cw);
+            C.hw = wg_of(gh, 20, false);
+            C.head_t0 = gh.t0;
+            C.head_nt = gh.nt;
+        }
+        Slot S[NSLOT];
+        sfor<NSLOT>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int tp = seq_phase(k);
+            const bool hd = NL == 0;
+            unit_issue(S[k], hd ? A.hpack : A.wpack + phOFF(tp), hd ? C.hw.start : C.w[tp].start,
+                       hd ? C.hw.last : C.w[tp].last, hd ? k : k - seq_base(tp));
+        });
+        __syncthreads(); /* (init) */
+        for (int l = 0; l < NL; l++) {
+            /* Q */
+            __syncthreads();
+            norm_rows<2560>(smem, M);
+            c_gemv<PQ>(S, A, l, cw, C, smem, M);
+            __syncthreads();
+            reduce_phase<PQ>(smem, M, wg);
+            /* attention */
+            attn_phase(A, l, epoch, smem);
+            /* O */
+            __syncthreads();
+            c_gemv<PO>(S, A, l, cw, C, smem, M);
+            __syncthreads();
+            reduce_phase<PO>(smem, M, wg);
+            /* G */
+            __syncthreads();
+            norm_rows<2560>(smem, M);
+            c_gemv<PG>(S, A, l, cw, C, smem, M);
+            __syncthreads();
+            reduce_phase<PG>(smem, M, wg);
+            /* D */
+            __syncthreads();
+            c_gemv<PD>(S, A, l, cw, C, smem, M);
+            __syncthreads();
+            reduce_phase<PD>(smem, M, wg);
+        }
+        /* head */
+        __syncthreads();
+        norm_rows<2560>(smem, M);
+        c_head(S, A, cw, C, smem, M);
+        __syncthreads();
+        head_reduce(A, C, smem, M);
+        /* drain this wave's remaining (clamped, unused) prefetches */
+        vm_drain();
+    } else {
+        /* ================= IO wave ================= */
+        asm volatile("; IOPATH_BEGIN");
+        /* residual stream init: x = x_in for this workgroup's 16-column
+         * tile (the w2 geometry) and its sums of squares */
+        const Geo gd = geoP<PD>(wg, 0);
+        {
+            for (int i = lane; i < M * 16 * gd.np; i += 64) {
+                const int m = i / 16, cc = i & 15;
+                const size_t ix = (size_t)m * 2560 + gd.t0 * 16 + cc;
+                const uint16_t v = A.x_in[ix];
+                coh_st16(A.x + ix, v);
+                const float f = bf2f(v);
+                const float t = sum_lanes16(f * f);
+                if (cc == 0) coh_stf(A.ssq + m * 160 + gd.t0, t);
+            }
+            flags_set(A, MK2_F_INIT, gd.t0, gd.np, flag_val(epoch, -1, MK2_F_INIT));
+        }
+        __syncthreads(); /* (init) */
+        const Geo gq = geoP<PQ>(wg, 0), go = geoP<PO>(wg, 0), gg = geoP<PG>(wg, 0);
+        for (int l = 0; l < NL; l++) {
+            const uint16_t* nl = A.norms + (size_t)l * MK2_NORM_STRIDE;
+            /* Q: x (previous w2, or the init) -> qkv */
+            if (l == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
+            else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, l - 1, MK2_F_D));
+            io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_ATTN, M, smem, gq.t0, gq.np);
+            __syncthreads();
+            norm_rows<2560>(smem, M);
+            __syncthreads();
+            reduce_phase<PQ>(smem, M, wg);
+            io_store(A, smem, A.qkv, 6144, gq.t0, gq.np, M, false, MK2_F_Q, flag_val(epoch, l, MK2_F_Q));
+            /* attention */
+            attn_phase(A, l, epoch, smem);
+            /* O: attn -> x += wo attn */
+            flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8, flag_val(epoch, l, MK2_F_ATT));
+            io_stage<4096, false, true>(A, A.attn, nullptr, M, smem, go.t0, go.np);
+            __syncthreads();
+            __syncthreads();
+            reduce_phase<PO>(smem, M, wg);
+            io_store(A, smem, A.x, 2560, go.t0, go.np, M, true, MK2_F_O, flag_val(epoch, l, MK2_F_O));
+            /* G: x -> h */
+            flags_wait(A, MK2_F_O, 0, 160, flag_val(epoch, l, MK2_F_O));
+            io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_FFN, M, smem, gg.t0, gg.np);
+            __syncthreads();
+            norm_rows<2560>(smem, M);
+            __syncthreads();
+            reduce_phase<PG>(smem, M, wg);
+            io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, MK2_F_G, flag_val(epoch, l, MK2_F_G));
+            /* D: h -> x += w2 h */
+            flags_wait(A, MK2_F_G, 0, 608, flag_val(epoch, l, MK2_F_G));
+            io_stage<9728, false, true>(A, A.h, nullptr, M, smem, gd.t0, gd.np);
+            __syncthreads();
+            __syncthreads();
+            reduce_phase<PD>(smem, M, wg);
+            io_store(A, smem, A.x, 2560, gd.t0, gd.np, M, true, MK2_F_D, flag_val(epoch, l, MK2_F_D));
+        }
+        /* head: final RMSNorm of x */
+        if (NL == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
+        else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, NL - 1, MK2_F_D));
+        io_stage<2560, true, false>(A, A.x, A.final_norm, M, smem, 0, 0);
+        __syncthreads();
+        norm_rows<2560>(smem, M);
+        __syncthreads();
+        {
+            const Geo gh = geo_of(A.head_tiles, 20, false, wg, 0);
+            Ctx C;
+            C.head_t0 = gh.t0;
+            C.head_nt = gh.nt;
+            head_reduce(A, C, smem, M);
+        }
+        /* launch bookkeeping: the last workgroup to finish advances the epoch */
+        vm_drain();
+        if (lane == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(A.state + 1, 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            if (done + 1 == (epoch + 1) * (uint32_t)gridDim.x)
+                __hip_atomic_store(A.state, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+/* ---- packing ---- */
+/* one thread per (tile, block, lane): 16 bytes of codes (4 groups of the
+ * lane's row and quarter) and, lanes 0..15, the row's 4 group scales */
+__global__ void k_mk2_pack(const uint8_t* __restrict__ w, const uint16_t* __restrict__ sc, int N,
+                           int K, int pairs, uint8_t* __restrict__ dst) {
+    const int nb = K / 128;
+    const int T = (N + 15) / 16;
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = (int)(gid & 63);
+    const long tb = gid >> 6;
+    if (tb >= (long)T * nb) return;
+    const int t = (int)(tb / nb), b = (int)(tb % nb);
+    const int q = lane >> 4, r = lane & 15;
+    /* packed tile t -> source tile: pairs interleave gate tile p and up tile p */
+    int st = t;
+    if (pairs) st = (t & 1) ? (N / 32) + (t >> 1) : (t >> 1);
+    const int n = st * 16 + r;
+    uint32_t o[4];
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+        const int grp = 4 * b + gg;
+        uint32_t d = 0x88888888u; /* padding rows: code 8 = weight 0 */
+        if (n < N) {
+            const uint32_t s = *(const uint32_t*)(w + (size_t)n * (K / 2) + grp * 16 + 4 * q);
+            /* source nibble p = weight k = 8q + p; target nibble j = k 8q + 2j,
+             * nibble 4 + j = k 8q + 2j + 1, each biased by 8 */
+            d = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t lo = ((s >> (8 * j)) & 0xFu) ^ 8u;
+                const uint32_t hi = ((s >> (8 * j + 4)) & 0xFu) ^ 8u;
+                d |= lo << (4 * j);
+                d |= hi << (16 + 4 * j);
+            }
+        }
+        o[gg] = d;
+    }
+    uint8_t* blk = dst + ((size_t)t * nb + b) * MK2_BLK;
+    *(s2p_u32x4*)(blk + 16 * lane) = (s2p_u32x4){o[0], o[1], o[2], o[3]};
+    if (lane < 16) {
+        uint16_t s4[4];
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) s4[gg] = n < N ? sc[(size_t)n * (K / 32) + 4 * b + gg] : 0;
+        uint16_t* sd = (uint16_t*)(blk + 1024) + r * 4;
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) sd[gg] = s4[gg];
+    }
+}
+
+extern "C" hipError_t s2p_mk2_pack(const void* w_pack, const void* scales, int N, int K, int pairs,
+                                   void* dst, hipStream_t st) {
+    if (!w_pack || !scales || !dst || N <= 0 || (K % 128) || (pairs && (N % 32)))
+        return hipErrorInvalidValue;
+    const long threads = (long)((N + 15) / 16) * (K / 128) * 64;
+    hipLaunchKernelGGL(k_mk2_pack, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       (const uint8_t*)w_pack, (const uint16_t*)scales, N, K, pairs, (uint8_t*)dst);
+    return hipGetLastError();
+}
+
+/* ---- launch ---- */
+static int g_mk2_ok = -1;
+
+extern "C" int s2p_mk2_supported(void) {
+    if (g_mk2_ok >= 0) return g_mk2_ok ? 0 : -1;
+    int dev = 0, cus = 0, per_cu = 0;
+    bool ok = hipGetDevice(&dev) == hipSuccess &&
+              hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+              cus == MK2_NWG &&
+              hipFuncSetAttribute((const void*)k_mk2, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)L_TOTAL) == hipSuccess &&
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2, NTH, L_TOTAL) ==
+                  hipSuccess &&
+              per_cu >= 1;
+    (void)hipGetLastError();
+    g_mk2_ok = ok ? 1 : 0;
+    return ok ? 0 : -1;
+}
+
+extern "C" hipError_t s2p_mk2_launch(const Mk2Args* args, hipStream_t st) {
+    if (s2p_mk2_supported() != 0) return hipErrorNotSupported;
+    if (!args || args->rows < 1 || args->rows > MK2_MAX_ROWS || args->n_seg * 8 > MK2_F_STRIDE ||
+        args->head_tiles > 39 * MK2_NWG)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mk2, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    return hipGetLastError();
+}

@@ -1,0 +1,90 @@
+/* s2pro MI355X — descriptor of the persistent verify kernel (mk2.hip),
+ * shared with the C host code (verify.c).  Not public ABI. */
+#ifndef S2P_MK2_INTERNAL_H
+#define S2P_MK2_INTERNAL_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#include "prims_internal.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Tile-packed INT4-g32 weights: a 16-row tile's 4-group block is 1152 B:
+ * 1024 B of codes (lane l = quarter q = l / 16, row r = l % 16: 16 B = one
+ * dword per group, the row's k = 8q..8q+7 of that group, nibbles biased by
+ * +8 and placed so that dword >> 4j & 0x000F000F holds k = 8q+2j, 8q+2j+1)
+ * then 128 B of f16 scales [16 rows][4 groups].  A linear is [tile][block];
+ * gate_up is [pair][gate tile, up tile][block]. */
+#define MK2_BLK 1152
+#define MK2_MAX_ROWS 6    /* rows the kernel serves (the w2 activations fill LDS) */
+#define MK2_NWG 256       /* one workgroup per CU of an MI355X */
+
+/* per-layer packed block counts and offsets (blocks) */
+#define MK2_BLK_Q (384 * 20)
+#define MK2_BLK_O (160 * 32)
+#define MK2_BLK_G (1216 * 20)
+#define MK2_BLK_D (160 * 76)
+#define MK2_LAYER_BLKS (MK2_BLK_Q + MK2_BLK_O + MK2_BLK_G + MK2_BLK_D)
+
+/* per-layer norm weights, packed: attn 2560 | ffn 2560 | q 128 | k 128 */
+#define MK2_NORM_ATTN 0
+#define MK2_NORM_FFN 2560
+#define MK2_NORM_Q 5120
+#define MK2_NORM_K 5248
+#define MK2_NORM_STRIDE 5376
+
+/* flag kinds: one 32-bit word per producing tile (or attention block) */
+enum { MK2_F_INIT = 0, MK2_F_Q = 1, MK2_F_ATT = 2, MK2_F_O = 3, MK2_F_G = 4, MK2_F_D = 5,
+       MK2_F_KINDS = 6 };
+#define MK2_F_STRIDE 1024
+/* the backbone's mk2 state block (uint32 words): flags, then the launch
+ * epoch and done count, the error flag, the attention split counters */
+#define MK2_STATE_WORD (MK2_F_KINDS * MK2_F_STRIDE)
+#define MK2_ERR_WORD (MK2_STATE_WORD + 2)
+#define MK2_CTR_WORD (MK2_STATE_WORD + 4)
+#define MK2_STATE_WORDS (MK2_CTR_WORD + MK2_F_STRIDE)
+
+typedef struct {
+    const uint8_t* wpack;          /* [n_layers][MK2_LAYER_BLKS] packed blocks */
+    const uint8_t* hpack;          /* head [head_tiles][20] */
+    int head_tiles, head_n;        /* tiles (rows padded to 16) and real rows */
+    const uint16_t* norms;         /* [n_layers][MK2_NORM_STRIDE]: attn, ffn, q, k norm weights */
+    const uint16_t* final_norm;
+    int n_layers, rows;
+    const uint16_t* x_in;
+    uint16_t* x;                   /* [rows][2560] residual stream */
+    uint16_t* qkv;                 /* [rows][6144] */
+    uint16_t* q;                   /* [rows][4096] (inspection copy of the roped q rows) */
+    uint16_t* attn;                /* [rows][4096] */
+    uint16_t* h;                   /* [rows][9728] */
+    uint16_t* logits;              /* [rows][head_n] */
+    float* ssq;                    /* [MK2_MAX_ROWS][160] per-16-column sums of squares of x */
+    uint32_t* flags;               /* [MK2_F_KINDS][MK2_F_STRIDE] */
+    uint32_t* state;               /* [0] launch epoch, [1] workgroups done (monotonic) */
+    int* err;                      /* sticky: a wait timed out */
+    /* attention */
+    S2pRowPlan plan;
+    const S2pAttnSeg* segs;
+    int n_seg, nsplit, split_pos;
+    float* attn_part;
+    unsigned* attn_ctr;            /* [n_seg * 8], zero between launches */
+    const float* rope_tab;
+    float eps;
+} Mk2Args;
+
+/* 0 when the device can run the kernel (MK2_NWG co-resident workgroups) */
+int s2p_mk2_supported(void);
+/* pack one INT4-g32 linear (codes [N][K/2], f16 scales [N][K/32]) into the
+ * tile layout at dst; pairs = 1: rows [0, N/2) gate, [N/2, N) up */
+hipError_t s2p_mk2_pack(const void* w_pack, const void* scales, int N, int K, int pairs,
+                        void* dst, hipStream_t st);
+/* args: host copy, passed by value (kernel arguments) */
+hipError_t s2p_mk2_launch(const Mk2Args* args, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

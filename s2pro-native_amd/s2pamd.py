@@ -168,10 +168,7 @@ EXTRA = {
     "s2p_attn_set_probe": (None, [P, I]),
     "s2p_test_f2bf": (I, [P, P, I64, P]),
     "s2p_test_desc_bytes": (SZ, [I]),
-    "s2p_backbone_mk_grid": (I, [P]),
     "s2p_backbone_mk_status": (I, [P]),
-    "s2p_backbone_mk_times": (I, [P, P, I]),
-    "s2p_backbone_mk_times_wg": (I, [P, P, ctypes.c_size_t]),
     "s2p_synth_bytes": (I, [P, I64, U64, P]),
     "s2p_synth_int8": (I, [P, I64, U64, P]),
     "s2p_synth_f16_absnormal": (I, [P, I64, F, U64, P]),
