@@ -474,13 +474,17 @@ static s2p_status mk2_pack_all(s2p_backbone* b, hipStream_t st) {
 static int mk2_build(s2p_backbone* b, hipStream_t st) {
     if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS || b->kvb != 16 ||
         b->o.quant != S2P_WQ_INT4_G32 || b->o.head_quant != S2P_WQ_INT4_G32 ||
-        b->head.out_features > 39 * 16 * MK2_NWG || b->n_seg * 8 > MK2_F_STRIDE)
+        b->head.out_features > 39 * 16 * MK2_NWG || b->n_seg > 8 ||
+        b->o.n_layers > MK2_MAX_LAYERS)
         return 0;
     const int split_pos = 128;
     const int nsplit = (b->max_span + split_pos - 1) / split_pos;
-    if ((int64_t)b->rows * 32 * nsplit * (2 + S2P_HEAD_DIM) > b->attn_part_floats || nsplit > 64)
+    if ((int64_t)b->rows * 32 * nsplit * (2 + S2P_HEAD_DIM) > b->attn_part_floats ||
+        nsplit > MK2_MAX_SPLIT || b->n_seg * 8 * nsplit > MK2_ATT_MAX)
         return 0;
     if (!b->d_wpack && mk2_pack_all(b, st) != S2P_OK) return 0;
+    /* a fresh state block per plan: flags, launch epoch, split counters */
+    if (hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st) != hipSuccess) return 0;
     Mk2Args* A = &b->mk2;
     memset(A, 0, sizeof(*A));
     A->wpack = b->d_wpack;

@@ -58,7 +58,7 @@
 #define NWAVE 8
 #define CW 7 /* compute waves */
 #define NTH (64 * NWAVE)
-#define NSLOT 10
+#define NSLOT 20
 #define SPIN_LIMIT (1u << 22)
 #define LDSP(T) __attribute__((address_space(3))) T
 
@@ -66,6 +66,23 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 typedef const __attribute__((address_space(1))) s2p_u32x4 G4;
 
 enum { PQ = 0, PO = 1, PG = 2, PD = 3 };
+
+/* Build with -DMK2_TRACE for per-workgroup phase clocks (diagnostics; not
+ * in the product build): g_mk2_tr[wg][layer][event], s2p_mk2_trace copies
+ * them out. */
+#ifdef MK2_TRACE
+#define TR_L 40
+#define TR_E 32
+__device__ uint64_t g_mk2_tr[MK2_NWG][TR_L][TR_E];
+#define TRACE(l, e)                                                                    \
+    do {                                                                               \
+        if ((threadIdx.x & 63) == 0 && (l) < TR_L) g_mk2_tr[blockIdx.x][l][e] = wall_clock64(); \
+    } while (0)
+#else
+#define TRACE(l, e) \
+    do {            \
+    } while (0)
+#endif
 
 /* ---- static geometry of the four layer GEMVs ---- */
 constexpr int phT(int P) { return P == PQ ? 384 : P == PO ? 160 : P == PG ? 608 : 160; } /* tiles / pairs */
@@ -90,6 +107,14 @@ static_assert(maxu(PQ) + maxu(PO) + maxu(PG) + maxu(PD) == LSEQ, "sequence lengt
 S2P_DEV int opq(int v) {
     v = __builtin_amdgcn_readfirstlane(v); /* wave-uniform by construction */
     asm volatile("" : "+s"(v));
+    return v;
+}
+/* opaque thread index: lane-dependent addresses of a phase are computed in
+ * that phase (hoisted out of the layer loop, they would hold VGPRs across
+ * every other phase) */
+S2P_DEV int tid_opq() {
+    int v = threadIdx.x;
+    asm volatile("" : "+v"(v));
     return v;
 }
 
@@ -186,41 +211,57 @@ S2P_DEV s2p_f32x4 mfma32(s2p_u32x4 a, s2p_u32x4 b, s2p_f32x4 c) {
 }
 
 /* one unit: 4 groups of the slot against the staged rows at xa (lane (q, r)
- * reads row min(r, M - 1); rows >= M of the MFMA output are never used) */
-S2P_DEV s2p_f32x4 unit_mul(const Slot& S, const LDSP(uint16_t)* xa, uint32_t mask, uint32_t one,
-                           s2p_u32x4 NEG) {
+ * reads row min(r, M - 1); rows >= M of the MFMA output are never used),
+ * the code bias of each group from the table at nb (lane's rows 4q..4q+3,
+ * q taken mod 2: rows >= 8 are never used).  All LDS reads first, then four
+ * independent MFMAs. */
+S2P_DEV s2p_f32x4 unit_mul(const Slot& S, const LDSP(uint16_t)* xa, const LDSP(float)* nb, uint32_t mask,
+                           uint32_t one) {
 #pragma clang fp contract(off)
-    const uint32_t wd[4] = {S.w.x, S.w.y, S.w.z, S.w.w};
-    s2p_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    s2p_u32x4 ag[4];
+    s2p_f32x4 bias[4];
 #pragma unroll
     for (int gg = 0; gg < 4; gg++) {
-        const s2p_u32x4 ag = *(const LDSP(s2p_u32x4)*)(xa + gg * 32);
-        const s2p_f32x4 nb = mfma32(ag, NEG, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+        ag[gg] = *(const LDSP(s2p_u32x4)*)(xa + gg * 32);
+        bias[gg] = *(const LDSP(s2p_f32x4)*)(nb + gg * 8);
+    }
+    const uint32_t wd[4] = {S.w.x, S.w.y, S.w.z, S.w.w};
+    s2p_f32x4 D[4];
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
         const uint32_t d = wd[gg];
         s2p_u32x4 wv;
         wv.x = (d & mask) | one;
         wv.y = ((d >> 4) & mask) | one;
         wv.z = ((d >> 8) & mask) | one;
         wv.w = ((d >> 12) & mask) | one;
-        const s2p_f32x4 D = mfma32(ag, wv, nb);
+        D[gg] = mfma32(ag[gg], wv, bias[gg]);
+    }
+    s2p_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
         const uint32_t sw = gg < 2 ? S.s.x : S.s.y;
         const _Float16 sh =
             __builtin_bit_cast(_Float16, (uint16_t)((gg & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
         const float sf = (float)sh;
 #pragma unroll
-        for (int i = 0; i < 4; i++) t[i] = fmaf(sf, D[i], t[i]);
+        for (int i = 0; i < 4; i++) t[i] = fmaf(sf, D[gg][i], t[i]);
     }
     return t;
 }
 
 /* ---- LDS carve-up (bytes) ----
- * layer GEMVs: staged rows [M][K + 8] bf16 at 0 (w2 at M = 6: 116.8 KB),
+ * layer GEMVs: staged rows [M][XRS(K)] bf16 at 0 (w2 at M = 6: 117.1 KB),
  *              partials [tile][cw][M][16] f32 at L_PART (6 tiles: 16 KB);
- * head:        staged rows at 0 (30.8 KB), partials at L_HPART (39 tiles:
+ * head:        staged rows at 0 (31.1 KB), partials at L_HPART (39 tiles:
  *              105 KB);
  * attention:   its own carve-up from 0 (< 100 KB);
  * small state from L_INV up (all phases). */
 #define L_XS 0
+/* staged row stride (elements): K + 32 puts consecutive rows 16 banks apart,
+ * so the units' 16-byte row reads (lane (q, r): row r, offset 16 q bytes)
+ * hit distinct banks for rows 0..3 */
+constexpr int XRS(int K) { return K + 32; }
 #define L_PART (117 * 1024)
 #define L_HPART (32 * 1024)
 #define L_INV (140 * 1024)       /* [M] inverse RMS */
@@ -229,7 +270,11 @@ S2P_DEV s2p_f32x4 unit_mul(const Slot& S, const LDSP(uint16_t)* xa, uint32_t mas
 #define L_SSQO (L_XOLD + 256)    /* [M][16] f32 sums of squares of the new residual */
 #define L_FLAG (L_SSQO + 512)    /* [16] int broadcast words */
 #define L_NW (L_FLAG + 64)       /* [2560] bf16 norm weights */
-#define L_TOTAL (L_NW + 5120)
+#define L_BIAS (L_NW + 5120)     /* [NB][4 groups][8 rows] f32: -136 x the group's row sums */
+#define L_TOTAL (L_BIAS + 76 * 4 * 8 * 4)
+static_assert(MK2_MAX_ROWS * XRS(9728) * 2 <= L_PART && MK2_MAX_ROWS * XRS(2560) * 2 <= L_HPART &&
+                  L_TOTAL <= 160 * 1024,
+              "LDS carve-up");
 
 /* ---- shared (all waves) pieces of a GEMV phase ---- */
 /* RMSNorm of the staged rows in place: xn = bf16(bf16?(x * inv) * w) with
@@ -237,7 +282,7 @@ S2P_DEV s2p_f32x4 unit_mul(const Slot& S, const LDSP(uint16_t)* xa, uint32_t mas
 template <int K>
 S2P_DEV void norm_rows(LDSP(unsigned char)* smem, int M) {
 #pragma clang fp contract(off)
-    constexpr int KC = K / 8, RS = K + 8;
+    constexpr int KC = K / 8, RS = XRS(K);
     LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
     const LDSP(uint16_t)* nw = (const LDSP(uint16_t)*)(smem + L_NW);
     const LDSP(float)* inv = (const LDSP(float)*)(smem + L_INV);
@@ -256,6 +301,34 @@ S2P_DEV void norm_rows(LDSP(unsigned char)* smem, int M) {
             vv[d] = lo | (hi << 16);
         }
         *p = (s2p_u32x4){vv[0], vv[1], vv[2], vv[3]};
+    }
+    __syncthreads();
+}
+
+/* the code bias of the staged rows: the packed codes are w + 136, so a
+ * group's dot product carries 136 x (sum of the row's 32 values of the
+ * group); this table holds -136 x that sum per (K block, group, row < 8)
+ * for the units' MFMA accumulator input.  Rows >= M hold 0. */
+template <int K>
+S2P_DEV void bias_rows(LDSP(unsigned char)* smem, int M) {
+#pragma clang fp contract(off)
+    constexpr int NB = K / 128, RS = XRS(K);
+    const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS);
+    LDSP(float)* tb = (LDSP(float)*)(smem + L_BIAS);
+    for (int i = threadIdx.x; i < NB * 32; i += NTH) {
+        const int m = i & 7, bg = i >> 3; /* bg = block * 4 + group */
+        float sum = 0.f;
+        if (m < M) {
+            const LDSP(uint16_t)* px = xs + m * RS + bg * 32;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const s2p_u32x4 v = *(const LDSP(s2p_u32x4)*)(px + 8 * c);
+                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int d = 0; d < 4; d++) sum += bf2f_lo(vv[d]) + bf2f_hi(vv[d]);
+            }
+        }
+        tb[i] = -136.f * sum;
     }
     __syncthreads();
 }
@@ -305,43 +378,75 @@ S2P_DEV void reduce_phase(LDSP(unsigned char)* smem, int M, int wg) {
 template <int P>
 S2P_DEV void c_gemv(Slot (&S)[NSLOT], const Mk2Args& A, int l, int cw, const Ctx& C,
                     LDSP(unsigned char)* smem, int M) {
-    constexpr int NU = maxu(P), NB = phNB(P), RS = NB * 128 + 8;
-    const WG& w = C.w[P];
+    constexpr int NU = maxu(P), NB = phNB(P), RS = XRS(NB * 128);
+    /* opaque per phase: the unit addresses below are recomputed in every
+     * layer instead of being hoisted into dozens of live registers */
+    WG w = C.w[P];
+    w.start = opq(w.start);
+    w.nu = opq(w.nu);
+    w.jb = opq(w.jb);
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
     const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS) + min(r, M - 1) * RS + q * 8;
-    uint32_t mask = 0x000F000Fu, one = 0x43004300u, neg = 0xC308C308u;
-    asm volatile("" : "+v"(mask), "+v"(one), "+v"(neg));
-    const s2p_u32x4 NEG = {neg, neg, neg, neg};
-    s2p_f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    sfor<NU>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        constexpr int K = seq_base(P) + j;
-        slot_wait<WAITN>(S[K % NSLOT]);
-        if (j < w.nu) {
-            const int b = (w.start + j) % NB;
-            const s2p_f32x4 t = unit_mul(S[K % NSLOT], xs + b * 128, mask, one, NEG);
-            if (j >= w.jb) acc1 += t;
-            else acc0 += t;
-        }
-        refill<K>(S, A, l, C);
-        __builtin_amdgcn_sched_barrier(0);
-    });
-    /* partials [lt][cw][m][16]; zeros for the workgroup's tiles this wave
-     * did not touch */
+    const LDSP(float)* nbt = (const LDSP(float)*)(smem + L_BIAS) + 4 * (q & 1);
+    uint32_t mask = 0x000F000Fu, one = 0x43004300u;
+    asm volatile("" : "+v"(mask), "+v"(one));
+    /* partials [lt][cw][m][16]: the wave's first local tile is written when
+     * its units cross into the second (at j == jb), the last one at the end */
     LDSP(float)* part = (LDSP(float)*)(smem + L_PART);
-    const Geo g = geoP<P>(blockIdx.x, cw);
-    const int ntouch = w.nu == 0 ? 0 : (w.nu > w.jb ? 2 : 1);
-    for (int lt = 0; lt < g.nt; lt++) {
-        const int k = lt - w.lt0;
-        s2p_f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (k == 0 && ntouch > 0) v = acc0;
-        if (k == 1 && ntouch > 1) v = acc1;
+    auto put = [&](int lt, const s2p_f32x4& v) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = 4 * q + i;
             if (m < M) part[((lt * CW + cw) * M + m) * 16 + r] = v[i];
         }
-    }
+    };
+    s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#ifdef MK2_TRACE
+    uint64_t tw = 0, tr = 0;
+    if (cw == 0) TRACE(l, P == PD ? 30 : 17 + P);
+#endif
+    sfor<NU>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int K = seq_base(P) + j;
+#ifdef MK2_TRACE
+        const uint64_t t0 = wall_clock64();
+        slot_wait<WAITN>(S[K % NSLOT]);
+        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(mask) : "a"(S[K % NSLOT].s.x)); /* make the wait observable */
+        mask = (mask & 0u) | 0x000F000Fu;
+        tw += wall_clock64() - t0 + (__builtin_amdgcn_readfirstlane(mask) & 0u);
+#else
+        slot_wait<WAITN>(S[K % NSLOT]);
+#endif
+        if (j < w.nu) {
+            if (j == w.jb) {
+                put(w.lt0, acc);
+                acc = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            }
+            const int b = (w.start + j) % NB;
+            acc += unit_mul(S[K % NSLOT], xs + b * 128, nbt + b * 32, mask, one);
+        }
+#ifdef MK2_TRACE
+        __builtin_amdgcn_sched_barrier(0);
+        const uint64_t t1 = wall_clock64();
+        refill<K>(S, A, l, C);
+        asm volatile("s_nop 0" ::: "memory");
+        tr += wall_clock64() - t1;
+#else
+        refill<K>(S, A, l, C);
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+    });
+#ifdef MK2_TRACE
+    if (cw == 0 && (threadIdx.x & 63) == 0 && l < TR_L) g_mk2_tr[blockIdx.x][l][26 + P] = tw;
+    if (P == PG && cw == 0 && (threadIdx.x & 63) == 0 && l < TR_L) g_mk2_tr[blockIdx.x][l][31] = tr;
+#endif
+    /* the last touched tile, then zeros for the workgroup's tiles this wave
+     * did not touch */
+    const int ntouch = w.nu == 0 ? 0 : (w.nu > w.jb ? 2 : 1);
+    if (ntouch > 0) put(w.lt0 + ntouch - 1, acc);
+    const Geo g = geoP<P>(blockIdx.x, cw);
+    for (int lt = 0; lt < g.nt; lt++)
+        if (lt < w.lt0 || lt >= w.lt0 + ntouch) put(lt, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
 }
 
 /* ---- flags ---- */
@@ -349,15 +454,23 @@ S2P_DEV void c_gemv(Slot (&S)[NSLOT], const Mk2Args& A, int l, int cw, const Ctx
 S2P_DEV uint32_t flag_val(uint32_t epoch, int l, int kind) {
     return epoch * 2048u + (uint32_t)((l + 2) * 8 + kind);
 }
-/* one wave: wait until flags f[i0 .. i0 + n) all read want (n <= 1024) */
+/* one wave: wait until flags f[i0 .. i0 + n) all read want */
+S2P_DEV void flags_wait1(const Mk2Args& A, const uint32_t* f, int n, uint32_t want);
 S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want) {
+    for (int c = 0; c < n; c += 1024) flags_wait1(A, A.flags + kind + i0 + c, min(1024, n - c), want);
+}
+/* n <= 1024: every flag of a poll in flight at once (16 per lane) */
+S2P_DEV void flags_wait1(const Mk2Args& A, const uint32_t* f, int n, uint32_t want) {
     const int lane = threadIdx.x & 63;
-    const uint32_t* f = A.flags + kind * MK2_F_STRIDE + i0;
     if (coh_ld32(A.err)) return;
     unsigned spins = 0;
     while (true) {
+        uint32_t v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = lane + 64 * j < n ? coh_ld32(f + lane + 64 * j) : want;
         bool ok = true;
-        for (int i = lane; i < n; i += 64) ok = ok && coh_ld32(f + i) == want;
+#pragma unroll
+        for (int j = 0; j < 16; j++) ok = ok && v[j] == want;
         if (__all(ok)) break;
         __builtin_amdgcn_s_sleep(1);
         if (++spins > SPIN_LIMIT || ((spins & 1023) == 0 && coh_ld32(A.err))) {
@@ -370,7 +483,7 @@ S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want
 S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) {
     vm_drain();
     const int lane = threadIdx.x & 63;
-    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind * MK2_F_STRIDE + i0 + i, val);
+    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind + i0 + i, val);
 }
 
 /* ---- IO wave pieces of a GEMV phase ---- */
@@ -381,7 +494,7 @@ template <int K, bool NORM, bool RESID>
 S2P_DEV void io_stage(const Mk2Args& A, const uint16_t* src, const uint16_t* nw, int M,
                       LDSP(unsigned char)* smem, int t0, int np) {
     const int lane = threadIdx.x & 63;
-    constexpr int RS = K + 8;
+    constexpr int RS = XRS(K);
     LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
     for (int m = 0; m < M; m++)
 #pragma unroll 4
@@ -436,129 +549,189 @@ S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst
 }
 
 /* ---- attention: one (segment, kv head, 128-position split) unit per
- * workgroup, all 8 waves; qk-norm + RoPE of the unit's q vectors and new K
- * rows fused in (prims_dev.h rule arithmetic), new K/V rows appended to the
- * cache by the split that holds them.  Wave w owns positions 16w..16w+15 of
- * the split for the scores and dims 16w..16w+15 of the output for PV; the
- * last split of a (segment, kv head) to finish merges the splits. */
-#define A_SQ 0                     /* [32][128] bf16 q vectors */
-#define A_SV (8 * 1024)            /* [128][128] bf16 V, 16-byte chunks swizzled */
-#define A_SP (40 * 1024)           /* P hi [32][136] bf16 */
-#define A_SPL (49 * 1024)          /* P lo [32][136] bf16 */
-#define A_SKN (58 * 1024)          /* new K rows [8][128] bf16 */
-#define A_SM (60 * 1024)           /* [32 q][8 waves] f32 row maxima */
-#define A_SL (61 * 1024)           /* [32 q][8 waves] f32 row sums */
-#define A_SO (62 * 1024)           /* [32][128] f32 O (merge input / final) */
-#define A_SW (78 * 1024)           /* merge: [32][nsplit] weights, [32] denominators */
+ * workgroup, all 8 waves.  Every global read of the phase is the IO wave's
+ * (direct-to-LDS loads): the unit's old K/V rows (before waiting for this
+ * step's qkv tiles), the raw q / k / v vectors of its items, their RoPE rows
+ * and the visibility masks; the compute waves work from LDS only.  qk-norm +
+ * RoPE of the unit's q vectors and new K rows use the rule arithmetic of
+ * prims_dev.h; new K/V rows are appended to the cache by the split that
+ * holds them.  Wave w owns positions 16w..16w+15 of the split for the
+ * scores and dims 16w..16w+15 of the output for PV.  Every split writes its
+ * partial (m, l, O), waits until all splits of its (segment, kv head) have
+ * arrived, and merges its share of the outputs. */
+#define A_SQ 0                     /* [32][128] bf16 roped q vectors */
+#define A_SK (8 * 1024)            /* [128][128] bf16 K: chunk k of row t at slot k ^ (t & 15) */
+#define A_SV (40 * 1024)           /* [128][128] bf16 V, SVX swizzle */
+#define A_SP (72 * 1024)           /* P hi [32][136] bf16 */
+#define A_SPL (81 * 1024)          /* P lo [32][136] bf16 */
+#define A_SM (90 * 1024)           /* [32 q][8 waves] f32 row maxima */
+#define A_SL (91 * 1024)           /* [32 q][8 waves] f32 row sums */
+#define A_SO (92 * 1024)           /* [32][128] f32 O */
+#define A_RAW (108 * 1024)         /* raw items: q vectors [32][128] bf16, then new slots [8][k, v][128] */
+#define A_ROPE (123 * 1024)        /* items [30][128] f32 (cos, sin) of the item's row */
+#define A_VIS (138 * 1024)         /* [8] u64 visibility masks of the segment's rows */
+#define A_SEG (A_VIS + 64)         /* the segment record */
+#define A_NW (A_VIS + 256)         /* q-norm then k-norm weights [2][128] bf16 */
 #define A_PST 136
 #define SVX(t, d) ((t) * 128 + ((((d) >> 3) ^ (((t) >> 2) & 6)) << 3) + ((d) & 7))
+#define SKX(t, ch) ((t) * 128 + (((ch) ^ ((t) & 15)) << 3))
+static_assert(A_NW + 512 <= L_INV && sizeof(S2pAttnSeg) <= 192, "attention LDS overlaps the shared state");
 
+/* direct-to-LDS 16-byte load of lane's chunk (LDS base is wave-uniform:
+ * lane l lands at base + 16 l) */
+S2P_DEV void dma16(const void* g, LDSP(void)* base, bool coherent) {
+    if (coherent) __builtin_amdgcn_global_load_lds(g, base, 16, 0, 16);
+    else __builtin_amdgcn_global_load_lds(g, base, 16, 0, 0);
+}
+
+template <bool IO>
 S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32_t epoch,
                        LDSP(unsigned char)* smem) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tidx = tid_opq();
+    const int lane = tidx & 63, wave = tidx >> 6;
     const int qq = lane >> 4, c = lane & 15;
-    const bool io = wave == CW;
-    const S2pAttnSeg g = A.segs[seg];
-    const uint16_t* kvb = (const uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
-    uint16_t* kp = (uint16_t*)kvb + (size_t)kvh * A.plan.max_seq * 128;
-    uint16_t* vp = (uint16_t*)kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
-    const int L = g.L, span = g.span, nrows = g.nrows;
-    const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, span);
-    const int oend = min(p1, L);     /* old positions [p0, oend) */
-    const int s0 = max(p0, L);       /* new positions [s0, p1) */
-    const int nq = nrows * 4, nnew = max(0, p1 - s0);
+    constexpr bool io = IO;
+#ifdef MK2_TRACE
+#define ATRACE(e)                                                                                  \
+    do {                                                                                           \
+        asm volatile("; ATRACE %0 IO %1" ::"n"(e), "n"((int)IO));                                   \
+        if (l == 18 && lane == 0) g_mk2_tr[blockIdx.x][37 + ((e) >> 2)][wave * 4 + ((e) & 3)] = wall_clock64(); \
+    } while (0)
+#else
+#define ATRACE(e) \
+    do {          \
+    } while (0)
+#endif
+    ATRACE(0);
     LDSP(uint16_t)* s_q = (LDSP(uint16_t)*)(smem + A_SQ);
+    LDSP(uint16_t)* s_k = (LDSP(uint16_t)*)(smem + A_SK);
     LDSP(uint16_t)* s_v = (LDSP(uint16_t)*)(smem + A_SV);
     LDSP(uint16_t)* s_p = (LDSP(uint16_t)*)(smem + A_SP);
     LDSP(uint16_t)* s_pl = (LDSP(uint16_t)*)(smem + A_SPL);
-    LDSP(uint16_t)* s_kn = (LDSP(uint16_t)*)(smem + A_SKN);
     LDSP(float)* s_m = (LDSP(float)*)(smem + A_SM);
     LDSP(float)* s_l = (LDSP(float)*)(smem + A_SL);
     LDSP(float)* s_o = (LDSP(float)*)(smem + A_SO);
-    LDSP(int)* s_flag = (LDSP(int)*)(smem + L_FLAG);
+    LDSP(uint16_t)* s_raw = (LDSP(uint16_t)*)(smem + A_RAW);
+    LDSP(float)* s_rope = (LDSP(float)*)(smem + A_ROPE);
+    LDSP(uint64_t)* s_vis = (LDSP(uint64_t)*)(smem + A_VIS);
+    LDSP(uint32_t)* s_seg = (LDSP(uint32_t)*)(smem + A_SEG); /* the segment record's words */
+    LDSP(uint16_t)* s_nw = (LDSP(uint16_t)*)(smem + A_NW);
+    const int ns = A.nsplit;
 
-    /* 1. old K rows of this wave's 16 positions into registers, old V rows
-     * of the split into LDS (independent of this step's outputs) */
-    const int pos = p0 + 16 * wave + c;
-    s2p_u32x4 kr[4];
-#pragma unroll
-    for (int ch = 0; ch < 4; ch++) kr[ch] = (s2p_u32x4){0u, 0u, 0u, 0u};
-    if (p0 + 16 * wave < oend) {
-        const int pk = min(pos, oend - 1);
-#pragma unroll
-        for (int ch = 0; ch < 4; ch++) kr[ch] = gld_nt128(kp + (size_t)pk * 128 + 32 * ch + 8 * qq);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = 16 * wave + 4 * i + (lane >> 4);
-            const int pv = min(p0 + t, oend - 1);
-            const int k = (lane & 15) ^ ((t >> 2) & 6);
-            __builtin_amdgcn_global_load_lds((const void*)(vp + (size_t)pv * 128 + 8 * k),
-                                             (LDSP(void)*)(s_v + (16 * wave + 4 * i) * 128), 16, 0, 0);
-        }
-    }
-    /* 2. the unit's qkv tiles (q heads 4 kvh..4 kvh + 3, k and v head kvh) */
+    /* 1. IO wave: the segment record, the split's old K/V rows (independent
+     * of this step's outputs), then the unit's qkv tiles, its items' raw
+     * vectors, RoPE rows and visibility masks */
     if (io) {
+        const S2pAttnSeg g = A.segs[seg];
+        const uint16_t* kvb = (const uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
+        const uint16_t* kp = kvb + (size_t)kvh * A.plan.max_seq * 128;
+        const uint16_t* vp = kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
+        const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, g.span);
+        const int oend = min(p1, g.L);
+        if (oend > p0) {
+            for (int i = 0; i < 32; i++) { /* rows 4i .. 4i + 3 */
+                const int t = 4 * i + (lane >> 4);
+                const int pos = min(p0 + t, oend - 1);
+                dma16(kp + (size_t)pos * 128 + 8 * ((lane & 15) ^ (t & 15)), (LDSP(void)*)(s_k + 4 * i * 128), false);
+                dma16(vp + (size_t)pos * 128 + 8 * ((lane & 15) ^ ((t >> 2) & 6)), (LDSP(void)*)(s_v + 4 * i * 128), false);
+            }
+        }
+        if (lane < (int)(sizeof(S2pAttnSeg) / 4)) s_seg[lane] = ((const uint32_t*)(A.segs + seg))[lane];
+        /* q-norm and k-norm weights are adjacent: 512 B */
+        if (lane < 32) dma16(A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_Q + 8 * lane, (LDSP(void)*)s_nw, false);
         const uint32_t want = flag_val(epoch, l, MK2_F_Q);
         flags_wait(A, MK2_F_Q, 32 * kvh, 32, want);
         flags_wait(A, MK2_F_Q, 256 + 8 * kvh, 8, want);
         flags_wait(A, MK2_F_Q, 320 + 8 * kvh, 8, want);
+        const int s0 = max(p0, g.L), nq = g.nrows * 4, nnew = max(0, p1 - s0);
+        /* q items: the row's 4 q heads of kv head kvh are 1 KB contiguous */
+        for (int rl = 0; rl < g.nrows; rl++) {
+            const int row = g.row0 + rl;
+            dma16(A.qkv + (size_t)row * 6144 + 512 * kvh + 8 * lane, (LDSP(void)*)(s_raw + 4 * rl * 128), true);
+        }
+        /* new-slot items: k head then v head (32 lanes) */
+        for (int j = 0; j < nnew; j++) {
+            const int row = g.first + (s0 + j - g.L);
+            const uint16_t* src = A.qkv + (size_t)row * 6144 + (lane < 16 ? 4096 + 128 * kvh + 8 * lane
+                                                                          : 5120 + 128 * kvh + 8 * (lane - 16));
+            if (lane < 32) dma16(src, (LDSP(void)*)(s_raw + 32 * 128 + j * 256), true);
+        }
+        /* RoPE rows of the items (512 B each, 32 lanes) */
+        for (int it = 0; it < nq + nnew; it++) {
+            const int row = it < nq ? g.row0 + (it >> 2) : g.first + (s0 + (it - nq) - g.L);
+            if (lane < 32) dma16(A.rope_tab + (size_t)row * 128 + 4 * lane, (LDSP(void)*)(s_rope + it * 128), false);
+        }
+        if (lane < g.nrows) s_vis[lane] = A.plan.vis[g.row0 + lane];
+        vm_drain();
     }
-    vm_drain(); /* this wave's V rows are in LDS */
+    ATRACE(1);
     __syncthreads();
-    /* 3. qk-norm + RoPE: item it < nq is q vector (row it / 4, head 4 kvh +
-     * it % 4); item nq + j is the new slot s0 + j (K normed and roped, V as
-     * is), kept in LDS and appended to the cache */
-    const uint16_t* qn = A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_Q;
-    const uint16_t* kn = A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_K;
-    for (int it = wave; it < nq + nnew; it += NWAVE) {
+    ATRACE(2);
+    S2pAttnSeg g;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(S2pAttnSeg) / 4); i++) ((uint32_t*)&g)[i] = s_seg[i];
+    const int L = g.L, span = g.span, nrows = g.nrows;
+    const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, span);
+    const int s0 = max(p0, L);       /* new positions [s0, p1) */
+    const int nq = nrows * 4, nnew = max(0, p1 - s0), nit = nq + nnew;
+    TRACE(l, 20);
+    /* 2. items: qk-norm + RoPE from LDS into the q rows and the K / V
+     * tiles; rows past the split's end zeroed (their P is 0, stale LDS could
+     * be Inf / NaN) */
+    for (int it = wave; it < nit; it += NWAVE) {
         const bool isq = it < nq;
-        const int row = isq ? g.row0 + (it >> 2) : g.first + (s0 + (it - nq) - L);
-        const int head = isq ? 4 * kvh + (it & 3) : 32 + kvh;
-        const uint16_t* src = A.qkv + (size_t)row * 6144 + head * 128;
-        const float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
-        const float* tab = A.rope_tab + (size_t)row * 128;
-        const float c0 = tab[(lane >> 1) * 2], sn0 = tab[(lane >> 1) * 2 + 1];
-        const float c1 = tab[((lane + 64) >> 1) * 2], sn1 = tab[((lane + 64) >> 1) * 2 + 1];
-        const uint16_t* nw = isq ? qn : kn;
+        const LDSP(uint16_t)* rv = isq ? s_raw + it * 128 : s_raw + 32 * 128 + (it - nq) * 256;
+        const LDSP(float)* rp = s_rope + it * 128;
+        const float v0 = bf2f(rv[lane]), v1 = bf2f(rv[lane + 64]);
+        const float c0 = rp[(lane >> 1) * 2], sn0 = rp[(lane >> 1) * 2 + 1];
+        const float c1 = rp[((lane + 64) >> 1) * 2], sn1 = rp[((lane + 64) >> 1) * 2 + 1];
+        const LDSP(uint16_t)* nw = s_nw + (isq ? 0 : 128);
         float o0, o1;
         qkrope_math(v0, v1, nw[lane], nw[lane + 64], c0, sn0, c1, sn1, A.eps, lane, &o0, &o1);
         const uint16_t b0 = f2bf(o0), b1 = f2bf(o1);
         if (isq) {
             s_q[it * 128 + lane] = b0;
             s_q[it * 128 + lane + 64] = b1;
-            if (sp == 0) { /* inspection copy of the roped q rows */
-                uint16_t* gq = A.q + (size_t)row * 4096 + head * 128;
-                gq[lane] = b0;
-                gq[lane + 64] = b1;
-            }
         } else {
-            const int j = it - nq, slot = s0 + j, t = slot - p0;
-            s_kn[j * 128 + lane] = b0;
-            s_kn[j * 128 + lane + 64] = b1;
-            const uint16_t* vs = src + 8 * 128;
-            const uint16_t x0 = coh_ld16(vs + lane), x1 = coh_ld16(vs + lane + 64);
-            s_v[SVX(t, lane)] = x0;
-            s_v[SVX(t, lane + 64)] = x1;
-            coh_st16(kp + (size_t)slot * 128 + lane, b0);
-            coh_st16(kp + (size_t)slot * 128 + lane + 64, b1);
-            coh_st16(vp + (size_t)slot * 128 + lane, x0);
-            coh_st16(vp + (size_t)slot * 128 + lane + 64, x1);
+            const int t = s0 + (it - nq) - p0;
+            s_k[SKX(t, lane >> 3) + (lane & 7)] = b0;
+            s_k[SKX(t, (lane + 64) >> 3) + (lane & 7)] = b1;
+            s_v[SVX(t, lane)] = rv[128 + lane];
+            s_v[SVX(t, lane + 64)] = rv[128 + lane + 64];
         }
     }
-    /* rows past the split's end hold zeros (their P is 0; stale LDS could be
-     * Inf / NaN) */
-    for (int i = threadIdx.x; i < (p0 + 128 - max(p1, p0)) * 128; i += NTH) {
+    for (int i = tidx; i < (p0 + 128 - max(p1, p0)) * 128; i += NTH) {
         const int t = max(p1, p0) - p0 + (i >> 7), d = i & 127;
         s_v[SVX(t, d)] = 0;
+        s_k[t * 128 + d] = 0;
     }
+    ATRACE(3);
     __syncthreads();
-    /* 4. scores of this wave's 16 positions for the 32 q vectors */
-    if (pos >= s0 && pos < p1) {
-#pragma unroll
-        for (int ch = 0; ch < 4; ch++)
-            kr[ch] = *(const LDSP(s2p_u32x4)*)(s_kn + (pos - s0) * 128 + 32 * ch + 8 * qq);
+    ATRACE(4);
+    if (io) {
+        /* the new slots' K / V rows appended to the cache; split 0 keeps an
+         * inspection copy of the roped q rows */
+        uint16_t* kvb = (uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
+        for (int j = 0; j < nnew; j++) {
+            const int slot = s0 + j, t = slot - p0;
+            if (lane < 32) {
+                const int ch = lane & 15;
+                const bool isv = lane >= 16;
+                const s2p_u32x4 v = *(const LDSP(s2p_u32x4)*)(isv ? s_v + SVX(t, 8 * ch) : s_k + SKX(t, ch));
+                coh_st128(kvb + ((size_t)((isv ? 8 : 0) + kvh) * A.plan.max_seq + slot) * 128 + 8 * ch, v);
+            }
+        }
+        if (sp == 0)
+            for (int idx = lane; idx < nq * 16; idx += 64) {
+                const int qv = idx >> 4, ch = idx & 15;
+                coh_st128(A.q + (size_t)(g.row0 + (qv >> 2)) * 4096 + (4 * kvh + (qv & 3)) * 128 + 8 * ch,
+                          *(const LDSP(s2p_u32x4)*)(s_q + qv * 128 + 8 * ch));
+            }
     }
+    TRACE(l, 21);
+    /* 3. scores of this wave's 16 positions for the 32 q vectors */
+    const int t = 16 * wave + c, pos = p0 + t;
     const float scale = 0.08838834764831845f;
     s2p_f32x4 sc[2];
 #pragma unroll
@@ -567,30 +740,32 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
 #pragma unroll
         for (int ch = 0; ch < 4; ch++) {
             const s2p_u32x4 qa = *(const LDSP(s2p_u32x4)*)(s_q + (16 * qt + c) * 128 + 32 * ch + 8 * qq);
-            acc = mfma16x16x32(qa, kr[ch], acc);
+            const s2p_u32x4 kb = *(const LDSP(s2p_u32x4)*)(s_k + SKX(t, 4 * ch + qq));
+            acc = mfma16x16x32(qa, kb, acc);
         }
         sc[qt] = acc;
     }
-    /* visibility: lane (qq, c) element i is q vector 16 qt + 4 qq + i
-     * (row (16 qt + 4 qq + i) / 4 = 4 qt + qq), position pos */
+    /* visibility: lane (qq, c) element i is q vector 16 qt + 4 qq + i (row
+     * 4 qt + qq), position pos */
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
         const int rl = 4 * qt + qq;
         bool vis = rl < nrows && pos < p1;
         if (vis && pos >= L) {
-            const int b = pos - L;
-            vis = b < 64 && ((A.plan.vis[g.row0 + rl] >> b) & 1ull);
+            const int bb = pos - L;
+            vis = bb < 64 && ((s_vis[rl] >> bb) & 1ull);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float t = vis ? sc[qt][i] * scale : -INFINITY;
-            sc[qt][i] = t;
-            const float mx = max16(t);
+            const float tv = vis ? sc[qt][i] * scale : -INFINITY;
+            sc[qt][i] = tv;
+            const float mx = max16(tv);
             if (c == 0) s_m[(16 * qt + 4 * qq + i) * 8 + wave] = mx;
         }
     }
+    ATRACE(5);
     __syncthreads();
-    /* 5. P = e^(s - M) (M over the split), row sums, P as bf16 hi + lo */
+    /* 4. P = e^(s - M) (M over the split), row sums, P as bf16 hi + lo */
 #pragma unroll
     for (int qt = 0; qt < 2; qt++)
 #pragma unroll
@@ -605,21 +780,22 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             const float ps = sum16(p);
             if (c == 0) s_l[qv * 8 + wave] = ps;
             const uint16_t h = f2bf(p);
-            s_p[qv * A_PST + 16 * wave + c] = h;
-            s_pl[qv * A_PST + 16 * wave + c] = f2bf(p - bf2f(h));
+            s_p[qv * A_PST + t] = h;
+            s_pl[qv * A_PST + t] = f2bf(p - bf2f(h));
         }
+    ATRACE(6);
     __syncthreads();
-    /* 6. O[:, 16 wave .. 16 wave + 15] = P V */
+    /* 5. O[:, 16 wave .. 16 wave + 15] = P V */
     s2p_f32x4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int ch = 0; ch < 4; ch++) {
-        uint32_t b[4];
+        uint32_t bw[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int t = 32 * ch + 8 * qq + 2 * e;
-            b[e] = (uint32_t)s_v[SVX(t, 16 * wave + c)] | ((uint32_t)s_v[SVX(t + 1, 16 * wave + c)] << 16);
+            const int tt = 32 * ch + 8 * qq + 2 * e;
+            bw[e] = (uint32_t)s_v[SVX(tt, 16 * wave + c)] | ((uint32_t)s_v[SVX(tt + 1, 16 * wave + c)] << 16);
         }
-        const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+        const s2p_u32x4 bv = {bw[0], bw[1], bw[2], bw[3]};
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
             const s2p_u32x4 pa = *(const LDSP(s2p_u32x4)*)(s_p + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
@@ -628,100 +804,103 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             o[qt] = mfma16x16x32(pa, bv, o[qt]);
         }
     }
-    /* O and the split's (m, l) per q vector into LDS */
 #pragma unroll
     for (int qt = 0; qt < 2; qt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) s_o[(16 * qt + 4 * qq + i) * 128 + 16 * wave + c] = o[qt][i];
+    ATRACE(7);
     __syncthreads();
-    const int ns = A.nsplit;
-    const int nrow_all = A.rows;
+    TRACE(l, 22);
+    /* this unit's share of the (segment, kv head)'s outputs: q vectors
+     * [v0s, v1s) x 128 dims */
+    const int per = (nq + ns - 1) / ns;
+    const int v0s = min(nq, sp * per), v1s = min(nq, v0s + per), nv = v1s - v0s;
     float* part = A.attn_part;
-    float* po = part + (size_t)nrow_all * 32 * ns * 2;
-    bool fin = ns == 1;
-    if (!fin) {
-        /* partial of this split: written by the IO wave, then the arrival */
+    float* po = part + (size_t)A.rows * 32 * ns * 2;
+    auto pidx = [&](int qv, int s2) __attribute__((always_inline)) {
+        return ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns + s2;
+    };
+    if (ns > 1) {
+        /* 6. partial (m, l, O) of this split; arrival; wait for every split;
+         * the share's partials of all splits into LDS (K / V tiles' space) */
+        LDSP(float)* s_po = (LDSP(float)*)(smem + A_SK); /* [nv][ns][128] */
+        LDSP(float)* s_ml = (LDSP(float)*)(smem + A_SP); /* [nv][ns][2] */
         if (io) {
             for (int idx = lane; idx < nq * 32; idx += 64) {
                 const int qv = idx >> 5, d4 = (idx & 31) * 4;
-                const size_t pi = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns + sp;
+                const size_t pi = pidx(qv, sp);
                 coh_st128(po + pi * 128 + d4, *(const LDSP(s2p_u32x4)*)(s_o + qv * 128 + d4));
                 if (d4 == 0) {
                     const s2p_f32x4 ma = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8);
                     const s2p_f32x4 mb = *(const LDSP(s2p_f32x4)*)(s_m + qv * 8 + 4);
                     const s2p_f32x4 la = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8);
                     const s2p_f32x4 lb = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8 + 4);
-                    const float M = fmaxf(fmaxf(fmaxf(ma[0], ma[1]), fmaxf(ma[2], ma[3])),
-                                          fmaxf(fmaxf(mb[0], mb[1]), fmaxf(mb[2], mb[3])));
+                    const float Mx = fmaxf(fmaxf(fmaxf(ma[0], ma[1]), fmaxf(ma[2], ma[3])),
+                                           fmaxf(fmaxf(mb[0], mb[1]), fmaxf(mb[2], mb[3])));
                     const float ls = ((la[0] + la[1]) + (la[2] + la[3])) + ((lb[0] + lb[1]) + (lb[2] + lb[3]));
-                    coh_st64(part + pi * 2, (uint64_t)__float_as_uint(M) | ((uint64_t)__float_as_uint(ls) << 32));
+                    coh_st64(part + pi * 2, (uint64_t)__float_as_uint(Mx) | ((uint64_t)__float_as_uint(ls) << 32));
                 }
             }
             vm_drain();
             if (lane == 0) {
-                const unsigned prev = __hip_atomic_fetch_add(A.attn_ctr + seg * 8 + kvh, 1u,
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *s_flag = prev == (unsigned)(ns - 1);
+                unsigned* ctr = A.attn_ctr + l * 64 + seg * 8 + kvh;
+                const unsigned target = (epoch + 1u) * (unsigned)ns;
+                __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                unsigned spins = 0;
+                if (!coh_ld32(A.err))
+                    while ((int)(coh_ld32(ctr) - target) < 0) {
+                        __builtin_amdgcn_s_sleep(1);
+                        if (++spins > SPIN_LIMIT || ((spins & 1023) == 0 && coh_ld32(A.err))) {
+                            __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            break;
+                        }
+                    }
             }
+            /* every split's partial of the share: 512 B each, two per load */
+            for (int i = 0; 2 * i < nv * ns; i++) {
+                const int e = 2 * i + (lane >> 5);
+                const int k = e / ns, s2 = e - k * ns;
+                const int ec = min(e, nv * ns - 1), kc = ec / ns, sc2 = ec - kc * ns;
+                (void)k;
+                (void)s2;
+                dma16(po + pidx(v0s + kc, sc2) * 128 + 4 * (lane & 31), (LDSP(void)*)(s_po + 2 * i * 128), true);
+            }
+            for (int e = lane; e < nv * ns; e += 64) {
+                const int k = e / ns, s2 = e - k * ns;
+                const uint64_t ml = coh_ld64(part + pidx(v0s + k, s2) * 2);
+                s_ml[2 * e] = __uint_as_float((uint32_t)ml);
+                s_ml[2 * e + 1] = __uint_as_float((uint32_t)(ml >> 32));
+            }
+            vm_drain();
         }
         __syncthreads();
-        fin = *s_flag != 0;
-        if (fin) {
-            /* merge: split weights e^(m_s - M) and denominators per q vector,
-             * then every output with all of its split loads in flight */
-            LDSP(float)* wm = (LDSP(float)*)(smem + A_SW);
-            LDSP(float)* lt = wm + 32 * ns;
-            LDSP(float)* wl = lt + 32;
-            for (int idx = threadIdx.x; idx < nq * ns; idx += NTH) {
-                const int qv = idx / ns, s2 = idx - qv * ns;
-                const size_t pi = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns + s2;
-                const uint64_t ml = coh_ld64(part + pi * 2);
-                wm[idx] = __uint_as_float((uint32_t)ml);
-                wl[idx] = __uint_as_float((uint32_t)(ml >> 32));
+        TRACE(l, 23);
+        /* 7. merge of the share: split weights e^(m_s - M), denominators */
+        LDSP(float)* s_w = (LDSP(float)*)(smem + A_SPL); /* [nv][ns] weights, [nv] denominators */
+        if (tidx < nv) {
+            const int k = tidx;
+            float Mx = -INFINITY;
+            for (int s2 = 0; s2 < ns; s2++) Mx = fmaxf(Mx, s_ml[2 * (k * ns + s2)]);
+            const float Ms = Mx == -INFINITY ? 0.f : Mx;
+            float lsum = 0.f;
+            for (int s2 = 0; s2 < ns; s2++) {
+                const float w = __expf(s_ml[2 * (k * ns + s2)] - Ms);
+                lsum = fmaf(s_ml[2 * (k * ns + s2) + 1], w, lsum);
+                s_w[k * ns + s2] = w;
             }
-            __syncthreads();
-            if ((int)threadIdx.x < nq) {
-                const int qv = threadIdx.x;
-                float M = -INFINITY;
-                for (int k = 0; k < ns; k++) M = fmaxf(M, wm[qv * ns + k]);
-                const float Ms = M == -INFINITY ? 0.f : M;
-                float lsum = 0.f;
-                for (int k = 0; k < ns; k++) {
-                    const float w = __expf(wm[qv * ns + k] - Ms);
-                    lsum = fmaf(wl[qv * ns + k], w, lsum);
-                    wm[qv * ns + k] = w;
-                }
-                lt[qv] = lsum;
-            }
-            __syncthreads();
-            for (int idx = threadIdx.x; idx < nq * 32; idx += NTH) {
-                const int qv = idx >> 5, d = (idx & 31) * 4;
-                const size_t p0i = ((size_t)(g.row0 + (qv >> 2)) * 32 + 4 * kvh + (qv & 3)) * ns;
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
-                for (int k0 = 0; k0 < ns; k0 += 8) {
-                    s2p_u32x4 ov[8];
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        ov[j] = k0 + j < ns ? coh_ld128(po + (p0i + k0 + j) * 128 + d) : (s2p_u32x4){0u, 0u, 0u, 0u};
-#pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        if (k0 + j >= ns) break;
-                        const float w = wm[qv * ns + k0 + j];
-                        acc[0] = fmaf(__uint_as_float(ov[j].x), w, acc[0]);
-                        acc[1] = fmaf(__uint_as_float(ov[j].y), w, acc[1]);
-                        acc[2] = fmaf(__uint_as_float(ov[j].z), w, acc[2]);
-                        acc[3] = fmaf(__uint_as_float(ov[j].w), w, acc[3]);
-                    }
-                }
-                const float lp = lt[qv];
-#pragma unroll
-                for (int k = 0; k < 4; k++) s_o[qv * 128 + d + k] = acc[k] / lp;
-            }
-            __syncthreads();
+            s_w[nv * ns + k] = lsum;
         }
+        __syncthreads();
+        for (int idx = tidx; idx < nv * 128; idx += NTH) {
+            const int k = idx >> 7, d = idx & 127;
+            float acc = 0.f;
+            for (int s2 = 0; s2 < ns; s2++) acc = fmaf(s_po[(k * ns + s2) * 128 + d], s_w[k * ns + s2], acc);
+            s_o[(v0s + k) * 128 + d] = acc / s_w[nv * ns + k];
+        }
+        __syncthreads();
     } else {
         /* one split: normalise in place */
-        for (int idx = threadIdx.x; idx < nq * 128; idx += NTH) {
+        for (int idx = tidx; idx < nq * 128; idx += NTH) {
             const int qv = idx >> 7;
             const s2p_f32x4 la = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8);
             const s2p_f32x4 lb = *(const LDSP(s2p_f32x4)*)(s_l + qv * 8 + 4);
@@ -730,10 +909,10 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         }
         __syncthreads();
     }
-    if (fin && io) {
-        /* final rows: attn[row][(4 kvh + g) * 128 + d] as bf16, then the flag */
-        for (int idx = lane; idx < nq * 16; idx += 64) {
-            const int qv = idx >> 4, d = (idx & 15) * 8;
+    if (io) {
+        /* the share of attn[row][(4 kvh + g) * 128 + d] as bf16, then its flag */
+        for (int idx = lane; idx < nv * 16; idx += 64) {
+            const int qv = v0s + (idx >> 4), d = (idx & 15) * 8;
             const LDSP(float)* sv = s_o + qv * 128 + d;
             s2p_u32x4 ob;
             ob.x = (uint32_t)f2bf(sv[0]) | ((uint32_t)f2bf(sv[1]) << 16);
@@ -742,33 +921,36 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             ob.w = (uint32_t)f2bf(sv[6]) | ((uint32_t)f2bf(sv[7]) << 16);
             coh_st128(A.attn + (size_t)(g.row0 + (qv >> 2)) * 4096 + (4 * kvh + (qv & 3)) * 128 + d, ob);
         }
-        if (ns > 1 && lane == 0)
-            __hip_atomic_store(A.attn_ctr + seg * 8 + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        flags_set(A, MK2_F_ATT, seg * 8 + kvh, 1, flag_val(epoch, l, MK2_F_ATT));
+        flags_set(A, MK2_F_ATT, (seg * 8 + kvh) * ns + sp, 1, flag_val(epoch, l, MK2_F_ATT));
+        TRACE(l, 24);
     }
     __syncthreads();
 }
 
-/* attention phase of layer l: this workgroup's units */
+/* attention phase of layer l: this workgroup's units.  A split waits for
+ * every split of its (segment, kv head), so the splits of one group are
+ * handed out in the same round of workgroups: a round holds
+ * floor(gridDim / nsplit) whole groups, split sp of the round's group i on
+ * workgroup i * nsplit + sp. */
+template <bool IO>
 S2P_DEV void attn_phase(const Mk2Args& A, int l, uint32_t epoch, LDSP(unsigned char)* smem) {
-    const int nu = A.n_seg * 8 * A.nsplit;
-    for (int u = blockIdx.x; u < nu; u += gridDim.x) {
-        const int seg = u % A.n_seg, kvh = (u / A.n_seg) % 8, sp = u / (A.n_seg * 8);
-        attn_unit(A, l, seg, kvh, sp, epoch, smem);
-    }
+    const int ns = A.nsplit, ng = A.n_seg * 8, gpr = (int)gridDim.x / ns;
+    const int gi = (int)blockIdx.x / ns, sp = (int)blockIdx.x - gi * ns;
+    if (gi >= gpr) return;
+    for (int grp = gi; grp < ng; grp += gpr) attn_unit<IO>(A, l, grp % A.n_seg, grp / A.n_seg, sp, epoch, smem);
 }
 
 /* ---- head: the ring continues over this wave's head units ---- */
 S2P_DEV void c_head(Slot (&S)[NSLOT], const Mk2Args& A, int cw, const Ctx& C,
                     LDSP(unsigned char)* smem, int M) {
-    constexpr int RS = 2560 + 8;
+    constexpr int RS = XRS(2560);
     const WG& w = C.hw;
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
     const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS) + min(r, M - 1) * RS + q * 8;
     LDSP(float)* part = (LDSP(float)*)(smem + L_HPART);
-    uint32_t mask = 0x000F000Fu, one = 0x43004300u, neg = 0xC308C308u;
-    asm volatile("" : "+v"(mask), "+v"(one), "+v"(neg));
-    const s2p_u32x4 NEG = {neg, neg, neg, neg};
+    const LDSP(float)* nbt = (const LDSP(float)*)(smem + L_BIAS) + 4 * (q & 1);
+    uint32_t mask = 0x000F000Fu, one = 0x43004300u;
+    asm volatile("" : "+v"(mask), "+v"(one));
     /* the wave's units are tiles (start / 20) .. (last / 20) of the packed
      * head, local tile = tile - head_t0 */
     s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -794,7 +976,7 @@ S2P_DEV void c_head(Slot (&S)[NSLOT], const Mk2Args& A, int cw, const Ctx& C,
                     flush();
                     cur = tile;
                 }
-                acc += unit_mul(S[j], xs + b * 128, mask, one, NEG);
+                acc += unit_mul(S[j], xs + b * 128, nbt + b * 32, mask, one);
             }
             unit_issue(S[j], A.hpack, w.start, w.last, u + NSLOT);
             __builtin_amdgcn_sched_barrier(0);
@@ -862,32 +1044,42 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             /* Q */
             __syncthreads();
             norm_rows<2560>(smem, M);
+            bias_rows<2560>(smem, M);
             c_gemv<PQ>(S, A, l, cw, C, smem, M);
+            if (cw == 0) TRACE(l, 13);
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
             /* attention */
-            attn_phase(A, l, epoch, smem);
+            attn_phase<false>(A, l, epoch, smem);
             /* O */
             __syncthreads();
+            bias_rows<4096>(smem, M);
             c_gemv<PO>(S, A, l, cw, C, smem, M);
+            if (cw == 0) TRACE(l, 14);
             __syncthreads();
             reduce_phase<PO>(smem, M, wg);
             /* G */
             __syncthreads();
             norm_rows<2560>(smem, M);
+            bias_rows<2560>(smem, M);
             c_gemv<PG>(S, A, l, cw, C, smem, M);
+            if (cw == 0) TRACE(l, 15);
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
             /* D */
             __syncthreads();
+            bias_rows<9728>(smem, M);
             c_gemv<PD>(S, A, l, cw, C, smem, M);
+            if (cw == 0) TRACE(l, 16);
             __syncthreads();
             reduce_phase<PD>(smem, M, wg);
         }
         /* head */
         __syncthreads();
         norm_rows<2560>(smem, M);
+        bias_rows<2560>(smem, M);
         c_head(S, A, cw, C, smem, M);
+        if (cw == 0) TRACE(NL, 2);
         __syncthreads();
         head_reduce(A, C, smem, M);
         /* drain this wave's remaining (clamped, unused) prefetches */
@@ -917,43 +1109,63 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             /* Q: x (previous w2, or the init) -> qkv */
             if (l == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
             else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, l - 1, MK2_F_D));
+            TRACE(l, 0);
             io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_ATTN, M, smem, gq.t0, gq.np);
+            TRACE(l, 1);
             __syncthreads();
             norm_rows<2560>(smem, M);
+            bias_rows<2560>(smem, M);
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
             io_store(A, smem, A.qkv, 6144, gq.t0, gq.np, M, false, MK2_F_Q, flag_val(epoch, l, MK2_F_Q));
+            TRACE(l, 2);
             /* attention */
-            attn_phase(A, l, epoch, smem);
+            attn_phase<true>(A, l, epoch, smem);
+            TRACE(l, 3);
             /* O: attn -> x += wo attn */
-            flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8, flag_val(epoch, l, MK2_F_ATT));
+            flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8 * A.nsplit, flag_val(epoch, l, MK2_F_ATT));
+            TRACE(l, 4);
             io_stage<4096, false, true>(A, A.attn, nullptr, M, smem, go.t0, go.np);
+            TRACE(l, 5);
             __syncthreads();
+            bias_rows<4096>(smem, M);
             __syncthreads();
             reduce_phase<PO>(smem, M, wg);
             io_store(A, smem, A.x, 2560, go.t0, go.np, M, true, MK2_F_O, flag_val(epoch, l, MK2_F_O));
+            TRACE(l, 6);
             /* G: x -> h */
             flags_wait(A, MK2_F_O, 0, 160, flag_val(epoch, l, MK2_F_O));
+            TRACE(l, 7);
             io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_FFN, M, smem, gg.t0, gg.np);
+            TRACE(l, 8);
             __syncthreads();
             norm_rows<2560>(smem, M);
+            bias_rows<2560>(smem, M);
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
             io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, MK2_F_G, flag_val(epoch, l, MK2_F_G));
+            TRACE(l, 9);
             /* D: h -> x += w2 h */
             flags_wait(A, MK2_F_G, 0, 608, flag_val(epoch, l, MK2_F_G));
+            TRACE(l, 10);
             io_stage<9728, false, true>(A, A.h, nullptr, M, smem, gd.t0, gd.np);
+            TRACE(l, 11);
             __syncthreads();
+            bias_rows<9728>(smem, M);
             __syncthreads();
             reduce_phase<PD>(smem, M, wg);
             io_store(A, smem, A.x, 2560, gd.t0, gd.np, M, true, MK2_F_D, flag_val(epoch, l, MK2_F_D));
+            TRACE(l, 12);
         }
         /* head: final RMSNorm of x */
         if (NL == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
         else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, NL - 1, MK2_F_D));
+        TRACE(NL, 0);
         io_stage<2560, true, false>(A, A.x, A.final_norm, M, smem, 0, 0);
+        TRACE(NL, 1);
         __syncthreads();
         norm_rows<2560>(smem, M);
+        bias_rows<2560>(smem, M);
         __syncthreads();
         {
             const Geo gh = geo_of(A.head_tiles, 20, false, wg, 0);
@@ -962,6 +1174,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             C.head_nt = gh.nt;
             head_reduce(A, C, smem, M);
         }
+        TRACE(NL, 3);
         /* launch bookkeeping: the last workgroup to finish advances the epoch */
         vm_drain();
         if (lane == 0) {
@@ -1032,6 +1245,13 @@ extern "C" hipError_t s2p_mk2_pack(const void* w_pack, const void* scales, int N
     return hipGetLastError();
 }
 
+#ifdef MK2_TRACE
+extern "C" int s2p_mk2_trace(void* host, size_t bytes) {
+    if (bytes < sizeof(g_mk2_tr)) return -1;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_mk2_tr), sizeof(g_mk2_tr)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 /* ---- launch ---- */
 static int g_mk2_ok = -1;
 
@@ -1053,7 +1273,9 @@ extern "C" int s2p_mk2_supported(void) {
 
 extern "C" hipError_t s2p_mk2_launch(const Mk2Args* args, hipStream_t st) {
     if (s2p_mk2_supported() != 0) return hipErrorNotSupported;
-    if (!args || args->rows < 1 || args->rows > MK2_MAX_ROWS || args->n_seg * 8 > MK2_F_STRIDE ||
+    if (!args || args->rows < 1 || args->rows > MK2_MAX_ROWS || args->n_seg > 8 ||
+        args->nsplit < 1 || args->nsplit > MK2_MAX_SPLIT ||
+        args->n_seg * 8 * args->nsplit > MK2_ATT_MAX || args->n_layers > MK2_MAX_LAYERS ||
         args->head_tiles > 39 * MK2_NWG)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_mk2, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);

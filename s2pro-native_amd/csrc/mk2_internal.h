@@ -36,16 +36,26 @@ extern "C" {
 #define MK2_NORM_K 5248
 #define MK2_NORM_STRIDE 5376
 
-/* flag kinds: one 32-bit word per producing tile (or attention block) */
-enum { MK2_F_INIT = 0, MK2_F_Q = 1, MK2_F_ATT = 2, MK2_F_O = 3, MK2_F_G = 4, MK2_F_D = 5,
-       MK2_F_KINDS = 6 };
-#define MK2_F_STRIDE 1024
+/* flags: one 32-bit word per producing tile (or attention unit), by kind:
+ * offset and capacity in words */
+#define MK2_F_INIT 0       /* 160 residual tiles of the input */
+#define MK2_F_Q 256        /* 384 qkv tiles */
+#define MK2_F_ATT 1024     /* n_seg x 8 x nsplit attention units (<= 3072) */
+#define MK2_F_O 4096       /* 160 residual tiles after wo */
+#define MK2_F_G 4352       /* 608 SwiGLU pair tiles */
+#define MK2_F_D 5120       /* 160 residual tiles after w2 */
+#define MK2_F_WORDS 5376
+#define MK2_ATT_MAX 3072
+#define MK2_MAX_LAYERS 40
+#define MK2_MAX_SPLIT 64
 /* the backbone's mk2 state block (uint32 words): flags, then the launch
- * epoch and done count, the error flag, the attention split counters */
-#define MK2_STATE_WORD (MK2_F_KINDS * MK2_F_STRIDE)
+ * epoch and done count, the error flag, the attention split arrival
+ * counters [layer][segment x 8 + kv head] (64 per layer).  Zeroed at every
+ * plan; within a plan every word only grows. */
+#define MK2_STATE_WORD MK2_F_WORDS
 #define MK2_ERR_WORD (MK2_STATE_WORD + 2)
 #define MK2_CTR_WORD (MK2_STATE_WORD + 4)
-#define MK2_STATE_WORDS (MK2_CTR_WORD + MK2_F_STRIDE)
+#define MK2_STATE_WORDS (MK2_CTR_WORD + MK2_MAX_LAYERS * 64)
 
 typedef struct {
     const uint8_t* wpack;          /* [n_layers][MK2_LAYER_BLKS] packed blocks */
@@ -70,7 +80,7 @@ typedef struct {
     const S2pAttnSeg* segs;
     int n_seg, nsplit, split_pos;
     float* attn_part;
-    unsigned* attn_ctr;            /* [n_seg * 8], zero between launches */
+    unsigned* attn_ctr;            /* [MK2_MAX_LAYERS][64] split arrivals, monotonic per plan */
     const float* rope_tab;
     float eps;
 } Mk2Args;

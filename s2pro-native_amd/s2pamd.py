@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libs2pamd.so")
+LIB_PATH = os.environ.get("S2PAMD_LIB") or os.path.join(_HERE, "libs2pamd.so")
 
 P = ctypes.c_void_p
 I = ctypes.c_int
