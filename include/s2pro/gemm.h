@@ -138,6 +138,15 @@ s2p_status s2p_int4p_gemv(void* y_bf16, const void* x_bf16,
 s2p_status s2p_int4p_gemm_tc(void* y_bf16, const void* x_bf16,
                              const void* w_pack, const void* scales_f16,
                              int M, int N, int K, int G, hipStream_t stream);
+/* Test seam, no counterpart in the reference: one INT4-g32 (wfmt 0: packed
+ * codes, f16 scales [N][K/32]) or INT8 (wfmt 1: f32 per-row scales) GEMV,
+ * 1 <= M <= 128, K % 512 == 0, with the engine chosen per call (0: the
+ * launcher's choice, 2: the split-K engine only), so that the split-K engine
+ * is exercised on shapes the launcher gives to another engine. */
+s2p_status s2p_gemv_engine_run(int engine, int wfmt, void* y_bf16,
+                               const void* x_bf16, const void* w,
+                               const void* scales, int M, int N, int K,
+                               hipStream_t stream);
 s2p_status s2p_int4p_dequant(void* w_bf16, const void* w_pack,
                              const void* scales_f16, int N, int K, int G,
                              hipStream_t stream);

@@ -60,33 +60,18 @@ static int64_t part_floats(int rows, int qh, int nsplit) {
     return (int64_t)rows * qh * nsplit * (AT_HD + 2);
 }
 
-static uint64_t* g_attn_probe = nullptr;
-static int g_attn_probe_at = -1;
-/* diagnostics: stage clocks of the attention launch `index` launches from now */
-extern "C" void s2p_attn_set_probe(uint64_t* buf, int index) {
-    g_attn_probe = buf;
-    g_attn_probe_at = buf ? index : -1;
-}
-
-static int g_attn_waves = AT_WAVES;
-/* test hook: blocks of 8 waves (the persistent kernel's shape) or 4 */
-extern "C" void s2p_attn_set_waves(int w) { g_attn_waves = w == 8 ? 8 : AT_WAVES; }
-
 template <int MQT, int W>
 static void attn_launch(const AttnArgs& a, dim3 grid, hipStream_t st) {
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_attn<MQT, W>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES_W(W));
-        attr = true;
-    }
+    /* once per instantiation (thread-safe static initialisation) */
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)k_attn<MQT, W>, hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES_W(W));
+    (void)attr;
     hipLaunchKernelGGL((k_attn<MQT, W>), grid, dim3(64 * W), AT_LDS_BYTES_W(W), st, a);
 }
 
 static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
                            int64_t part_cap, hipStream_t st) {
-    if (g_attn_probe_at >= 0 && g_attn_probe_at-- == 0) a.probe = g_attn_probe;
-    const int W = g_attn_waves;
+    constexpr int W = AT_WAVES;
     const int tiles = (max_span + AT_TILE * W - 1) / (AT_TILE * W);
     int tpw = 1; /* tiles per wave per split */
     if (a.part && part_cap > 0) {
@@ -103,13 +88,8 @@ static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
     a.nsplit = (max_span + a.split_pos - 1) / a.split_pos;
     if (a.nsplit < 1) a.nsplit = 1;
     dim3 grid((unsigned)n_seg, (unsigned)a.kvh_n, (unsigned)a.nsplit);
-    if (W == 8) {
-        if (max_nrows <= 4) attn_launch<1, 8>(a, grid, st);
-        else attn_launch<2, 8>(a, grid, st);
-    } else {
-        if (max_nrows <= 4) attn_launch<1, AT_WAVES>(a, grid, st);
-        else attn_launch<2, AT_WAVES>(a, grid, st);
-    }
+    if (max_nrows <= 4) attn_launch<1, W>(a, grid, st);
+    else attn_launch<2, W>(a, grid, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1 || a.counters) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,

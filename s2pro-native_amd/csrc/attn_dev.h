@@ -60,7 +60,9 @@ struct AttnArgs {
     /* non-NULL: the last split to finish a (segment, kv head) merges the
      * splits itself (persistent kernel); NULL: k_attn_combine does */
     unsigned* counters;
-    uint64_t* probe; /* diagnostics: [grid][8] stage clocks */
+#ifdef S2P_DIAG
+    uint64_t* probe; /* diagnostics build: [grid][8] stage clocks */
+#endif
     /* PLAN, fused qk-norm + RoPE + KV append (qkv != NULL): q is computed
      * from the raw fused qkv rows into q (written, then read back by the
      * same block), and the blocks whose positions cover a segment's new
@@ -213,9 +215,13 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
     const int qrow_stride = a.qh * AT_HD;
+#ifdef S2P_DIAG
     uint64_t* const probe =
         a.probe ? a.probe + ((size_t)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8
                 : nullptr;
+#else
+    uint64_t* const probe = nullptr; /* stage clocks: diagnostics build only */
+#endif
     auto stamp = [&](int i) __attribute__((always_inline)) {
         if (probe && threadIdx.x == 0) probe[i] = wall_clock64();
     };

@@ -48,9 +48,15 @@ S2P_DEV void coh_st32(uint32_t* p, uint32_t v) {
 S2P_DEV void coh_st64(void* p, uint64_t v) {
     __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-/* 16 bytes written through in one instruction (p 16-byte aligned) */
+/* 16 bytes written through as two 8-byte agent-scope stores (p 16-byte
+ * aligned).  The stores stay visible to the compiler: a store hidden in
+ * inline asm escapes its hazard tracking, and a VALU write of the store's
+ * data registers issued right after a 16-byte store can then replace data
+ * the store has not read yet (seen as a corrupted first element of some
+ * lanes' stores). */
 S2P_DEV void coh_st128(void* p, s2p_u32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+    coh_st64(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
+    coh_st64((char*)p + 8, (uint64_t)v.z | ((uint64_t)v.w << 32));
 }
 
 /* wait for this wave's outstanding vector memory operations (stores

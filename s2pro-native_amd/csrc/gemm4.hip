@@ -1,5 +1,5 @@
 /* s2pro MI355X — INT4-g32 weight GEMM for the batched / tree verify rows
- * (16 < M <= 80: configs 4 and 5 of the verify path).
+ * (16 < M <= 96: configs 4 and 5 of the verify path).
  *
  * Replaces the reference's M > 16 path (dequant + cuBLAS, gemm.c:467-490, or
  * the WMMA kernel int8_gemv.cu:535-618) for packed INT4 weights.
@@ -32,10 +32,7 @@
 
 #define G4_WAVES 8
 #define G4_WIN 16 /* groups per window = one weight chunk (GV_CHG_INT4) */
-/* M <= 80 (five column tiles).  At six tiles (M = 81..96) rows 76-79 came out
- * wrong now and then in the GPU tests (not deterministic); that shape is left
- * to the split-K GEMV engine until the cause is found. */
-#define G4_MAX_M 80
+#define G4_MAX_M 96 /* six column tiles */
 
 static __host__ __device__ size_t g4_xs() { return (size_t)G4_WIN * 32 + GV_XPAD; }
 static __host__ __device__ size_t g4_xg() { return (size_t)gv_round32(G4_WIN) + 8; }
@@ -191,8 +188,10 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         vm_drain();
         __syncthreads();
         if (tid == 0) {
+            /* acquire-release at agent scope: the partials of every split
+             * that arrived before are visible to this workgroup's reads */
             const unsigned prev = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1u,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                                         __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             *L.flag = prev == (unsigned)(a.splits - 1);
         }
         __syncthreads();
@@ -261,17 +260,15 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
 
 template <int MT>
 static hipError_t g4_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_gemm4<MT>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        attr_set = true;
-    }
+    /* once per instantiation (thread-safe static initialisation) */
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)k_gemm4<MT>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)attr;
     hipLaunchKernelGGL((k_gemm4<MT>), grid, dim3(64 * G4_WAVES), lds, st, a);
     return hipGetLastError();
 }
 
-/* INT4 weights, 16 < M <= 80, any epilogue; hipErrorNotSupported otherwise
+/* INT4 weights, 16 < M <= 96, any epilogue; hipErrorNotSupported otherwise
  * (the caller falls back to the split-K GEMV engine). */
 extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const GemvArgs& a = *ap;
@@ -292,11 +289,7 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     /* too few row blocks to fill the chip: split K over about one workgroup
      * per CU (needs the caller's split-K scratch: partials and counters) */
     const int nch = ((a.K >> 5) + G4_WIN - 1) / G4_WIN;
-    int cus = 256, dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-        cus = 256;
+    const int cus = s2p_cu_count();
     int ks = (int)(((unsigned)cus + nblk - 1) / nblk);
     if (ks > nch) ks = nch;
     if (ks < 1) ks = 1;
@@ -315,6 +308,7 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         case 2: return g4_launch_mt<2>(b, grid, lds, st);
         case 3: return g4_launch_mt<3>(b, grid, lds, st);
         case 4: return g4_launch_mt<4>(b, grid, lds, st);
-        default: return g4_launch_mt<5>(b, grid, lds, st);
+        case 5: return g4_launch_mt<5>(b, grid, lds, st);
+        default: return g4_launch_mt<6>(b, grid, lds, st);
     }
 }

@@ -49,6 +49,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "gemv_dev.h"
 #include "s2pro/gemm.h"
 
@@ -60,7 +62,7 @@ __global__ __launch_bounds__(MT == 1 ? 1024 : 512) void k_gemv3(GemvArgs a) {
      * compiler issues them next to their first uses, three dependent
      * kernarg round trips before the first weight load */
     asm volatile("" ::"s"(a.w), "s"(a.s), "s"(a.x), "s"(a.y), "s"(a.norm_w), "s"(a.ssq_in),
-                 "s"(a.ssq_out), "s"(a.probe), "s"(a.ldx), "s"(a.ldy), "s"(a.M), "s"(a.N),
+                 "s"(a.ssq_out), "s"(a.ldx), "s"(a.ldy), "s"(a.M), "s"(a.N),
                  "s"(a.K), "s"(a.gps), "s"(a.ks), "s"(a.rt), "s"(a.xmode), "s"(a.epi),
                  "s"(a.ssq_in_blocks), "s"(a.norm_eps), "s"(gridDim.x));
     GvBuf b0, b1;
@@ -138,38 +140,27 @@ extern "C" hipError_t s2p_gemv_bf16_generic_launch(const void* w, const void* x,
 
 /* ------------------------------------------------------------- launchers */
 
-static int g_slots_override = 0;
-/* test hook: plan every GEMV for `slots` resident workgroups (0 = default) */
-extern "C" void s2p_gemv_set_slots(int slots) { g_slots_override = slots > 0 ? slots : 0; }
-
-extern "C" int s2p_gemv_slots(void) {
-    static int cache[64];
-    if (g_slots_override) return g_slots_override;
+extern "C" int s2p_cu_count(void) {
+    static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cache[dev]) return cache[dev];
-    int slots = 0;
-    const char* e = getenv("S2P_GEMV_TARGET_WG");
-    if (e && atoi(e) > 0) slots = atoi(e);
-    if (!slots) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-        slots = 4 * cus;
-    }
-    cache[dev] = slots;
-    return slots;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+        v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
 }
+
+extern "C" int s2p_gemv_slots(void) { return 4 * s2p_cu_count(); }
 
 template <int WFMT, int MT, bool WIN1>
 static hipError_t gv_launch_w(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_gemv<WFMT, MT, WIN1>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, GV_LDS_MAX);
-        attr_set = true;
-    }
+    /* once per instantiation (thread-safe static initialisation) */
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemv<WFMT, MT, WIN1>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       GV_LDS_MAX);
+    (void)attr;
     hipLaunchKernelGGL((k_gemv<WFMT, MT, WIN1>), grid, dim3(256), lds, st, a);
     return hipGetLastError();
 }
@@ -256,18 +247,9 @@ extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_
     const int tiles = swiglu ? (a->N >> 1) / 16 : (a->N + 15) / 16;
     const int nwmax = mt == 1 ? 16 : 8;
     const int chg = gv_chg(a->wfmt);
-    int cus = 0, dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-        cus = 256;
+    const int cus = s2p_cu_count();
     const int kmax = swiglu ? nwmax / 2 : nwmax;
-    static int gps0 = -1;
-    if (gps0 < 0) {
-        const char* e = getenv("S2P_GV3_GPS0"); /* tuning: groups per K slice to start from */
-        gps0 = e && atoi(e) >= 4 ? (atoi(e) & ~3) : 0;
-    }
-    int gps = gps0 ? gps0 : chg;
+    int gps = chg;
     while ((G + gps - 1) / gps > kmax) gps += 4;
     int ks = (G + gps - 1) / gps;
     /* units: output tiles per group (SWIGLU: a unit is a gate + up pair) */
@@ -310,65 +292,21 @@ extern "C" hipError_t s2p_gemv3_plan(GemvArgs* a, dim3* grid, dim3* block, size_
     }
 }
 
-/* Whole-K plan for workgroups of exactly nw waves (the persistent kernel's
- * shape): rt tiles x ks = nw / rt K slices with no idle wave; one tile
- * (SWIGLU: one gate + up pair) preferred, then two. */
-extern "C" hipError_t s2p_gemv3_plan_nw(GemvArgs* a, int nw, size_t lds_cap, size_t* lds_out) {
-    const hipError_t ce = s2p_gemv_plan_check(a);
-    if (ce != hipSuccess) return ce;
-    const int G = a->K >> 5;
-    const bool swiglu = a->epi == GEMV_EPI_SWIGLU;
-    for (int rt = swiglu ? 2 : 1; rt <= 2; rt++) {
-        if (nw % rt) continue;
-        const int ks = nw / rt;
-        const int gps = (((G + ks - 1) / ks) + 3) & ~3;
-        if ((G + gps - 1) / gps != ks) continue; /* a slice would be empty */
-        const size_t lds = gv3_lds_bytes(a->M, gps, a->wfmt, ks, nw, 2);
-        if (lds > lds_cap) continue;
-        a->gps = gps;
-        a->ks = ks;
-        a->rt = rt;
-        a->splits = 1;
-        *lds_out = lds;
-        return hipSuccess;
-    }
-    return hipErrorNotSupported;
-}
-
-static int g_v3_nw = 0;
-/* test hook: plan whole-K launches for workgroups of nw waves on a grid of
- * s2p_gemv_slots() workgroups (the persistent kernel's decomposition) */
-extern "C" void s2p_gemv_set_v3_nw(int nw) { g_v3_nw = nw > 0 ? nw : 0; }
-
-static int g_engine = 0;
-extern "C" void s2p_gemv_set_engine(int engine) { g_engine = engine; }
-static uint64_t* g_probe = nullptr;
-static int g_probe_at = -1;
-extern "C" void s2p_gemv_set_probe(uint64_t* buf, int index) {
-    g_probe = buf;
-    g_probe_at = buf ? index : -1;
-}
-
 template <int WFMT, int MT, bool NOTR>
 static hipError_t gv3_launch_k(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
                                hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)k_gemv3<WFMT, MT, NOTR>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, GV3_LDS_MAX);
-        attr_set = true;
-    }
+    /* once per instantiation (thread-safe static initialisation) */
+    static const hipError_t attr = hipFuncSetAttribute((const void*)k_gemv3<WFMT, MT, NOTR>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       GV3_LDS_MAX);
+    (void)attr;
     hipLaunchKernelGGL((k_gemv3<WFMT, MT, NOTR>), grid, block, lds, st, a);
     return hipGetLastError();
 }
 
-/* launches shaped like the persistent kernel's GEMVs (test hook) also use
- * its untransposed INT4 tile, so the two agree bit for bit */
 template <int WFMT, int MT>
 static hipError_t gv3_launch_mt(const GemvArgs& a, dim3 grid, dim3 block, size_t lds,
                                 hipStream_t st) {
-    if constexpr (WFMT == GEMV_W_INT4 && MT == 1)
-        if (g_v3_nw) return gv3_launch_k<WFMT, MT, true>(a, grid, block, lds, st);
     return gv3_launch_k<WFMT, MT, false>(a, grid, block, lds, st);
 }
 
@@ -391,27 +329,19 @@ extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
     GemvArgs a = *ap;
     dim3 grid;
     size_t lds = 0;
-    /* INT4 at 16 < M <= 80: the row-split GEMM with streamed activation
+    /* INT4 at 16 < M <= 96: the row-split GEMM with streamed activation
      * windows (gemm4.hip) */
-    if (g_engine == 0 && a.gps == 0 && !g_v3_nw && a.wfmt == GEMV_W_INT4 && a.M > 16) {
+    if (a.engine == GEMV_ENGINE_AUTO && a.gps == 0 && a.wfmt == GEMV_W_INT4 && a.M > 16) {
         const hipError_t e4 = s2p_gemm4_launch(&a, st);
         if (e4 != hipErrorNotSupported) return e4;
     }
-    if (g_engine != 2 && a.gps == 0) {
+    if (a.engine != GEMV_ENGINE_SPLITK && a.gps == 0) {
         GemvArgs a3 = a;
         dim3 block;
         const hipError_t e3 = s2p_gemv_plan_check(&a3);
         if (e3 != hipSuccess) return e3;
-        hipError_t pe3;
-        if (g_v3_nw) {
-            pe3 = s2p_gemv3_plan_nw(&a3, g_v3_nw, GV3_LDS_MAX, &lds);
-            grid = dim3((unsigned)s2p_gemv_slots());
-            block = dim3((unsigned)(64 * g_v3_nw));
-        } else {
-            pe3 = s2p_gemv3_plan(&a3, &grid, &block, &lds);
-        }
+        const hipError_t pe3 = s2p_gemv3_plan(&a3, &grid, &block, &lds);
         if (pe3 == hipSuccess) {
-            if (g_probe_at >= 0 && g_probe_at-- == 0) a3.probe = g_probe;
             switch (a3.wfmt) {
                 case GEMV_W_INT4: return gv3_launch<GEMV_W_INT4>(a3, grid, block, lds, st);
                 case GEMV_W_INT8: return gv3_launch<GEMV_W_INT8>(a3, grid, block, lds, st);

@@ -622,11 +622,18 @@ __device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y, int tid = threa
 template <int WFMT, int MT, bool WIN1, bool COH>
 __device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned char)* smem,
                          uint16_t* y_override = nullptr, uint64_t* probe = nullptr) {
-    /* probe (diagnostics): wall clock at the stages of the block */
+    /* probe (diagnostics build only): wall clock at the stages of the block */
+#ifdef S2P_DIAG
 #define GV_PROBE(i)                                                   \
     do {                                                              \
         if (probe && threadIdx.x == 0) probe[i] = wall_clock64();     \
     } while (0)
+#else
+#define GV_PROBE(i) \
+    do {            \
+        (void)probe; \
+    } while (0)
+#endif
     GV_PROBE(0);
     uint16_t* const Y = y_override ? y_override : a.y;
     constexpr int CHG = WFMT == GEMV_W_INT4 ? GV_CHG_INT4 : GV_CHG_INT8; /* groups per chunk */
@@ -713,12 +720,14 @@ __device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned c
             }
             return;
         }
-        /* Split-K handoff without cache maintenance: the 8 XCD L2s are not
-         * coherent and an agent-scope fence would write back / invalidate a
-         * whole L2, so the partials are written through to memory (sc1, the
-         * encoding of an agent-scope store; one 16-byte store per lane), read
-         * back with agent-scope atomic loads, and each workgroup waits for
-         * its partial stores to complete before it signals arrival. */
+        /* Split-K handoff across the 8 non-coherent XCD L2s: the partials
+         * are written through (sc1, the encoding of an agent-scope store; one
+         * 16-byte store per lane) and read back with agent-scope atomic
+         * loads; each workgroup waits for its partial stores to complete,
+         * then signals arrival with an agent-scope acquire-release fetch_add
+         * (the memory model's L2 writeback before and invalidate after), so
+         * the last arriver's reads are ordered after every split's stores by
+         * the model, not only by the completion waits. */
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const int m = t * 16 + r;
@@ -732,7 +741,9 @@ __device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned c
         __syncthreads();
         GV_PROBE(4);
         if (tid == 0) {
-            const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_RELAXED,
+            /* acquire-release at agent scope: the partials of every split
+             * that arrived before are visible to this workgroup's reads */
+            const unsigned prev = __hip_atomic_fetch_add(&a.counters[rb], 1u, __ATOMIC_ACQ_REL,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             *L.flag = prev == (unsigned)(a.splits - 1);
         }
@@ -993,7 +1004,11 @@ __device__ void gv3_block(const GemvArgs& a, int p, int P, LDS(unsigned char)* s
     const int F = a.N >> 1;
     const int sp = geo.sp, gb = geo.gb, gn = geo.gn;
     (void)r;
+#ifdef S2P_DIAG
     uint64_t* const probe = a.probe ? a.probe + (size_t)blockIdx.x * 8 : nullptr;
+#else
+    uint64_t* const probe = nullptr; /* stage clocks: diagnostics build only */
+#endif
     auto stamp = [&](int i) __attribute__((always_inline)) {
         if (probe && tid == 0) probe[i] = wall_clock64();
     };

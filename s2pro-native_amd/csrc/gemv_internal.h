@@ -19,6 +19,7 @@ enum { GEMV_X_PLAIN = 0, GEMV_X_NORM = 1 };            /* activation staging */
  * sums of squares; SWIGLU: W = [gate; up] (2F rows), y[m][F] =
  * silu(bf16(gate)) * bf16(up) with the rule's roundings. */
 enum { GEMV_EPI_STORE = 0, GEMV_EPI_RESID = 1, GEMV_EPI_SWIGLU = 2 };
+enum { GEMV_ENGINE_AUTO = 0, GEMV_ENGINE_SPLITK = 2 };
 
 typedef struct {
     const uint8_t*  w;       /* INT4: packed [N][K/2]; INT8: [N][K]; BF16: bf16 [N][K] */
@@ -45,22 +46,19 @@ typedef struct {
     float*          part;    /* [splits][M][nrb][64] fp32 */
     int64_t         part_cap;/* floats available at part */
     unsigned*       counters;/* [ceil(N/64)], zero between calls */
-    uint64_t*       probe;   /* diagnostics (whole-K engine): [grid][8] stage clocks */
+    int             engine;  /* GEMV_ENGINE_AUTO, or GEMV_ENGINE_SPLITK: the split-K engine only */
+#ifdef S2P_DIAG
+    uint64_t*       probe;   /* diagnostics build (whole-K engine): [grid][8] stage clocks */
+#endif
 } GemvArgs;
 
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
 /* INT4, 16 < M <= 80 (gemm4.hip); hipErrorNotSupported outside that range */
 hipError_t s2p_gemm4_launch(const GemvArgs* a, hipStream_t st);
-/* test hook: 0 = launcher's choice, 2 = split-K engine only */
-void s2p_gemv_set_engine(int engine);
-/* test hook: whole-K launches shaped like the persistent kernel's GEMVs */
-void s2p_gemv_set_v3_nw(int nw);
-/* whole-K plan for workgroups of exactly nw waves (persistent kernel) */
-hipError_t s2p_gemv3_plan_nw(GemvArgs* a, int nw, size_t lds_cap, size_t* lds_out);
-/* diagnostics: stage clocks of the whole-K launch `index` launches from now */
-void s2p_gemv_set_probe(uint64_t* buf, int index);
-/* resident-workgroup target the launcher plans GEMVs for (env S2P_GEMV_TARGET_WG) */
+/* resident-workgroup target the split-K engine plans for (4 per CU) */
 int s2p_gemv_slots(void);
+/* compute units of the current device, queried once per device */
+int s2p_cu_count(void);
 hipError_t s2p_gemv_bf16_generic_launch(const void* w, const void* x, void* y, int M, int N,
                                          int K, hipStream_t st);
 hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,

@@ -4,8 +4,8 @@
  * One process-wide context (reference gemm.c:42-73) owns the split-K partial
  * buffer and the per-row-block arrival counters of the GEMV engine; GEMVs
  * issued on one stream reuse them in order.  The split count of each call is
- * chosen so that about S2P_GEMV_TARGET_WG workgroups stream the weights
- * (256 CUs x 4) while each split covers at least 8 groups of 32 k. */
+ * chosen so that about 4 workgroups per CU stream the weights while each
+ * split covers at least 8 groups of 32 k. */
 #include <pthread.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -25,8 +25,7 @@ static struct {
     int max_m;
     float* part;
     unsigned* counters;
-    int target_wg;
-} g = {0, PTHREAD_MUTEX_INITIALIZER, 0, NULL, NULL, 1024};
+} g = {0, PTHREAD_MUTEX_INITIALIZER, 0, NULL, NULL};
 
 s2p_status s2p_gemm_init(int max_m) {
     pthread_mutex_lock(&g.mu);
@@ -50,8 +49,6 @@ s2p_status s2p_gemm_init(int max_m) {
         pthread_mutex_unlock(&g.mu);
         return rc;
     }
-    const char* e = getenv("S2P_GEMV_TARGET_WG");
-    if (e && atoi(e) > 0) g.target_wg = atoi(e);
     g.max_m = max_m > 0 ? max_m : 16;
     g.inited = 1;
     pthread_mutex_unlock(&g.mu);
@@ -171,6 +168,20 @@ static s2p_status int4p_any_m(void* y, const void* x, const void* w, const void*
     }
     hipError_t e = s2p_gemv_generic_launch(0, w, sc, x, y, M, N, K, gshift_of(G), stream);
     return e == hipSuccess ? S2P_OK : S2P_ERR_CUDA;
+}
+
+s2p_status s2p_gemv_engine_run(int engine, int wfmt, void* y_bf16, const void* x_bf16,
+                               const void* w, const void* scales, int M, int N, int K,
+                               hipStream_t stream) {
+    if (!y_bf16 || !x_bf16 || !w || !scales || M <= 0 || M > GEMV_MAX_M || N <= 0 ||
+        K <= 0 || K % 512 != 0 || (engine != GEMV_ENGINE_AUTO && engine != GEMV_ENGINE_SPLITK) ||
+        (wfmt != GEMV_W_INT4 && wfmt != GEMV_W_INT8))
+        return S2P_ERR_INVALID;
+    if (!g.inited) return S2P_ERR_STATE;
+    GemvArgs a;
+    s2p_gemv_args_plain(&a, wfmt, w, scales, x_bf16, y_bf16, M, N, K);
+    a.engine = engine;
+    return run_gemv(&a, stream);
 }
 
 s2p_status s2p_int4p_gemv(void* y_bf16, const void* x_bf16, const void* w_pack,

@@ -318,6 +318,7 @@ extern "C" hipError_t s2pk_attention8_decode(const s2p_bf16* q, const int8_t* co
  * slot plan.slot[r], has RoPE position plan.pos[r] and sees [0, L) plus the
  * node slots of plan.vis[r], whose highest bit is the row's own node. */
 #include "attn_dev.h"
+#include "gemv_internal.h"
 #include "prims_dev.h"
 
 
@@ -726,14 +727,7 @@ extern "C" hipError_t s2p_attn8_plan_launch(const void* q, void* out, const S2pR
         return hipErrorInvalidValue;
     /* splits of >= 128 slots (the part scratch is sized for 128), as short
      * as one resident round of waves allows (two per SIMD: 8 per CU) */
-    static int cus = 0;
-    if (cus <= 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-    }
+    const int cus = s2p_cu_count();
     const int64_t per_split = (int64_t)n_seg * 8;
     int64_t ns_max = (int64_t)cus * 8 / per_split;
     if (ns_max < 1) ns_max = 1;

@@ -110,6 +110,7 @@ SIGS = {
     "s2p_intq_dequant": (I, [P, P, P, I, I, I, P]),
     "s2p_int4_pack": (I, [P, P, I, I, P]),
     "s2p_int4p_gemv": (I, [P, P, P, P, I, I, I, I, P]),
+    "s2p_gemv_engine_run": (I, [I, I, P, P, P, P, I, I, I, P]),
     "s2p_int4p_gemm_tc": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_int4p_dequant": (I, [P, P, P, I, I, I, P]),
     "s2p_gemm_bf16": (I, [P, P, P, I, I, I, P]),
@@ -160,12 +161,6 @@ SIGS = {
 # synthetic-data launchers (csrc/synth_internal.h), used by tests/benchmarks
 EXTRA = {
     "s2p_backbone_set_mk": (None, [P, I]),
-    "s2p_gemv_set_slots": (None, [I]),
-    "s2p_gemv_set_engine": (None, [I]),
-    "s2p_gemv_set_v3_nw": (None, [I]),
-    "s2p_attn_set_waves": (None, [I]),
-    "s2p_gemv_set_probe": (None, [P, I]),
-    "s2p_attn_set_probe": (None, [P, I]),
     "s2p_test_f2bf": (I, [P, P, I64, P]),
     "s2p_test_desc_bytes": (SZ, [I]),
     "s2p_backbone_mk_status": (I, [P]),

@@ -27,10 +27,16 @@ def lib():
 @pytest.fixture(params=[0, 2], ids=["auto", "splitk"])
 def engine(request, lib):
     """launcher's engine choice (whole-K workgroups where they fit), then the
-    split-K engine forced"""
-    lib.s2p_gemv_set_engine(request.param)
-    yield request.param
-    lib.s2p_gemv_set_engine(0)
+    split-K engine forced (per call: s2p_gemv_engine_run)"""
+    return request.param
+
+
+def int4p_gemv(lib, engine, y, x, w, s, M, N, K):
+    """the public INT4-g32 GEMV (engine 0) or the same GEMV on the split-K
+    engine"""
+    if engine == 0:
+        return lib.s2p_int4p_gemv(P(y), P(x), P(w), P(s), M, N, K, 32, S())
+    return lib.s2p_gemv_engine_run(engine, 0, P(y), P(x), P(w), P(s), M, N, K, S())
 
 
 def rand_int4(r, N, K):
@@ -48,8 +54,8 @@ def test_int4p_gemv_vs_oracle(lib, engine, M, N, K):
     packed, scales = rand_int4(r, N, K)
     x = bf16_bits(r.standard_normal((M, K)).astype(np.float32))
     y = empty((M, N))
-    s2pamd.check(lib.s2p_int4p_gemv(P(y), P(to_dev(x)), P(to_dev(packed)), P(to_dev(scales)),
-                                    M, N, K, 32, S()), "int4p gemv")
+    s2pamd.check(int4p_gemv(lib, engine, y, to_dev(x), to_dev(packed), to_dev(scales), M, N, K),
+                 "int4p gemv")
     got = bf16_vals(to_host(y, np.uint16))
     exact = po.int4p_gemv_f64(x, packed, scales, M, N, K)
     assert_close_rel(got, exact, what=f"int4p M={M} N={N} K={K}")
@@ -72,6 +78,29 @@ def test_int4p_gemm_large_m(lib, M, N, K):
     assert_close_rel(got, po.int4p_gemv_f64(x, packed, scales, M, N, K), what=f"M={M}")
 
 
+@pytest.mark.parametrize("M,N,K", [(96, 4097, 2560), (81, 6144, 2560), (88, 2560, 4096)])
+def test_int4p_gemm_six_tiles_repeat(lib, M, N, K):
+    """k_gemm4 at six column tiles (M = 81..96) with its split-K handoff:
+    eight calls on the same inputs give the same bits, within the oracle's
+    tolerance"""
+    r = np.random.default_rng(5000 + M)
+    packed, scales = rand_int4(r, N, K)
+    x = bf16_bits(r.standard_normal((M, K)).astype(np.float32))
+    xd, wd, sd = to_dev(x), to_dev(packed), to_dev(scales)
+    first = None
+    for i in range(8):
+        y = empty((M, N))
+        s2pamd.check(lib.s2p_int4p_gemm_tc(P(y), P(xd), P(wd), P(sd), M, N, K, 32, S()))
+        got = to_host(y, np.uint16)
+        if first is None:
+            first = got
+            assert_close_rel(bf16_vals(got), po.int4p_gemv_f64(x, packed, scales, M, N, K),
+                             what=f"M={M}")
+        else:
+            bad = np.argwhere(got != first)
+            assert bad.size == 0, f"call {i}: {len(bad)} outputs differ, first at {bad[:4].tolist()}"
+
+
 def test_int4p_gemv_closed_forms(lib, engine):
     """All weights -8, unit scales: y = -8 * sum(x); single nonzero weight."""
     M, N, K = 4, 64, 2560
@@ -81,8 +110,7 @@ def test_int4p_gemv_closed_forms(lib, engine):
     one = np.full((N, K // 32), np.float16(1.0).view(np.uint16), np.uint16)
     packed = np.full((N, K // 2), 0x88, np.uint8)
     y = empty((M, N))
-    s2pamd.check(lib.s2p_int4p_gemv(P(y), P(to_dev(x)), P(to_dev(packed)), P(to_dev(one)), M, N,
-                                    K, 32, S()))
+    s2pamd.check(int4p_gemv(lib, engine, y, to_dev(x), to_dev(packed), to_dev(one), M, N, K))
     got = bf16_vals(to_host(y, np.uint16))
     assert_close_rel(got, np.repeat((-8 * xf.sum(1))[:, None], N, 1), what="all -8")
     # a single nonzero weight of +-1 with a power-of-two scale: y = +-x/2,
@@ -92,8 +120,7 @@ def test_int4p_gemv_closed_forms(lib, engine):
         q[n, (n * 37) % K] = 1 if n % 2 else -1
     packed = po.int4_pack(q, N, K)
     half = np.full((N, K // 32), np.float16(0.5).view(np.uint16), np.uint16)
-    s2pamd.check(lib.s2p_int4p_gemv(P(y), P(to_dev(x)), P(to_dev(packed)), P(to_dev(half)), M,
-                                    N, K, 32, S()))
+    s2pamd.check(int4p_gemv(lib, engine, y, to_dev(x), to_dev(packed), to_dev(half), M, N, K))
     got = bf16_vals(to_host(y, np.uint16))
     want = np.stack([xf[:, (n * 37) % K] * (1 if n % 2 else -1) * 0.5 for n in range(N)], 1)
     # exact up to the output rounding and the fp32 group-bias cancellation
@@ -114,7 +141,10 @@ def test_int8_gemv_vs_oracle(lib, engine, M, N, K):
     lin.int8_ready, lin.q_group, lin.q_packed = 1, 0, 0
     qd, sd = to_dev(q), to_dev(s)
     lin.w_int8.data, lin.w_iscale.data = qd.data_ptr(), sd.data_ptr()
-    if M <= 16:
+    if engine != 0:
+        s2pamd.check(lib.s2p_gemv_engine_run(engine, 1, P(y), P(to_dev(x)), P(qd), P(sd), M, N, K,
+                                             S()))
+    elif M <= 16:
         s2pamd.check(lib.s2p_int8_gemv(P(y), P(to_dev(x)), P(qd), P(sd), M, N, K, S()))
     else:
         s2pamd.check(lib.s2p_linear_forward(ctypes_ref(lin), P(to_dev(x)), P(y), M, 2, S()))
