@@ -147,6 +147,18 @@ s2p_status s2p_gemv_engine_run(int engine, int wfmt, void* y_bf16,
                                const void* x_bf16, const void* w,
                                const void* scales, int M, int N, int K,
                                hipStream_t stream);
+/* No counterpart in the reference: s2p_int4p_gemm_tc for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  G == 32, K % 128 == 0,
+ * 1 <= M <= 128, N <= 262144.  The split partials (8 MiB) and arrival
+ * counters live in a fixed per-GPU device array instead of the context
+ * scratch, so s2p_gemm_init is not needed and nothing is allocated; sizes
+ * beyond the array return S2P_ERR_INVALID with a message.  Calls that overlap
+ * on one GPU share the array and race: serialise them. */
+s2p_status s2p_int4p_gemm_tc_noalloc(void* y_bf16, const void* x_bf16,
+                                     const void* w_pack, const void* scales_f16,
+                                     int M, int N, int K, int G,
+                                     hipStream_t stream);
 s2p_status s2p_int4p_dequant(void* w_bf16, const void* w_pack,
                              const void* scales_f16, int N, int K, int G,
                              hipStream_t stream);

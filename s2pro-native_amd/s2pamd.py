@@ -111,6 +111,7 @@ SIGS = {
     "s2p_int4_pack": (I, [P, P, I, I, P]),
     "s2p_int4p_gemv": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_gemv_engine_run": (I, [I, I, P, P, P, P, I, I, I, P]),
+    "s2p_int4p_gemm_tc_noalloc": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_int4p_gemm_tc": (I, [P, P, P, P, I, I, I, I, P]),
     "s2p_int4p_dequant": (I, [P, P, P, I, I, I, P]),
     "s2p_gemm_bf16": (I, [P, P, P, I, I, I, P]),
