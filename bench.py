@@ -76,14 +76,15 @@ def step_alg_bytes(lens=(CTX,), rows=K + 1, kv_bits=16):
     return w, kv, w + kv + act
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_config3_traffic.md")
+TRAFFIC_FILES = {"gemv": "gemv_int4_config3_traffic.md", "mk2": "mk2_config3_traffic.md"}
 
 
-def measured_traffic():
-    """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (copy-calibrated); None if the summary is absent."""
+def measured_traffic(kind):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (copy-calibrated); None if the
+    summary is absent."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(os.path.join(ROOT, "profiles", TRAFFIC_FILES[kind])):
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(line.split(":")[1])
     except OSError:
@@ -259,45 +260,64 @@ def main():
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / args.steps
 
-        # dominant kernel: the GEMV engine, every weight GEMV of one step
-        # (36 x {wqkv, wo, gate_up, w2} + head at the step's M), replayed as one graph on
-        # this stream and bracketed by HIP events
-        lins = []
-        for l in range(N_LAYERS):
-            L = lib.s2p_backbone_layer(bb, l).contents
-            lins += [L.wqkv, L.wo, L.gate_up, L.w2]
-        lins.append(lib.s2p_backbone_head(bb).contents)
-        ybuf = torch.empty((M, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
-        xbuf = torch.empty((M, 9728), dtype=torch.int16, device=dev)
-        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(xbuf), xbuf.numel(), 0.0, 1.0, 3, S))
+        mk2 = lib.s2p_backbone_mk_status(bb) == 1
+        if mk2:
+            # dominant kernel: the persistent verify kernel k_mk2, the whole forward
+            # (36 layers + head) in one launch; back-to-back launches on this stream,
+            # bracketed by HIP events
+            reps = 50
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record(side)
+            for _ in range(reps):
+                s2pamd.check(lib.s2p_verify_forward(bb, s2pamd.dptr(x), s2pamd.dptr(logits), S))
+            g1.record(side)
+            side.synchronize()
+            avg_launch_s = g0.elapsed_time(g1) / 1e3 / reps
+            _, _, per_launch = step_alg_bytes(lens, M, args.kv_bits)
+            kern_gbs = per_launch / avg_launch_s / 1e9
+            kern_name = "k_mk2 (persistent verify forward: 36 layers + head, one launch)"
+        # otherwise the GEMV engine is the dominant kernel: every weight GEMV of one
+        # step (36 x {wqkv, wo, gate_up, w2} + head at the step's M), replayed as one
+        # graph on this stream and bracketed by HIP events
+        if not mk2:
+            lins = []
+            for l in range(N_LAYERS):
+                L = lib.s2p_backbone_layer(bb, l).contents
+                lins += [L.wqkv, L.wo, L.gate_up, L.w2]
+            lins.append(lib.s2p_backbone_head(bb).contents)
+            ybuf = torch.empty((M, s2pamd.S2P_VOCAB), dtype=torch.int16, device=dev)
+            xbuf = torch.empty((M, 9728), dtype=torch.int16, device=dev)
+            s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(xbuf), xbuf.numel(), 0.0, 1.0, 3, S))
 
-        def gemvs():
-            for lin in lins:
-                s2pamd.check(lib.s2p_linear_forward(ctypes.byref(lin), s2pamd.dptr(xbuf),
-                                                    s2pamd.dptr(ybuf), M, 2, S), "gemv")
-        gemvs()
-        side.synchronize()
-        # the 145 launches captured once and replayed: the events then time
-        # the kernels back to back, not the host's per-launch call overhead
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=side):
+            def gemvs():
+                for lin in lins:
+                    s2pamd.check(lib.s2p_linear_forward(ctypes.byref(lin), s2pamd.dptr(xbuf),
+                                                        s2pamd.dptr(ybuf), M, 2, S), "gemv")
             gemvs()
-        graph.replay()
-        side.synchronize()
-        reps = 5
-        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        g0.record(side)
-        for _ in range(reps):
+            side.synchronize()
+            # the 145 launches captured once and replayed: the events then time
+            # the kernels back to back, not the host's per-launch call overhead
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                gemvs()
             graph.replay()
-        g1.record(side)
-        side.synchronize()
-        del graph
-        n_launch = reps * len(lins)
-        avg_launch_s = g0.elapsed_time(g1) / 1e3 / n_launch
-        wbytes = sum(lin.w_pack.bytes + lin.w_iscale.bytes for lin in lins)
-        abytes = sum(2 * M * (lin.in_features + lin.out_features) for lin in lins)
-        per_launch = (wbytes + abytes) / len(lins)
-        gemv_gbs = per_launch / avg_launch_s / 1e9
+            side.synchronize()
+            reps = 5
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record(side)
+            for _ in range(reps):
+                graph.replay()
+            g1.record(side)
+            side.synchronize()
+            del graph
+            n_launch = reps * len(lins)
+            avg_launch_s = g0.elapsed_time(g1) / 1e3 / n_launch
+            wbytes = sum(lin.w_pack.bytes + lin.w_iscale.bytes for lin in lins)
+            abytes = sum(2 * M * (lin.in_features + lin.out_features) for lin in lins)
+            per_launch = (wbytes + abytes) / len(lins)
+            kern_gbs = per_launch / avg_launch_s / 1e9
+            kern_name = (f"k_gemv3<INT4, MT={(M + 15) // 16}> (all 145 weight GEMVs of a step, "
+                         f"layer path)")
         lib.s2p_backbone_free(bb)
 
     w, kvb, alg = step_alg_bytes(lens, M, args.kv_bits)
@@ -323,13 +343,12 @@ def main():
         "step_hbm_gbs": round(step_gbs, 1),
         "step_frac_of_peak": round(step_gbs / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 3),
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gemv_gbs / PEAK_GBS, 4),
-                     "traffic": measured_traffic() if headline else None,
-                     "traffic_source": "profiles/gemv_int4_config3_traffic.md" if headline
-                     else None,
-                     "kernel": f"k_gemv3<INT4, MT={(M + 15) // 16}> (all 145 weight GEMVs of "
-                               f"a step)",
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kern_gbs / PEAK_GBS, 4),
+                     "traffic": measured_traffic("mk2" if mk2 else "gemv") if headline else None,
+                     "traffic_source": ("profiles/" + TRAFFIC_FILES["mk2" if mk2 else "gemv"])
+                     if headline else None,
+                     "kernel": kern_name,
                      "avg_launch_us": round(avg_launch_s * 1e6, 3),
                      "alg_bytes_per_launch": int(per_launch)},
     }
