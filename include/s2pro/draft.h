@@ -18,6 +18,7 @@
 
 #include "s2pro/status.h"
 #include "s2pro/tensor.h"
+#include "s2pro/gemm.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -70,6 +71,23 @@ static inline void s2p_draft_state_reset(s2p_draft_state* s) { s->pos = 0; }
  * once the state holds S2P_DRAFT_CTX frames. */
 s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s,
                           const void* h, const void* e, void* out,
+                          hipStream_t st);
+
+/* Semantic token rows of the tied head (reference config.h:45-49). */
+#define S2P_TOK_EOS 151645
+#define S2P_TOK_SEMANTIC_START 151678
+#define S2P_DRAFT_HEAD_ROWS 4097 /* 4096 semantic rows + EOS */
+
+/* The draft's q logits: the frozen tied-head slice scores the draft's output
+ * (the predicted final-normed hidden), reference docs/SPECULATIVE.md:55-56,
+ * with the slice of slowar.c:519-541 (semantic rows S2P_TOK_SEMANTIC_START
+ * .. +4095, then EOS).  head is the backbone's lm head as a quantised linear
+ * (INT4-g32 packed or per-channel INT8): either the 4,097-row slice itself
+ * (out_features == S2P_DRAFT_HEAD_ROWS, one GEMV) or the full head
+ * (out_features > S2P_TOK_SEMANTIC_START + 4095: the slice's rows are read in
+ * place, two GEMVs).  hidden [rows][2560] bf16, logits [rows][4097] bf16,
+ * 1 <= rows <= 16; device pointers, asynchronous on st; needs s2p_gemm_init. */
+s2p_status s2p_draft_head(const s2p_linear* head, const void* hidden, void* logits, int rows,
                           hipStream_t st);
 
 #ifdef __cplusplus

@@ -1,10 +1,24 @@
 /* s2pro MI355X — draft model: safetensors loader and the one-row forward.
  *
  * Same contract as the reference src/draft/draft.c (loader :73-139, state
- * :149-155, step :157-202): the step is the reference's op sequence over
- * this build's launchers, so its numerics are those of the contract
- * kernels, and s2p_gemm_bf16 runs the bf16 path of the MFMA GEMV engine.
- */
+ * :149-155, step :157-202), with the step built on this build's fused verify
+ * engine instead of the reference's standalone launchers:
+ *   - the five GEMVs are the MFMA engine's bf16 path with their neighbours
+ *     fused in: RMSNorm in the activation staging (attn / ffn norms, from the
+ *     sums of squares the previous epilogue wrote), the residual adds and
+ *     the next norm's sums of squares in the epilogues, SiLU(w1 x) * (w3 x)
+ *     as one gate+up GEMV over w1 and w3 stored back to back;
+ *   - qk-norm, RoPE, the K/V append and the attention over the state's
+ *     cache are the verify path's fused plan-mode attention (one launch, the
+ *     position splits merged in-kernel), on a one-row plan that a prologue
+ *     kernel writes on the stream from the step's position;
+ *   - every launch takes its arguments by value and allocates nothing, so
+ *     the step can be captured into a graph (the position is an argument:
+ *     one graph per position).
+ * Launches per step: two copies ([h ; e]), the prologue, five GEMVs, the
+ * attention and the final RMSNorm (ten; the reference issues seventeen).
+ * The arithmetic is the reference rule's: the same bf16 roundings at the
+ * same points (norm, GEMV outputs, residual adds, SwiGLU). */
 #include "s2pro/draft.h"
 
 #include <ctype.h>
@@ -14,6 +28,12 @@
 
 #include "s2pro/gemm.h"
 #include "s2pro/kernels.h"
+#include "../gemv_internal.h"
+#include "../prims_internal.h"
+
+float* s2p_gemm_ctx_part(void);
+int64_t s2p_gemm_ctx_part_cap(void);
+unsigned* s2p_gemm_ctx_counters(void);
 
 #define D_DIM S2P_DRAFT_DIM
 #define D_FFN S2P_DRAFT_FFN
@@ -36,6 +56,34 @@
             return S2P_ERR_CUDA;                                            \
         }                                                                   \
     } while (0)
+
+/* The step's device workspace, held in the model's scratch tensor `a` (a
+ * [1, 2560] temporary in the reference sequence, which the fused step does
+ * not need): sums of squares [160][GEMV_MAX_M] f32 twice (ping-pong), the
+ * one-row attention plan, its RoPE row, the split counters and partials. */
+#define WS_SSQ_A 0
+#define WS_SSQ_B (WS_SSQ_A + (size_t)(D_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M * 4)
+#define WS_PLAN (WS_SSQ_B + (size_t)(D_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M * 4)
+#define WS_PL_POS (WS_PLAN + 0)
+#define WS_PL_SLOT (WS_PLAN + 4)
+#define WS_PL_SESS (WS_PLAN + 8)
+#define WS_PL_VIS (WS_PLAN + 16)
+#define WS_PL_KV (WS_PLAN + 24)
+#define WS_PL_SEG (WS_PLAN + 64)
+#define WS_ROPE (WS_PLAN + 256)
+#define WS_CTR (WS_ROPE + 64 * 2 * 4)
+#define WS_NCTR 64
+#define WS_PART (WS_CTR + WS_NCTR * 4)
+static size_t ws_bytes(void) {
+    return WS_PART + (size_t)s2p_attn_plan_part_floats(1, S2P_DRAFT_CTX) * 4;
+}
+
+/* w3 (and the state's vc) are views into the allocation of w1 (kc): the
+ * gate+up GEMV reads [w1 ; w3] as one [2F][D] matrix, the fused attention
+ * reads K then V planes of one cache */
+static int is_view_after(const s2p_tensor* base, const s2p_tensor* v) {
+    return base->data && v->data && (const char*)v->data == (const char*)base->data + base->bytes;
+}
 
 /* ---- safetensors header ------------------------------------------------ */
 
@@ -176,13 +224,35 @@ s2p_status s2p_draft_load(s2p_draft_model* m, const char* path) {
         rc = load_one(spec[i].t, json, f, data0, spec[i].n, spec[i].nd, spec[i].s);
     free(json);
     fclose(f);
+    if (rc == S2P_OK) { /* w1 and w3 back to back: [w1 ; w3] is the gate+up matrix */
+        s2p_tensor gu;
+        const int64_t sh[2] = {2 * F, D};
+        rc = s2p_tensor_device_alloc(&gu, S2P_DT_BF16, 2, sh);
+        if (rc == S2P_OK &&
+            (hipMemcpy(gu.data, m->w1.data, m->w1.bytes, hipMemcpyDeviceToDevice) != hipSuccess ||
+             hipMemcpy((char*)gu.data + m->w1.bytes, m->w3.data, m->w3.bytes,
+                       hipMemcpyDeviceToDevice) != hipSuccess)) {
+            s2p_tensor_free(&gu);
+            rc = S2P_ERR_CUDA;
+        }
+        if (rc == S2P_OK) {
+            const size_t half = m->w1.bytes;
+            s2p_tensor_free(&m->w1);
+            s2p_tensor_free(&m->w3);
+            m->w1 = gu;
+            m->w1.shape[0] = F;
+            m->w1.bytes = half;
+            m->w3 = m->w1;
+            m->w3.data = (char*)gu.data + half;
+        }
+    }
     if (rc == S2P_OK) {
         struct {
             s2p_tensor* t;
             int64_t w;
         } scr[] = {
-            {&m->xcat, 2 * D}, {&m->x, D},       {&m->a, D},       {&m->qkv, 6144},
-            {&m->attn, 4096},  {&m->gu, 2 * F},  {&m->ffn, F},
+            {&m->xcat, 2 * D}, {&m->x, D},       {&m->a, (int64_t)(ws_bytes() / 2)},
+            {&m->qkv, 6144},   {&m->attn, 4096}, {&m->gu, 2 * F},  {&m->ffn, F},
         };
         for (size_t i = 0; i < sizeof(scr) / sizeof(scr[0]) && rc == S2P_OK; i++) {
             const int64_t sh[2] = {1, scr[i].w};
@@ -195,6 +265,7 @@ s2p_status s2p_draft_load(s2p_draft_model* m, const char* path) {
 
 void s2p_draft_free(s2p_draft_model* m) {
     if (!m) return;
+    if (is_view_after(&m->w1, &m->w3)) memset(&m->w3, 0, sizeof(m->w3)); /* freed with w1 */
     s2p_tensor* ts[] = {&m->fuse,      &m->wqkv,     &m->wo,        &m->w1,   &m->w3,
                         &m->w2,        &m->q_norm,   &m->k_norm,    &m->attn_norm,
                         &m->ffn_norm,  &m->final_norm, &m->xcat,    &m->x,    &m->a,
@@ -205,54 +276,159 @@ void s2p_draft_free(s2p_draft_model* m) {
 s2p_status s2p_draft_state_init(s2p_draft_state* s) {
     if (!s) return S2P_ERR_INVALID;
     memset(s, 0, sizeof(*s));
-    const int64_t sh[3] = {D_KVH, S2P_DRAFT_CTX, D_HD};
-    s2p_status rc = s2p_tensor_device_alloc(&s->kc, S2P_DT_BF16, 3, sh);
-    if (rc == S2P_OK) rc = s2p_tensor_device_alloc(&s->vc, S2P_DT_BF16, 3, sh);
-    if (rc != S2P_OK) s2p_draft_state_free(s);
-    return rc;
+    /* K planes then V planes in one allocation ([16][ctx][128], the verify
+     * path's per-layer cache layout); vc views the second half */
+    const int64_t sh2[3] = {2 * D_KVH, S2P_DRAFT_CTX, D_HD};
+    s2p_status rc = s2p_tensor_device_alloc(&s->kc, S2P_DT_BF16, 3, sh2);
+    if (rc != S2P_OK) return rc;
+    s->kc.shape[0] = D_KVH;
+    s->kc.bytes /= 2;
+    s->vc = s->kc;
+    s->vc.data = (char*)s->kc.data + s->kc.bytes;
+    return S2P_OK;
 }
 
 void s2p_draft_state_free(s2p_draft_state* s) {
     if (!s) return;
+    if (is_view_after(&s->kc, &s->vc)) memset(&s->vc, 0, sizeof(s->vc)); /* freed with kc */
     s2p_tensor_free(&s->kc);
     s2p_tensor_free(&s->vc);
 }
 
 #define BF(t) ((s2p_bf16*)(t).data)
 
+/* one bf16-weight GEMV of the step: y = W · x (x staged plain, or RMSNormed
+ * with norm_w from ssq_in), epilogue store / residual add (+ sums of squares
+ * into ssq_out) / SwiGLU */
+static s2p_status draft_gemv(const s2p_tensor* w, int N, int K, const void* x, void* y, int xmode,
+                             const void* norm_w, const float* ssq_in, int epi, float* ssq_out,
+                             hipStream_t st) {
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wfmt = GEMV_W_BF16;
+    a.w = (const uint8_t*)w->data;
+    a.x = (const uint16_t*)x;
+    a.ldx = K;
+    a.y = (uint16_t*)y;
+    a.ldy = epi == GEMV_EPI_SWIGLU ? N / 2 : N;
+    a.M = 1;
+    a.N = N;
+    a.K = K;
+    a.xmode = xmode;
+    a.norm_w = (const uint16_t*)norm_w;
+    a.norm_eps = D_EPS;
+    a.ssq_in = ssq_in;
+    a.ssq_in_blocks = D_DIM / GEMV_SSQ_COLS;
+    a.epi = epi;
+    a.ssq_out = ssq_out;
+    a.part = s2p_gemm_ctx_part();
+    a.part_cap = s2p_gemm_ctx_part_cap();
+    a.counters = s2p_gemm_ctx_counters();
+    HIPTRY(s2p_gemv_launch(&a, st));
+    return S2P_OK;
+}
+
 s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h, const void* e,
                           void* out, hipStream_t st) {
     if (!m || !s || !h || !e || !out || !m->fuse.data || !s->kc.data) return S2P_ERR_INVALID;
-    const int D = D_DIM, F = D_FFN;
-    if (s->pos >= S2P_DRAFT_CTX) return S2P_ERR_INVALID;
-    /* xcat = [h ; e] */
+    if (s->pos < 0 || s->pos >= S2P_DRAFT_CTX) return S2P_ERR_INVALID;
+    if (!is_view_after(&m->w1, &m->w3) || !is_view_after(&s->kc, &s->vc) ||
+        m->a.bytes < ws_bytes())
+        return S2P_ERR_STATE; /* not made by s2p_draft_load / s2p_draft_state_init */
+    if (!s2p_gemm_ctx_part()) return S2P_ERR_STATE; /* s2p_gemm_init not called */
+    const int D = D_DIM, F = D_FFN, pos = s->pos;
+    unsigned char* ws = (unsigned char*)m->a.data;
+    float* ssq_a = (float*)(ws + WS_SSQ_A);
+    float* ssq_b = (float*)(ws + WS_SSQ_B);
+    /* the one-row plan: row 0 at slot pos of the state's cache, seeing
+     * slots [0, pos] */
+    S2pRowPlan plan;
+    memset(&plan, 0, sizeof(plan));
+    plan.pos = (const int32_t*)(ws + WS_PL_POS);
+    plan.slot = (const int32_t*)(ws + WS_PL_SLOT);
+    plan.sess = (const int32_t*)(ws + WS_PL_SESS);
+    plan.vis = (const uint64_t*)(ws + WS_PL_VIS);
+    plan.kv = (void* const*)(ws + WS_PL_KV);
+    plan.kvs = NULL;
+    plan.layer_stride = (int64_t)2 * D_KVH * S2P_DRAFT_CTX * D_HD;
+    plan.max_seq = S2P_DRAFT_CTX;
+    S2pAttnSeg* seg = (S2pAttnSeg*)(ws + WS_PL_SEG);
+    /* [h ; e] */
     HIPTRY(hipMemcpyAsync(BF(m->xcat), h, (size_t)D * 2, hipMemcpyDeviceToDevice, st));
     HIPTRY(hipMemcpyAsync(BF(m->xcat) + D, e, (size_t)D * 2, hipMemcpyDeviceToDevice, st));
-    /* x = fuse(xcat): the residual stream */
-    TRY(s2p_gemm_bf16(BF(m->xcat), BF(m->fuse), BF(m->x), 1, D, 2 * D, st));
-    /* attention */
-    HIPTRY(s2pk_rms_norm(BF(m->x), BF(m->attn_norm), BF(m->a), 1, D, D_EPS, st));
-    TRY(s2p_gemm_bf16(BF(m->a), BF(m->wqkv), BF(m->qkv), 1, 6144, D, st));
-    s2p_bf16* q = BF(m->qkv);
-    s2p_bf16* k = q + D_QH * D_HD;
-    s2p_bf16* v = k + D_KVH * D_HD;
-    HIPTRY(s2pk_qk_norm(q, BF(m->q_norm), 1, D_QH, D_HD, D_EPS, st));
-    HIPTRY(s2pk_qk_norm(k, BF(m->k_norm), 1, D_KVH, D_HD, D_EPS, st));
-    HIPTRY(s2pk_rope(q, k, 1, D_QH, D_KVH, D_HD, s->pos, D_ROPE_BASE, st));
-    HIPTRY(s2pk_kv_append(k, v, BF(s->kc), BF(s->vc), 1, D_KVH, D_HD, s->pos, S2P_DRAFT_CTX, st));
-    HIPTRY(s2pk_attention(q, BF(s->kc), BF(s->vc), BF(m->attn), 1, D_QH, D_KVH, D_HD, s->pos,
-                          S2P_DRAFT_CTX, st));
-    TRY(s2p_gemm_bf16(BF(m->attn), BF(m->wo), BF(m->a), 1, D, 4096, st));
-    HIPTRY(s2pk_add(BF(m->x), BF(m->a), D, st));
-    /* ffn */
-    HIPTRY(s2pk_rms_norm(BF(m->x), BF(m->ffn_norm), BF(m->a), 1, D, D_EPS, st));
-    TRY(s2p_gemm_bf16(BF(m->a), BF(m->w1), BF(m->gu), 1, F, D, st));
-    TRY(s2p_gemm_bf16(BF(m->a), BF(m->w3), BF(m->gu) + F, 1, F, D, st));
-    HIPTRY(s2pk_silu_mul(BF(m->gu), BF(m->ffn), 1, F, st));
-    TRY(s2p_gemm_bf16(BF(m->ffn), BF(m->w2), BF(m->a), 1, D, F, st));
-    HIPTRY(s2pk_add(BF(m->x), BF(m->a), D, st));
-    /* predicted next final-normed hidden */
+    /* plan, RoPE row, x = 0, counters = 0 */
+    HIPTRY(s2p_draft_prologue_launch(&plan, seg, s->kc.data, pos, D_ROPE_BASE, (float*)(ws + WS_ROPE),
+                                     m->x.data, D, (unsigned*)(ws + WS_CTR), WS_NCTR, st));
+    /* x = 0 + fuse · [h ; e], and its sums of squares */
+    TRY(draft_gemv(&m->fuse, D, 2 * D, m->xcat.data, m->x.data, GEMV_X_PLAIN, NULL, NULL,
+                   GEMV_EPI_RESID, ssq_a, st));
+    /* qkv = wqkv · RMSNorm(x; attn_norm) */
+    TRY(draft_gemv(&m->wqkv, 6144, D, m->x.data, m->qkv.data, GEMV_X_NORM, m->attn_norm.data,
+                   ssq_a, GEMV_EPI_STORE, NULL, st));
+    /* qk-norm, RoPE, K/V append at slot pos and attention over [0, pos]
+     * (the normed q rows land in xcat, no longer needed) */
+    HIPTRY(s2p_attn_plan_fused_launch(m->xcat.data, m->attn.data, &plan, seg, 1, 1, 0, pos + 1,
+                                      (float*)(ws + WS_PART), m->qkv.data, m->q_norm.data,
+                                      m->k_norm.data, (const float*)(ws + WS_ROPE), D_EPS,
+                                      (unsigned*)(ws + WS_CTR), st));
+    /* x += wo · attn */
+    TRY(draft_gemv(&m->wo, D, 4096, m->attn.data, m->x.data, GEMV_X_PLAIN, NULL, NULL,
+                   GEMV_EPI_RESID, ssq_b, st));
+    /* ffn = SiLU(w1 · n) * (w3 · n), n = RMSNorm(x; ffn_norm) */
+    TRY(draft_gemv(&m->w1, 2 * F, D, m->x.data, m->ffn.data, GEMV_X_NORM, m->ffn_norm.data, ssq_b,
+                   GEMV_EPI_SWIGLU, NULL, st));
+    /* x += w2 · ffn */
+    TRY(draft_gemv(&m->w2, D, F, m->ffn.data, m->x.data, GEMV_X_PLAIN, NULL, NULL, GEMV_EPI_RESID,
+                   NULL, st));
+    /* the predicted next final-normed hidden */
     HIPTRY(s2pk_rms_norm(BF(m->x), BF(m->final_norm), (s2p_bf16*)out, 1, D, D_EPS, st));
     s->pos++;
     return S2P_OK;
+}
+
+/* One GEMV over rows [r0, r0 + n) of a quantised linear, outputs into
+ * columns of y with row stride ldy. */
+static s2p_status head_rows(const s2p_linear* lin, int r0, int n, const void* x, int M, void* y,
+                            int ldy, hipStream_t st) {
+    const int K = lin->in_features;
+    GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    if (lin->q_packed) {
+        if (lin->q_group != 32) return S2P_ERR_INVALID;
+        a.wfmt = GEMV_W_INT4;
+        a.w = (const uint8_t*)lin->w_pack.data + (size_t)r0 * (K / 2);
+        a.s = (const uint16_t*)lin->w_iscale.data + (size_t)r0 * (K / 32);
+    } else {
+        if (lin->q_group != 0 || !lin->int8_ready) return S2P_ERR_INVALID;
+        a.wfmt = GEMV_W_INT8;
+        a.w = (const uint8_t*)lin->w_int8.data + (size_t)r0 * K;
+        a.s = (const float*)lin->w_iscale.data + r0;
+    }
+    a.x = (const uint16_t*)x;
+    a.ldx = K;
+    a.y = (uint16_t*)y;
+    a.ldy = ldy;
+    a.M = M;
+    a.N = n;
+    a.K = K;
+    a.xmode = GEMV_X_PLAIN;
+    a.epi = GEMV_EPI_STORE;
+    a.part = s2p_gemm_ctx_part();
+    a.part_cap = s2p_gemm_ctx_part_cap();
+    a.counters = s2p_gemm_ctx_counters();
+    HIPTRY(s2p_gemv_launch(&a, st));
+    return S2P_OK;
+}
+
+s2p_status s2p_draft_head(const s2p_linear* head, const void* hidden, void* logits, int rows,
+                          hipStream_t st) {
+    if (!head || !hidden || !logits || rows < 1 || rows > 16 || head->in_features != D_DIM)
+        return S2P_ERR_INVALID;
+    if (!s2p_gemm_ctx_part()) return S2P_ERR_STATE;
+    const int W = S2P_DRAFT_HEAD_ROWS;
+    if (head->out_features == W) return head_rows(head, 0, W, hidden, rows, logits, W, st);
+    if (head->out_features < S2P_TOK_SEMANTIC_START + 4096 || head->out_features <= S2P_TOK_EOS)
+        return S2P_ERR_INVALID;
+    TRY(head_rows(head, S2P_TOK_SEMANTIC_START, 4096, hidden, rows, logits, W, st));
+    return head_rows(head, S2P_TOK_EOS, 1, hidden, rows, (uint16_t*)logits + 4096, W, st);
 }

@@ -370,6 +370,47 @@ extern "C" hipError_t s2p_rope_tab_launch(const S2pRowPlan* plan, int rows, floa
     return hipGetLastError();
 }
 
+/* Draft step prologue (one block): the one-row attention plan of the step at
+ * position pos over the draft's KV (the backbone's [16][max_seq][128]
+ * layout, one layer), its RoPE row, and zeros for the residual row x (the
+ * fuse GEMV adds onto it, producing the row's sums of squares) and the
+ * attention's split counters. */
+__global__ __launch_bounds__(256) void k_draft_prologue(S2pRowPlan plan, S2pAttnSeg* seg,
+                                                        void* kv, int pos, float base,
+                                                        float* __restrict__ tab,
+                                                        uint16_t* __restrict__ x, int nx,
+                                                        unsigned* __restrict__ ctr, int nctr) {
+    const int t = threadIdx.x;
+    if (t == 0) {
+        *(int32_t*)plan.pos = pos;
+        *(int32_t*)plan.slot = pos;
+        *(int32_t*)plan.sess = 0;
+        *(uint64_t*)plan.vis = 1ull; /* the row sees its own slot */
+        *(void**)plan.kv = kv;
+        S2pAttnSeg g;
+        g.sess = 0;
+        g.L = pos;
+        g.row0 = 0;
+        g.nrows = 1;
+        g.span = pos + 1;
+        g.first = 0;
+        g.kv = kv;
+        *seg = g;
+    }
+    for (int i = t; i < nx; i += 256) x[i] = 0;
+    for (int i = t; i < nctr; i += 256) ctr[i] = 0u;
+    __syncthreads();
+    if (t < 64) rope_tab_item(plan, base, tab, 0, t);
+}
+
+extern "C" hipError_t s2p_draft_prologue_launch(const S2pRowPlan* plan, S2pAttnSeg* seg, void* kv,
+                                               int pos, float base, float* tab, void* x, int nx,
+                                               unsigned* ctr, int nctr, hipStream_t st) {
+    hipLaunchKernelGGL(k_draft_prologue, dim3(1), dim3(256), 0, st, *plan, seg, kv, pos, base, tab,
+                       (uint16_t*)x, nx, ctr, nctr);
+    return hipGetLastError();
+}
+
 /* Tree commit: session s, layer l, plane h (16 = 8 K + 8 V heads).  Accepted
  * node path[d-1] (index >= d) moves to slot L + d in increasing d, so no
  * source is overwritten before it is read. */

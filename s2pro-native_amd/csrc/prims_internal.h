@@ -38,6 +38,13 @@ typedef struct {
 hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
                                     const void* kn_w, const S2pRowPlan* plan, int rows,
                                     int layer, float eps, float base, hipStream_t st);
+/* Draft step prologue: the one-row plan (pos/slot/sess/vis/kv arrays behind
+ * the plan's pointers) and segment at position pos over the cache at kv,
+ * the RoPE row into tab [64][2], zeros into x [nx] bf16 and ctr [nctr]. */
+hipError_t s2p_draft_prologue_launch(const S2pRowPlan* plan, S2pAttnSeg* seg, void* kv, int pos,
+                                     float base,
+                                     float* tab, void* x, int nx, unsigned* ctr, int nctr,
+                                     hipStream_t st);
 /* Move accepted tree nodes' K/V from slot L + node to L + depth. */
 hipError_t s2p_kv_commit_launch(const S2pRowPlan* plan, const int32_t* path,
                                 const int32_t* n_acc, int n_sess, int R, int n_layers,

@@ -121,6 +121,7 @@ SIGS = {
     "s2p_draft_state_init": (I, [P]),
     "s2p_draft_state_free": (None, [P]),
     "s2p_draft_step": (I, [P, P, P, P, P, P]),
+    "s2p_draft_head": (I, [P, P, P, I, P]),
     # kernels.h
     "s2pk_rms_norm": (I, [P, P, P, I, I, F, P]),
     "s2pk_qk_norm": (I, [P, P, I, I, I, F, P]),

@@ -130,3 +130,85 @@ def test_draft_steps_vs_oracle(lib, draft):
                                   S()) == -1
     finally:
         lib.s2p_draft_state_free(ctypes.byref(st))
+
+
+def int4_linear(packed_d, scales_d, N, K):
+    lin = s2pamd.Linear()
+    lin.in_features, lin.out_features = K, N
+    lin.q_packed, lin.q_group = 1, 32
+    lin.w_pack.data, lin.w_pack.bytes, lin.w_pack.on_device = packed_d.data_ptr(), N * K // 2, 1
+    lin.w_iscale.data, lin.w_iscale.bytes, lin.w_iscale.on_device = (scales_d.data_ptr(),
+                                                                     N * K // 16, 1)
+    return lin
+
+
+def test_draft_head_slice(lib):
+    """s2p_draft_head: the draft's q logits over the tied-head slice (semantic
+    rows 151678.. + EOS 151645) from the full INT4 head read in place, and from
+    a 4,097-row slice head; both against binary64 on the gathered rows."""
+    N, K, rows = 155776, 2560, 3
+    r = np.random.default_rng(41)
+    packed = r.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    scales = np.abs(r.standard_normal((N, K // 32)) * 0.02).astype(np.float16).view(np.uint16)
+    hid = du.bf16_bits(r.standard_normal((rows, K)).astype(np.float32))
+    sel = np.r_[151678:151678 + 4096, 151645]
+    ps, ss = np.ascontiguousarray(packed[sel]), np.ascontiguousarray(scales[sel])
+    want = po.int4p_gemv_f64(hid, ps, ss, rows, 4097, K)
+    full_p, full_s = to_dev(packed), to_dev(scales)
+    sl_p, sl_s = to_dev(ps), to_dev(ss)
+    hd = to_dev(hid)
+    for name, lin in (("full", int4_linear(full_p, full_s, N, K)),
+                      ("slice", int4_linear(sl_p, sl_s, 4097, K))):
+        out = empty((rows, 4097))
+        s2pamd.check(lib.s2p_draft_head(ctypes.byref(lin), P(hd), P(out), rows, S()),
+                     f"draft head {name}")
+        got = bf16_vals(to_host(out, np.uint16))
+        assert_close_norm(got, want, rel=1e-2, what=f"draft head ({name})")
+    bad = int4_linear(sl_p, sl_s, 4000, K)
+    assert lib.s2p_draft_head(ctypes.byref(bad), P(hd), P(out), rows, S()) == -1
+
+
+def test_draft_step_graph_replay(lib, draft):
+    """The step captured into a graph at one position and replayed three
+    times (eager work and synchronisation between replays) gives the eager
+    step's bits every time."""
+    import torch
+    m, w = draft
+    st = s2pamd.DraftState()
+    s2pamd.check(lib.s2p_draft_state_init(ctypes.byref(st)), "state init")
+    try:
+        r = np.random.default_rng(9)
+        kc = du.bf16_bits(r.standard_normal((8, 4096, 128)).astype(np.float32) * 0.5)
+        vc = du.bf16_bits(r.standard_normal((8, 4096, 128)).astype(np.float32) * 0.5)
+        h = to_dev(du.bf16_bits(r.standard_normal(2560).astype(np.float32)))
+        e = to_dev(du.bf16_bits(r.standard_normal(2560).astype(np.float32)))
+        pos = 37
+
+        def reset():
+            h2d_raw(kc, st.kc.data)
+            h2d_raw(vc, st.vc.data)
+            st.pos = pos
+
+        reset()
+        out_eager = empty((2560,))
+        s2pamd.check(lib.s2p_draft_step(ctypes.byref(m), ctypes.byref(st), P(h), P(e),
+                                        P(out_eager), S()), "eager step")
+        torch.cuda.synchronize()
+        want = to_host(out_eager, np.uint16)
+        reset()
+        out = empty((2560,))
+        side = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            s2pamd.check(lib.s2p_draft_step(ctypes.byref(m), ctypes.byref(st), P(h), P(e),
+                                            P(out), s2pamd.stream_ptr()), "captured step")
+        for i in range(3):
+            reset()
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = to_host(out, np.uint16)
+            assert np.array_equal(got, want), f"replay {i}: {int((got != want).sum())} differ"
+    finally:
+        lib.s2p_draft_state_free(ctypes.byref(st))
