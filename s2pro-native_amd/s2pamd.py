@@ -122,6 +122,12 @@ SIGS = {
     "s2p_draft_state_free": (None, [P]),
     "s2p_draft_step": (I, [P, P, P, P, P, P]),
     "s2p_draft_head": (I, [P, P, P, I, P]),
+    "s2p_qcache_open": (I, [ctypes.c_char_p, I, P]),
+    "s2p_qcache_reading": (I, [P]),
+    "s2p_qcache_try_load": (I, [P, ctypes.c_char_p, I, I, P, P]),
+    "s2p_qcache_put_linear": (I, [P, ctypes.c_char_p, P, P]),
+    "s2p_qcache_finish": (I, [P, P]),
+    "s2p_qcache_free": (None, [P]),
     # kernels.h
     "s2pk_rms_norm": (I, [P, P, P, I, I, F, P]),
     "s2pk_qk_norm": (I, [P, P, I, I, I, F, P]),
