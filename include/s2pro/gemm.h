@@ -84,7 +84,8 @@ s2p_status s2p_linear_forward(const s2p_linear* lin, const void* x_bf16,
 void       s2p_linear_free(s2p_linear* lin);
 
 /* Random-init linears directly in the quantised formats (synthetic
- * workloads): INT4 values uniform in [-8,7], f16 group scales |N(0,sigma)|;
+ * workloads): INT4 values uniform in [-7,7] (the quantiser's symmetric code
+ * range, zero mean), f16 group scales |N(0,sigma)|;
  * or INT8 values uniform in [-127,127] with f32 row scales |N(0,sigma)|.
  * Deterministic in (seed). */
 s2p_status s2p_linear_init_random_int4(s2p_linear* lin, int in_features,

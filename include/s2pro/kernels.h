@@ -60,6 +60,16 @@ hipError_t s2pk_add(s2p_bf16* y, const s2p_bf16* x, int64_t n, hipStream_t st);
 hipError_t s2pk_sample_prepare(const s2p_bf16* logits, float* scratch, int vocab,
                                hipStream_t st);
 
+/* Gather rows of an embedding table: out[i] = table[ids[i]] (reference
+ * kernels.h:58-60). */
+hipError_t s2pk_embed(const s2p_bf16* table, const int64_t* ids, s2p_bf16* out, int rows,
+                      int dim, hipStream_t st);
+
+/* argmax over logits [rows, vocab] -> ids[rows]; the lowest index among
+ * equal maxima (reference kernels.h:68-70, the fast-AR residuals). */
+hipError_t s2pk_argmax(const s2p_bf16* logits, int32_t* ids, int rows, int vocab,
+                       hipStream_t st);
+
 #ifdef __cplusplus
 }
 #endif

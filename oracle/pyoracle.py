@@ -78,6 +78,8 @@ _SIGS = {
     "or_gemm_bf16": (None, [P, P, P, I, I, I]),
     "or_gemm_bf16_f64": (None, [P, P, P, I, I, I]),
     "or_draft_step": (None, [P, P, P, I, I, P, P, P]),
+    "or_fastar_frame": (None, [P, P, I, P, P]),
+    "or_vq_embed_add": (None, [P, P, I, P]),
 }
 
 
@@ -368,6 +370,26 @@ def layer8(lw, x, rows, kc, vc, ks, vs, max_seq, prefix, pos, vis, bw, append=Tr
     va = None if vis is None else np.ascontiguousarray(vis, np.uint64)
     lib().or_layer8(ctypes.addressof(lw), ptr(x), rows, ptr(kc), ptr(vc), ptr(ks), ptr(vs),
                     max_seq, prefix, ptr(pa), ptr(va), bw, 1 if append else 0)
+
+
+class OrFaW(ctypes.Structure):
+    _fields_ = [("layers", OrLayerW * 4), ("norm", P), ("output", OrLinear), ("emb", P)]
+
+
+def fastar_frame(faw, hidden, sem):
+    """One fast-AR frame of one row (the oracle's or_fastar_frame): returns
+    (codes [9] int32, logits [9, 4096] uint16 bf16 bits)."""
+    h = np.ascontiguousarray(hidden, np.uint16)
+    codes = np.zeros(9, np.int32)
+    lg = np.zeros((9, 4096), np.uint16)
+    lib().or_fastar_frame(ctypes.addressof(faw), ptr(h), int(sem), ptr(codes), ptr(lg))
+    return codes, lg
+
+
+def vq_embed_add(cb_emb, codes, rows):
+    """In place on rows [T, 2560]; codes [10, T]."""
+    c = np.ascontiguousarray(codes, np.int32)
+    lib().or_vq_embed_add(ptr(cb_emb), ptr(c), c.shape[1], ptr(rows))
 
 
 def gemm_bf16(x, w, M, N, K):

@@ -1187,8 +1187,10 @@ void or_layer(const or_layer_w* lw, uint16_t* x, int rows, uint16_t* kc,
     or_rms_norm(x, lw->attn_norm, xn, rows, dim, eps);
     or_linear_fwd(&lw->wqkv, xn, qkv, rows);
     or_qkv_split(qkv, q, k, v, rows, qw, kvw);
-    or_qk_norm(q, lw->q_norm, rows, 32, 128, eps);
-    or_qk_norm(k, lw->k_norm, rows, 8, 128, eps);
+    if (lw->q_norm) { /* NULL: a layer without qk-norm (the fast-AR, fastar.cu:654) */
+        or_qk_norm(q, lw->q_norm, rows, 32, 128, eps);
+        or_qk_norm(k, lw->k_norm, rows, 8, 128, eps);
+    }
     or_rope(q, rows, 32, 128, 0, pos, 1000000.0f);
     or_rope(k, rows, 8, 128, 0, pos, 1000000.0f);
     or_kv_append(k, v, kc, vc, rows, 8, 128, 0, slots, max_seq);
@@ -1311,4 +1313,68 @@ void or_draft_step(const or_draft_w* d, uint16_t* kc, uint16_t* vc, int max_seq,
     or_add(x, a, D);
     or_rms_norm(x, d->final_norm, out, 1, D, eps);
     free(xcat); free(x); free(a); free(qkv); free(att); free(gu); free(ffn);
+}
+
+/* ---- the fast-AR frame (src/fastar/fastar.cu:726-789, fa_run_layers
+ * :647-723): prime the depth-11 cache at position 0 on the final-normed
+ * hidden (logits discarded), then for cb = 1..9: x = emb[code] (the previous
+ * code, clamped to 0..4095; cb 1 takes the semantic code), the 4 layers at
+ * position cb (no qk-norm), RMSNorm, the untied head, argmax (largest
+ * value, lowest index on ties, kernels.cu:1326-1357). ---- */
+void or_fastar_frame(const or_fa_w* w, const uint16_t* hidden, int sem, int32_t* codes,
+                     uint16_t* logits) {
+    const int dim = 2560, seq = 11, ncb = 10, cbs = 4096;
+    uint16_t* kc = (uint16_t*)calloc((size_t)4 * 8 * seq * 128, 2);
+    uint16_t* vc = (uint16_t*)calloc((size_t)4 * 8 * seq * 128, 2);
+    uint16_t* x = (uint16_t*)malloc((size_t)dim * 2);
+    uint16_t* xn = (uint16_t*)malloc((size_t)dim * 2);
+    uint16_t* lg = (uint16_t*)malloc((size_t)cbs * 2);
+    const size_t plane = (size_t)8 * seq * 128;
+    memcpy(x, hidden, (size_t)dim * 2);
+    for (int p = 0; p < ncb; p++) {
+        if (p > 0) {
+            int c = p == 1 ? sem : codes[p - 2];
+            c = c < 0 ? 0 : (c >= cbs ? cbs - 1 : c);
+            memcpy(x, w->emb + (size_t)c * dim, (size_t)dim * 2);
+        }
+        const int32_t pos = p;
+        for (int l = 0; l < 4; l++)
+            or_layer(&w->layers[l], x, 1, kc + l * plane, vc + l * plane, seq, p, &pos, NULL);
+        if (p == 0) continue;
+        or_rms_norm(x, w->norm, xn, 1, dim, 1e-6f);
+        or_linear_fwd(&w->output, xn, lg, 1);
+        int best = 0;
+        float bv = or_bf2f(lg[0]);
+        for (int i = 1; i < cbs; i++) {
+            const float v = or_bf2f(lg[i]);
+            if (v > bv) {
+                bv = v;
+                best = i;
+            }
+        }
+        codes[p - 1] = best;
+        if (logits) memcpy(logits + (size_t)(p - 1) * cbs, lg, (size_t)cbs * 2);
+    }
+    free(kc);
+    free(vc);
+    free(x);
+    free(xn);
+    free(lg);
+}
+
+/* s2pfa_vq_embed_add (fastar.cu:104-127): rows[t] += bf16(f32 sum over the
+ * ten codebooks, in order, of cb_emb[cb * 4096 + clamp(code)]). */
+void or_vq_embed_add(const uint16_t* cb_emb, const int32_t* codes, int T, uint16_t* rows) {
+    const int dim = 2560, ncb = 10, cbs = 4096;
+    for (int t = 0; t < T; t++)
+        for (int d = 0; d < dim; d++) {
+            float acc = 0.f;
+            for (int cb = 0; cb < ncb; cb++) {
+                int c = codes[(size_t)cb * T + t];
+                c = c < 0 ? 0 : (c >= cbs ? cbs - 1 : c);
+                acc += or_bf2f(cb_emb[((size_t)cb * cbs + c) * dim + d]);
+            }
+            uint16_t* o = rows + (size_t)t * dim + d;
+            *o = or_f2bf(or_bf2f(*o) + or_bf2f(or_f2bf(acc)));
+        }
 }

@@ -210,6 +210,21 @@ void or_layer8(const or_layer_w* lw, uint16_t* x, int rows, int8_t* kc, int8_t* 
                uint16_t* ks, uint16_t* vs, int max_seq, int prefix, const int32_t* pos,
                const uint64_t* vis, int bw, int append);
 
+/* ---- the fast-AR frame (src/fastar/fastar.cu:726-789) ------------------ */
+typedef struct {
+    or_layer_w layers[4];     /* q_norm = k_norm = NULL: no qk-norm */
+    const uint16_t* norm;     /* final RMSNorm [2560] */
+    or_linear output;         /* untied head [4096, 2560] */
+    const uint16_t* emb;      /* embeddings [4096, 2560] */
+} or_fa_w;
+
+/* One frame of one row: codes[0..8] the nine residual codes; logits (may be
+ * NULL) [9][4096] the head outputs of the nine steps. */
+void or_fastar_frame(const or_fa_w* w, const uint16_t* hidden, int sem, int32_t* codes,
+                     uint16_t* logits);
+/* codes [10][T] codebook-major; rows [T, 2560] bf16 in/out */
+void or_vq_embed_add(const uint16_t* cb_emb, const int32_t* codes, int T, uint16_t* rows);
+
 /* ---- the draft model (src/draft/draft.c:157-202) ---------------------- */
 /* y[M,N] = bf16(sum_k w[n,k] x[m,k]) with an fp32 sum in increasing k: the
  * contract of s2p_gemm_bf16 (reference gemm.h:93-96, cuBLAS there, whose

@@ -179,7 +179,7 @@ extern "C" hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRo
                                                  const void* kn_w, const float* rope_tab,
                                                  float eps, unsigned* counters, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    if (!qkv || !qn_w || !kn_w || !rope_tab) return hipErrorInvalidValue;
+    if (!qkv || !rope_tab || (!qn_w) != (!kn_w)) return hipErrorInvalidValue; /* both or no norm */
     AttnArgs a = {};
     a.mode = AM_PLAN;
     a.q = (const uint16_t*)q;

@@ -269,8 +269,9 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         early = !appends && tb0 < p_end;
         constexpr int IB = 8; /* every item of a 4-wave block in one batch at M <= 5 */
         /* the norm weights of this lane's two elements, once per wave (q and k) */
-        const uint16_t qw0 = a.qn_w[lane], qw1 = a.qn_w[lane + 64];
-        const uint16_t kw0 = a.kn_w[lane], kw1 = a.kn_w[lane + 64];
+        const bool qkn = a.qn_w != nullptr; /* no norm weights: RoPE only */
+        const uint16_t qw0 = qkn ? a.qn_w[lane] : 0, qw1 = qkn ? a.qn_w[lane + 64] : 0;
+        const uint16_t kw0 = qkn ? a.kn_w[lane] : 0, kw1 = qkn ? a.kn_w[lane + 64] : 0;
         for (int base = wave; base < nit; base += IB * W) {
             float v0[IB], v1[IB], cs[IB][4];
             uint16_t x0[IB], x1[IB];
@@ -315,7 +316,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 float o0, o1;
                 const bool isq = it < nq;
                 qkrope_math(v0[j], v1[j], isq ? qw0 : kw0, isq ? qw1 : kw1, cs[j][0], cs[j][1],
-                            cs[j][2], cs[j][3], a.eps, lane, &o0, &o1);
+                            cs[j][2], cs[j][3], a.eps, lane, &o0, &o1, qkn);
                 if (it < nq) {
                     LDS(uint16_t)* dq = s_q + it * AT_HD; /* q vector (rl, g) = it */
                     const uint16_t q0 = f2bf(o0), q1 = f2bf(o1);

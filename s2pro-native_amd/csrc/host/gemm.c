@@ -350,7 +350,7 @@ s2p_status s2p_linear_init_random_int4(s2p_linear* lin, int in_features, int out
     int64_t sshape[1] = {(int64_t)out_features * (in_features / G)};
     s2p_status rc = s2p_tensor_device_alloc(&lin->w_iscale, S2P_DT_F16, 1, sshape);
     if (rc == S2P_OK &&
-        (s2p_synth_bytes(lin->w_pack.data, (int64_t)lin->w_pack.bytes, seed, stream) != hipSuccess ||
+        (s2p_synth_int4(lin->w_pack.data, (int64_t)lin->w_pack.bytes, seed, stream) != hipSuccess ||
          s2p_synth_f16_absnormal(lin->w_iscale.data, sshape[0], sigma, seed ^ 0x5CA1E5ULL,
                                  stream) != hipSuccess))
         rc = S2P_ERR_CUDA;

@@ -99,13 +99,13 @@ static s2p_status norm_weight(s2p_tensor* t, int n, uint64_t seed, hipStream_t s
 
 /* Random weights at rms 1/sqrt(in), the scale of trained projections, so a
  * synthetic stack keeps activations O(1) layer to layer.  The scale sigma is
- * the group / row scale; the code rms is sqrt(255/12) for uniform nibbles
- * (offset 8) and ~73.9 for uniform bytes (offset 128). */
+ * the group / row scale; the code rms is sqrt(56/3) ~ 4.32 for nibbles
+ * uniform over -7..7 and ~73.9 for uniform bytes over -127..127. */
 static s2p_status rand_linear(s2p_linear* l, s2p_weight_q q, int in, int out, uint64_t seed,
                               hipStream_t st) {
     const float w_rms = 1.0f / sqrtf((float)in);
     if (q == S2P_WQ_INT4_G32)
-        return s2p_linear_init_random_int4(l, in, out, 32, w_rms / 4.61f, seed, st);
+        return s2p_linear_init_random_int4(l, in, out, 32, w_rms / 4.32f, seed, st);
     return s2p_linear_init_random_int8(l, in, out, w_rms / 73.9f, seed, st);
 }
 

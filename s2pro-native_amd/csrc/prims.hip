@@ -370,6 +370,140 @@ extern "C" hipError_t s2p_rope_tab_launch(const S2pRowPlan* plan, int rows, floa
     return hipGetLastError();
 }
 
+/* Embedding gather, out[r] = table[ids[r]] (reference kernels.h:58-60): one
+ * 64-lane block per (row, 8-column group of 64 lanes), 16-byte copies. */
+__global__ __launch_bounds__(64) void k_embed(const uint16_t* __restrict__ table,
+                                              const int64_t* __restrict__ ids,
+                                              uint16_t* __restrict__ out, int dim) {
+    const int r = blockIdx.y, c = (blockIdx.x * 64 + threadIdx.x) * 8;
+    if (c >= dim) return;
+    const s2p_u32x4 v = *(const s2p_u32x4*)(table + (size_t)ids[r] * dim + c);
+    *(s2p_u32x4*)(out + (size_t)r * dim + c) = v;
+}
+
+extern "C" hipError_t s2pk_embed(const s2p_bf16* table, const int64_t* ids, s2p_bf16* out,
+                                 int rows, int dim, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!table || !ids || !out || dim <= 0 || dim % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)((dim / 8 + 63) / 64), (unsigned)rows), dim3(64), 0,
+                       st, (const uint16_t*)table, ids, (uint16_t*)out, dim);
+    return hipGetLastError();
+}
+
+/* argmax of each row (reference kernels.h:68-70, kernels.cu:1326-1357): the
+ * largest value, the lowest index among equal values; NaN never wins.  One
+ * 256-thread block per row: each lane keeps its best (value, index) over a
+ * strided walk, then a wave reduction and one across the four waves. */
+S2P_DEV bool am_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__global__ __launch_bounds__(256) void k_argmax(const uint16_t* __restrict__ logits,
+                                                int32_t* __restrict__ ids, int vocab) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint16_t* row = logits + (size_t)r * vocab;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = t; i < vocab; i += 256) {
+        const float v = bf2f(row[i]);
+        if (am_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (am_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 4; w++)
+            if (am_better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        ids[r] = bi == 0x7FFFFFFF ? 0 : bi; /* an all-NaN row: index 0 */
+    }
+}
+
+extern "C" hipError_t s2pk_argmax(const s2p_bf16* logits, int32_t* ids, int rows, int vocab,
+                                  hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!logits || !ids || vocab <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, st, (const uint16_t*)logits,
+                       ids, vocab);
+    return hipGetLastError();
+}
+
+/* Fast-AR step input: x[r] = table[clamp(ids[r], 0, n_ids - 1)] and the
+ * sums of squares of its 16-column blocks for the next RMSNorm (the
+ * residual-init arithmetic of resid_init_item). */
+__global__ __launch_bounds__(64) void k_fa_embed_ssq(const uint16_t* __restrict__ table,
+                                                     const int32_t* __restrict__ ids, int n_ids,
+                                                     uint16_t* __restrict__ x,
+                                                     float* __restrict__ ssq, int width) {
+    const int m = blockIdx.y, blk = blockIdx.x, lane = threadIdx.x;
+    int id = ids[m];
+    id = id < 0 ? 0 : (id >= n_ids ? n_ids - 1 : id);
+    const int c = blk * 64 + lane;
+    const uint16_t v = table[(size_t)id * width + c];
+    coh_st16(x + (size_t)m * width + c, v);
+    const float f = bf2f(v);
+    const float t = sum_lanes16(f * f);
+    if ((lane & 15) == 0) coh_stf(ssq + (size_t)(blk * 4 + (lane >> 4)) * 128 + m, t);
+}
+
+extern "C" hipError_t s2p_fa_embed_ssq_launch(const void* table, const int32_t* ids, int n_ids,
+                                              void* x, float* ssq, int rows, int width,
+                                              hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (width % 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_fa_embed_ssq, dim3(width / 64, rows), dim3(64), 0, st,
+                       (const uint16_t*)table, ids, n_ids, (uint16_t*)x, ssq, width);
+    return hipGetLastError();
+}
+
+/* The 10-codebook VQ embedding of frame t added onto rows[t] (reference
+ * fastar.h:46-52): codes [10][T] codebook-major, clamped to 0..4095; the ten
+ * rows of table [10 * 4096][dim] summed in f32 in codebook order, rounded to
+ * bf16 once, then added to the row with one bf16 rounding. */
+__global__ __launch_bounds__(256) void k_vq_embed_add(const uint16_t* __restrict__ table,
+                                                      const int32_t* __restrict__ codes, int T,
+                                                      uint16_t* __restrict__ rows, int dim) {
+    const int t = blockIdx.x;
+    int idx[10];
+#pragma unroll
+    for (int cb = 0; cb < 10; cb++) {
+        int c = codes[(size_t)cb * T + t];
+        c = c < 0 ? 0 : (c > 4095 ? 4095 : c);
+        idx[cb] = cb * 4096 + c;
+    }
+    for (int d = threadIdx.x; d < dim; d += 256) {
+        float acc = 0.f;
+#pragma unroll
+        for (int cb = 0; cb < 10; cb++) acc += bf2f(table[(size_t)idx[cb] * dim + d]);
+        uint16_t* y = rows + (size_t)t * dim + d;
+        *y = f2bf(__fadd_rn(bf2f(*y), bf2f(f2bf(acc))));
+    }
+}
+
+extern "C" hipError_t s2p_fa_vq_embed_add_launch(const void* table, const int32_t* codes, int T,
+                                                 void* rows, int dim, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_vq_embed_add, dim3((unsigned)T), dim3(256), 0, st, (const uint16_t*)table,
+                       codes, T, (uint16_t*)rows, dim);
+    return hipGetLastError();
+}
+
 /* Draft step prologue (one block): the one-row attention plan of the step at
  * position pos over the draft's KV (the backbone's [16][max_seq][128]
  * layout, one layer), its RoPE row, and zeros for the residual row x (the

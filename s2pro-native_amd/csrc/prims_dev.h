@@ -27,16 +27,20 @@ S2P_DEV void rope_cs(int p, int i, int head_dim, float base, float* c, float* s)
 
 /* qk-norm + RoPE arithmetic of one (row, head), lane = elements lane and
  * lane + 64 (v0, v1) with norm weights w0, w1 and the (cos, sin) of their
- * pairs; the partner of element e (e ^ 1) lives in lane ^ 1 */
+ * pairs; the partner of element e (e ^ 1) lives in lane ^ 1.  norm false:
+ * RoPE of the values as they are (a model without qk-norm, the fast-AR). */
 S2P_DEV void qkrope_math(float v0, float v1, uint16_t w0, uint16_t w1, float c0, float s0,
-                         float c1, float s1, float eps, int lane, float* o0, float* o1) {
+                         float c1, float s1, float eps, int lane, float* o0, float* o1,
+                         bool norm = true) {
 #pragma clang fp contract(off)
-    float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
-    s = wave_sum_down(s);
-    s = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(s), 0)); /* lane 0's total */
-    const float inv = rsqrt_rule(s / 128.0f + eps);
-    v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(w0))));
-    v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(w1))));
+    if (norm) {
+        float s = fmaf(v0, v0, 0.f) + fmaf(v1, v1, 0.f);
+        s = wave_sum_down(s);
+        s = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(s), 0)); /* lane 0's total */
+        const float inv = rsqrt_rule(s / 128.0f + eps);
+        v0 = bf2f(f2bf(__fmul_rn(__fmul_rn(v0, inv), bf2f(w0))));
+        v1 = bf2f(f2bf(__fmul_rn(__fmul_rn(v1, inv), bf2f(w1))));
+    }
     const float pv0 = dpp_f<0xB1>(v0), pv1 = dpp_f<0xB1>(v1); /* lane ^ 1 */
     if ((lane & 1) == 0) {
         *o0 = __fsub_rn(__fmul_rn(v0, c0), __fmul_rn(pv0, s0)); /* x0' */

@@ -38,6 +38,12 @@ typedef struct {
 hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
                                     const void* kn_w, const S2pRowPlan* plan, int rows,
                                     int layer, float eps, float base, hipStream_t st);
+/* Fast-AR: step input x[r] = table[clamp(ids[r])] plus its sums of squares
+ * ([width/16][128]); the 10-codebook VQ embedding added onto rows. */
+hipError_t s2p_fa_embed_ssq_launch(const void* table, const int32_t* ids, int n_ids, void* x,
+                                   float* ssq, int rows, int width, hipStream_t st);
+hipError_t s2p_fa_vq_embed_add_launch(const void* table, const int32_t* codes, int T, void* rows,
+                                      int dim, hipStream_t st);
 /* Draft step prologue: the one-row plan (pos/slot/sess/vis/kv arrays behind
  * the plan's pointers) and segment at position pos over the cache at kv,
  * the RoPE row into tab [64][2], zeros into x [nx] bf16 and ctr [nctr]. */
@@ -64,6 +70,7 @@ hipError_t s2p_attn_plan_launch(const void* q, void* out, const S2pRowPlan* plan
 /* The same, fused with qk-norm + RoPE + KV append (q is the scratch the q
  * rows are written to) and, with counters ([n_seg * 8], zero between calls),
  * with the split merge done by the last split of each block. */
+/* qn_w = kn_w = NULL: RoPE without qk-norm (a model without qk-norm) */
 hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan,
                                       const S2pAttnSeg* segs, int n_seg, int rows, int layer,
                                       int max_span, float* part, const void* qkv,

@@ -24,7 +24,7 @@ S2P_DEV double normal_of(uint64_t seed, uint64_t i) {
     return sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925 * u2);
 }
 
-enum { SY_BYTES = 0, SY_INT8 = 1, SY_F16_ABSN = 2, SY_F32_ABSN = 3, SY_BF16_N = 4 };
+enum { SY_BYTES = 0, SY_INT8 = 1, SY_F16_ABSN = 2, SY_F32_ABSN = 3, SY_BF16_N = 4, SY_INT4 = 5 };
 
 __global__ __launch_bounds__(256) void k_synth(void* p, int64_t n, int kind, float a, float b,
                                                uint64_t seed) {
@@ -33,6 +33,12 @@ __global__ __launch_bounds__(256) void k_synth(void* p, int64_t n, int kind, flo
         switch (kind) {
             case SY_BYTES: {
                 ((uint8_t*)p)[i] = (uint8_t)(h64(seed, (uint64_t)i, 2) >> 56);
+                break;
+            }
+            case SY_INT4: { /* two nibbles, each uniform over -7..7 (zero mean) */
+                const uint64_t h = h64(seed, (uint64_t)i, 3);
+                const int lo = (int)((h >> 8) % 15ULL) - 7, hi = (int)((h >> 40) % 15ULL) - 7;
+                ((uint8_t*)p)[i] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
                 break;
             }
             case SY_INT8: {
@@ -63,6 +69,9 @@ static hipError_t run(void* p, int64_t n, int kind, float a, float b, uint64_t s
 
 extern "C" hipError_t s2p_synth_bytes(void* p, int64_t n, uint64_t seed, hipStream_t st) {
     return run(p, n, SY_BYTES, 0.f, 0.f, seed, st);
+}
+extern "C" hipError_t s2p_synth_int4(void* p, int64_t n, uint64_t seed, hipStream_t st) {
+    return run(p, n, SY_INT4, 0.f, 0.f, seed, st);
 }
 extern "C" hipError_t s2p_synth_int8(void* p, int64_t n, uint64_t seed, hipStream_t st) {
     return run(p, n, SY_INT8, 0.f, 0.f, seed, st);

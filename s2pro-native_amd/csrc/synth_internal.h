@@ -11,6 +11,9 @@ extern "C" {
 #endif
 
 hipError_t s2p_synth_bytes(void* p, int64_t n, uint64_t seed, hipStream_t st);
+/* packed INT4 codes: both nibbles of each byte uniform over -7..7 (the
+ * symmetric code range of the reference quantiser, zero mean) */
+hipError_t s2p_synth_int4(void* p, int64_t n, uint64_t seed, hipStream_t st);
 hipError_t s2p_synth_int8(void* p, int64_t n, uint64_t seed, hipStream_t st);
 hipError_t s2p_synth_f16_absnormal(void* p, int64_t n, float sigma, uint64_t seed,
                                    hipStream_t st);

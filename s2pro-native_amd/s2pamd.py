@@ -72,6 +72,18 @@ class SlowLayer(ctypes.Structure):
                 ("k_norm", Tensor)]
 
 
+class FaLayer(ctypes.Structure):
+    """s2pfa_layer (include/s2pro/fastar.h)"""
+    _fields_ = [("wqkv", Linear), ("wo", Linear), ("w13", Linear), ("w2", Linear),
+                ("attn_norm", Tensor), ("ffn_norm", Tensor)]
+
+
+class FaWeights(ctypes.Structure):
+    """s2pfa_weights (include/s2pro/fastar.h)"""
+    _fields_ = [("layers", FaLayer * 4), ("norm", Tensor), ("output", Linear),
+                ("cb_emb", Tensor), ("emb", Tensor)]
+
+
 class DraftModel(ctypes.Structure):
     """s2p_draft_model (include/s2pro/draft.h)"""
     _fields_ = [(n, Tensor) for n in
@@ -149,6 +161,18 @@ SIGS = {
     "s2pk_attention8": (I, [P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "s2pk_attention8_decode": (I, [P, P, P, P, P, P, I, I, I, I, P, I, I, P, I, P]),
     "s2pk_sample": (I, [P, I64, P, P, I, P, P, P, P, P]),
+    "s2pk_embed": (I, [P, P, P, I, I, P]),
+    "s2pk_argmax": (I, [P, P, I, I, P]),
+    # fastar.h
+    "s2pfa_create": (I, [P, P, I, P]),
+    "s2pfa_create_random": (I, [P, I, I, U64, P]),
+    "s2pfa_free": (None, [P]),
+    "s2pfa_weights_of": (ctypes.POINTER(FaWeights), [P]),
+    "s2pfa_decode_frame_batch": (I, [P, P, P, I, P, P]),
+    "s2pfa_decode_frame_batch_dev": (I, [P, P, P, I, P, P]),
+    "s2pfa_decode_frame_logits_dev": (I, [P, P, P, I, P, P, P]),
+    "s2pfa_vq_embed_add_dev": (I, [P, P, I, P, P]),
+    "s2pfa_vq_embed_add": (I, [P, P, I, P, P]),
     # verify.h
     "s2p_backbone_create_random": (I, [P, U64, P, P]),
     "s2p_backbone_free": (None, [P]),

@@ -57,8 +57,9 @@ def layer(W, x, kc, vc, L, pos, vis):
     R = x.shape[0]
     qkv = rms(x, W["attn_norm"]) @ W["wqkv"].T
     q, k, v = qkv[:, :4096], qkv[:, 4096:5120], qkv[:, 5120:]
-    q = rms(q.reshape(R, 32, 128), W["q_norm"]).reshape(R, 4096)
-    k = rms(k.reshape(R, 8, 128), W["k_norm"]).reshape(R, 1024)
+    if W.get("q_norm") is not None:  # the fast-AR layers have no qk-norm
+        q = rms(q.reshape(R, 32, 128), W["q_norm"]).reshape(R, 4096)
+        k = rms(k.reshape(R, 8, 128), W["k_norm"]).reshape(R, 1024)
     q, k = rope(q, pos, 32), rope(k, pos, 8)
     kc[:, L:L + R] = k.reshape(R, 8, 128).transpose(1, 0, 2)
     vc[:, L:L + R] = v.reshape(R, 8, 128).transpose(1, 0, 2)
@@ -113,3 +114,16 @@ def draft_step(W, h, e, kc, vc, pos):
     Wl = dict(W, gate_up=np.vstack([W["w1"], W["w3"]]))
     x = layer(Wl, x, kc, vc, pos, [pos], [1])
     return rms(x, W["final_norm"])[0]
+
+
+def fastar_step(layers, final_norm, head, hidden, emb_rows, cb):
+    """Binary64 logits of fast-AR step cb (src/fastar/fastar.cu:726-789) as
+    the uncached causal forward over [hidden, emb_rows[0..cb-1]] at positions
+    0..cb (each layer's cache starts empty, depth 11)."""
+    x = np.concatenate([bf(hidden)[None], bf(emb_rows[:cb])], axis=0)
+    n = cb + 1
+    vis = [(1 << (r + 1)) - 1 for r in range(n)]
+    for W in layers:
+        kc, vc = np.zeros((8, 11, 128)), np.zeros((8, 11, 128))
+        x = layer(W, x, kc, vc, 0, list(range(n)), vis)
+    return rms(x[-1:], final_norm) @ head.T
