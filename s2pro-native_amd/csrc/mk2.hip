@@ -58,7 +58,9 @@
 #define NWAVE 8
 #define CW 7 /* compute waves */
 #define NTH (64 * NWAVE)
-#define NSLOT 20
+#ifndef NSLOT
+#define NSLOT 8 /* measured: 8 slots beat 20 (less queueing in front of the exchanges), 4 within 1% */
+#endif
 #define SPIN_LIMIT (1u << 22)
 #define LDSP(T) __attribute__((address_space(3))) T
 
@@ -454,30 +456,57 @@ S2P_DEV void c_gemv(Slot (&S)[NSLOT], const Mk2Args& A, int l, int cw, const Ctx
 S2P_DEV uint32_t flag_val(uint32_t epoch, int l, int kind) {
     return epoch * 2048u + (uint32_t)((l + 2) * 8 + kind);
 }
-/* one wave: wait until flags f[i0 .. i0 + n) all read want */
-S2P_DEV void flags_wait1(const Mk2Args& A, const uint32_t* f, int n, uint32_t want);
-S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want) {
-    for (int c = 0; c < n; c += 1024) flags_wait1(A, A.flags + kind + i0 + c, min(1024, n - c), want);
-}
-/* n <= 1024: every flag of a poll in flight at once (16 per lane) */
-S2P_DEV void flags_wait1(const Mk2Args& A, const uint32_t* f, int n, uint32_t want) {
+/* one wave: wait until the flags of up to three ranges [i0, i0 + n) of the
+ * flag words at f all read want (fewer than 64 * NLD flags in total), one
+ * poll over all the ranges at a time.  (Deeper polling, several polls in
+ * flight, measured slower: the extra reads of the hot flag lines delay the
+ * producers' stores more than they shorten the detection.) */
+template <int NLD>
+S2P_DEV void flags_poll(const Mk2Args& A, const uint32_t* f, int ia, int na, int ib, int nb, int ic,
+                        int nc, uint32_t want) {
     const int lane = threadIdx.x & 63;
     if (coh_ld32(A.err)) return;
-    unsigned spins = 0;
-    while (true) {
-        uint32_t v[16];
+    const int n = na + nb + nc; /* < 64 * NLD: element n is the error word */
+    const uint32_t* ptr[NLD];
+    bool val[NLD], errw[NLD];
 #pragma unroll
-        for (int j = 0; j < 16; j++) v[j] = lane + 64 * j < n ? coh_ld32(f + lane + 64 * j) : want;
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < 16; j++) ok = ok && v[j] == want;
-        if (__all(ok)) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++spins > SPIN_LIMIT || ((spins & 1023) == 0 && coh_ld32(A.err))) {
-            if (lane == 0) __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
+    for (int j = 0; j < NLD; j++) {
+        const int e = lane + 64 * j;
+        val[j] = e < n;
+        errw[j] = e == n;
+        /* past the set: the error word, then the first flag again */
+        ptr[j] = e < na ? f + ia + e
+                        : (e < na + nb ? f + ib + (e - na)
+                                       : (e < n ? f + ic + (e - na - nb) : (e == n ? (const uint32_t*)A.err : f + ia)));
     }
+    for (unsigned spins = 0; spins < SPIN_LIMIT; spins++) {
+        uint32_t r[NLD];
+#pragma unroll
+        for (int j = 0; j < NLD; j++) r[j] = coh_ld32(ptr[j]);
+        bool o = true, e = false;
+#pragma unroll
+        for (int j = 0; j < NLD; j++) {
+            o = o && (!val[j] || r[j] == want);
+            e = e || (errw[j] && r[j] != 0u);
+        }
+        if (__any(e) || __all(o)) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+S2P_DEV void flags_wait3(const Mk2Args& A, int kind, int ia, int na, int ib, int nb, int ic, int nc,
+                         uint32_t want) {
+    const uint32_t* f = A.flags + kind;
+    const int n = na + nb + nc;
+    if (n < 64) flags_poll<1>(A, f, ia, na, ib, nb, ic, nc, want);
+    else if (n < 192) flags_poll<3>(A, f, ia, na, ib, nb, ic, nc, want);
+    else if (n < 640) flags_poll<10>(A, f, ia, na, ib, nb, ic, nc, want);
+    else
+        for (int c = 0; c < n; c += 1023) /* one range of 640 flags or more */
+            flags_poll<16>(A, f, ia + c, min(1023, n - c), 0, 0, 0, 0, want);
+}
+S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want) {
+    flags_wait3(A, kind, i0, n, 0, 0, 0, 0, want);
 }
 /* one wave: publish flags f[i0 .. i0 + n) = val once this wave's stores completed */
 S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) {
@@ -641,9 +670,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         /* q-norm and k-norm weights are adjacent: 512 B */
         if (lane < 32) dma16(A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_Q + 8 * lane, (LDSP(void)*)s_nw, false);
         const uint32_t want = flag_val(epoch, l, MK2_F_Q);
-        flags_wait(A, MK2_F_Q, 32 * kvh, 32, want);
-        flags_wait(A, MK2_F_Q, 256 + 8 * kvh, 8, want);
-        flags_wait(A, MK2_F_Q, 320 + 8 * kvh, 8, want);
+        flags_wait3(A, MK2_F_Q, 32 * kvh, 32, 256 + 8 * kvh, 8, 320 + 8 * kvh, 8, want);
         const int s0 = max(p0, g.L), nq = g.nrows * 4, nnew = max(0, p1 - s0);
         /* q items: the row's 4 q heads of kv head kvh are 1 KB contiguous */
         for (int rl = 0; rl < g.nrows; rl++) {
