@@ -176,7 +176,7 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)2 * S * sizeof(void*) +
                      (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_rope, R * 64 * 2 * sizeof(float));
-    if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_STATE_WORDS * sizeof(uint32_t));
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_AUX_OFF + MK2_AUX_BYTES);
     if (rc == S2P_OK) /* flags, epoch and counters start at zero once; the kernel keeps them */
         rc = hip_ok(hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st), "mk2 init");
     if (rc == S2P_OK) {
@@ -484,7 +484,9 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
         return 0;
     if (!b->d_wpack && mk2_pack_all(b, st) != S2P_OK) return 0;
     /* a fresh state block per plan: flags, launch epoch, split counters */
-    if (hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st) != hipSuccess) return 0;
+    if (hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st) != hipSuccess ||
+        hipMemsetAsync((unsigned char*)b->d_mk2 + MK2_AUX_OFF, 0, MK2_AUX_BYTES, st) != hipSuccess)
+        return 0;
     Mk2Args* A = &b->mk2;
     memset(A, 0, sizeof(*A));
     A->wpack = b->d_wpack;
@@ -501,6 +503,13 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
     A->attn = (uint16_t*)b->attn;
     A->h = (uint16_t*)b->gu;
     A->ssq = b->ssq;
+    {
+        unsigned char* aux = (unsigned char*)b->d_mk2 + MK2_AUX_OFF;
+        A->xw = (uint16_t*)(aux + MK2_AUX_XW);
+        A->gsx = (float*)(aux + MK2_AUX_GSX);
+        A->gsh = (float*)(aux + MK2_AUX_GSH);
+        A->gsa = (float*)(aux + MK2_AUX_GSA);
+    }
     A->flags = b->d_mk2;
     A->state = b->d_mk2 + MK2_STATE_WORD;
     A->err = (int*)(b->d_mk2 + MK2_ERR_WORD);

@@ -271,69 +271,25 @@ constexpr int XRS(int K) { return K + 32; }
 #define L_XOLD (L_OUTB + 1280)   /* [M][16] bf16 residual before the add */
 #define L_SSQO (L_XOLD + 256)    /* [M][16] f32 sums of squares of the new residual */
 #define L_FLAG (L_SSQO + 512)    /* [16] int broadcast words */
-#define L_NW (L_FLAG + 64)       /* [2560] bf16 norm weights */
+#define L_NW (L_FLAG + 64)       /* (5120 B) weighted outputs, their sums, next-norm weights: */
+#define L_OUTW L_NW              /*   [M][96] bf16 bf16(new residual x next norm weight) */
+#define L_HS (L_NW + 1280)       /*   [M][8] f32 per-tile sums of L_OUTW (w2/wo) or of h (gate_up) */
+#define L_NWT (L_NW + 1536)      /*   [96] bf16 next-norm weights of the workgroup's columns */
 #define L_BIAS (L_NW + 5120)     /* [NB][4 groups][8 rows] f32: -136 x the group's row sums */
 #define L_TOTAL (L_BIAS + 76 * 4 * 8 * 4)
-static_assert(MK2_MAX_ROWS * XRS(9728) * 2 <= L_PART && MK2_MAX_ROWS * XRS(2560) * 2 <= L_HPART &&
+static_assert(MK2_MAX_ROWS * XRS(9728) * 2 <= L_PART && L_PART + 608 * 8 * 4 <= L_INV && MK2_MAX_ROWS * XRS(2560) * 2 <= L_HPART &&
                   L_TOTAL <= 160 * 1024,
               "LDS carve-up");
 
-/* ---- shared (all waves) pieces of a GEMV phase ---- */
-/* RMSNorm of the staged rows in place: xn = bf16(bf16?(x * inv) * w) with
- * the rule's two multiplies and one rounding (kernels.cu:46-80) */
-template <int K>
-S2P_DEV void norm_rows(LDSP(unsigned char)* smem, int M) {
-#pragma clang fp contract(off)
-    constexpr int KC = K / 8, RS = XRS(K);
-    LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
-    const LDSP(uint16_t)* nw = (const LDSP(uint16_t)*)(smem + L_NW);
-    const LDSP(float)* inv = (const LDSP(float)*)(smem + L_INV);
-    for (int i = threadIdx.x; i < M * KC; i += NTH) {
-        const int m = i / KC, c = i - m * KC;
-        const float iv = inv[m];
-        LDSP(s2p_u32x4)* p = (LDSP(s2p_u32x4)*)(xs + m * RS + c * 8);
-        const s2p_u32x4 v = *p;
-        const s2p_u32x4 w4 = *(const LDSP(s2p_u32x4)*)(nw + c * 8);
-        uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-            const uint32_t lo = f2bf(__fmul_rn(__fmul_rn(bf2f_lo(vv[d]), iv), bf2f_lo(ww[d])));
-            const uint32_t hi = f2bf(__fmul_rn(__fmul_rn(bf2f_hi(vv[d]), iv), bf2f_hi(ww[d])));
-            vv[d] = lo | (hi << 16);
-        }
-        *p = (s2p_u32x4){vv[0], vv[1], vv[2], vv[3]};
-    }
-    __syncthreads();
-}
-
-/* the code bias of the staged rows: the packed codes are w + 136, so a
- * group's dot product carries 136 x (sum of the row's 32 values of the
- * group); this table holds -136 x that sum per (K block, group, row < 8)
- * for the units' MFMA accumulator input.  Rows >= M hold 0. */
-template <int K>
-S2P_DEV void bias_rows(LDSP(unsigned char)* smem, int M) {
-#pragma clang fp contract(off)
-    constexpr int NB = K / 128, RS = XRS(K);
-    const LDSP(uint16_t)* xs = (const LDSP(uint16_t)*)(smem + L_XS);
-    LDSP(float)* tb = (LDSP(float)*)(smem + L_BIAS);
-    for (int i = threadIdx.x; i < NB * 32; i += NTH) {
-        const int m = i & 7, bg = i >> 3; /* bg = block * 4 + group */
-        float sum = 0.f;
-        if (m < M) {
-            const LDSP(uint16_t)* px = xs + m * RS + bg * 32;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const s2p_u32x4 v = *(const LDSP(s2p_u32x4)*)(px + 8 * c);
-                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int d = 0; d < 4; d++) sum += bf2f_lo(vv[d]) + bf2f_hi(vv[d]);
-            }
-        }
-        tb[i] = -136.f * sum;
-    }
-    __syncthreads();
-}
+/* ---- shared (all waves) pieces of a GEMV phase ----
+ * The RMSNorm is split between producer and consumer: the producer of a
+ * residual tile also writes bf16(x * w) with the weight of the norm that
+ * follows, and the per-16-column sums of those values; the consumer stages
+ * the weighted rows as they are, builds the code-bias table from the sums,
+ * and scales its dot products by the row's inverse RMS in the reduction.
+ * (The reference rounds x * inv * w to bf16 before the GEMV, kernels.cu:
+ * 46-80; here x * w is rounded and inv applied to the f32 dot product:
+ * one rounding of the same product, at another point.) */
 
 /* sum of the waves' partials of local tile lt, element (m, n) */
 S2P_DEV float tile_sum(const LDSP(float)* part, int lt, int m, int n, int M) {
@@ -349,8 +305,12 @@ S2P_DEV void reduce_phase(LDSP(unsigned char)* smem, int M, int wg) {
 #pragma clang fp contract(off)
     const LDSP(float)* part = (const LDSP(float)*)(smem + L_PART);
     const LDSP(uint16_t)* xold = (const LDSP(uint16_t)*)(smem + L_XOLD);
+    const LDSP(float)* inv = (const LDSP(float)*)(smem + L_INV);
+    const LDSP(uint16_t)* nwt = (const LDSP(uint16_t)*)(smem + L_NWT);
     LDSP(uint16_t)* outb = (LDSP(uint16_t)*)(smem + L_OUTB);
+    LDSP(uint16_t)* outw = (LDSP(uint16_t)*)(smem + L_OUTW);
     LDSP(float)* ssqo = (LDSP(float)*)(smem + L_SSQO);
+    LDSP(float)* hs = (LDSP(float)*)(smem + L_HS);
     const Geo g0 = geoP<P>(wg, 0);
     const int ncol = g0.np * 16;
     for (int i = threadIdx.x; i < ncol * M; i += NTH) {
@@ -359,19 +319,24 @@ S2P_DEV void reduce_phase(LDSP(unsigned char)* smem, int M, int wg) {
         const int c = k * 16 + n;
         uint16_t o;
         if (P == PG) {
-            o = silu_mul_bf16(f2bf(tile_sum(part, 2 * k, m, n, M)),
-                              f2bf(tile_sum(part, 2 * k + 1, m, n, M)));
+            const float iv = inv[m];
+            o = silu_mul_bf16(f2bf(__fmul_rn(iv, tile_sum(part, 2 * k, m, n, M))),
+                              f2bf(__fmul_rn(iv, tile_sum(part, 2 * k + 1, m, n, M))));
+            const float t = sum_lanes16(bf2f(o)); /* the tile's sum of h: the w2 code-bias term */
+            if (n == 0) hs[m * 8 + k] = -136.f * t;
         } else if (P == PO || P == PD) {
             o = f2bf(__fadd_rn(bf2f(xold[m * 16 + c]), bf2f(f2bf(tile_sum(part, k, m, n, M)))));
+            const float v = bf2f(o);
+            const float t = sum_lanes16(v * v); /* the tile's sum of squares of the new residual */
+            if (n == 0) ssqo[m * 16 + k] = t;
+            const uint16_t xw = f2bf(__fmul_rn(v, bf2f(nwt[c])));
+            outw[m * 96 + c] = xw;
+            const float tw = sum_lanes16(bf2f(xw)); /* and of its weighted values: a code-bias term */
+            if (n == 0) hs[m * 8 + k] = -136.f * tw;
         } else {
-            o = f2bf(tile_sum(part, k, m, n, M));
+            o = f2bf(__fmul_rn(inv[m], tile_sum(part, k, m, n, M)));
         }
         outb[m * 96 + c] = o;
-        if (P == PO || P == PD) { /* the tile's sum of squares of the new residual row */
-            const float v = bf2f(o);
-            const float t = sum_lanes16(v * v);
-            if (n == 0) ssqo[m * 16 + k] = t;
-        }
     }
     __syncthreads();
 }
@@ -516,25 +481,34 @@ S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) 
 }
 
 /* ---- IO wave pieces of a GEMV phase ---- */
-/* stage M rows of K activations (sc1 loads straight to LDS), the layer's
- * norm weights and the rows' inverse RMS (NORM), the residual's old values
- * of this workgroup's tiles (RESID) */
-template <int K, bool NORM, bool RESID>
-S2P_DEV void io_stage(const Mk2Args& A, const uint16_t* src, const uint16_t* nw, int M,
-                      LDSP(unsigned char)* smem, int t0, int np) {
+/* stage M rows of K activations (sc1 loads straight to LDS) and the code-bias
+ * table from the producers' terms gs ([block][8 rows]: per 32 columns, or per
+ * 16 when half, then summed in pairs); NORM: the rows' inverse RMS; RESID:
+ * the residual's old values of this workgroup's tiles and the next norm's
+ * weights of its columns (nwn) */
+template <int K, bool NORM, bool RESID, bool HALF>
+S2P_DEV void io_stage(const Mk2Args& A, const uint16_t* src, const float* gs, const uint16_t* nwn,
+                      int M, LDSP(unsigned char)* smem, int t0, int np) {
     const int lane = threadIdx.x & 63;
-    constexpr int RS = XRS(K);
+    constexpr int RS = XRS(K), NG = K / 32;
     LDSP(uint16_t)* xs = (LDSP(uint16_t)*)(smem + L_XS);
     for (int m = 0; m < M; m++)
 #pragma unroll 4
         for (int c = 0; c < K / 512; c++)
             __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)m * K + c * 512 + lane * 8),
                                              (LDSP(void)*)(xs + m * RS + c * 512), 16, 0, 16);
+    /* the bias terms straight into LDS, 1 KB per load: into the table, or
+     * (HALF) into the partials' space, free until the GEMV */
+    LDSP(float)* tb = (LDSP(float)*)(smem + L_BIAS);
+    LDSP(float)* gsr = HALF ? (LDSP(float)*)(smem + L_PART) : tb;
+    {
+        constexpr int tot = (HALF ? 2 : 1) * NG * 8 * 4;
+#pragma unroll 4
+        for (int c = 0; c * 1024 < tot; c++)
+            __builtin_amdgcn_global_load_lds((const void*)((const char*)gs + min(c * 1024 + lane * 16, tot - 16)),
+                                             (LDSP(void)*)((LDSP(unsigned char)*)gsr + c * 1024), 16, 0, 16);
+    }
     if (NORM) {
-#pragma unroll
-        for (int c = 0; c < 5; c++)
-            __builtin_amdgcn_global_load_lds((const void*)(nw + c * 512 + lane * 8),
-                                             (LDSP(void)*)(smem + L_NW + c * 1024), 16, 0, 0);
         /* inverse RMS from the [M][160] per-16-column sums of squares */
         s2p_u32x4 v[MK2_MAX_ROWS];
 #pragma unroll
@@ -551,29 +525,54 @@ S2P_DEV void io_stage(const Mk2Args& A, const uint16_t* src, const uint16_t* nw,
             if (lane == 0) inv[m] = rsqrt_rule(s / 2560.0f + A.eps);
         }
     }
-    if (RESID) {
-        LDSP(uint16_t)* xold = (LDSP(uint16_t)*)(smem + L_XOLD);
-        for (int i = lane; i < M * 16 * np; i += 64) {
-            const int m = i / (16 * np), c = i - m * 16 * np;
-            xold[m * 16 + c] = coh_ld16(A.x + (size_t)m * 2560 + t0 * 16 + c);
-        }
+    if (RESID && np > 0) {
+        /* (np <= 1 here) 4-byte loads straight to LDS, lane l at + 4 l: the
+         * tile's old residual [M][16] and its next-norm weights [16] */
+        if (lane < 8 * M)
+            __builtin_amdgcn_global_load_lds((const void*)(A.x + (size_t)(lane >> 3) * 2560 + t0 * 16 + 2 * (lane & 7)),
+                                             (LDSP(void)*)(smem + L_XOLD), 4, 0, 16);
+        if (lane < 8)
+            __builtin_amdgcn_global_load_lds((const void*)(nwn + t0 * 16 + 2 * lane), (LDSP(void)*)(smem + L_NWT), 4, 0, 0);
     }
     vm_drain();
+}
+
+/* all waves, after the staging barrier (HALF inputs): table[group][row] =
+ * the sum of the group's two 16-column terms, 4 rows per thread; then a
+ * barrier */
+template <int K>
+S2P_DEV void bias_pairs(LDSP(unsigned char)* smem) {
+    constexpr int NG = K / 32;
+    const LDSP(s2p_f32x4)* r4 = (const LDSP(s2p_f32x4)*)(smem + L_PART);
+    LDSP(s2p_f32x4)* t4 = (LDSP(s2p_f32x4)*)(smem + L_BIAS);
+    for (int j = threadIdx.x; j < NG * 2; j += NTH) {
+        const int g2 = j >> 1, h = j & 1;
+        t4[j] = r4[4 * g2 + h] + r4[4 * g2 + 2 + h];
+    }
+    __syncthreads();
 }
 
 /* write the workgroup's output columns [t0 * 16, (t0 + np) * 16) of M rows
  * (and, for the residual, the tiles' sums of squares), then the flags */
 S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst, int ldd,
-                      int t0, int np, int M, bool resid, int kind, uint32_t val) {
+                      int t0, int np, int M, bool resid, float* gs, int kind, uint32_t val) {
     const int lane = threadIdx.x & 63;
     const LDSP(uint16_t)* outb = (const LDSP(uint16_t)*)(smem + L_OUTB);
+    const LDSP(uint16_t)* outw = (const LDSP(uint16_t)*)(smem + L_OUTW);
     const int nch = np * 2; /* 16-byte chunks per row */
     for (int i = lane; i < M * nch; i += 64) {
         const int m = i / nch, c = i - m * nch;
         coh_st128(dst + (size_t)m * ldd + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outb + m * 96 + c * 8));
+        if (resid)
+            coh_st128(A.xw + (size_t)m * 2560 + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outw + m * 96 + c * 8));
     }
     if (resid && np > 0 && lane < M)
         coh_stf(A.ssq + lane * 160 + t0, ((const LDSP(float)*)(smem + L_SSQO))[lane * 16]);
+    if (gs) /* the tiles' code-bias terms, [tile][row] */
+        for (int i = lane; i < M * np; i += 64) {
+            const int m = i / np, k = i - m * np;
+            coh_stf(gs + (t0 + k) * 8 + m, ((const LDSP(float)*)(smem + L_HS))[m * 8 + k]);
+        }
     flags_set(A, kind, t0, np, val);
 }
 
@@ -947,6 +946,14 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             ob.z = (uint32_t)f2bf(sv[4]) | ((uint32_t)f2bf(sv[5]) << 16);
             ob.w = (uint32_t)f2bf(sv[6]) | ((uint32_t)f2bf(sv[7]) << 16);
             coh_st128(A.attn + (size_t)(g.row0 + (qv >> 2)) * 4096 + (4 * kvh + (qv & 3)) * 128 + d, ob);
+            /* the sum of each 32 columns (4 lanes) of the stored values: the
+             * wo code bias */
+            float t = ((bf2f_lo(ob.x) + bf2f_hi(ob.x)) + (bf2f_lo(ob.y) + bf2f_hi(ob.y))) +
+                      ((bf2f_lo(ob.z) + bf2f_hi(ob.z)) + (bf2f_lo(ob.w) + bf2f_hi(ob.w)));
+            t += __shfl_xor(t, 1, 64);
+            t += __shfl_xor(t, 2, 64);
+            if ((idx & 3) == 0) /* [32-column block][row] */
+                coh_stf(A.gsa + ((4 * kvh + (qv & 3)) * 4 + (idx & 15) / 4) * 8 + g.row0 + (qv >> 2), -136.f * t);
         }
         flags_set(A, MK2_F_ATT, (seg * 8 + kvh) * ns + sp, 1, flag_val(epoch, l, MK2_F_ATT));
         TRACE(l, 24);
@@ -1017,6 +1024,7 @@ S2P_DEV void c_head(Slot (&S)[NSLOT], const Mk2Args& A, int cw, const Ctx& C,
  * wave order */
 S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* smem, int M) {
     const LDSP(float)* part = (const LDSP(float)*)(smem + L_HPART);
+    const LDSP(float)* inv = (const LDSP(float)*)(smem + L_INV);
     const int nout = C.head_nt * 16 * M;
     const int U = C.head_nt * 20;
     for (int i = threadIdx.x; i < nout; i += NTH) {
@@ -1029,7 +1037,7 @@ S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* sm
             const int u0 = w * U / CW, u1 = (w + 1) * U / CW;
             if (u0 < (lt + 1) * 20 && u1 > lt * 20) s += part[((lt * CW + w) * M + m) * 16 + n];
         }
-        if (row < A.head_n) A.logits[(size_t)m * A.head_n + row] = f2bf(s);
+        if (row < A.head_n) A.logits[(size_t)m * A.head_n + row] = f2bf(__fmul_rn(inv[m], s));
     }
 }
 
@@ -1070,8 +1078,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
         for (int l = 0; l < NL; l++) {
             /* Q */
             __syncthreads();
-            norm_rows<2560>(smem, M);
-            bias_rows<2560>(smem, M);
+            bias_pairs<2560>(smem);
             c_gemv<PQ>(S, A, l, cw, C, smem, M);
             if (cw == 0) TRACE(l, 13);
             __syncthreads();
@@ -1080,22 +1087,20 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             attn_phase<false>(A, l, epoch, smem);
             /* O */
             __syncthreads();
-            bias_rows<4096>(smem, M);
             c_gemv<PO>(S, A, l, cw, C, smem, M);
             if (cw == 0) TRACE(l, 14);
             __syncthreads();
             reduce_phase<PO>(smem, M, wg);
             /* G */
             __syncthreads();
-            norm_rows<2560>(smem, M);
-            bias_rows<2560>(smem, M);
+            bias_pairs<2560>(smem);
             c_gemv<PG>(S, A, l, cw, C, smem, M);
             if (cw == 0) TRACE(l, 15);
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
             /* D */
             __syncthreads();
-            bias_rows<9728>(smem, M);
+            bias_pairs<9728>(smem);
             c_gemv<PD>(S, A, l, cw, C, smem, M);
             if (cw == 0) TRACE(l, 16);
             __syncthreads();
@@ -1103,8 +1108,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
         }
         /* head */
         __syncthreads();
-        norm_rows<2560>(smem, M);
-        bias_rows<2560>(smem, M);
+        bias_pairs<2560>(smem);
         c_head(S, A, cw, C, smem, M);
         if (cw == 0) TRACE(NL, 2);
         __syncthreads();
@@ -1115,9 +1119,11 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
         /* ================= IO wave ================= */
         asm volatile("; IOPATH_BEGIN");
         /* residual stream init: x = x_in for this workgroup's 16-column
-         * tile (the w2 geometry) and its sums of squares */
+         * tile (the w2 geometry), its sums of squares, its values weighted by
+         * the first norm and their sums */
         const Geo gd = geoP<PD>(wg, 0);
         {
+            const uint16_t* nw0 = NL > 0 ? A.norms + MK2_NORM_ATTN : A.final_norm;
             for (int i = lane; i < M * 16 * gd.np; i += 64) {
                 const int m = i / 16, cc = i & 15;
                 const size_t ix = (size_t)m * 2560 + gd.t0 * 16 + cc;
@@ -1126,6 +1132,10 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                 const float f = bf2f(v);
                 const float t = sum_lanes16(f * f);
                 if (cc == 0) coh_stf(A.ssq + m * 160 + gd.t0, t);
+                const uint16_t xw = f2bf(__fmul_rn(f, bf2f(nw0[gd.t0 * 16 + cc])));
+                coh_st16(A.xw + ix, xw);
+                const float tw = sum_lanes16(bf2f(xw));
+                if (cc == 0) coh_stf(A.gsx + gd.t0 * 8 + m, -136.f * tw);
             }
             flags_set(A, MK2_F_INIT, gd.t0, gd.np, flag_val(epoch, -1, MK2_F_INIT));
         }
@@ -1137,14 +1147,14 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             if (l == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
             else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, l - 1, MK2_F_D));
             TRACE(l, 0);
-            io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_ATTN, M, smem, gq.t0, gq.np);
+            io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, gq.t0, gq.np);
             TRACE(l, 1);
             __syncthreads();
-            norm_rows<2560>(smem, M);
-            bias_rows<2560>(smem, M);
+            bias_pairs<2560>(smem);
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
-            io_store(A, smem, A.qkv, 6144, gq.t0, gq.np, M, false, MK2_F_Q, flag_val(epoch, l, MK2_F_Q));
+            io_store(A, smem, A.qkv, 6144, gq.t0, gq.np, M, false, nullptr, MK2_F_Q,
+                     flag_val(epoch, l, MK2_F_Q));
             TRACE(l, 2);
             /* attention */
             attn_phase<true>(A, l, epoch, smem);
@@ -1152,47 +1162,49 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             /* O: attn -> x += wo attn */
             flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8 * A.nsplit, flag_val(epoch, l, MK2_F_ATT));
             TRACE(l, 4);
-            io_stage<4096, false, true>(A, A.attn, nullptr, M, smem, go.t0, go.np);
+            io_stage<4096, false, true, false>(A, A.attn, A.gsa, nl + MK2_NORM_FFN, M, smem, go.t0, go.np);
             TRACE(l, 5);
             __syncthreads();
-            bias_rows<4096>(smem, M);
             __syncthreads();
             reduce_phase<PO>(smem, M, wg);
-            io_store(A, smem, A.x, 2560, go.t0, go.np, M, true, MK2_F_O, flag_val(epoch, l, MK2_F_O));
+            io_store(A, smem, A.x, 2560, go.t0, go.np, M, true, A.gsx, MK2_F_O,
+                     flag_val(epoch, l, MK2_F_O));
             TRACE(l, 6);
             /* G: x -> h */
             flags_wait(A, MK2_F_O, 0, 160, flag_val(epoch, l, MK2_F_O));
             TRACE(l, 7);
-            io_stage<2560, true, false>(A, A.x, nl + MK2_NORM_FFN, M, smem, gg.t0, gg.np);
+            io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, gg.t0, gg.np);
             TRACE(l, 8);
             __syncthreads();
-            norm_rows<2560>(smem, M);
-            bias_rows<2560>(smem, M);
+            bias_pairs<2560>(smem);
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
-            io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, MK2_F_G, flag_val(epoch, l, MK2_F_G));
+            io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, A.gsh, MK2_F_G,
+                     flag_val(epoch, l, MK2_F_G));
             TRACE(l, 9);
             /* D: h -> x += w2 h */
             flags_wait(A, MK2_F_G, 0, 608, flag_val(epoch, l, MK2_F_G));
             TRACE(l, 10);
-            io_stage<9728, false, true>(A, A.h, nullptr, M, smem, gd.t0, gd.np);
+            io_stage<9728, false, true, true>(A, A.h, A.gsh,
+                                        l + 1 < NL ? nl + MK2_NORM_STRIDE + MK2_NORM_ATTN : A.final_norm, M,
+                                        smem, gd.t0, gd.np);
             TRACE(l, 11);
             __syncthreads();
-            bias_rows<9728>(smem, M);
+            bias_pairs<9728>(smem);
             __syncthreads();
             reduce_phase<PD>(smem, M, wg);
-            io_store(A, smem, A.x, 2560, gd.t0, gd.np, M, true, MK2_F_D, flag_val(epoch, l, MK2_F_D));
+            io_store(A, smem, A.x, 2560, gd.t0, gd.np, M, true, A.gsx, MK2_F_D,
+                     flag_val(epoch, l, MK2_F_D));
             TRACE(l, 12);
         }
         /* head: final RMSNorm of x */
         if (NL == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
         else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, NL - 1, MK2_F_D));
         TRACE(NL, 0);
-        io_stage<2560, true, false>(A, A.x, A.final_norm, M, smem, 0, 0);
+        io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, 0, 0);
         TRACE(NL, 1);
         __syncthreads();
-        norm_rows<2560>(smem, M);
-        bias_rows<2560>(smem, M);
+        bias_pairs<2560>(smem);
         __syncthreads();
         {
             const Geo gh = geo_of(A.head_tiles, 20, false, wg, 0);

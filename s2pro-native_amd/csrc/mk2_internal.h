@@ -56,6 +56,17 @@ extern "C" {
 #define MK2_ERR_WORD (MK2_STATE_WORD + 2)
 #define MK2_CTR_WORD (MK2_STATE_WORD + 4)
 #define MK2_STATE_WORDS (MK2_CTR_WORD + MK2_MAX_LAYERS * 64)
+/* after the state block (256-aligned): the norm-weighted residual rows
+ * [MK2_MAX_ROWS][2560] bf16 and the code-bias terms of the GEMV inputs,
+ * -136 x (sum of a row's values), f32, [column block][8 rows] (rows >= the
+ * plan's rows stay 0): weighted residual [160][8] and h [608][8] per 16
+ * columns, attention output [128][8] per 32 columns.  Zeroed at every plan. */
+#define MK2_AUX_OFF (((MK2_STATE_WORDS * 4 + 255) / 256) * 256)
+#define MK2_AUX_XW 0
+#define MK2_AUX_GSX (MK2_AUX_XW + MK2_MAX_ROWS * 2560 * 2)
+#define MK2_AUX_GSH (MK2_AUX_GSX + 160 * 8 * 4)
+#define MK2_AUX_GSA (MK2_AUX_GSH + 608 * 8 * 4)
+#define MK2_AUX_BYTES (MK2_AUX_GSA + 128 * 8 * 4)
 
 typedef struct {
     const uint8_t* wpack;          /* [n_layers][MK2_LAYER_BLKS] packed blocks */
@@ -72,6 +83,10 @@ typedef struct {
     uint16_t* h;                   /* [rows][9728] */
     uint16_t* logits;              /* [rows][head_n] */
     float* ssq;                    /* [MK2_MAX_ROWS][160] per-16-column sums of squares of x */
+    uint16_t* xw;                  /* [rows][2560] bf16(x * the next RMSNorm's weight) */
+    float* gsx;                    /* [160][8] code-bias terms of xw per 16 columns */
+    float* gsh;                    /* [608][8] of h per 16 columns */
+    float* gsa;                    /* [128][8] of attn per 32 columns */
     uint32_t* flags;               /* [MK2_F_KINDS][MK2_F_STRIDE] */
     uint32_t* state;               /* [0] launch epoch, [1] workgroups done (monotonic) */
     int* err;                      /* sticky: a wait timed out */

@@ -349,11 +349,34 @@ def test_verify_stages_one_layer(lib, quant, L):
         exact = po.attention_f64(g_q, np.ascontiguousarray(g_kv[0, :8]),
                                  np.ascontiguousarray(g_kv[0, 8:]), R, 32, 8, 128, L, ctx)
         assert np.max(np.abs(bf16_vals(g_attn) - exact)) < 2e-2, "attention"
-        # (d) wo + residual, ffn norm + gate_up with the fused SwiGLU epilogue
+        # (d) wo + residual, ffn norm + gate_up with the fused SwiGLU epilogue.
+        # The persistent kernel (INT4 plans) rounds x * w to bf16 and applies
+        # the inverse RMS to the f32 dot product, where the reference rounds
+        # x * inv * w: per row within 1e-2 of the oracle (L2, max norm 2e-2)
+        # and, against binary64 on the same weights and attention output, no
+        # less accurate than the oracle's order (rms error <= 1.25x)
         x_mid = po.add(x_in, po.linear_fwd(lw.wo, g_attn, R))
         xn2 = po.rms_norm(x_mid, norms[1], R, 2560)
         h_ref = po.silu_mul(po.linear_fwd(lw.gate_up, xn2, R), R, 9728)
-        assert_close_rel(bf16_vals(g_h), bf16_vals(h_ref), what="gate_up + SwiGLU")
+        if quant == s2pamd.WQ_INT8:
+            assert_close_rel(bf16_vals(g_h), bf16_vals(h_ref), what="gate_up + SwiGLU")
+        else:
+            L0 = lib.s2p_backbone_layer(bb, 0).contents
+            Wd = {}
+            for name in ("wo", "gate_up"):
+                lin = getattr(L0, name)
+                _, (w, sc) = host_linear(lin)
+                Wd[name] = f64.dequant(w, sc, lin.out_features, lin.in_features)
+            xm64 = f64.bf(x_in) + f64.bf(g_attn) @ Wd["wo"].T
+            gu64 = f64.rms(xm64, f64.bf(norms[1])) @ Wd["gate_up"].T
+            g64, u64 = gu64[:, :9728], gu64[:, 9728:]
+            h64 = g64 / (1 + np.exp(-g64)) * u64
+            got, want = bf16_vals(g_h).astype(np.float64), bf16_vals(h_ref).astype(np.float64)
+            assert_close_norm(got, want, rel=1e-2, what="gate_up + SwiGLU")
+            e_gpu = np.sqrt(np.mean((got - h64) ** 2))
+            e_ref = np.sqrt(np.mean((want - h64) ** 2))
+            print(f"gate_up + SwiGLU rms err vs binary64: gpu {e_gpu:.4g} oracle {e_ref:.4g}")
+            assert e_gpu <= 1.25 * e_ref, (e_gpu, e_ref)
         # (e) w2 + residual on the GPU's SwiGLU output
         x_out = po.add(x_mid, po.linear_fwd(lw.w2, g_h, R))
         assert_close_rel(bf16_vals(g_x), bf16_vals(x_out), what="layer output")
