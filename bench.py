@@ -9,10 +9,12 @@ weights, synthetic inputs resident in HBM before the timed region.  A step is
 one replay of the captured hipGraph (forward + acceptance).
 
 Prints one JSON line (see README of the driver contract): value = verify
-steps/s, plus `roofline` for the dominant kernel (the INT4 GEMV engine) timed
-with HIP events on its own stream, and `cpu_baseline` (the scalar C oracle on
-one host core over a bounded sample: one backbone layer + the head GEMV,
-extrapolated to 36 layers).
+steps/s, plus `roofline` for the dominant kernel timed with HIP events on its
+own stream (the persistent verify kernel k_mk2, the whole forward in one
+launch, when the plan runs on it; otherwise the INT4 GEMV engine's 145 weight
+GEMVs of a step), and `cpu_baseline` (the scalar C oracle on one host core
+over a bounded sample: one backbone layer + 1/8 of the head GEMV,
+extrapolated to 36 layers and the full head).
 
 `--workload config4|config5` runs the batch (8 sessions x K=4, M = 40) and tree
 (4 sessions x 16-node tree, M = 68, KV 8192) configurations the same way; their
