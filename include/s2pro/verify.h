@@ -132,6 +132,37 @@ s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const 
                              int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
                              int32_t* out_n_emit, void* work, hipStream_t st);
 
+/* The chain condition of speculative frames (reference docs/SPECULATIVE.md:
+ * 26-41: a drafted frame survives only if its semantic token is accepted AND
+ * the nine greedy residual codes the fast-AR gives on the true hidden equal
+ * the codes the draft built the next input from).  For every drafted node
+ * (row s*R + i, i >= 1) of the current plan: the greedy fast-AR frame on the
+ * final-normed hidden of its parent's row from the last forward (the
+ * backbone's final RMSNorm of its residual rows) with the node's semantic
+ * code (tok - 151678; 0 for EOS); parent [R] and tok [n_sess*R] as for
+ * s2p_verify_accept (device).  chain_ok [n_sess*R] (device): 1 for
+ * roots, EOS nodes, and nodes whose codes equal draft_codes [n_sess*R][9]
+ * (device); codes_out [n_sess*R][9] (device): the fast-AR codes of every
+ * drafted node (the emitted frame's codes), zeros for roots.  Needs
+ * n_sess*(R-1) <= the decoder's max_b.  Asynchronous, capturable. */
+typedef struct s2pfa s2pfa;
+s2p_status s2p_verify_chain(s2p_backbone* b, s2pfa* fa, const int32_t* parent, const int64_t* tok,
+                            const int32_t* draft_codes, uint8_t* chain_ok, int32_t* codes_out,
+                            hipStream_t st);
+
+/* s2p_verify_accept under the chain condition: chain_ok as written by
+ * s2p_verify_chain (NULL: every node passes).  An accepted node whose frame
+ * failed ends the walk: its token is the last emitted id, the node is not in
+ * out_path (its forward row had the wrong input, so its K/V is not
+ * committed) and no bonus token is drawn. */
+s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
+                                   const void* drf_logits, const void* drf_eos,
+                                   int64_t row_stride, const int32_t* parent, const int64_t* tok,
+                                   s2ps_dev_state* const* states, int n_sess, int rows,
+                                   const uint8_t* chain_ok, int32_t* out_path, int32_t* out_n_acc,
+                                   int64_t* out_emit, int32_t* out_n_emit, void* work,
+                                   hipStream_t st);
+
 /* Move the K/V of accepted tree nodes from slot L + node to L + depth for
  * every layer (no-op for chains).  Uses the current plan. */
 s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,

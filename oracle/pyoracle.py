@@ -71,7 +71,7 @@ _SIGS = {
     "or_gumbel_draw": (I, [P, P]),
     "or_xoshiro_draw": (I, [P, P]),
     "or_rule_u24": (ctypes.c_uint32, [P, ctypes.c_uint32]),
-    "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P]),
+    "or_accept_tree": (None, [P, P, P, P, P, I64, P, P, I, P, P, P, P, P]),
     "or_linear_fwd": (None, [P, P, P, I]),
     "or_layer": (None, [P, P, I, P, P, I, I, P, P]),
     "or_layer8": (None, [P, P, I, P, P, P, P, I, I, P, P, I, I]),
@@ -314,7 +314,7 @@ def state_push(st, tok):
     lib().or_state_push(ptr(st), int(tok))
 
 
-def accept_tree(st, tgt, drf, parent, tok, tgt_eos=None, drf_eos=None):
+def accept_tree(st, tgt, drf, parent, tok, tgt_eos=None, drf_eos=None, chain=None):
     """tgt/drf: [R, stride] uint16; parent/tok: [R]; returns (path, emitted)."""
     tgt = np.ascontiguousarray(tgt, np.uint16)
     drf = np.ascontiguousarray(drf, np.uint16)
@@ -328,9 +328,10 @@ def accept_tree(st, tgt, drf, parent, tok, tgt_eos=None, drf_eos=None):
     nemit = ctypes.c_int()
     te = None if tgt_eos is None else np.ascontiguousarray(tgt_eos, np.uint16)
     de = None if drf_eos is None else np.ascontiguousarray(drf_eos, np.uint16)
+    ch = None if chain is None else np.ascontiguousarray(chain, np.uint8)
     lib().or_accept_tree(ptr(st), ptr(tgt), ptr(te), ptr(drf), ptr(de), tgt.shape[1],
                          ptr(par), ptr(tk), R, ptr(path), ctypes.addressof(nacc),
-                         ptr(emitted), ctypes.addressof(nemit))
+                         ptr(emitted), ctypes.addressof(nemit), ptr(ch))
     return path[: nacc.value].copy(), emitted[: nemit.value].copy()
 
 

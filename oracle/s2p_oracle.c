@@ -1088,7 +1088,7 @@ void or_accept_tree(or_state* st, const uint16_t* tgt, const uint16_t* tgt_eos,
                     const uint16_t* drf, const uint16_t* drf_eos,
                     int64_t row_stride, const int32_t* parent,
                     const int64_t* tok, int R, int32_t* path, int* n_acc,
-                    int64_t* emitted, int* n_emit) {
+                    int64_t* emitted, int* n_emit, const uint8_t* chain) {
     int v = 0;
     *n_acc = 0;
     *n_emit = 0;
@@ -1128,6 +1128,16 @@ void or_accept_tree(or_state* st, const uint16_t* tgt, const uint16_t* tgt_eos,
                     for (int k = 0; k < TOP_K; k++) p[k] = rsd[k] / z;
                 j++;
             }
+        }
+        if (accepted >= 0 && chain && !chain[accepted]) {
+            /* the chain condition (docs/SPECULATIVE.md:26-41): the drafted
+             * frame's residual codes differ from the fast-AR's on the true
+             * hidden, so the node's own forward row is void: its token is
+             * emitted (a valid sample of the target at that position), its
+             * row is not committed and the walk ends without a bonus draw */
+            emitted[(*n_emit)++] = tok[accepted];
+            if (tok[accepted] != TOK_EOS) or_state_push(st, tok[accepted]);
+            return;
         }
         if (accepted >= 0) {
             path[(*n_acc)++] = accepted;

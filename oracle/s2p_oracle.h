@@ -177,7 +177,7 @@ void or_accept_tree(or_state* st, const uint16_t* tgt, const uint16_t* tgt_eos,
                     const uint16_t* drf, const uint16_t* drf_eos,
                     int64_t row_stride, const int32_t* parent,
                     const int64_t* tok, int R, int32_t* path, int* n_acc,
-                    int64_t* emitted, int* n_emit);
+                    int64_t* emitted, int* n_emit, const uint8_t* chain);
 
 /* ---- the verify forward (src/slowar/slowar.c:156-260, 503-565) --------- */
 typedef struct {

@@ -21,6 +21,7 @@
 #include <string.h>
 
 #include "s2pro/verify.h"
+#include "s2pro/fastar.h"
 #include "../gemv_internal.h"
 #include "../mk2_internal.h"
 #include "../prims_internal.h"
@@ -68,6 +69,9 @@ struct s2p_backbone {
     uint8_t* d_hpack;      /* tile-packed head */
     uint16_t* d_norms;     /* [n_layers][MK2_NORM_STRIDE] norm weights */
     uint32_t* d_mk2;       /* flags, launch state, error flag, attention counters */
+    void* d_chain_hidden;  /* [max_rows][2560] bf16: final-normed hidden (chain condition) */
+    void* d_chain_par;     /* [max_rows][2560] bf16: the drafted nodes' parent rows */
+    int32_t* d_chain_sem;  /* [max_rows] their semantic codes */
     Mk2Args mk2;           /* launch arguments of the current plan */
     int mk2_enabled;       /* off: layer-by-layer launches (env S2P_VERIFY_MK2=0) */
     int mk2_ready;         /* the current plan runs on the persistent kernel */
@@ -177,6 +181,9 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
                      (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_rope, R * 64 * 2 * sizeof(float));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_AUX_OFF + MK2_AUX_BYTES);
+    if (rc == S2P_OK) rc = dalloc(&b->d_chain_hidden, R * S2P_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc(&b->d_chain_par, R * S2P_DIM * 2);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_chain_sem, R * sizeof(int32_t));
     if (rc == S2P_OK) /* flags, epoch and counters start at zero once; the kernel keeps them */
         rc = hip_ok(hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st), "mk2 init");
     if (rc == S2P_OK) {
@@ -219,7 +226,8 @@ void s2p_backbone_free(s2p_backbone* b) {
     void* bufs[] = {b->x,        b->qkv,       b->q,           b->attn,          b->gu,
                     b->ssq,      b->attn_part, b->d_pos,       b->d_slot,        b->d_sess,
                     b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_rope,
-                    (void*)b->d_wpack, (void*)b->d_hpack, (void*)b->d_norms, (void*)b->d_mk2};
+                    (void*)b->d_wpack, (void*)b->d_hpack, (void*)b->d_norms, (void*)b->d_mk2,
+                    b->d_chain_hidden, b->d_chain_par, (void*)b->d_chain_sem};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
     if (b->h_stage) (void)hipHostFree(b->h_stage);
@@ -581,10 +589,12 @@ static s2p_status accept_run(const void* tgt, const void* tgt_eos, int64_t tgt_e
                              int64_t drf_eos_stride, int64_t drf_stride, const int32_t* parent,
                              const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
                              int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
-                             int32_t* out_n_emit, void* work, hipStream_t st) {
+                             int32_t* out_n_emit, void* work, const uint8_t* chain_ok,
+                             hipStream_t st) {
     if (tgt_stride != drf_stride) return S2P_ERR_INVALID;
     AcceptArgs a;
     memset(&a, 0, sizeof(a));
+    a.chain_ok = chain_ok;
     a.tgt = (const uint16_t*)tgt;
     a.tgt_eos = (const uint16_t*)tgt_eos;
     a.drf = (const uint16_t*)drf;
@@ -618,7 +628,45 @@ s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const 
     if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
     return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
                       parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
-                      work, st);
+                      work, NULL, st);
+}
+
+s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
+                                   const void* drf_logits, const void* drf_eos,
+                                   int64_t row_stride, const int32_t* parent, const int64_t* tok,
+                                   s2ps_dev_state* const* states, int n_sess, int rows,
+                                   const uint8_t* chain_ok, int32_t* out_path, int32_t* out_n_acc,
+                                   int64_t* out_emit, int32_t* out_n_emit, void* work,
+                                   hipStream_t st) {
+    if (!tgt_logits || !drf_logits || !parent || !tok || !states || !out_path || !out_n_acc ||
+        !out_emit || !out_n_emit || !work || n_sess <= 0 || rows <= 0 ||
+        rows > S2P_VERIFY_MAX_ROWS || (!tgt_eos) != (!drf_eos))
+        return S2P_ERR_INVALID;
+    if (!tgt_eos && row_stride < 155774) return S2P_ERR_INVALID;
+    if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
+    return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
+                      parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
+                      work, chain_ok, st);
+}
+
+s2p_status s2p_verify_chain(s2p_backbone* b, s2pfa* fa, const int32_t* parent, const int64_t* tok,
+                            const int32_t* draft_codes, uint8_t* chain_ok, int32_t* codes_out,
+                            hipStream_t st) {
+    if (!b || !fa || !parent || !tok || !draft_codes || !chain_ok || !codes_out) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    const int n = b->n_sess, R = b->R;
+    if (R < 2) return S2P_ERR_INVALID; /* no drafted node */
+    const int rows = n * R, B = n * (R - 1);
+    S2P_TRY(hip_ok(s2pk_rms_norm((const s2p_bf16*)b->x, (const s2p_bf16*)b->final_norm.data,
+                                 (s2p_bf16*)b->d_chain_hidden, rows, S2P_DIM, NORM_EPS, st),
+                   "chain final norm"));
+    S2P_TRY(hip_ok(s2p_chain_prep_launch(parent, tok, b->d_chain_hidden, b->d_chain_par,
+                                         b->d_chain_sem, n, R, S2P_DIM, st),
+                   "chain prep"));
+    const int32_t* stage = NULL;
+    S2P_TRY(s2pfa_decode_frame_batch_dev(fa, b->d_chain_par, b->d_chain_sem, B, &stage, st));
+    return hip_ok(s2p_chain_check_launch(stage, draft_codes, tok, chain_ok, codes_out, n, R, st),
+                  "chain check");
 }
 
 s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,
@@ -645,7 +693,7 @@ static s2p_status step_enqueue(s2p_backbone* b, const s2p_verify_step_io* io, hi
     return accept_run(lg, sliced ? lg + 4096 : NULL, ts, ts, dg, sliced ? dg + 4096 : NULL, ts,
                       io->drf_stride, io->parent_dev, io->tok_dev,
                       io->states_dev, b->n_sess, b->R, io->out_path, io->out_n_acc,
-                      io->out_emit, io->out_n_emit, io->work, st);
+                      io->out_emit, io->out_n_emit, io->work, NULL, st);
 }
 
 s2p_status s2p_verify_step(s2p_backbone* b, const s2p_verify_step_io* io, int use_graph,

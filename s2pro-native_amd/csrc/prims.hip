@@ -609,3 +609,68 @@ extern "C" hipError_t s2p_test_f2bf(const float* in, uint16_t* out, int64_t n, h
     hipLaunchKernelGGL(k_f2bf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, in, out, n);
     return hipGetLastError();
 }
+
+/* ---- the chain condition of speculative frames ----
+ * prep: for every drafted node (session s, node i >= 1; b = s (R - 1) + i - 1)
+ * the final-normed hidden of its parent's row and the node's semantic code
+ * (vocab id - the semantic base, 0 for EOS and anything outside the 4,096
+ * codes), the fast-AR's inputs; one block per node */
+__global__ __launch_bounds__(64) void k_chain_prep(const int32_t* __restrict__ parent,
+                                                   const int64_t* __restrict__ tok,
+                                                   const uint16_t* __restrict__ hidden,
+                                                   uint16_t* __restrict__ par_hidden,
+                                                   int32_t* __restrict__ sem, int R, int dim) {
+    const int b = blockIdx.x, s = b / (R - 1), i = b - s * (R - 1) + 1;
+    const int src = s * R + parent[i];
+    for (int c = threadIdx.x * 8; c < dim; c += 64 * 8)
+        *(s2p_u32x4*)(par_hidden + (size_t)b * dim + c) = *(const s2p_u32x4*)(hidden + (size_t)src * dim + c);
+    if (threadIdx.x == 0) {
+        const int64_t t = tok[(size_t)s * R + i] - S2P_TOK_SEMANTIC_START;
+        sem[b] = (t >= 0 && t < 4096) ? (int32_t)t : 0;
+    }
+}
+
+/* check: chain_ok[row] = 1 for roots and EOS nodes, else whether the node's
+ * nine fast-AR codes (stage [9][B]) equal the drafted ones; the codes to
+ * codes_out [row][9] (zeros for roots) */
+__global__ __launch_bounds__(64) void k_chain_check(const int32_t* __restrict__ stage,
+                                                    const int32_t* __restrict__ draft_codes,
+                                                    const int64_t* __restrict__ tok,
+                                                    uint8_t* __restrict__ chain_ok,
+                                                    int32_t* __restrict__ codes_out, int n_sess,
+                                                    int R) {
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    if (row >= n_sess * R) return;
+    const int s = row / R, i = row - s * R, B = n_sess * (R - 1);
+    if (i == 0) {
+        chain_ok[row] = 1;
+        for (int c = 0; c < 9; c++) codes_out[(size_t)row * 9 + c] = 0;
+        return;
+    }
+    const int b = s * (R - 1) + i - 1;
+    bool same = true;
+    for (int c = 0; c < 9; c++) {
+        const int32_t v = stage[(size_t)c * B + b];
+        codes_out[(size_t)row * 9 + c] = v;
+        same = same && v == draft_codes[(size_t)row * 9 + c];
+    }
+    chain_ok[row] = (same || tok[row] == S2P_TOK_EOS) ? 1 : 0;
+}
+
+extern "C" hipError_t s2p_chain_prep_launch(const int32_t* parent, const int64_t* tok, const void* hidden,
+                                            void* par_hidden, int32_t* sem, int n_sess, int R, int dim,
+                                            hipStream_t st) {
+    if (n_sess < 1 || R < 2 || dim % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_chain_prep, dim3((unsigned)(n_sess * (R - 1))), dim3(64), 0, st, parent, tok,
+                       (const uint16_t*)hidden, (uint16_t*)par_hidden, sem, R, dim);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2p_chain_check_launch(const int32_t* stage, const int32_t* draft_codes,
+                                             const int64_t* tok, uint8_t* chain_ok, int32_t* codes_out,
+                                             int n_sess, int R, hipStream_t st) {
+    if (n_sess < 1 || R < 2) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_chain_check, dim3((unsigned)((n_sess * R + 63) / 64)), dim3(64), 0, st, stage,
+                       draft_codes, tok, chain_ok, codes_out, n_sess, R);
+    return hipGetLastError();
+}

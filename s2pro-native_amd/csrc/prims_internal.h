@@ -96,6 +96,16 @@ hipError_t s2p_kv_commit8_launch(const S2pRowPlan* plan, const int32_t* path,
                                  const int32_t* n_acc, int n_sess, int R, int n_layers, int bw,
                                  hipStream_t st);
 
+/* the chain condition of speculative frames (verify.c s2p_verify_chain):
+ * gather each drafted node's parent hidden row and semantic code; compare
+ * the fast-AR codes (stage [9][n_sess (R - 1)]) with the drafted ones */
+hipError_t s2p_chain_prep_launch(const int32_t* parent, const int64_t* tok, const void* hidden,
+                                 void* par_hidden, int32_t* sem, int n_sess, int R, int dim,
+                                 hipStream_t st);
+hipError_t s2p_chain_check_launch(const int32_t* stage, const int32_t* draft_codes,
+                                  const int64_t* tok, uint8_t* chain_ok, int32_t* codes_out,
+                                  int n_sess, int R, hipStream_t st);
+
 #ifdef __cplusplus
 }
 #endif

@@ -595,6 +595,17 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
             __syncthreads();
             j++;
         }
+        if (accepted >= 0 && a.chain_ok && !a.chain_ok[(size_t)s * R + accepted]) {
+            /* the drafted frame failed the chain condition: its token is
+             * emitted, its row is not accepted, no bonus draw */
+            if (lane == 0) {
+                emit[n_emit] = tok[accepted];
+                if (tok[accepted] != TOK_EOS) state_push(&st, tok[accepted]);
+            }
+            n_emit++;
+            __syncthreads();
+            break;
+        }
         if (accepted >= 0) {
             if (lane == 0) {
                 path[n_acc] = accepted;

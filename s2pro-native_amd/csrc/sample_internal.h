@@ -29,6 +29,9 @@ typedef struct {
     int64_t*        out_emit;  /* [n_sess*(R+1)] emitted vocab ids */
     int32_t*        out_n_emit;/* [n_sess] */
     void*           work;      /* s2p_accept_work_bytes(n_sess, R) */
+    const uint8_t*  chain_ok;  /* NULL, or [n_sess*R]: 0 = the node's drafted frame failed
+                                  the chain condition (its token ends the walk, its row is
+                                  not accepted) */
 } AcceptArgs;
 
 size_t     s2p_accept_work_bytes(int n_sess, int rows);

@@ -187,6 +187,8 @@ SIGS = {
     "s2p_verify_accept_work_bytes": (SZ, [I, I]),
     "s2p_verify_accept": (I, [P, P, P, P, I64, P, P, P, I, I, P, P, P, P, P, P]),
     "s2p_verify_kv_commit": (I, [P, P, P, P]),
+    "s2p_verify_chain": (I, [P, P, P, P, P, P, P, P]),
+    "s2p_verify_accept_chain": (I, [P, P, P, P, I64, P, P, P, I, I, P, P, P, P, P, P, P]),
     "s2p_verify_step": (I, [P, P, I, P]),
 }
 

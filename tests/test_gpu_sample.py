@@ -191,3 +191,46 @@ def test_accept_tree_bit_exact(lib):
         assert list(path[s, :nacc[s]]) == list(p_ref), s
         assert list(emit[s, :nemit[s]]) == list(e_ref), s
         assert bytes(new_states[s]) == bytes(st), s
+
+
+def test_accept_chain_condition_bit_exact(lib):
+    """s2p_verify_accept_chain against the host rule with the chain
+    condition: random failing nodes on the config-1 chain and the 16-node
+    tree; path, emitted ids and state bytes equal the oracle's."""
+    r = np.random.default_rng(41)
+    for parent in ([-1, 0, 1, 2, 3], TREE16):
+        R = len(parent)
+        n_sess = 12
+        tgt, drf, te, de = chain_inputs(r, R - 1, n_sess, "config1")
+        states = [po.state(temperature=0.8, top_p=0.8, seed=0 if s % 3 == 0 else 200 + s, entropy=s)
+                  for s in range(n_sess)]
+        tok = draft_tokens(states, drf, de, parent, R)
+        chain = (r.random(n_sess * R) > 0.3).astype(np.uint8)
+        chain[::R] = 1
+        d_states, d_ptrs = states_to_dev(states)
+        work = torch.empty(lib.s2p_verify_accept_work_bytes(n_sess, R), dtype=torch.uint8,
+                           device="cuda")
+        path = torch.full((n_sess * R,), -1, dtype=torch.int32, device="cuda")
+        nacc = torch.zeros(n_sess, dtype=torch.int32, device="cuda")
+        emit = torch.zeros(n_sess * (R + 1), dtype=torch.int64, device="cuda")
+        nemit = torch.zeros(n_sess, dtype=torch.int32, device="cuda")
+        s2pamd.check(lib.s2p_verify_accept_chain(
+            P(to_dev(tgt)), P(to_dev(te)), P(to_dev(drf)), P(to_dev(de)), 4096,
+            P(to_dev(np.asarray(parent, np.int32))), P(to_dev(tok)), P(d_ptrs), n_sess, R,
+            P(to_dev(chain)), P(path), P(nacc), P(emit), P(nemit), P(work), S()), "accept chain")
+        path_h, nacc_h = to_host(path).reshape(n_sess, R), to_host(nacc)
+        emit_h, nemit_h = to_host(emit).reshape(n_sess, R + 1), to_host(nemit)
+        new_states = states_from_dev(d_states, n_sess)
+        cut = 0
+        for s in range(n_sess):
+            st = po.copy_state(states[s])
+            sl = slice(s * R, (s + 1) * R)
+            p_ref, e_ref = po.accept_tree(st, tgt[sl], drf[sl], parent, tok[sl], te[sl], de[sl],
+                                          chain=chain[sl])
+            assert list(path_h[s, :nacc_h[s]]) == list(p_ref), s
+            assert list(emit_h[s, :nemit_h[s]]) == list(e_ref), s
+            assert bytes(new_states[s]) == bytes(st), s
+            p0, e0 = po.accept_tree(po.copy_state(states[s]), tgt[sl], drf[sl], parent, tok[sl],
+                                    te[sl], de[sl])
+            cut += list(p0) != list(p_ref)  # the condition changed this session's walk
+        assert cut > 0

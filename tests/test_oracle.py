@@ -734,3 +734,36 @@ def test_rule_u24_literal_and_uniformity():
             for sl in range(30):
                 cnt[(lib.or_rule_u24(po.ptr(st), sl) * 30) >> 24] += 1
     assert float(((cnt - 1000.0) ** 2 / 1000.0).sum()) < 58.3
+
+
+def test_accept_chain_condition_truncates_the_walk():
+    """The chain condition (reference docs/SPECULATIVE.md:26-41) on top of the
+    rule: an accepted node whose drafted frame failed ends the walk with its
+    token as the last emitted id, out of the path, with no bonus draw; the
+    walk up to it is the rule's own (same decisions, same emitted prefix)."""
+    r = RNG(23)
+    K = 4
+    rows = np.stack([_logits(r) for _ in range(K + 1)])
+    for s in range(1, 30):
+        st = po.state(seed=s)
+        sd = po.copy_state(st)
+        tok = [0]
+        for i in range(K):
+            t, _, _ = po.sample(sd, rows[i], 0)
+            tok.append(t)
+        z = np.zeros(K + 1, np.uint16)
+        ref_st = po.copy_state(st)
+        path, emitted = po.accept_tree(ref_st, rows, rows, _chain(K), tok, z, z)
+        assert list(path) == [1, 2, 3, 4]
+        for bad in range(1, K + 1):
+            chain = np.ones(K + 1, np.uint8)
+            chain[bad] = 0
+            st2 = po.copy_state(st)
+            p2, e2 = po.accept_tree(st2, rows, rows, _chain(K), tok, z, z, chain=chain)
+            assert list(p2) == list(path[:bad - 1])
+            assert list(e2) == list(emitted[:bad])
+            assert st2.count == st.count + bad  # the emitted ids only, no bonus
+        # all pass: identical to the rule
+        st3 = po.copy_state(st)
+        p3, e3 = po.accept_tree(st3, rows, rows, _chain(K), tok, z, z, chain=np.ones(K + 1, np.uint8))
+        assert list(p3) == list(path) and list(e3) == list(emitted) and bytes(st3) == bytes(ref_st)
