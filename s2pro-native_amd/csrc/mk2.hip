@@ -21,10 +21,11 @@
  *     Nothing else on those waves issues vector memory loads between
  *     prefetches except the attention phase, whose own (compiler-counted)
  *     waits can only wait longer, never shorter;
- *   - phases depend on each other through per-tile flags (one 32-bit word
- *     per producing tile, holding a per-launch epoch): a consumer polls
- *     exactly the tiles it reads (attention: its kv head's 48 qkv tiles),
- *     no grid-wide barrier.  Outputs are written through (sc1) and read
+ *   - phases depend on each other through flags (one 32-bit word per
+ *     producing workgroup or attention unit, each in its own 64-byte line,
+ *     holding a per-launch epoch): a consumer polls exactly the producers
+ *     it reads (attention: the owners of its kv head's 48 qkv tiles), no
+ *     grid-wide barrier.  Outputs are written through (sc1) and read
  *     back with sc1 loads, so no cache maintenance is needed (the 8 XCD L2s
  *     are not coherent with each other inside a kernel);
  *   - every wait is bounded: a timeout sets a sticky error flag and every
@@ -440,9 +441,8 @@ S2P_DEV void flags_poll(const Mk2Args& A, const uint32_t* f, int ia, int na, int
         val[j] = e < n;
         errw[j] = e == n;
         /* past the set: the error word, then the first flag again */
-        ptr[j] = e < na ? f + ia + e
-                        : (e < na + nb ? f + ib + (e - na)
-                                       : (e < n ? f + ic + (e - na - nb) : (e == n ? (const uint32_t*)A.err : f + ia)));
+        const int fi = e < na ? ia + e : (e < na + nb ? ib + (e - na) : (e < n ? ic + (e - na - nb) : ia));
+        ptr[j] = e == n ? (const uint32_t*)A.err : f + fi * MK2_FSTR;
     }
     for (unsigned spins = 0; spins < SPIN_LIMIT; spins++) {
         uint32_t r[NLD];
@@ -465,6 +465,7 @@ S2P_DEV void flags_wait3(const Mk2Args& A, int kind, int ia, int na, int ib, int
     const int n = na + nb + nc;
     if (n < 64) flags_poll<1>(A, f, ia, na, ib, nb, ic, nc, want);
     else if (n < 192) flags_poll<3>(A, f, ia, na, ib, nb, ic, nc, want);
+    else if (n < 320) flags_poll<5>(A, f, ia, na, ib, nb, ic, nc, want);
     else if (n < 640) flags_poll<10>(A, f, ia, na, ib, nb, ic, nc, want);
     else
         for (int c = 0; c < n; c += 1023) /* one range of 640 flags or more */
@@ -477,7 +478,7 @@ S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want
 S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) {
     vm_drain();
     const int lane = threadIdx.x & 63;
-    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind + i0 + i, val);
+    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind + (i0 + i) * MK2_FSTR, val);
 }
 
 /* ---- IO wave pieces of a GEMV phase ---- */
@@ -573,7 +574,7 @@ S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst
             const int m = i / np, k = i - m * np;
             coh_stf(gs + (t0 + k) * 8 + m, ((const LDSP(float)*)(smem + L_HS))[m * 8 + k]);
         }
-    flags_set(A, kind, t0, np, val);
+    flags_set(A, kind, blockIdx.x, 1, val); /* one flag per workgroup, tiles or none */
 }
 
 /* ---- attention: one (segment, kv head, 128-position split) unit per
@@ -669,7 +670,12 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         /* q-norm and k-norm weights are adjacent: 512 B */
         if (lane < 32) dma16(A.norms + (size_t)l * MK2_NORM_STRIDE + MK2_NORM_Q + 8 * lane, (LDSP(void)*)s_nw, false);
         const uint32_t want = flag_val(epoch, l, MK2_F_Q);
-        flags_wait3(A, MK2_F_Q, 32 * kvh, 32, 256 + 8 * kvh, 8, 320 + 8 * kvh, 8, want);
+        /* the workgroups that own the kv head's 32 q, 8 k and 8 v tiles (tile t
+         * of the 384 is owned by workgroup ((t + 1) 256 - 1) / 384) */
+        auto own = [](int t) { return ((t + 1) * MK2_NWG - 1) / 384; };
+        const int qa = own(32 * kvh), ka = own(256 + 8 * kvh), va = own(320 + 8 * kvh);
+        flags_wait3(A, MK2_F_Q, qa, own(32 * kvh + 31) - qa + 1, ka, own(263 + 8 * kvh) - ka + 1, va,
+                    own(327 + 8 * kvh) - va + 1, want);
         const int s0 = max(p0, g.L), nq = g.nrows * 4, nnew = max(0, p1 - s0);
         /* q items: the row's 4 q heads of kv head kvh are 1 KB contiguous */
         for (int rl = 0; rl < g.nrows; rl++) {
@@ -1137,15 +1143,15 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                 const float tw = sum_lanes16(bf2f(xw));
                 if (cc == 0) coh_stf(A.gsx + gd.t0 * 8 + m, -136.f * tw);
             }
-            flags_set(A, MK2_F_INIT, gd.t0, gd.np, flag_val(epoch, -1, MK2_F_INIT));
+            flags_set(A, MK2_F_INIT, wg, 1, flag_val(epoch, -1, MK2_F_INIT));
         }
         __syncthreads(); /* (init) */
         const Geo gq = geoP<PQ>(wg, 0), go = geoP<PO>(wg, 0), gg = geoP<PG>(wg, 0);
         for (int l = 0; l < NL; l++) {
             const uint16_t* nl = A.norms + (size_t)l * MK2_NORM_STRIDE;
             /* Q: x (previous w2, or the init) -> qkv */
-            if (l == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
-            else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, l - 1, MK2_F_D));
+            if (l == 0) flags_wait(A, MK2_F_INIT, 0, MK2_NWG, flag_val(epoch, -1, MK2_F_INIT));
+            else flags_wait(A, MK2_F_D, 0, MK2_NWG, flag_val(epoch, l - 1, MK2_F_D));
             TRACE(l, 0);
             io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, gq.t0, gq.np);
             TRACE(l, 1);
@@ -1171,7 +1177,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                      flag_val(epoch, l, MK2_F_O));
             TRACE(l, 6);
             /* G: x -> h */
-            flags_wait(A, MK2_F_O, 0, 160, flag_val(epoch, l, MK2_F_O));
+            flags_wait(A, MK2_F_O, 0, MK2_NWG, flag_val(epoch, l, MK2_F_O));
             TRACE(l, 7);
             io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, gg.t0, gg.np);
             TRACE(l, 8);
@@ -1183,7 +1189,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                      flag_val(epoch, l, MK2_F_G));
             TRACE(l, 9);
             /* D: h -> x += w2 h */
-            flags_wait(A, MK2_F_G, 0, 608, flag_val(epoch, l, MK2_F_G));
+            flags_wait(A, MK2_F_G, 0, MK2_NWG, flag_val(epoch, l, MK2_F_G));
             TRACE(l, 10);
             io_stage<9728, false, true, true>(A, A.h, A.gsh,
                                         l + 1 < NL ? nl + MK2_NORM_STRIDE + MK2_NORM_ATTN : A.final_norm, M,
@@ -1198,8 +1204,8 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             TRACE(l, 12);
         }
         /* head: final RMSNorm of x */
-        if (NL == 0) flags_wait(A, MK2_F_INIT, 0, 160, flag_val(epoch, -1, MK2_F_INIT));
-        else flags_wait(A, MK2_F_D, 0, 160, flag_val(epoch, NL - 1, MK2_F_D));
+        if (NL == 0) flags_wait(A, MK2_F_INIT, 0, MK2_NWG, flag_val(epoch, -1, MK2_F_INIT));
+        else flags_wait(A, MK2_F_D, 0, MK2_NWG, flag_val(epoch, NL - 1, MK2_F_D));
         TRACE(NL, 0);
         io_stage<2560, true, false, true>(A, A.xw, A.gsx, nullptr, M, smem, 0, 0);
         TRACE(NL, 1);

@@ -36,15 +36,18 @@ extern "C" {
 #define MK2_NORM_K 5248
 #define MK2_NORM_STRIDE 5376
 
-/* flags: one 32-bit word per producing tile (or attention unit), by kind:
- * offset and capacity in words */
-#define MK2_F_INIT 0       /* 160 residual tiles of the input */
-#define MK2_F_Q 256        /* 384 qkv tiles */
-#define MK2_F_ATT 1024     /* n_seg x 8 x nsplit attention units (<= 3072) */
-#define MK2_F_O 4096       /* 160 residual tiles after wo */
-#define MK2_F_G 4352       /* 608 SwiGLU pair tiles */
-#define MK2_F_D 5120       /* 160 residual tiles after w2 */
-#define MK2_F_WORDS 5376
+/* flags: one 32-bit word per producing workgroup (GEMV phases, the init) or
+ * attention unit, each in its own 64-byte line (MK2_FSTR words apart: flags
+ * sharing a line made every hop ~1.4 us slower, the writers and the pollers
+ * of all workgroups contending for the same lines); offsets in words */
+#define MK2_FSTR 16
+#define MK2_F_INIT 0                          /* 256 workgroups */
+#define MK2_F_Q (256 * MK2_FSTR)              /* 256 workgroups */
+#define MK2_F_ATT (512 * MK2_FSTR)            /* n_seg x 8 x nsplit units (<= 3072) */
+#define MK2_F_O ((512 + 3072) * MK2_FSTR)     /* 256 workgroups */
+#define MK2_F_G ((768 + 3072) * MK2_FSTR)     /* 256 workgroups */
+#define MK2_F_D ((1024 + 3072) * MK2_FSTR)    /* 256 workgroups */
+#define MK2_F_WORDS ((1280 + 3072) * MK2_FSTR)
 #define MK2_ATT_MAX 3072
 #define MK2_MAX_LAYERS 40
 #define MK2_MAX_SPLIT 64
