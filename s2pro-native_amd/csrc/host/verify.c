@@ -491,7 +491,7 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
         nsplit > MK2_MAX_SPLIT || b->n_seg * 8 * nsplit > MK2_ATT_MAX)
         return 0;
     if (!b->d_wpack && mk2_pack_all(b, st) != S2P_OK) return 0;
-    /* a fresh state block per plan: flags, launch epoch, split counters */
+    /* a fresh state block per plan: flags, launch epoch, error word */
     if (hipMemsetAsync(b->d_mk2, 0, MK2_STATE_WORDS * sizeof(uint32_t), st) != hipSuccess ||
         hipMemsetAsync((unsigned char*)b->d_mk2 + MK2_AUX_OFF, 0, MK2_AUX_BYTES, st) != hipSuccess)
         return 0;
@@ -521,7 +521,6 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
     A->flags = b->d_mk2;
     A->state = b->d_mk2 + MK2_STATE_WORD;
     A->err = (int*)(b->d_mk2 + MK2_ERR_WORD);
-    A->attn_ctr = b->d_mk2 + MK2_CTR_WORD;
     A->plan = row_plan(b);
     A->segs = b->d_segs;
     A->n_seg = b->n_seg;

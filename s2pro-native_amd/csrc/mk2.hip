@@ -873,21 +873,12 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
                     coh_st64(part + pi * 2, (uint64_t)__float_as_uint(Mx) | ((uint64_t)__float_as_uint(ls) << 32));
                 }
             }
-            vm_drain();
-            if (lane == 0) {
-                unsigned* ctr = A.attn_ctr + l * 64 + seg * 8 + kvh;
-                const unsigned target = (epoch + 1u) * (unsigned)ns;
-                __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                unsigned spins = 0;
-                if (!coh_ld32(A.err))
-                    while ((int)(coh_ld32(ctr) - target) < 0) {
-                        __builtin_amdgcn_s_sleep(1);
-                        if (++spins > SPIN_LIMIT || ((spins & 1023) == 0 && coh_ld32(A.err))) {
-                            __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            break;
-                        }
-                    }
-            }
+            /* this split's partials are written: its flag, then every split's
+             * flag of the group (the flags' own lines; an arrival counter's
+             * atomics queue up on one line) */
+            const int u0 = (seg * 8 + kvh) * ns;
+            flags_set(A, MK2_F_PART, u0 + sp, 1, flag_val(epoch, l, MK2_F_PART));
+            flags_wait(A, MK2_F_PART, u0, ns, flag_val(epoch, l, MK2_F_PART));
             /* every split's partial of the share: 512 B each, two per load */
             for (int i = 0; 2 * i < nv * ns; i++) {
                 const int e = 2 * i + (lane >> 5);

@@ -47,18 +47,17 @@ extern "C" {
 #define MK2_F_O ((512 + 3072) * MK2_FSTR)     /* 256 workgroups */
 #define MK2_F_G ((768 + 3072) * MK2_FSTR)     /* 256 workgroups */
 #define MK2_F_D ((1024 + 3072) * MK2_FSTR)    /* 256 workgroups */
-#define MK2_F_WORDS ((1280 + 3072) * MK2_FSTR)
+#define MK2_F_PART ((1280 + 3072) * MK2_FSTR) /* attention units: their split partials written */
+#define MK2_F_WORDS ((1280 + 2 * 3072) * MK2_FSTR)
 #define MK2_ATT_MAX 3072
 #define MK2_MAX_LAYERS 40
 #define MK2_MAX_SPLIT 64
 /* the backbone's mk2 state block (uint32 words): flags, then the launch
- * epoch and done count, the error flag, the attention split arrival
- * counters [layer][segment x 8 + kv head] (64 per layer).  Zeroed at every
- * plan; within a plan every word only grows. */
+ * epoch and done count, the error flag.  Zeroed at every plan; within a
+ * plan every word only grows. */
 #define MK2_STATE_WORD MK2_F_WORDS
 #define MK2_ERR_WORD (MK2_STATE_WORD + 2)
-#define MK2_CTR_WORD (MK2_STATE_WORD + 4)
-#define MK2_STATE_WORDS (MK2_CTR_WORD + MK2_MAX_LAYERS * 64)
+#define MK2_STATE_WORDS (MK2_STATE_WORD + 4)
 /* after the state block (256-aligned): the norm-weighted residual rows
  * [MK2_MAX_ROWS][2560] bf16 and the code-bias terms of the GEMV inputs,
  * -136 x (sum of a row's values), f32, [column block][8 rows] (rows >= the
@@ -98,7 +97,6 @@ typedef struct {
     const S2pAttnSeg* segs;
     int n_seg, nsplit, split_pos;
     float* attn_part;
-    unsigned* attn_ctr;            /* [MK2_MAX_LAYERS][64] split arrivals, monotonic per plan */
     const float* rope_tab;
     float eps;
 } Mk2Args;
