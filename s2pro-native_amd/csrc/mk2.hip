@@ -422,54 +422,64 @@ S2P_DEV void c_gemv(Slot (&S)[NSLOT], const Mk2Args& A, int l, int cw, const Ctx
 S2P_DEV uint32_t flag_val(uint32_t epoch, int l, int kind) {
     return epoch * 2048u + (uint32_t)((l + 2) * 8 + kind);
 }
-/* one wave: wait until the flags of up to three ranges [i0, i0 + n) of the
- * flag words at f all read want (fewer than 64 * NLD flags in total), one
- * poll over all the ranges at a time.  (Deeper polling, several polls in
- * flight, measured slower: the extra reads of the hot flag lines delay the
- * producers' stores more than they shorten the detection.) */
+/* flag i of a kind: word (i / 2) MK2_FSTR + i % 2, two producers per 64-byte
+ * line (a hop probe over 256 workgroups: one flag per line 2.9 us, two per
+ * line polled with one 8-byte load 1.95 us, sixteen per line 3.7 us) */
+S2P_DEV uint32_t* flag_at(const Mk2Args& A, int kind, int i) {
+    return A.flags + kind + (i >> 1) * MK2_FSTR + (i & 1);
+}
+
+/* one wave: wait until the flags of up to three ranges [i0, i0 + n) all read
+ * want, one poll over all of them at a time: one 8-byte load per flag pair
+ * (fewer than 64 * NLD pairs in total).  (Deeper polling, several polls in
+ * flight, measured slower: the extra reads of the flag lines delay the
+ * producers more than they shorten the detection.) */
 template <int NLD>
-S2P_DEV void flags_poll(const Mk2Args& A, const uint32_t* f, int ia, int na, int ib, int nb, int ic,
-                        int nc, uint32_t want) {
+S2P_DEV void flags_poll(const Mk2Args& A, int kind, int ia, int na, int ib, int nb, int ic, int nc,
+                        uint32_t want) {
     const int lane = threadIdx.x & 63;
     if (coh_ld32(A.err)) return;
-    const int n = na + nb + nc; /* < 64 * NLD: element n is the error word */
-    const uint32_t* ptr[NLD];
-    bool val[NLD], errw[NLD];
+    const int pa = na ? ((ia + na - 1) >> 1) - (ia >> 1) + 1 : 0;
+    const int pb = nb ? ((ib + nb - 1) >> 1) - (ib >> 1) + 1 : 0;
+    const int pc = nc ? ((ic + nc - 1) >> 1) - (ic >> 1) + 1 : 0;
+    const int n = pa + pb + pc; /* < 64 * NLD: slot n reads the error word */
+    const uint64_t* ptr[NLD];
+    bool lo[NLD], hi[NLD], errw[NLD];
 #pragma unroll
     for (int j = 0; j < NLD; j++) {
         const int e = lane + 64 * j;
-        val[j] = e < n;
+        int i0 = ia, i1 = ia + na, p = (ia >> 1) + e;
+        if (e >= pa) { i0 = ib; i1 = ib + nb; p = (ib >> 1) + (e - pa); }
+        if (e >= pa + pb) { i0 = ic; i1 = ic + nc; p = (ic >> 1) + (e - pa - pb); }
+        const bool in = e < n;
+        lo[j] = in && 2 * p >= i0 && 2 * p < i1;
+        hi[j] = in && 2 * p + 1 >= i0 && 2 * p + 1 < i1;
         errw[j] = e == n;
-        /* past the set: the error word, then the first flag again */
-        const int fi = e < na ? ia + e : (e < na + nb ? ib + (e - na) : (e < n ? ic + (e - na - nb) : ia));
-        ptr[j] = e == n ? (const uint32_t*)A.err : f + fi * MK2_FSTR;
+        ptr[j] = e == n ? (const uint64_t*)A.err : (const uint64_t*)flag_at(A, kind, in ? 2 * p : 0);
     }
     for (unsigned spins = 0; spins < SPIN_LIMIT; spins++) {
-        uint32_t r[NLD];
+        uint64_t r[NLD];
 #pragma unroll
-        for (int j = 0; j < NLD; j++) r[j] = coh_ld32(ptr[j]);
-        bool o = true, e = false;
+        for (int j = 0; j < NLD; j++) r[j] = coh_ld64(ptr[j]);
+        bool o = true, er = false;
 #pragma unroll
         for (int j = 0; j < NLD; j++) {
-            o = o && (!val[j] || r[j] == want);
-            e = e || (errw[j] && r[j] != 0u);
+            o = o && (!lo[j] || (uint32_t)r[j] == want) && (!hi[j] || (uint32_t)(r[j] >> 32) == want);
+            er = er || (errw[j] && (uint32_t)r[j] != 0u);
         }
-        if (__any(e) || __all(o)) return;
+        if (__any(er) || __all(o)) return;
         __builtin_amdgcn_s_sleep(1);
     }
     if (lane == 0) __hip_atomic_store(A.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 S2P_DEV void flags_wait3(const Mk2Args& A, int kind, int ia, int na, int ib, int nb, int ic, int nc,
                          uint32_t want) {
-    const uint32_t* f = A.flags + kind;
-    const int n = na + nb + nc;
-    if (n < 64) flags_poll<1>(A, f, ia, na, ib, nb, ic, nc, want);
-    else if (n < 192) flags_poll<3>(A, f, ia, na, ib, nb, ic, nc, want);
-    else if (n < 320) flags_poll<5>(A, f, ia, na, ib, nb, ic, nc, want);
-    else if (n < 640) flags_poll<10>(A, f, ia, na, ib, nb, ic, nc, want);
+    const int n = (na + nb + nc) / 2 + 3; /* pairs, at most */
+    if (n < 64) flags_poll<1>(A, kind, ia, na, ib, nb, ic, nc, want);
+    else if (n < 192) flags_poll<3>(A, kind, ia, na, ib, nb, ic, nc, want);
     else
-        for (int c = 0; c < n; c += 1023) /* one range of 640 flags or more */
-            flags_poll<16>(A, f, ia + c, min(1023, n - c), 0, 0, 0, 0, want);
+        for (int c = 0; c < na; c += 1024) /* one range of 378 flags or more */
+            flags_poll<9>(A, kind, ia + c, min(1024, na - c), 0, 0, 0, 0, want);
 }
 S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want) {
     flags_wait3(A, kind, i0, n, 0, 0, 0, 0, want);
@@ -478,7 +488,7 @@ S2P_DEV void flags_wait(const Mk2Args& A, int kind, int i0, int n, uint32_t want
 S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) {
     vm_drain();
     const int lane = threadIdx.x & 63;
-    for (int i = lane; i < n; i += 64) coh_st32(A.flags + kind + (i0 + i) * MK2_FSTR, val);
+    for (int i = lane; i < n; i += 64) coh_st32(flag_at(A, kind, i0 + i), val);
 }
 
 /* ---- IO wave pieces of a GEMV phase ---- */
