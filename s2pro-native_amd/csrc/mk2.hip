@@ -77,6 +77,7 @@ enum { PQ = 0, PO = 1, PG = 2, PD = 3 };
 #define TR_L 40
 #define TR_E 32
 __device__ uint64_t g_mk2_tr[MK2_NWG][TR_L][TR_E];
+
 #define TRACE(l, e)                                                                    \
     do {                                                                               \
         if ((threadIdx.x & 63) == 0 && (l) < TR_L) g_mk2_tr[blockIdx.x][l][e] = wall_clock64(); \
@@ -566,11 +567,15 @@ S2P_DEV void bias_pairs(LDSP(unsigned char)* smem) {
 /* write the workgroup's output columns [t0 * 16, (t0 + np) * 16) of M rows
  * (and, for the residual, the tiles' sums of squares), then the flags */
 S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst, int ldd,
-                      int t0, int np, int M, bool resid, float* gs, int kind, uint32_t val) {
+                      int t0, int np, int M, bool resid, float* gs, int kind, uint32_t val, int l) {
     const int lane = threadIdx.x & 63;
     const LDSP(uint16_t)* outb = (const LDSP(uint16_t)*)(smem + L_OUTB);
     const LDSP(uint16_t)* outw = (const LDSP(uint16_t)*)(smem + L_OUTW);
     const int nch = np * 2; /* 16-byte chunks per row */
+#ifdef MK2_TRACE
+    const int trk = kind == MK2_F_Q ? 0 : kind == MK2_F_O ? 1 : kind == MK2_F_G ? 2 : 3;
+    uint64_t tst0 = wall_clock64();
+#endif
     for (int i = lane; i < M * nch; i += 64) {
         const int m = i / nch, c = i - m * nch;
         coh_st128(dst + (size_t)m * ldd + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outb + m * 96 + c * 8));
@@ -584,6 +589,13 @@ S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst
             const int m = i / np, k = i - m * np;
             coh_stf(gs + (t0 + k) * 8 + m, ((const LDSP(float)*)(smem + L_HS))[m * 8 + k]);
         }
+#ifdef MK2_TRACE
+    vm_drain();
+    if (lane == 0 && l == 18) {
+        g_mk2_tr[blockIdx.x][39][trk * 3 + 0] = tst0;
+        g_mk2_tr[blockIdx.x][39][trk * 3 + 1] = wall_clock64();
+    }
+#endif
     flags_set(A, kind, blockIdx.x, 1, val); /* one flag per workgroup, tiles or none */
 }
 
@@ -1102,6 +1114,9 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             bias_pairs<2560>(smem);
             c_gemv<PG>(S, A, l, cw, C, smem, M);
+#ifdef MK2_TRACE
+            if (l == 18 && (threadIdx.x & 63) == 0) g_mk2_tr[blockIdx.x][39][19 + cw] = wall_clock64();
+#endif
             if (cw == 0) TRACE(l, 15);
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
@@ -1109,6 +1124,9 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             bias_pairs<9728>(smem);
             c_gemv<PD>(S, A, l, cw, C, smem, M);
+#ifdef MK2_TRACE
+            if (l == 18 && (threadIdx.x & 63) == 0) g_mk2_tr[blockIdx.x][39][12 + cw] = wall_clock64();
+#endif
             if (cw == 0) TRACE(l, 16);
             __syncthreads();
             reduce_phase<PD>(smem, M, wg);
@@ -1161,7 +1179,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
             io_store(A, smem, A.qkv, 6144, gq.t0, gq.np, M, false, nullptr, MK2_F_Q,
-                     flag_val(epoch, l, MK2_F_Q));
+                     flag_val(epoch, l, MK2_F_Q), l);
             TRACE(l, 2);
             /* attention */
             attn_phase<true>(A, l, epoch, smem);
@@ -1175,7 +1193,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PO>(smem, M, wg);
             io_store(A, smem, A.x, 2560, go.t0, go.np, M, true, A.gsx, MK2_F_O,
-                     flag_val(epoch, l, MK2_F_O));
+                     flag_val(epoch, l, MK2_F_O), l);
             TRACE(l, 6);
             /* G: x -> h */
             flags_wait(A, MK2_F_O, 0, MK2_NWG, flag_val(epoch, l, MK2_F_O));
@@ -1187,7 +1205,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
             io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, A.gsh, MK2_F_G,
-                     flag_val(epoch, l, MK2_F_G));
+                     flag_val(epoch, l, MK2_F_G), l);
             TRACE(l, 9);
             /* D: h -> x += w2 h */
             flags_wait(A, MK2_F_G, 0, MK2_NWG, flag_val(epoch, l, MK2_F_G));
@@ -1201,7 +1219,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PD>(smem, M, wg);
             io_store(A, smem, A.x, 2560, gd.t0, gd.np, M, true, A.gsx, MK2_F_D,
-                     flag_val(epoch, l, MK2_F_D));
+                     flag_val(epoch, l, MK2_F_D), l);
             TRACE(l, 12);
         }
         /* head: final RMSNorm of x */
