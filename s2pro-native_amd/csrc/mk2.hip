@@ -610,7 +610,7 @@ S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst
  * scores and dims 16w..16w+15 of the output for PV.  Every split writes its
  * partial (m, l, O), waits until all splits of its (segment, kv head) have
  * arrived, and merges its share of the outputs. */
-#define A_SQ 0                     /* [32][128] bf16 roped q vectors */
+#define A_SQ 0                     /* [32][128] bf16 roped q vectors, chunk k of row v at slot k ^ (v & 15) */
 #define A_SK (8 * 1024)            /* [128][128] bf16 K: chunk k of row t at slot k ^ (t & 15) */
 #define A_SV (40 * 1024)           /* [128][128] bf16 V, SVX swizzle */
 #define A_SP (72 * 1024)           /* P hi [32][136] bf16 */
@@ -745,8 +745,8 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         qkrope_math(v0, v1, nw[lane], nw[lane + 64], c0, sn0, c1, sn1, A.eps, lane, &o0, &o1);
         const uint16_t b0 = f2bf(o0), b1 = f2bf(o1);
         if (isq) {
-            s_q[it * 128 + lane] = b0;
-            s_q[it * 128 + lane + 64] = b1;
+            s_q[SKX(it, lane >> 3) + (lane & 7)] = b0;
+            s_q[SKX(it, (lane + 64) >> 3) + (lane & 7)] = b1;
         } else {
             const int t = s0 + (it - nq) - p0;
             s_k[SKX(t, lane >> 3) + (lane & 7)] = b0;
@@ -780,7 +780,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             for (int idx = lane; idx < nq * 16; idx += 64) {
                 const int qv = idx >> 4, ch = idx & 15;
                 coh_st128(A.q + (size_t)(g.row0 + (qv >> 2)) * 4096 + (4 * kvh + (qv & 3)) * 128 + 8 * ch,
-                          *(const LDSP(s2p_u32x4)*)(s_q + qv * 128 + 8 * ch));
+                          *(const LDSP(s2p_u32x4)*)(s_q + SKX(qv, ch)));
             }
     }
     TRACE(l, 21);
@@ -793,7 +793,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ch = 0; ch < 4; ch++) {
-            const s2p_u32x4 qa = *(const LDSP(s2p_u32x4)*)(s_q + (16 * qt + c) * 128 + 32 * ch + 8 * qq);
+            const s2p_u32x4 qa = *(const LDSP(s2p_u32x4)*)(s_q + SKX(16 * qt + c, 4 * ch + qq));
             const s2p_u32x4 kb = *(const LDSP(s2p_u32x4)*)(s_k + SKX(t, 4 * ch + qq));
             acc = mfma16x16x32(qa, kb, acc);
         }
@@ -925,9 +925,11 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         if (tidx < nv) {
             const int k = tidx;
             float Mx = -INFINITY;
+#pragma unroll 8
             for (int s2 = 0; s2 < ns; s2++) Mx = fmaxf(Mx, s_ml[2 * (k * ns + s2)]);
             const float Ms = Mx == -INFINITY ? 0.f : Mx;
             float lsum = 0.f;
+#pragma unroll 8
             for (int s2 = 0; s2 < ns; s2++) {
                 const float w = __expf(s_ml[2 * (k * ns + s2)] - Ms);
                 lsum = fmaf(s_ml[2 * (k * ns + s2) + 1], w, lsum);
@@ -939,6 +941,8 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         for (int idx = tidx; idx < nv * 128; idx += NTH) {
             const int k = idx >> 7, d = idx & 127;
             float acc = 0.f;
+            /* unrolled: the loads of a batch issue together, the sum keeps split order */
+#pragma unroll 8
             for (int s2 = 0; s2 < ns; s2++) acc = fmaf(s_po[(k * ns + s2) * 128 + d], s_w[k * ns + s2], acc);
             s_o[(v0s + k) * 128 + d] = acc / s_w[nv * ns + k];
         }
