@@ -139,6 +139,26 @@ S2P_DEV void state_push(s2ps_dev_state* sp, int64_t tok) {
     sp->count++;
 }
 
+/* state_push by the 64 lanes of one wave (wave-uniform arguments): the
+ * window shift is one LDS read and one write per lane instead of a serial
+ * loop; a wave's read completes for all lanes before its write */
+S2P_DEV void state_push_wave(s2ps_dev_state* sp, int64_t tok, int lane) {
+    if (tok == TOK_EOS) return;
+    const int W = sp->window;
+    if (sp->count < (uint64_t)W) {
+        if (lane == 0) sp->prev[sp->count] = tok;
+    } else {
+        const int64_t nx = lane < W - 1 ? sp->prev[lane + 1] : 0;
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        if (lane < W - 1) sp->prev[lane] = nx;
+        if (lane == 0) sp->prev[W - 1] = tok;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) sp->count++;
+    __builtin_amdgcn_wave_barrier();
+}
+
 S2P_DEV int64_t cand_to_vocab(int ci) { return ci == CAND_EOS ? TOK_EOS : SEM_START + ci; }
 S2P_DEV int vocab_to_cand(int64_t t) {
     if (t >= SEM_START && t <= SEM_END) return (int)(t - SEM_START);
@@ -169,25 +189,33 @@ struct TxShared {
     int greedy;
     float temp, topp, m, sum, t, m2, s2;
     int masked[32];
-    /* lane 0's scratch (in LDS rather than private memory) */
-    int ridx[64];
-    float rval[64];
+    /* the tree (accept transform): parents, drafted tokens, a root path */
+    int par[64];
+    int64_t tks[64];
     int path[64];
+    int npath;
 };
 
 /* Sampler transform of one logits row into sh.ti / sh.p2 (ranks 0..29). */
 __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t* eos_ptr) {
     const int tid = threadIdx.x;
-    /* gather */
-    if (eos_ptr) {
-        for (int i = tid; i < N_SEM; i += TX_THREADS) sh.cand[i] = bf2f(lrow[i]);
-        if (tid == 0) sh.cand[CAND_EOS] = bf2f(*eos_ptr);
-    } else {
-        for (int i = tid; i < N_SEM; i += TX_THREADS) sh.cand[i] = bf2f(lrow[SEM_START + i]);
-        if (tid == 0) sh.cand[CAND_EOS] = bf2f(lrow[TOK_EOS]);
+    /* gather: every load of the thread issued before the first is waited
+     * for (a load-store loop would wait out one memory round trip per
+     * element) */
+    {
+        constexpr int PG = N_SEM / TX_THREADS;
+        static_assert(N_SEM % TX_THREADS == 0, "gather split");
+        const uint16_t* src = eos_ptr ? lrow : lrow + SEM_START;
+        uint16_t r[PG];
+#pragma unroll
+        for (int j = 0; j < PG; j++) r[j] = src[tid + j * TX_THREADS];
+        const uint16_t re = *(eos_ptr ? eos_ptr : lrow + TOK_EOS); /* every thread: one more load in the batch */
+#pragma unroll
+        for (int j = 0; j < PG; j++) sh.cand[tid + j * TX_THREADS] = bf2f(r[j]);
+        if (tid == 0) sh.cand[CAND_EOS] = bf2f(re);
     }
     __syncthreads();
-    /* RAS + repetition penalty (sampling.c:129-174), lane 0 */
+    /* RAS detection (sampling.c:129-174) on lane 0, then the repetition penalty */
     if (tid == 0) {
         const s2ps_dev_state* sp = &sh.st;
         const int greedy = sp->temperature == 0.0f;
@@ -213,20 +241,24 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
         sh.greedy = greedy;
         sh.temp = use_ras ? 1.0f : sp->temperature;
         sh.topp = use_ras ? 0.9f : sp->top_p;
-        if (capped > 0) {
-            int* ridx = sh.ridx;
-            float* rval = sh.rval;
-            int rn = 0;
-            for (int j = 0; j < capped; j++) {
-                const int ci = vocab_to_cand(sp->prev[j]);
-                if (ci < 0) continue;
+    }
+    {
+        /* repetition penalty, one window entry per thread: every entry's
+         * value is read before any is written (the rule's gather, then its
+         * scatter; repeated tokens write the same value) */
+        const s2ps_dev_state* sp = &sh.st;
+        const int capped = sp->count < (uint64_t)sp->window ? (int)sp->count : sp->window;
+        int ci = -1;
+        float rv = 0.f;
+        if (tid < capped && tid < 64) {
+            ci = vocab_to_cand(sp->prev[tid]);
+            if (ci >= 0) {
                 const float v = sh.cand[ci];
-                ridx[rn] = ci;
-                rval[rn] = v < 0.f ? v * sp->rep_penalty : v / sp->rep_penalty;
-                rn++;
+                rv = v < 0.f ? v * sp->rep_penalty : v / sp->rep_penalty;
             }
-            for (int j = 0; j < rn; j++) sh.cand[ridx[j]] = rval[j];
         }
+        __syncthreads();
+        if (ci >= 0) sh.cand[ci] = rv;
     }
     __syncthreads();
     /* this thread's keys (a contiguous index range) stay in registers */
@@ -338,6 +370,7 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
         my_i = sh.ti[tid];
         my_v = sh.cand[my_i];
         const uint32_t mk = okey(my_v);
+#pragma unroll
         for (int j = 0; j < TOP_K; j++) {
             const int oi = sh.ti[j];
             const uint32_t ok = okey(sh.cand[oi]);
@@ -360,8 +393,10 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
     __syncthreads();
     if (tid == 0) {
         float sum = 0.f;
+#pragma unroll
         for (int j = 0; j < TOP_K; j++) sum += sh.e[j];
         float cum = 0.f;
+#pragma unroll
         for (int j = 0; j < TOP_K; j++) {
             cum += sh.e[j] / sum;
             sh.masked[j] = (j > 0 && cum > sh.topp) ? 1 : 0;
@@ -375,6 +410,7 @@ __device__ void transform_row(TxShared& sh, const uint16_t* lrow, const uint16_t
     __syncthreads();
     if (tid == 0) {
         float s2 = 0.f;
+#pragma unroll
         for (int j = 0; j < TOP_K; j++) s2 += sh.p2[j];
         sh.s2 = s2;
     }
@@ -440,38 +476,46 @@ struct TxOut {
     int32_t greedy;
     int32_t pad_[31];
 };
+static_assert(sizeof(TxOut) % 16 == 0 && offsetof(TxOut, greedy) == 64 * 4, "the walk copies TxOut words 0..67 as 17 16-byte chunks");
 
 __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
     __shared__ TxShared sh;
     const int gr = blockIdx.x;          /* global node row s * R + v */
     const int which = blockIdx.y;       /* 0 target, 1 draft */
     const int s = gr / a.R, v = gr - s * a.R;
-    /* leaves need no draft transform */
-    if (which == 1) {
-        bool has_child = false;
-        for (int c = v + 1; c < a.R; c++) has_child |= a.parent[c] == v;
-        if (!has_child) return;
-    }
+    /* the state and the tree in one batch of loads */
     {
         const uint32_t* src = (const uint32_t*)a.states[s];
         uint32_t* dst = (uint32_t*)&sh.st;
         for (int i = threadIdx.x; i < (int)(sizeof(sh.st) / 4); i += TX_THREADS) dst[i] = src[i];
+        if (threadIdx.x < a.R) {
+            sh.par[threadIdx.x] = a.parent[threadIdx.x];
+            sh.tks[threadIdx.x] = a.tok[(size_t)s * a.R + threadIdx.x];
+        }
     }
     __syncthreads();
+    /* leaves need no draft transform */
+    if (which == 1) {
+        bool has_child = false;
+        for (int c = v + 1; c < a.R; c++) has_child |= sh.par[c] == v;
+        if (!has_child) return;
+    }
     if (threadIdx.x == 0) {
-        /* push the drafted tokens of the root path (root excluded) */
-        /* root path; parent indices are validated (parent[u] in [0, u)) so a
-         * malformed tree ends the walk instead of reading out of bounds */
-        int* path = sh.path;
+        /* root path (root excluded); parent indices are validated (parent[u]
+         * in [0, u)) so a malformed tree ends the walk */
         int n = 0;
         for (int u = v; u > 0 && u < a.R && n < 64;) {
-            path[n++] = u;
-            const int p = a.parent[u];
+            sh.path[n++] = u;
+            const int p = sh.par[u];
             if (p < 0 || p >= u) break;
             u = p;
         }
-        for (int i = n - 1; i >= 0; i--) state_push(&sh.st, a.tok[(size_t)s * a.R + path[i]]);
+        sh.npath = n;
     }
+    __syncthreads();
+    /* push the path's drafted tokens, root side first (wave 0) */
+    if (threadIdx.x < 64)
+        for (int i = sh.npath - 1; i >= 0; i--) state_push_wave(&sh.st, sh.tks[sh.path[i]], threadIdx.x);
     __syncthreads();
     const uint16_t* base = which ? a.drf : a.tgt;
     const uint16_t* eos = which ? a.drf_eos : a.tgt_eos;
@@ -485,10 +529,14 @@ __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
     if (threadIdx.x == 0) o->greedy = sh.greedy;
 }
 
+/* p of the first j with ti[j] == ci, else 0: a branchless scan from the end
+ * (its reads are independent, so they issue together instead of one LDS
+ * round trip per step) */
 S2P_DEV float prob_of(const int32_t* ti, const float* p, int ci) {
-    for (int j = 0; j < TOP_K; j++)
-        if (ti[j] == ci) return p[j];
-    return 0.f;
+    float r = 0.f;
+#pragma unroll
+    for (int j = TOP_K - 1; j >= 0; j--) r = ti[j] == ci ? p[j] : r;
+    return r;
 }
 
 /* argmax over the wave with the sequential rule's tie order: the first
@@ -537,34 +585,56 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
     __shared__ float p[TOP_K], qp[TOP_K], rsd[TOP_K];
     __shared__ int32_t pti[TOP_K], qti[TOP_K];
     __shared__ uint32_t bcast;
+    /* the (target, draft) transforms of every node: the first 68 words
+     * (ti, p, greedy) of each TxOut entry */
+    __shared__ uint32_t wk[64 * 2 * 68];
+    __shared__ int32_t par[64];
+    __shared__ int64_t tks[64];
+    __shared__ uint8_t cok[64];
     const int s = blockIdx.x, lane = threadIdx.x;
+    const int R = a.R;
     {
+        /* everything the walk reads, in one batch of loads (the walk itself
+         * then runs from LDS: a load per node would put a memory round trip
+         * on every step of it) */
         const uint32_t* src = (const uint32_t*)a.states[s];
         uint32_t* dst = (uint32_t*)&st;
+#pragma unroll 4
         for (int i = lane; i < (int)(sizeof(st) / 4); i += 64) dst[i] = src[i];
+        if (lane < R) {
+            par[lane] = a.parent[lane];
+            tks[lane] = a.tok[(size_t)s * R + lane];
+            cok[lane] = a.chain_ok ? a.chain_ok[(size_t)s * R + lane] : (uint8_t)1;
+        }
+        const s2p_u32x4* ws = (const s2p_u32x4*)((const TxOut*)a.work + (size_t)s * R * 2);
+        s2p_u32x4* wd = (s2p_u32x4*)wk;
+        const int n = R * 2 * 17;
+#pragma unroll 4
+        for (int i = lane; i < n; i += 64) {
+            const int e = i / 17, c = i - e * 17;
+            wd[i] = ws[e * (int)(sizeof(TxOut) / 16) + c];
+        }
     }
     __syncthreads();
-    const TxOut* work = (const TxOut*)a.work;
-    const int R = a.R;
-    const int64_t* tok = a.tok + (size_t)s * R;
+    const int64_t* tok = tks;
     int32_t* path = a.out_path + (size_t)s * R;
     int64_t* emit = a.out_emit + (size_t)s * (R + 1);
     int n_acc = 0, n_emit = 0;
     int v = 0;
     for (;;) {
-        const TxOut* tp = work + ((size_t)(s * R + v) * 2 + 0);
-        const TxOut* tq = work + ((size_t)(s * R + v) * 2 + 1);
+        const uint32_t* tp = wk + (v * 2 + 0) * 68;
+        const uint32_t* tq = wk + (v * 2 + 1) * 68;
         if (lane < TOP_K) {
-            p[lane] = tp->p[lane];
-            pti[lane] = tp->ti[lane];
-            qp[lane] = tq->p[lane];
-            qti[lane] = tq->ti[lane];
+            p[lane] = __uint_as_float(tp[32 + lane]);
+            pti[lane] = (int32_t)tp[lane];
+            qp[lane] = __uint_as_float(tq[32 + lane]);
+            qti[lane] = (int32_t)tq[lane];
         }
         __syncthreads();
-        const int greedy = tp->greedy;
+        const int greedy = (int)tp[64];
         int accepted = -1, rejected_any = 0, j = 0;
         for (int c = v + 1; c < R && accepted < 0; c++) {
-            if (a.parent[c] != v) continue;
+            if (par[c] != v) continue;
             const int ci = vocab_to_cand(tok[c]);
             const float pc = ci < 0 ? 0.f : prob_of(pti, p, ci);
             const float qc = ci < 0 ? 0.f : prob_of(qti, qp, ci);
@@ -590,18 +660,17 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
             }
             __syncthreads();
             float z = 0.f;
+#pragma unroll
             for (int k = 0; k < TOP_K; k++) z += rsd[k]; /* the rule's order */
             if (z > 0.f && lane < TOP_K) p[lane] = rsd[lane] / z;
             __syncthreads();
             j++;
         }
-        if (accepted >= 0 && a.chain_ok && !a.chain_ok[(size_t)s * R + accepted]) {
+        if (accepted >= 0 && !cok[accepted]) {
             /* the drafted frame failed the chain condition: its token is
              * emitted, its row is not accepted, no bonus draw */
-            if (lane == 0) {
-                emit[n_emit] = tok[accepted];
-                if (tok[accepted] != TOK_EOS) state_push(&st, tok[accepted]);
-            }
+            if (lane == 0) emit[n_emit] = tok[accepted];
+            state_push_wave(&st, tok[accepted], lane);
             n_emit++;
             __syncthreads();
             break;
@@ -614,7 +683,7 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
             n_acc++;
             n_emit++;
             if (tok[accepted] == TOK_EOS) break;
-            if (lane == 0) state_push(&st, tok[accepted]);
+            state_push_wave(&st, tok[accepted], lane);
             __syncthreads();
             v = accepted;
             continue;
@@ -631,10 +700,8 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
             choice = (int)bcast;
         }
         const int64_t t = cand_to_vocab(pti[choice]);
-        if (lane == 0) {
-            emit[n_emit] = t;
-            state_push(&st, t);
-        }
+        if (lane == 0) emit[n_emit] = t;
+        state_push_wave(&st, t, lane);
         n_emit++;
         __syncthreads();
         break;
