@@ -89,7 +89,7 @@ __device__ uint64_t g_mk2_tr[MK2_NWG][TR_L][TR_E];
 #endif
 
 /* ---- static geometry of the four layer GEMVs ---- */
-constexpr int phT(int P) { return P == PQ ? 384 : P == PO ? 160 : P == PG ? 608 : 160; } /* tiles / pairs */
+constexpr int phT(int P) { return P == PQ ? 384 : P == PO ? 160 : P == PG ? 1216 : 160; } /* 16-row tiles */
 constexpr int phNB(int P) { return P == PQ ? 20 : P == PO ? 32 : P == PG ? 20 : 76; }    /* 4-group blocks */
 constexpr size_t phOFF(int P) {
     return P == PQ ? 0 : P == PO ? (size_t)MK2_BLK_Q * MK2_BLK
@@ -97,7 +97,8 @@ constexpr size_t phOFF(int P) {
                                            : (size_t)(MK2_BLK_Q + MK2_BLK_O + MK2_BLK_G) * MK2_BLK;
 }
 constexpr size_t LAYER_BYTES = (size_t)MK2_LAYER_BLKS * MK2_BLK;
-/* units per compute wave at most, and the per-layer unit sequence */
+/* units per compute wave at most (gate_up: 15, padded so that the layer
+ * sequence tiles the ring), and the per-layer unit sequence */
 constexpr int maxu(int P) { return P == PQ ? 6 : P == PO ? 5 : P == PG ? 18 : 11; }
 constexpr int LSEQ = 40;
 constexpr int seq_base(int P) { return P == PQ ? 0 : P == PO ? 6 : P == PG ? 11 : 29; }
@@ -131,27 +132,27 @@ S2P_DEV void sfor(F&& f) {
     sfor_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-/* workgroup wg's tiles (pairs for gate_up) and compute wave cw's units */
+/* workgroup wg's 16-row tiles and compute wave cw's units */
 struct Geo {
     int t0, np, nt, u0, nu;
 };
 /* gate_up splits its units 9:8 between waves 0-3 and waves 4-6: a wave
  * 4-6 shares its SIMD with an older wave and runs its loop ~0.7 us slower
- * (at 2 or 3 pairs, 12 or 18 units at most, as in the even split) */
+ * (at 4 or 5 tiles, 12 or 15 units at most) */
 static_assert(CW == 7, "the weighted split is written for seven compute waves");
 S2P_DEV int wave_cut(int U, int cw, bool weighted) {
     if (!weighted) return cw * U / CW;
     const int cum = cw <= 4 ? 9 * cw : 36 + 8 * (cw - 4);
     return U * cum / 60;
 }
-S2P_DEV Geo geo_of(int T, int nb, bool pairs, int wg, int cw) {
+S2P_DEV Geo geo_of(int T, int nb, bool weighted, int wg, int cw) {
     Geo g;
     g.t0 = wg * T / MK2_NWG;
     g.np = (wg + 1) * T / MK2_NWG - g.t0;
-    g.nt = pairs ? 2 * g.np : g.np;
+    g.nt = g.np;
     const int U = g.nt * nb;
-    g.u0 = wave_cut(U, cw, pairs);
-    g.nu = wave_cut(U, cw + 1, pairs) - g.u0;
+    g.u0 = wave_cut(U, cw, weighted);
+    g.nu = wave_cut(U, cw + 1, weighted) - g.u0;
     return g;
 }
 template <int P>
@@ -323,19 +324,44 @@ S2P_DEV void reduce_phase(LDSP(unsigned char)* smem, int M, int wg) {
     LDSP(float)* ssqo = (LDSP(float)*)(smem + L_SSQO);
     LDSP(float)* hs = (LDSP(float)*)(smem + L_HS);
     const Geo g0 = geoP<P>(wg, 0);
+    if constexpr (P == PG) {
+        /* tile k holds gate rows (n < 8) and up rows (n >= 8) of h columns
+         * 8 (t0 + k) + n; per tile and row the sum of its 8 h values */
+        const int ncol = g0.np * 8;
+        LDSP(float)* ts = ssqo; /* [M][8] tile sums (free in this phase) */
+        for (int i = threadIdx.x; i < ncol * M; i += NTH) {
+            const int n = i & 7, rest = i >> 3;
+            const int m = rest % M, k = rest / M;
+            const float iv = inv[m];
+            const uint16_t o = silu_mul_bf16(f2bf(__fmul_rn(iv, tile_sum(part, k, m, n, M))),
+                                             f2bf(__fmul_rn(iv, tile_sum(part, k, m, n + 8, M))));
+            outb[m * 96 + k * 8 + n] = o;
+            float t = bf2f(o); /* 8 aligned lanes: quads, then the other quad of the half-row */
+            t += dpp_f<0xB1>(t);
+            t += dpp_f<0x4E>(t);
+            t += dpp_f<0x141>(t);
+            if (n == 0) ts[m * 8 + k] = t;
+        }
+        __syncthreads();
+        /* the w2 code-bias terms: for each 32-column group of h that meets
+         * this workgroup's columns, -136 x the sum of its tile sums here */
+        const int gf = g0.t0 / 4, ng = (g0.t0 + g0.np - 1) / 4 - gf + 1;
+        if ((int)threadIdx.x < M * ng) {
+            const int m = threadIdx.x % M, gi = threadIdx.x / M;
+            float t = 0.f;
+            for (int k = max(0, 4 * (gf + gi) - g0.t0); k < min(g0.np, 4 * (gf + gi + 1) - g0.t0); k++) t += ts[m * 8 + k];
+            hs[m * 8 + gi] = -136.f * t;
+        }
+        __syncthreads();
+        return;
+    }
     const int ncol = g0.np * 16;
     for (int i = threadIdx.x; i < ncol * M; i += NTH) {
         const int n = i & 15, rest = i >> 4;
         const int m = rest % M, k = rest / M;
         const int c = k * 16 + n;
         uint16_t o;
-        if (P == PG) {
-            const float iv = inv[m];
-            o = silu_mul_bf16(f2bf(__fmul_rn(iv, tile_sum(part, 2 * k, m, n, M))),
-                              f2bf(__fmul_rn(iv, tile_sum(part, 2 * k + 1, m, n, M))));
-            const float t = sum_lanes16(bf2f(o)); /* the tile's sum of h: the w2 code-bias term */
-            if (n == 0) hs[m * 8 + k] = -136.f * t;
-        } else if (P == PO || P == PD) {
+        if (P == PO || P == PD) {
             o = f2bf(__fadd_rn(bf2f(xold[m * 16 + c]), bf2f(f2bf(tile_sum(part, k, m, n, M)))));
             const float v = bf2f(o);
             const float t = sum_lanes16(v * v); /* the tile's sum of squares of the new residual */
@@ -576,24 +602,32 @@ S2P_DEV void bias_pairs(LDSP(unsigned char)* smem) {
 /* write the workgroup's output columns [t0 * 16, (t0 + np) * 16) of M rows
  * (and, for the residual, the tiles' sums of squares), then the flags */
 S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst, int ldd,
-                      int t0, int np, int M, bool resid, float* gs, int kind, uint32_t val, int l) {
+                      int t0, int np, int M, bool resid, float* gs, int kind, uint32_t val, int l,
+                      bool half = false) {
     const int lane = threadIdx.x & 63;
     const LDSP(uint16_t)* outb = (const LDSP(uint16_t)*)(smem + L_OUTB);
     const LDSP(uint16_t)* outw = (const LDSP(uint16_t)*)(smem + L_OUTW);
-    const int nch = np * 2; /* 16-byte chunks per row */
+    const int tw = half ? 8 : 16; /* columns per tile (gate_up: 8 h columns) */
+    const int nch = np * tw / 8;  /* 16-byte chunks per row */
 #ifdef MK2_TRACE
     const int trk = kind == MK2_F_Q ? 0 : kind == MK2_F_O ? 1 : kind == MK2_F_G ? 2 : 3;
     uint64_t tst0 = wall_clock64();
 #endif
     for (int i = lane; i < M * nch; i += 64) {
         const int m = i / nch, c = i - m * nch;
-        coh_st128(dst + (size_t)m * ldd + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outb + m * 96 + c * 8));
+        coh_st128(dst + (size_t)m * ldd + t0 * tw + c * 8, *(const LDSP(s2p_u32x4)*)(outb + m * 96 + c * 8));
         if (resid)
             coh_st128(A.xw + (size_t)m * 2560 + t0 * 16 + c * 8, *(const LDSP(s2p_u32x4)*)(outw + m * 96 + c * 8));
     }
     if (resid && np > 0 && lane < M)
         coh_stf(A.ssq + lane * 160 + t0, ((const LDSP(float)*)(smem + L_SSQO))[lane * 16]);
-    if (gs) /* the tiles' code-bias terms, [tile][row] */
+    if (gs && half) { /* h: [32-column group][part][row], part 1 if the group began in an earlier workgroup */
+        const int gf = t0 / 4, ng = (t0 + np - 1) / 4 - gf + 1;
+        for (int i = lane; i < M * ng; i += 64) {
+            const int m = i % M, gi = i / M, g = gf + gi;
+            coh_stf(gs + (2 * g + (4 * g >= t0 ? 0 : 1)) * 8 + m, ((const LDSP(float)*)(smem + L_HS))[m * 8 + gi]);
+        }
+    } else if (gs) /* the tiles' code-bias terms, [tile][row] */
         for (int i = lane; i < M * np; i += 64) {
             const int m = i / np, k = i - m * np;
             coh_stf(gs + (t0 + k) * 8 + m, ((const LDSP(float)*)(smem + L_HS))[m * 8 + k]);
@@ -1090,7 +1124,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
         Ctx C;
         C.w[PQ] = wg_of(geoP<PQ>(wg, cw), phNB(PQ), false);
         C.w[PO] = wg_of(geoP<PO>(wg, cw), phNB(PO), false);
-        C.w[PG] = wg_of(geoP<PG>(wg, cw), phNB(PG), true);
+        C.w[PG] = wg_of(geoP<PG>(wg, cw), phNB(PG), false);
         C.w[PD] = wg_of(geoP<PD>(wg, cw), phNB(PD), false);
         {
             const Geo gh = geo_of(A.head_tiles, 20, false, wg, cw);
@@ -1218,7 +1252,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PG>(smem, M, wg);
             io_store(A, smem, A.h, 9728, gg.t0, gg.np, M, false, A.gsh, MK2_F_G,
-                     flag_val(epoch, l, MK2_F_G), l);
+                     flag_val(epoch, l, MK2_F_G), l, true);
             TRACE(l, 9);
             /* D: h -> x += w2 h */
             flags_wait(A, MK2_F_G, 0, MK2_NWG, flag_val(epoch, l, MK2_F_G));
@@ -1276,10 +1310,9 @@ __global__ void k_mk2_pack(const uint8_t* __restrict__ w, const uint16_t* __rest
     if (tb >= (long)T * nb) return;
     const int t = (int)(tb / nb), b = (int)(tb % nb);
     const int q = lane >> 4, r = lane & 15;
-    /* packed tile t -> source tile: pairs interleave gate tile p and up tile p */
-    int st = t;
-    if (pairs) st = (t & 1) ? (N / 32) + (t >> 1) : (t >> 1);
-    const int n = st * 16 + r;
+    /* packed tile t row r -> source row; gate_up (pairs): rows 0..7 gate
+     * rows 8t.., rows 8..15 the matching up rows N/2 + 8t.. */
+    const int n = !pairs ? t * 16 + r : r < 8 ? 8 * t + r : N / 2 + 8 * t + (r - 8);
     uint32_t o[4];
 #pragma unroll
     for (int gg = 0; gg < 4; gg++) {
