@@ -60,7 +60,7 @@
 #define CW 7 /* compute waves */
 #define NTH (64 * NWAVE)
 #ifndef NSLOT
-#define NSLOT 8 /* measured: 8 slots beat 20 (less queueing in front of the exchanges), 4 within 1% */
+#define NSLOT 8 /* measured: 8 slots beat 20 and 10 (less queueing in front of the exchanges); 5 is 0.7% slower, 4 within 1% */
 #endif
 #define SPIN_LIMIT (1u << 22)
 #define LDSP(T) __attribute__((address_space(3))) T
