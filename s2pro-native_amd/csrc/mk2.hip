@@ -141,7 +141,7 @@ struct Geo {
  * (at 4 or 5 tiles, 12 or 15 units at most) */
 static_assert(CW == 7, "the weighted split is written for seven compute waves");
 S2P_DEV int wave_cut(int U, int cw, bool weighted) {
-    if (!weighted) return cw * U / CW;
+    if (!weighted) return U - (CW - cw) * U / CW; /* uneven shares: the shorter ones to the last waves */
     const int cum = cw <= 4 ? 9 * cw : 36 + 8 * (cw - 4);
     return U * cum / 60;
 }
@@ -1100,7 +1100,7 @@ S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* sm
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < CW; w++) {
-            const int u0 = w * U / CW, u1 = (w + 1) * U / CW;
+            const int u0 = wave_cut(U, w, false), u1 = wave_cut(U, w + 1, false); /* as geo_of splits */
             if (u0 < (lt + 1) * 20 && u1 > lt * 20) s += part[((lt * CW + w) * M + m) * 16 + n];
         }
         if (row < A.head_n) A.logits[(size_t)m * A.head_n + row] = f2bf(__fmul_rn(inv[m], s));
