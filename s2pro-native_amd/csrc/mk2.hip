@@ -529,8 +529,9 @@ S2P_DEV void flags_set(const Mk2Args& A, int kind, int i0, int n, uint32_t val) 
 
 /* ---- IO wave pieces of a GEMV phase ---- */
 /* stage M rows of K activations (sc1 loads straight to LDS) and the code-bias
- * table from the producers' terms gs ([block][8 rows]: per 32 columns, or per
- * 16 when half, then summed in pairs); NORM: the rows' inverse RMS; RESID:
+ * table from the producers' terms gs ([block][8 rows]: per 32 columns, or when
+ * half two terms per 32 columns, summed in pairs: per 16 columns for the
+ * residual, per producing workgroup for h); NORM: the rows' inverse RMS; RESID:
  * the residual's old values of this workgroup's tiles and the next norm's
  * weights of its columns (nwn) */
 template <int K, bool NORM, bool RESID, bool HALF>

@@ -17,7 +17,8 @@ extern "C" {
  * dword per group, the row's k = 8q..8q+7 of that group, nibbles biased by
  * +8 and placed so that dword >> 4j & 0x000F000F holds k = 8q+2j, 8q+2j+1)
  * then 128 B of f16 scales [16 rows][4 groups].  A linear is [tile][block];
- * gate_up is [pair][gate tile, up tile][block]. */
+ * gate_up's tile t holds gate rows 8t..8t+7 (tile rows 0..7) and the
+ * matching up rows (tile rows 8..15): 1216 tiles, 8 h columns each. */
 #define MK2_BLK 1152
 #define MK2_MAX_ROWS 6    /* rows the kernel serves (the w2 activations fill LDS) */
 #define MK2_NWG 256       /* one workgroup per CU of an MI355X */
@@ -61,7 +62,7 @@ extern "C" {
 /* after the state block (256-aligned): the norm-weighted residual rows
  * [MK2_MAX_ROWS][2560] bf16 and the code-bias terms of the GEMV inputs,
  * -136 x (sum of a row's values), f32, [column block][8 rows] (rows >= the
- * plan's rows stay 0): weighted residual [160][8] and h [608][8] per 16
+ * plan's rows stay 0): weighted residual [160][8] per 16 columns, h [304][2][8] per 32
  * columns, attention output [128][8] per 32 columns.  Zeroed at every plan. */
 #define MK2_AUX_OFF (((MK2_STATE_WORDS * 4 + 255) / 256) * 256)
 #define MK2_AUX_XW 0
@@ -87,7 +88,8 @@ typedef struct {
     float* ssq;                    /* [MK2_MAX_ROWS][160] per-16-column sums of squares of x */
     uint16_t* xw;                  /* [rows][2560] bf16(x * the next RMSNorm's weight) */
     float* gsx;                    /* [160][8] code-bias terms of xw per 16 columns */
-    float* gsh;                    /* [608][8] of h per 16 columns */
+    float* gsh;                    /* [304][2][8] of h per 32 columns, in two parts: part 1
+                                      from a workgroup the group did not begin in (else 0) */
     float* gsa;                    /* [128][8] of attn per 32 columns */
     uint32_t* flags;               /* [MK2_F_KINDS][MK2_F_STRIDE] */
     uint32_t* state;               /* [0] launch epoch, [1] workgroups done (monotonic) */
