@@ -262,7 +262,17 @@ def main():
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / args.steps
 
-        mk2 = lib.s2p_backbone_mk_status(bb) == 1
+        # the timed steps must all have completed: a bounded flag wait of the
+        # persistent kernel that gave up makes a launch drain early (faster and
+        # wrong), so such a run reports no number
+        mk_status = lib.s2p_backbone_mk_status(bb)
+        n_acc_last = nacc.cpu().numpy()
+        if mk_status < 0 or np.any(n_acc_last < 0):
+            print(json.dumps({"error": "a flag wait of the persistent verify kernel timed out "
+                              "during the timed steps; no number is reported",
+                              "mk_status": int(mk_status)}), flush=True)
+            sys.exit(3)
+        mk2 = mk_status == 1
         if mk2:
             # dominant kernel: the persistent verify kernel k_mk2, the whole forward
             # (36 layers + head) in one launch; back-to-back launches on this stream,
@@ -275,6 +285,11 @@ def main():
             g1.record(side)
             side.synchronize()
             avg_launch_s = g0.elapsed_time(g1) / 1e3 / reps
+            if lib.s2p_backbone_mk_status(bb) != 1:
+                print(json.dumps({"error": "a flag wait of the persistent verify kernel timed "
+                                  "out during the roofline launches; no number is reported"}),
+                      flush=True)
+                sys.exit(3)
             _, _, per_launch = step_alg_bytes(lens, M, args.kv_bits)
             kern_gbs = per_launch / avg_launch_s / 1e9
             kern_name = "k_mk2 (persistent verify forward: 36 layers + head, one launch)"
@@ -345,6 +360,9 @@ def main():
         "step_hbm_gbs": round(step_gbs, 1),
         "step_frac_of_peak": round(step_gbs / PEAK_GBS, 4),
         "wall_s_timed": round(wall, 3),
+        # 1: the step ran on the persistent kernel and no bounded wait timed out
+        # (checked after the timed region); 0: the layer-by-layer forward
+        "mk_status": int(mk_status),
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / PEAK_GBS, 4),
                      "traffic": measured_traffic("mk2" if mk2 else "gemv") if headline else None,

@@ -112,8 +112,27 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
 
 /* Verify forward over the planned rows: x_in [n_sess*R, 2560] bf16 input
  * embeddings (read only); logits [n_sess*R, head_rows] bf16.  Appends every
- * row's K/V to its slot.  Asynchronous, capturable. */
+ * row's K/V to its slot.  Asynchronous, capturable.
+ *
+ * Plans of at most 6 rows over bf16 caches with INT4 weights run as ONE
+ * persistent launch of one workgroup per CU whose workgroups exchange data
+ * through flags in memory.  That needs every workgroup resident at once:
+ * while the forward runs, no other kernel may occupy the device's CUs (do
+ * not overlap it with work on another stream, e.g. a draft step).  Each wait
+ * is bounded; if one gives up (its producers were not resident), the launch
+ * still completes but its logits are not valid and the backbone's error word
+ * is set: s2p_verify_step then reports out_n_acc = -1 for every session, and
+ * s2p_verify_status reads the word.  The word stays set (every later forward
+ * also drains without waiting) until s2p_verify_status clears it or a new
+ * plan is uploaded. */
 s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, hipStream_t st);
+
+/* Status of the forwards since the word was last cleared, written to out
+ * (device or pinned host memory): 0 = every forward completed, 1 = a bounded
+ * wait of the persistent kernel timed out (logits invalid).  clear != 0
+ * resets the word.  Asynchronous (no host sync), capturable; with the
+ * layer-by-layer forward it always writes 0. */
+s2p_status s2p_verify_status(s2p_backbone* b, int32_t* out, int clear, hipStream_t st);
 
 /* Workspace of s2p_verify_accept. */
 size_t s2p_verify_accept_work_bytes(int n_sess, int rows);
@@ -170,7 +189,9 @@ s2p_status s2p_verify_kv_commit(s2p_backbone* b, const int32_t* out_path,
 
 /* One verify step (forward + acceptance) replayed from a hipGraph captured
  * on first use for the current plan shape; falls back to eager launches
- * when use_graph == 0. */
+ * when use_graph == 0.  When the forward's error word is set (see
+ * s2p_verify_forward) the acceptance decides nothing: out_n_acc[s] = -1,
+ * out_n_emit[s] = 0 and the sampler states are left unchanged. */
 typedef struct {
     const void* x_in;
     void* logits;                       /* target logits out */

@@ -392,63 +392,6 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
         /* a block's four activation reads are issued together, ahead of its
          * dequantisation (one LDS latency per 4 groups) */
         const LDS(uint16_t)* xrow = L.x + mrow[0] * L.xs + cg * 32 + q * 8;
-#ifdef GV_DOT2
-        /* Measurement variant (not the product): the main product on the
-         * VALU with v_dot2_f32_bf16 instead of the MFMA.  Lane (q, r) dots
-         * its 8 dequantised weights of row r with each staged row m's 8
-         * activations, scales per group, and the four q lanes of a row are
-         * summed at the end of the chunk; lane (q, r) keeps rows 4q..4q+3. */
-        typedef __attribute__((ext_vector_type(2))) __bf16 gv_bf2;
-        /* (a memcpy: __builtin_bit_cast of a vector element reads element 0) */
-        auto bf2 = [](uint32_t v) __attribute__((always_inline)) {
-            gv_bf2 r;
-            __builtin_memcpy(&r, &v, 4);
-            return r;
-        };
-        float pacc[16];
-#pragma unroll
-        for (int m = 0; m < 16; m++) pacc[m] = 0.f;
-        for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
-            if (it * 4 >= gn) break;
-            uint32_t d0 = B.w[it * 4 + 0], d1 = B.w[it * 4 + 1];
-            uint32_t d2 = B.w[it * 4 + 2], d3 = B.w[it * 4 + 3];
-            xpose4(d0, d1, d2, d3);
-            const uint32_t dj[4] = {d0, d1, d2, d3};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int g = it * 4 + j;
-                const s2p_u32x4 wv = deq_int4(dj[j], kmask, kone);
-                const uint32_t sw = (g & 2) ? B.sa[g >> 2].y : B.sa[g >> 2].x;
-                const float sf = (float)__builtin_bit_cast(
-                    _Float16, (uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
-#pragma unroll
-                for (int m = 0; m < 16; m++) {
-                    if (m < M) {
-                        const s2p_u32x4 xv = *(const LDS(s2p_u32x4)*)(L.x + m * L.xs + (cg + g) * 32 + q * 8);
-                        float p = __builtin_amdgcn_fdot2_f32_bf16(bf2(wv.x),
-                                                                  bf2(xv.x), 0.f, false);
-                        p = __builtin_amdgcn_fdot2_f32_bf16(bf2(wv.y),
-                                                            bf2(xv.y), p, false);
-                        p = __builtin_amdgcn_fdot2_f32_bf16(bf2(wv.z),
-                                                            bf2(xv.z), p, false);
-                        p = __builtin_amdgcn_fdot2_f32_bf16(bf2(wv.w),
-                                                            bf2(xv.w), p, false);
-                        pacc[m] = fmaf(sf, p, pacc[m]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < 16; m++) {
-            if (m < M) {
-                float t = pacc[m];
-                t += __shfl_xor(t, 16, 64);
-                t += __shfl_xor(t, 32, 64);
-                if ((m >> 2) == q) acc[0][m & 3] += t;
-            }
-        }
-        if (false)
-#endif
 #pragma unroll
         for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
             if (it * 4 >= gn) break;

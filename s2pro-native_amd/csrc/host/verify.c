@@ -75,6 +75,7 @@ struct s2p_backbone {
     Mk2Args mk2;           /* launch arguments of the current plan */
     int mk2_enabled;       /* off: layer-by-layer launches (env S2P_VERIFY_MK2=0) */
     int mk2_ready;         /* the current plan runs on the persistent kernel */
+    unsigned mk2_spin;     /* polls per flag wait (0: MK2_SPIN_LIMIT); tests shorten it */
     /* graph of one verify step */
     hipGraphExec_t gexec;
     int g_rows, g_nseg, g_span, g_valid;
@@ -283,6 +284,22 @@ void s2p_backbone_debug_ptrs(s2p_backbone* b, void** x, void** qkv, void** q, vo
  * launches timed out (-1, synchronises and clears the flag). */
 void s2p_backbone_set_mk(s2p_backbone* b, int on) {
     b->mk2_enabled = on && s2p_mk2_supported() == 0;
+}
+
+/* Test hook: polls per flag wait of later plans (0 = the default).  A tiny
+ * limit makes the waits give up early, which is how the tests reach the
+ * timeout path with every kernel still exiting normally. */
+void s2p_backbone_set_mk_spin(s2p_backbone* b, unsigned spins) {
+    b->mk2_spin = spins;
+    if (b->mk2_ready) b->mk2.spin_limit = spins ? spins : MK2_SPIN_LIMIT;
+}
+
+s2p_status s2p_verify_status(s2p_backbone* b, int32_t* out, int clear, hipStream_t st) {
+    if (!b || !out) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    /* the layer-by-layer forward has no bounded waits: always complete */
+    return hip_ok(s2p_word_status_launch(b->mk2_ready ? b->mk2.err : NULL, out, clear, st),
+                  "status");
 }
 
 int s2p_backbone_mk_status(s2p_backbone* b) {
@@ -521,6 +538,7 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
     A->flags = b->d_mk2;
     A->state = b->d_mk2 + MK2_STATE_WORD;
     A->err = (int*)(b->d_mk2 + MK2_ERR_WORD);
+    A->spin_limit = b->mk2_spin ? b->mk2_spin : MK2_SPIN_LIMIT;
     A->plan = row_plan(b);
     A->segs = b->d_segs;
     A->n_seg = b->n_seg;
@@ -589,11 +607,12 @@ static s2p_status accept_run(const void* tgt, const void* tgt_eos, int64_t tgt_e
                              const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
                              int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
                              int32_t* out_n_emit, void* work, const uint8_t* chain_ok,
-                             hipStream_t st) {
+                             const int* fwd_err, hipStream_t st) {
     if (tgt_stride != drf_stride) return S2P_ERR_INVALID;
     AcceptArgs a;
     memset(&a, 0, sizeof(a));
     a.chain_ok = chain_ok;
+    a.fwd_err = fwd_err;
     a.tgt = (const uint16_t*)tgt;
     a.tgt_eos = (const uint16_t*)tgt_eos;
     a.drf = (const uint16_t*)drf;
@@ -627,7 +646,7 @@ s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const 
     if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
     return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
                       parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
-                      work, NULL, st);
+                      work, NULL, NULL, st);
 }
 
 s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
@@ -645,7 +664,7 @@ s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
     if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
     return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
                       parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
-                      work, chain_ok, st);
+                      work, chain_ok, NULL, st);
 }
 
 s2p_status s2p_verify_chain(s2p_backbone* b, s2pfa* fa, const int32_t* parent, const int64_t* tok,
@@ -692,7 +711,8 @@ static s2p_status step_enqueue(s2p_backbone* b, const s2p_verify_step_io* io, hi
     return accept_run(lg, sliced ? lg + 4096 : NULL, ts, ts, dg, sliced ? dg + 4096 : NULL, ts,
                       io->drf_stride, io->parent_dev, io->tok_dev,
                       io->states_dev, b->n_sess, b->R, io->out_path, io->out_n_acc,
-                      io->out_emit, io->out_n_emit, io->work, NULL, st);
+                      io->out_emit, io->out_n_emit, io->work, NULL,
+                      b->mk2_ready ? b->mk2.err : NULL, st);
 }
 
 s2p_status s2p_verify_step(s2p_backbone* b, const s2p_verify_step_io* io, int use_graph,

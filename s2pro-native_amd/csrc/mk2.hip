@@ -62,7 +62,6 @@
 #ifndef NSLOT
 #define NSLOT 8 /* measured: 8 slots beat 20 and 10 (less queueing in front of the exchanges); 5 is 0.7% slower, 4 within 1% */
 #endif
-#define SPIN_LIMIT (1u << 22)
 #define LDSP(T) __attribute__((address_space(3))) T
 
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
@@ -493,7 +492,7 @@ S2P_DEV void flags_poll(const Mk2Args& A, int kind, int ia, int na, int ib, int 
         errw[j] = e == n;
         ptr[j] = e == n ? (const uint64_t*)A.err : (const uint64_t*)flag_at(A, kind, in ? 2 * p : 0);
     }
-    for (unsigned spins = 0; spins < SPIN_LIMIT; spins++) {
+    for (unsigned spins = 0; spins < A.spin_limit; spins++) {
         uint64_t r[NLD];
 #pragma unroll
         for (int j = 0; j < NLD; j++) r[j] = coh_ld64(ptr[j]);

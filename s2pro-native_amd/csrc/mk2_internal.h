@@ -53,6 +53,8 @@ extern "C" {
 #define MK2_ATT_MAX 3072
 #define MK2_MAX_LAYERS 40
 #define MK2_MAX_SPLIT 64
+/* default polls of one flag wait before it gives up (seconds, not a schedule) */
+#define MK2_SPIN_LIMIT (1u << 22)
 /* the backbone's mk2 state block (uint32 words): flags, then the launch
  * epoch and done count, the error flag.  Zeroed at every plan; within a
  * plan every word only grows. */
@@ -94,6 +96,7 @@ typedef struct {
     uint32_t* flags;               /* [MK2_F_KINDS][MK2_F_STRIDE] */
     uint32_t* state;               /* [0] launch epoch, [1] workgroups done (monotonic) */
     int* err;                      /* sticky: a wait timed out */
+    unsigned spin_limit;           /* polls per flag wait before it gives up */
     /* attention */
     S2pRowPlan plan;
     const S2pAttnSeg* segs;

@@ -674,3 +674,18 @@ extern "C" hipError_t s2p_chain_check_launch(const int32_t* stage, const int32_t
                        draft_codes, tok, chain_ok, codes_out, n_sess, R);
     return hipGetLastError();
 }
+
+/* The persistent forward's error word (word == NULL: a forward with no
+ * bounded waits, reported as 0) copied out, and cleared when asked: one
+ * thread, so it is capturable and needs no memset node. */
+__global__ void k_word_status(int* __restrict__ word, int32_t* __restrict__ out, int clear) {
+    const int v = word ? *(volatile int*)word : 0;
+    *out = v;
+    if (clear && v) *(volatile int*)word = 0;
+}
+
+extern "C" hipError_t s2p_word_status_launch(int* word, int32_t* out, int clear, hipStream_t st) {
+    if (!out) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_word_status, dim3(1), dim3(1), 0, st, word, out, clear);
+    return hipGetLastError();
+}

@@ -99,6 +99,9 @@ hipError_t s2p_kv_commit8_launch(const S2pRowPlan* plan, const int32_t* path,
 /* the chain condition of speculative frames (verify.c s2p_verify_chain):
  * gather each drafted node's parent hidden row and semantic code; compare
  * the fast-AR codes (stage [9][n_sess (R - 1)]) with the drafted ones */
+/* *out = *word (0: the forward completed, else a bounded wait timed out; a
+ * NULL word reads 0); clear != 0 also resets the word */
+hipError_t s2p_word_status_launch(int* word, int32_t* out, int clear, hipStream_t st);
 hipError_t s2p_chain_prep_launch(const int32_t* parent, const int64_t* tok, const void* hidden,
                                  void* par_hidden, int32_t* sem, int n_sess, int R, int dim,
                                  hipStream_t st);

@@ -483,6 +483,9 @@ __global__ __launch_bounds__(TX_THREADS) void k_accept_transform(AcceptArgs a) {
     const int gr = blockIdx.x;          /* global node row s * R + v */
     const int which = blockIdx.y;       /* 0 target, 1 draft */
     const int s = gr / a.R, v = gr - s * a.R;
+    /* a forward whose bounded wait timed out: its logits are not read (the
+     * walk reports the session as undecided) */
+    if (a.fwd_err && *(const volatile int*)a.fwd_err != 0) return;
     /* the state and the tree in one batch of loads */
     {
         const uint32_t* src = (const uint32_t*)a.states[s];
@@ -593,6 +596,15 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
     __shared__ uint8_t cok[64];
     const int s = blockIdx.x, lane = threadIdx.x;
     const int R = a.R;
+    if (a.fwd_err && *(const volatile int*)a.fwd_err != 0) {
+        /* the forward that produced the logits did not complete (a bounded
+         * wait of the persistent kernel timed out): decide nothing */
+        if (lane == 0) {
+            a.out_n_acc[s] = -1;
+            a.out_n_emit[s] = 0;
+        }
+        return;
+    }
     {
         /* everything the walk reads, in one batch of loads (the walk itself
          * then runs from LDS: a load per node would put a memory round trip

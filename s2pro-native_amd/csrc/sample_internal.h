@@ -32,6 +32,10 @@ typedef struct {
     const uint8_t*  chain_ok;  /* NULL, or [n_sess*R]: 0 = the node's drafted frame failed
                                   the chain condition (its token ends the walk, its row is
                                   not accepted) */
+    const int*      fwd_err;   /* NULL, or the forward's error word: when it is set the
+                                  logits are not trustworthy, so every session gets
+                                  out_n_acc = -1, out_n_emit = 0 and its state is left
+                                  as it was */
 } AcceptArgs;
 
 size_t     s2p_accept_work_bytes(int n_sess, int rows);

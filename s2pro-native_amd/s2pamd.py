@@ -190,6 +190,7 @@ SIGS = {
     "s2p_verify_chain": (I, [P, P, P, P, P, P, P, P]),
     "s2p_verify_accept_chain": (I, [P, P, P, P, I64, P, P, P, I, I, P, P, P, P, P, P, P]),
     "s2p_verify_step": (I, [P, P, I, P]),
+    "s2p_verify_status": (I, [P, P, I, P]),
 }
 
 # synthetic-data launchers (csrc/synth_internal.h), used by tests/benchmarks
@@ -198,6 +199,7 @@ EXTRA = {
     "s2p_test_f2bf": (I, [P, P, I64, P]),
     "s2p_test_desc_bytes": (SZ, [I]),
     "s2p_backbone_mk_status": (I, [P]),
+    "s2p_backbone_set_mk_spin": (None, [P, ctypes.c_uint]),
     "s2p_synth_bytes": (I, [P, I64, U64, P]),
     "s2p_synth_int8": (I, [P, I64, U64, P]),
     "s2p_synth_f16_absnormal": (I, [P, I64, F, U64, P]),

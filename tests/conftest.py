@@ -23,3 +23,17 @@ def _keep_device_buffers_alive():
         import torch
         torch.cuda.synchronize()
         gpu_util.LIVE.clear()
+
+
+def pytest_terminal_summary(terminalreporter):
+    """One line on the logits checks of this run: how close the GPU came to
+    the reference order, and whether any row used the exception cap."""
+    gu = sys.modules.get("gpu_util")
+    rec = getattr(gu, "LOGITS_RECORD", None)
+    if not rec:
+        return
+    worst = max(rec, key=lambda r: r[1])
+    n_exc = sum(r[2] for r in rec)
+    terminalreporter.write_line(
+        f"logits checks: {len(rec)} calls, {sum(r[3] for r in rec)} rows; largest per-row "
+        f"gpu-oracle L2 {worst[1]:.3e} ({worst[0]}); exception rows above 1e-2: {n_exc}")

@@ -14,6 +14,9 @@ _hip = None
 # the C ABI must never outlive their torch tensor, whose block the caching
 # allocator would otherwise hand to the next allocation.
 LIVE = []
+# (what, largest per-row gpu-oracle L2 distance, exception rows used, rows) of
+# every logits check, summarised at the end of the pytest run (conftest)
+LOGITS_RECORD = []
 
 
 def hip():

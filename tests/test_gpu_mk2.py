@@ -12,8 +12,10 @@ import torch
 
 import f64_forward as f64
 import s2pamd
-from gpu_util import P, S, assert_close_rel, bf16_bits, bf16_vals, empty, to_dev, to_host
-from test_gpu_verify import check_logits, f64_weights, make_backbone, new_kv, oracle_forward, plan
+import pyoracle as po
+from gpu_util import P, S, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
+from test_gpu_verify import (check_logits, f64_weights, host_layer, host_linear, make_backbone,
+                             new_kv, oracle_forward, plan)
 
 pytestmark = pytest.mark.gpu
 
@@ -111,3 +113,201 @@ def test_mk2_full_head_vs_oracle(lib):
         check_logits(got, want, truth, "mk2 full-head logits")
     finally:
         lib.s2p_backbone_free(bb)
+
+
+def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_rows):
+    """The oracle's reference-order forward and the binary64 forward of one
+    session, layer by layer (one layer's weights on the host at a time, so a
+    36-layer stack needs ~1 GB instead of ~30): returns (oracle logits bits,
+    binary64 logits)."""
+    import sys
+    import time
+    R = len(parent)
+    depth, vis = [0] * R, np.zeros(R, np.uint64)
+    for i in range(R):
+        if i:
+            depth[i] = depth[parent[i]] + 1
+        m, j = 0, i
+        while j >= 0:
+            m |= 1 << j
+            j = parent[j]
+        vis[i] = m
+    pos = np.array([L + d for d in depth], np.int32)
+    chain = all(parent[i] == i - 1 for i in range(1, R))
+    xo = np.array(x, np.uint16, copy=True)
+    x64 = f64.bf(x)
+    kv = kv_host.reshape(n_layers, 16, ctx, 128)
+    t0 = time.time()
+    for l in range(n_layers):
+        lw, keep = host_layer(lib, bb, l)
+        kc0 = f64.bf(kv[l, :8])
+        vc0 = f64.bf(kv[l, 8:])
+        kc = np.ascontiguousarray(kv[l, :8])
+        vc = np.ascontiguousarray(kv[l, 8:])
+        po.layer(lw, xo, R, kc, vc, ctx, L, pos, None if chain else vis)
+        W = {}
+        (w_qkv, w_o, w_gu, w_2), norms = keep[:4], keep[4]
+        Lr = lib.s2p_backbone_layer(bb, l).contents
+        for name, (w, sc) in zip(("wqkv", "wo", "gate_up", "w2"), (w_qkv, w_o, w_gu, w_2)):
+            lin = getattr(Lr, name)
+            W[name] = f64.dequant(w, sc, lin.out_features, lin.in_features)
+        for name, n in zip(("attn_norm", "ffn_norm", "q_norm", "k_norm"), norms):
+            W[name] = f64.bf(n)
+        x64 = f64.layer(W, x64, kc0, vc0, L, list(pos), [int(v) for v in vis])
+        del W
+        if l % 6 == 5:
+            print(f"  references: layer {l + 1}/{n_layers} ({time.time() - t0:.0f} s)", flush=True)
+            sys.stdout.flush()
+    fnorm = d2h(lib.s2p_backbone_final_norm(bb), 2560 * 2, np.uint16)
+    head, (hw, hs) = host_linear(lib.s2p_backbone_head(bb).contents)
+    want = po.linear_fwd(head, po.rms_norm(xo, fnorm, R, 2560), R)
+    hl = lib.s2p_backbone_head(bb).contents
+    truth = f64.rms(x64, f64.bf(fnorm)) @ f64.dequant(hw, hs, hl.out_features, hl.in_features).T
+    return want, truth
+
+
+@pytest.mark.timeout(400)
+def test_mk2_config3_depth_vs_oracle(lib):
+    """Config 3's exact backbone shape (36 INT4-g32 layers, K=4 chain, bf16
+    KV 2048, ctx 2304 as the bench plans it) on the persistent kernel,
+    against the oracle's 36-layer forward and binary64 (head: the 4,097-row
+    slice, so the CPU side stays ~1-2 minutes).  Pins what only full depth
+    exercises: every layer's weight block base, flag values and KV plane
+    strides.  No flag wait may time out."""
+    ctx, n_layers, parent, L = 2304, 36, [-1, 0, 1, 2, 3], 2048
+    R = len(parent)
+    print("config-3 depth test: building the 36-layer backbone", flush=True)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 8, 1, ctx, 2026)
+    try:
+        kv = new_kv(lib, bb, 31)
+        kv_host = to_host(kv, np.uint16).copy()
+        plan(lib, bb, parent, [kv], [L])
+        assert lib.s2p_backbone_mk_status(bb) == 1, "plan did not run on the persistent kernel"
+        x = bf16_bits(np.random.default_rng(36).standard_normal((R, 2560)).astype(np.float32))
+        got = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE))
+        assert lib.s2p_backbone_mk_status(bb) == 1, "a flag wait timed out"
+        kv_dev = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
+        print("config-3 depth test: GPU forward done, running the references", flush=True)
+        want, truth = _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent,
+                                           s2pamd.S2P_HEAD_SLICE)
+        check_logits(got, want, truth, "mk2 36-layer logits")
+        # every layer appended its rows at L..L+R-1 and touched nothing else
+        kv0 = kv_host.reshape(n_layers, 16, ctx, 128)
+        assert np.array_equal(kv_dev[:, :, :L], kv0[:, :, :L])
+        assert np.array_equal(kv_dev[:, :, L + R:], kv0[:, :, L + R:])
+        assert np.all(np.any(kv_dev[:, :, L:L + R] != kv0[:, :, L:L + R], axis=(2, 3))), \
+            "a layer's K/V plane was not appended"
+    finally:
+        lib.s2p_backbone_free(bb)
+
+
+@pytest.mark.timeout(200)
+def test_mk2_config3_full_head_vs_layer_path(lib):
+    """Config 3 end to end (36 layers, the full 155,776-row head): the
+    persistent kernel and the layer-by-layer path agree per row within the
+    logits bar, and neither run timed out."""
+    ctx, n_layers, parent, L = 2304, 36, [-1, 0, 1, 2, 3], 2048
+    R = len(parent)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB, 8, 1, ctx, 7)
+    try:
+        kv = new_kv(lib, bb, 11)
+        kv_host = to_host(kv, np.uint16).copy()
+        x = bf16_bits(np.random.default_rng(1).standard_normal((R, 2560)).astype(np.float32))
+        out = {}
+        for mode in (1, 0):
+            lib.s2p_backbone_set_mk(bb, mode)
+            kv.copy_(torch.from_numpy(kv_host.view(np.int16)).to(kv.device))
+            plan(lib, bb, parent, [kv], [L])
+            assert lib.s2p_backbone_mk_status(bb) == mode
+            out[mode] = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_VOCAB))
+            assert lib.s2p_backbone_mk_status(bb) == mode, "a flag wait timed out"
+        rel = np.linalg.norm(out[1] - out[0], axis=1) / np.linalg.norm(out[0], axis=1)
+        print("36-layer full head, mk2 vs layer path, per-row L2 rel:", rel)
+        assert np.all(rel < 1e-2), rel
+    finally:
+        lib.s2p_backbone_set_mk(bb, 1)
+        lib.s2p_backbone_free(bb)
+
+
+def test_mk2_wait_timeout_is_reported(lib):
+    """A flag wait that gives up (forced from the host with a tiny poll
+    limit, so every workgroup still drains and exits normally) is reported
+    on the product path: the step's acceptance decides nothing (n_acc = -1,
+    n_emit = 0, state untouched) and s2p_verify_status reads 1; after the
+    word is cleared and the limit restored, the same step is valid again and
+    matches the eager forward of a fresh plan."""
+    import ctypes
+    ctx, n_layers, parent, L = 512, 2, [-1, 0, 1, 2, 3], 200
+    R = len(parent)
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 8, 1, ctx, 99)
+        try:
+            kv = new_kv(lib, bb, 5)
+            plan(lib, bb, parent, [kv], [L])
+            assert lib.s2p_backbone_mk_status(bb) == 1
+            x = to_dev(bf16_bits(np.random.default_rng(4).standard_normal((R, 2560))
+                                 .astype(np.float32)))
+            ref = _forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE)
+            st = po.state(temperature=0.8, top_p=0.8, seed=3, entropy=0)
+            st_bytes = np.frombuffer(bytes(st), np.uint8).copy()
+            drf = to_dev(bf16_bits(bf16_vals(ref) + 0.5 * np.random.default_rng(5)
+                                   .standard_normal(ref.shape).astype(np.float32)))
+            tok = np.zeros(R, np.int64)
+            sd = po.copy_state(st)
+            dv = to_host(drf, np.uint16)
+            for i in range(1, R):
+                tok[i] = po.sample(sd, dv[i - 1, :4096], int(dv[i - 1, 4096]))[0]
+            d_states = to_dev(st_bytes)
+            d_ptrs = to_dev(np.array([d_states.data_ptr()], np.int64))
+            work = torch.empty(lib.s2p_verify_accept_work_bytes(1, R), dtype=torch.uint8,
+                               device="cuda")
+            path = torch.zeros(R, dtype=torch.int32, device="cuda")
+            nacc = torch.zeros(1, dtype=torch.int32, device="cuda")
+            emit = torch.zeros(R + 1, dtype=torch.int64, device="cuda")
+            nemit = torch.zeros(1, dtype=torch.int32, device="cuda")
+            status = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+            logits = empty((R, s2pamd.S2P_HEAD_SLICE))
+            io = s2pamd.StepIO(x.data_ptr(), logits.data_ptr(), drf.data_ptr(),
+                               s2pamd.S2P_HEAD_SLICE,
+                               to_dev(np.array(parent, np.int32)).data_ptr(),
+                               to_dev(tok).data_ptr(), d_ptrs.data_ptr(), path.data_ptr(),
+                               nacc.data_ptr(), emit.data_ptr(), nemit.data_ptr(),
+                               work.data_ptr())
+            # healthy step first: status 0
+            s2pamd.check(lib.s2p_verify_status(bb, P(status), 0, S()))
+            assert int(to_host(status)[0]) == 0
+            # forced timeout: 1 poll per wait
+            lib.s2p_backbone_set_mk_spin(bb, 1)
+            for use_graph in (0, 1):
+                d_states.copy_(torch.from_numpy(st_bytes).to(d_states.device))
+                s2pamd.check(lib.s2p_verify_step(bb, ctypes.byref(io), use_graph, S()), "step")
+                assert int(to_host(nacc)[0]) == -1, "a timed-out forward was accepted"
+                assert int(to_host(nemit)[0]) == 0
+                assert np.array_equal(to_host(d_states, np.uint8), st_bytes), "state advanced"
+                s2pamd.check(lib.s2p_verify_status(bb, P(status), 0, S()))
+                assert int(to_host(status)[0]) == 1
+            # recovery: default limit, clear the word, the step is valid again
+            lib.s2p_backbone_set_mk_spin(bb, 0)
+            s2pamd.check(lib.s2p_verify_status(bb, P(status), 1, S()))
+            assert int(to_host(status)[0]) == 1
+            d_states.copy_(torch.from_numpy(st_bytes).to(d_states.device))
+            s2pamd.check(lib.s2p_verify_step(bb, ctypes.byref(io), 1, S()), "step")
+            assert lib.s2p_backbone_mk_status(bb) == 1
+            s2pamd.check(lib.s2p_verify_status(bb, P(status), 0, S()))
+            assert int(to_host(status)[0]) == 0
+            assert int(to_host(nacc)[0]) >= 0
+            lg = to_host(logits, np.uint16)
+            # the K/V rows the drained launches wrote are rewritten by this one,
+            # so its logits equal the first forward's
+            assert np.array_equal(lg, ref)
+            p_ref, e_ref = po.accept_tree(po.copy_state(st), np.ascontiguousarray(lg[:, :4096]),
+                                          np.ascontiguousarray(dv[:, :4096]), parent, tok,
+                                          np.ascontiguousarray(lg[:, 4096]),
+                                          np.ascontiguousarray(dv[:, 4096]))
+            n = int(to_host(nemit)[0])
+            assert (int(to_host(nacc)[0]), list(to_host(emit)[:n])) == (len(p_ref), list(e_ref))
+        finally:
+            lib.s2p_backbone_free(bb)
+    torch.cuda.synchronize()

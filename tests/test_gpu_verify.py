@@ -19,6 +19,7 @@ import torch
 import pyoracle as po
 import s2pamd
 import f64_forward as f64
+import gpu_util
 from gpu_util import P, S, assert_close_norm, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
@@ -138,31 +139,38 @@ LOGITS_REL = 1e-2  # logits within 1e-2 of the reference
 LOGITS_CAP = 2e-2  # hard cap for a named exception row (see check_logits)
 
 
-def check_logits(got, want_bits, truth, what, rms=True):
+def check_logits(got, want_bits, truth, what, rms=True, allow_exceptions=False):
     """Per-row tolerance against the oracle and (rms=True) the accuracy
     criterion over these rows; callers pooling several sessions pass
-    rms=False and apply check_rms to all rows at once."""
+    rms=False and apply check_rms to all rows at once.
+
+    The bar is 1e-2 L2-relative per row against the reference order.  Only a
+    caller that passes allow_exceptions=True (and names why in its docstring)
+    may let a row exceed it, and then only when the GPU row is at least as
+    close to binary64 as the reference order is (the distance is then the
+    reference order's own rounding error), and never beyond LOGITS_CAP.
+    Every call is recorded (gpu_util.LOGITS_RECORD) and summarised at the end
+    of the pytest run: the largest gpu-oracle distance and the exception rows
+    used."""
     want = bf16_vals(want_bits)
     tn = np.linalg.norm(truth, axis=1)
     rows = [f"{r}: gpu {np.linalg.norm(got[r] - truth[r]) / tn[r]:.2e} "
             f"oracle {np.linalg.norm(want[r] - truth[r]) / tn[r]:.2e} "
             f"gpu-oracle {np.linalg.norm(got[r] - want[r]) / tn[r]:.2e}" for r in range(len(got))]
     print(what, "per-row L2 rel err vs binary64:\n  " + "\n  ".join(rows))
-    # The bar is 1e-2 L2-relative per row against the reference order.  A row
-    # may exceed it only when the GPU row is at least as close to binary64 as
-    # the reference order is (the distance is then the reference order's own
-    # rounding error), and never beyond LOGITS_CAP; such rows are printed
-    # with their numbers as named exceptions.
     e_ref = np.linalg.norm(want - truth, axis=1) / tn
     e_gpu = np.linalg.norm(got - truth, axis=1) / tn
     d = np.linalg.norm(got - want, axis=1) / np.maximum(np.linalg.norm(want, axis=1), 1e-30)
     exc = (d > LOGITS_REL) & (e_gpu <= e_ref)
+    if not allow_exceptions:
+        exc[:] = False
     tol = np.where(exc, LOGITS_CAP, LOGITS_REL)
     for r in np.nonzero(exc)[0]:
         print(f"{what}: EXCEPTION row {r}: gpu-oracle {d[r]:.3e} > {LOGITS_REL:g}, gpu vs "
               f"binary64 {e_gpu[r]:.3e} <= oracle vs binary64 {e_ref[r]:.3e}")
     print(f"{what}: largest per-row tolerance applied {tol.max():g} "
           f"(largest gpu-oracle {d.max():.3e}, {int(exc.sum())} exception rows)")
+    gpu_util.LOGITS_RECORD.append((what, float(d.max()), int(exc.sum()), len(d)))
     assert_close_norm(got, want, rel=tol, what=what)
     if rms:
         check_rms(got, want, truth, what)
@@ -299,6 +307,8 @@ def _full_size_body(lib, ctx):
             del keep
         assert outs[0] == outs[1] == outs[2]
         assert states
+        # the plan ran on the persistent kernel and no flag wait timed out
+        assert lib.s2p_backbone_mk_status(bb) == 1
     finally:
         lib.s2p_backbone_free(bb)
 
