@@ -110,6 +110,19 @@ typedef struct {
  * ctx_len. */
 s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStream_t st);
 
+/* Re-plan the current shape (same sessions, caches and draft shape) from
+ * device KV lengths kv_len_dev [n_sess]: every row's position and slot,
+ * each segment's prefix and the RoPE table, on the device.  Asynchronous,
+ * capturable, no host copy: consecutive verify steps replayed from one graph
+ * can advance their sessions (kv_len += 1 + n_accepted) without a host round
+ * trip.  Lengths must stay within the span the last s2p_verify_plan sized
+ * its launches for (the largest L + R of that plan rounded up to 512, at
+ * most ctx_len): a session with L + R beyond it keeps its previous plan and
+ * sets *overflow = 1 (overflow may be NULL); re-plan on the host before
+ * that. */
+s2p_status s2p_verify_plan_device(s2p_backbone* b, const int32_t* kv_len_dev, int32_t* overflow,
+                                  hipStream_t st);
+
 /* Verify forward over the planned rows: x_in [n_sess*R, 2560] bf16 input
  * embeddings (read only); logits [n_sess*R, head_rows] bf16.  Appends every
  * row's K/V to its slot.  Asynchronous, capturable.

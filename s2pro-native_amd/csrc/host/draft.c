@@ -328,15 +328,18 @@ static s2p_status draft_gemv(const s2p_tensor* w, int N, int K, const void* x, v
     return S2P_OK;
 }
 
-s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h, const void* e,
-                          void* out, hipStream_t st) {
+/* The step at a host position (pos_dev == NULL: pos, attention span pos + 1)
+ * or at the device position *pos_dev + pos, clamped below span_max, with
+ * the attention launched for span_max slots. */
+static s2p_status draft_step_at(s2p_draft_model* m, s2p_draft_state* s, const void* h,
+                                const void* e, void* out, const int32_t* pos_dev, int pos,
+                                int span_max, hipStream_t st) {
     if (!m || !s || !h || !e || !out || !m->fuse.data || !s->kc.data) return S2P_ERR_INVALID;
-    if (s->pos < 0 || s->pos >= S2P_DRAFT_CTX) return S2P_ERR_INVALID;
     if (!is_view_after(&m->w1, &m->w3) || !is_view_after(&s->kc, &s->vc) ||
         m->a.bytes < ws_bytes())
         return S2P_ERR_STATE; /* not made by s2p_draft_load / s2p_draft_state_init */
     if (!s2p_gemm_ctx_part()) return S2P_ERR_STATE; /* s2p_gemm_init not called */
-    const int D = D_DIM, F = D_FFN, pos = s->pos;
+    const int D = D_DIM, F = D_FFN;
     unsigned char* ws = (unsigned char*)m->a.data;
     float* ssq_a = (float*)(ws + WS_SSQ_A);
     float* ssq_b = (float*)(ws + WS_SSQ_B);
@@ -357,8 +360,9 @@ s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h,
     HIPTRY(hipMemcpyAsync(BF(m->xcat), h, (size_t)D * 2, hipMemcpyDeviceToDevice, st));
     HIPTRY(hipMemcpyAsync(BF(m->xcat) + D, e, (size_t)D * 2, hipMemcpyDeviceToDevice, st));
     /* plan, RoPE row, x = 0, counters = 0 */
-    HIPTRY(s2p_draft_prologue_launch(&plan, seg, s->kc.data, pos, D_ROPE_BASE, (float*)(ws + WS_ROPE),
-                                     m->x.data, D, (unsigned*)(ws + WS_CTR), WS_NCTR, st));
+    HIPTRY(s2p_draft_prologue_launch(&plan, seg, s->kc.data, pos, pos_dev, span_max, D_ROPE_BASE,
+                                     (float*)(ws + WS_ROPE), m->x.data, D,
+                                     (unsigned*)(ws + WS_CTR), WS_NCTR, st));
     /* x = 0 + fuse · [h ; e], and its sums of squares */
     TRY(draft_gemv(&m->fuse, D, 2 * D, m->xcat.data, m->x.data, GEMV_X_PLAIN, NULL, NULL,
                    GEMV_EPI_RESID, ssq_a, st));
@@ -367,7 +371,7 @@ s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h,
                    ssq_a, GEMV_EPI_STORE, NULL, st));
     /* qk-norm, RoPE, K/V append at slot pos and attention over [0, pos]
      * (the normed q rows land in xcat, no longer needed) */
-    HIPTRY(s2p_attn_plan_fused_launch(m->xcat.data, m->attn.data, &plan, seg, 1, 1, 0, pos + 1,
+    HIPTRY(s2p_attn_plan_fused_launch(m->xcat.data, m->attn.data, &plan, seg, 1, 1, 0, span_max,
                                       (float*)(ws + WS_PART), m->qkv.data, m->q_norm.data,
                                       m->k_norm.data, (const float*)(ws + WS_ROPE), D_EPS,
                                       (unsigned*)(ws + WS_CTR), st));
@@ -382,8 +386,25 @@ s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h,
                    NULL, st));
     /* the predicted next final-normed hidden */
     HIPTRY(s2pk_rms_norm(BF(m->x), BF(m->final_norm), (s2p_bf16*)out, 1, D, D_EPS, st));
+    return S2P_OK;
+}
+
+s2p_status s2p_draft_step(s2p_draft_model* m, s2p_draft_state* s, const void* h, const void* e,
+                          void* out, hipStream_t st) {
+    if (!s || s->pos < 0 || s->pos >= S2P_DRAFT_CTX) return S2P_ERR_INVALID;
+    TRY(draft_step_at(m, s, h, e, out, NULL, s->pos, s->pos + 1, st));
     s->pos++;
     return S2P_OK;
+}
+
+/* Internal (the speculative tick): the step at position *pos_dev + pos_add
+ * read on the device, attention launched for span_max <= S2P_DRAFT_CTX slots
+ * (the position is clamped below it); s->pos is not used or advanced. */
+s2p_status s2p_draft_step_dev(s2p_draft_model* m, s2p_draft_state* s, const void* h,
+                              const void* e, void* out, const int32_t* pos_dev, int pos_add,
+                              int span_max, hipStream_t st) {
+    if (!pos_dev || span_max < 1 || span_max > S2P_DRAFT_CTX) return S2P_ERR_INVALID;
+    return draft_step_at(m, s, h, e, out, pos_dev, pos_add, span_max, st);
 }
 
 /* One GEMV over rows [r0, r0 + n) of a quantised linear, outputs into
@@ -418,6 +439,24 @@ static s2p_status head_rows(const s2p_linear* lin, int r0, int n, const void* x,
     a.counters = s2p_gemm_ctx_counters();
     HIPTRY(s2p_gemv_launch(&a, st));
     return S2P_OK;
+}
+
+/* Internal (the speculative tick): q logits of rows hidden rows written into
+ * rows of a target-logits layout: ldy elements apart, width W = the head's
+ * out_features (the 4,097-row slice, or the full vocabulary with the slice's
+ * rows at their vocabulary columns; the other columns are not written). */
+s2p_status s2p_draft_head_into(const s2p_linear* head, const void* hidden, int rows, void* y,
+                               int64_t ldy, hipStream_t st) {
+    if (!head || !hidden || !y || rows < 1 || rows > 16 || head->in_features != D_DIM)
+        return S2P_ERR_INVALID;
+    if (!s2p_gemm_ctx_part()) return S2P_ERR_STATE;
+    uint16_t* o = (uint16_t*)y;
+    if (head->out_features == S2P_DRAFT_HEAD_ROWS)
+        return head_rows(head, 0, S2P_DRAFT_HEAD_ROWS, hidden, rows, o, (int)ldy, st);
+    if (head->out_features < S2P_TOK_SEMANTIC_START + 4096) return S2P_ERR_INVALID;
+    TRY(head_rows(head, S2P_TOK_SEMANTIC_START, 4096, hidden, rows, o + S2P_TOK_SEMANTIC_START,
+                  (int)ldy, st));
+    return head_rows(head, S2P_TOK_EOS, 1, hidden, rows, o + S2P_TOK_EOS, (int)ldy, st);
 }
 
 s2p_status s2p_draft_head(const s2p_linear* head, const void* hidden, void* logits, int rows,

@@ -1,417 +1,595 @@
 /* s2pro MI355X — prequantized-weight sidecar cache (include/s2pro/qcache.h).
  *
- * On-disk layout, kept byte-compatible with the reference
- * (src/sched/qcache.c:1-16; little-endian, payload offsets absolute and
- * 256-aligned, payloads in entry order, zero padding between them):
- *   u8 magic[8] "S2PQC\1\0\0" | u64 fingerprint | u32 n_entries | u32 0
- *   n x { u32 name_len, u32 kind, i32 N, i32 K, i32 group, u32 0,
- *         u64 q_off, u64 q_len, u64 s_off, u64 s_len, char name[name_len] }
- *   payloads
- * kind 1: per-channel INT8 (i8 [N][K], f32 [N]); kind 2: packed INT4
- * (u8 [N][K/2], f16 [N][K/G]); kind 3: INT4 codes in int8 (i8 [N][K],
- * f16 [N][K/G]).
+ * File format (kept so that a file written by either build is read by the
+ * other; reference src/sched/qcache.c:1-16): little-endian;
+ *   [0,8)   magic "S2PQC" 1 0 0      [8,16)  u64 stamp of the weights/settings
+ *   [16,20) u32 descriptor count     [20,24) u32 zero
+ *   count descriptors of 56 bytes, each followed by its name (no NUL):
+ *     u32 name bytes, u32 kind, i32 N, i32 K, i32 group, u32 zero,
+ *     u64 codes offset, u64 codes bytes, u64 scales offset, u64 scales bytes
+ *   payloads at absolute 256-aligned offsets, in descriptor order, codes then
+ *   scales, zero padding between them.
+ * Kinds: 1 per-channel INT8 (i8 [N][K] + f32 [N]), 2 packed INT4 (u8
+ * [N][K/2] + f16 [N][K/group]), 3 INT4 codes one per byte (i8 [N][K] + f16
+ * [N][K/group]).
  *
- * Reading maps the file instead of copying it into memory: the header is
- * parsed and bounds-checked in place, and a hit uploads straight from the
- * mapping; the mapping is released by s2p_qcache_finish once the stream's
- * uploads are complete.  Writing snapshots each linear's device tensors to
- * host memory at put time and writes the file at finish through a temporary
- * file and a rename, so a reader never sees a partial cache.  Every read
- * failure degrades to a miss and every write failure to "no cache". */
+ * This implementation never holds a whole model on the host:
+ * - Reading keeps the file open and only its descriptor table in memory
+ *   (sorted by name for lookups).  A hit streams the payload with pread()
+ *   through two pinned staging chunks, each H2D copy overlapping the next
+ *   read; a chunk is reused once the event recorded after its copy has
+ *   completed.  A file that shrinks or fails to read mid-load turns that
+ *   lookup into a miss (no mapping, so no SIGBUS).
+ * - Writing spools each linear's payload to a side file as it is put (one
+ *   bounded host chunk at a time) and, at finish, writes header + table +
+ *   the spooled payloads to a temporary file that is renamed over the cache,
+ *   so readers never see a partial file.
+ * Every read failure is a miss (the caller quantises live) and every write
+ * failure leaves no cache behind. */
 #define _GNU_SOURCE
 #include "s2pro/qcache.h"
 
 #include <dirent.h>
+#include <errno.h>
 #include <fcntl.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
-#include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
-#define QC_HDR 24
-#define QC_ENT 56
-#define QC_ALIGN 256
-#define QC_MAX 512
-#define QC_MAX_NAME 512
-#define QC_MAX_FILES 256
+enum {
+    HEAD_BYTES = 24,
+    DESC_BYTES = 56,
+    PAYLOAD_ALIGN = 256,
+    MAX_DESCS = 512,
+    MAX_NAME = 512,
+    MAX_WEIGHT_FILES = 256,
+};
+#define CHUNK_BYTES ((size_t)8 << 20)
 
-static const unsigned char qc_magic[8] = {'S', '2', 'P', 'Q', 'C', 1, 0, 0};
+static const unsigned char k_magic[8] = {0x53, 0x32, 0x50, 0x51, 0x43, 0x01, 0x00, 0x00};
 
 typedef struct {
     char* name;
     uint32_t kind;
-    int32_t N, K, group;
-    uint64_t q_off, q_len, s_off, s_len;
-    void* qh; /* write mode: host snapshots */
-    void* sh;
-} qc_ent;
+    int32_t n, k, group;
+    uint64_t codes_at, codes_len, scales_at, scales_len; /* write mode: spool-relative */
+} qc_desc;
 
 struct s2p_qcache {
-    char path[1024];
+    char file[1024];
     int reading;
-    uint64_t fp;
-    unsigned char* map; /* read mode: the mapped file */
-    size_t map_len;
-    int n;
-    qc_ent e[QC_MAX];
+    uint64_t stamp;
+    int count;
+    qc_desc desc[MAX_DESCS];
+    /* read mode */
+    int fd;
+    uint64_t file_len;
+    int by_name[MAX_DESCS];
+    unsigned char* stage[2];
+    int stage_pinned;
+    hipEvent_t copied[2];
+    int copied_live[2];
+    int turn;
+    /* write mode */
+    FILE* spool;
+    char spool_path[1100];
+    uint64_t spool_len;
+    int spool_failed;
 };
 
-/* FNV-1a, 64-bit (offset basis 0xcbf29ce484222325, prime 0x100000001b3) */
-static uint64_t fnv1a(uint64_t h, const void* p, size_t n) {
-    const unsigned char* b = (const unsigned char*)p;
-    for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 0x100000001b3ull;
+/* ------------------------------------------------------------- helpers */
+
+static uint64_t fnv1a64(uint64_t h, const void* bytes, size_t n) {
+    for (const unsigned char *p = (const unsigned char*)bytes, *e = p + n; p < e; p++) {
+        h ^= *p;
+        h *= 0x100000001b3ull;
+    }
     return h;
 }
 
-/* unset or empty: def; exactly "1": 1; anything else: 0 */
-static int env_flag(const char* name, int def) {
-    const char* v = getenv(name);
-    if (!v || !v[0]) return def;
-    return strcmp(v, "1") == 0;
+static uint32_t get_u32(const unsigned char* p) {
+    return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+static uint64_t get_u64(const unsigned char* p) { return get_u32(p) | (uint64_t)get_u32(p + 4) << 32; }
+static void put_u32(unsigned char* p, uint32_t v) {
+    for (int i = 0; i < 4; i++) p[i] = (unsigned char)(v >> (8 * i));
+}
+static void put_u64(unsigned char* p, uint64_t v) {
+    put_u32(p, (uint32_t)v);
+    put_u32(p + 4, (uint32_t)(v >> 32));
+}
+static uint64_t round_up(uint64_t v) { return (v + PAYLOAD_ALIGN - 1) / PAYLOAD_ALIGN * PAYLOAD_ALIGN; }
+
+/* a settings switch: unset or empty -> fallback, "1" -> 1, else 0 */
+static int switch_on(const char* var, int fallback) {
+    const char* v = getenv(var);
+    return (!v || !*v) ? fallback : strcmp(v, "1") == 0;
 }
 
-static int by_name(const void* a, const void* b) {
-    return strcmp(*(char* const*)a, *(char* const*)b);
+typedef struct {
+    char name[256];
+    int64_t size, mtime;
+} weight_file;
+
+static int weight_file_order(const void* a, const void* b) {
+    return strcmp(((const weight_file*)a)->name, ((const weight_file*)b)->name);
 }
 
-/* the quantisation config string, then (name, size, mtime) of every
- * *.safetensors of the directory in name order */
-static int fingerprint(const char* dir, s2p_gemm_mode mode, uint64_t* out) {
-    char cfg[256];
-    const char* g = getenv("S2P_INT4_GROUP");
-    snprintf(cfg, sizeof(cfg), "v1|mode=%d|int4=%d|g=%s|mse=%d|pk=%d|all=%d", (int)mode,
-             env_flag("S2P_INT4", 0), g ? g : "32", env_flag("S2P_INT4_MSE", 1),
-             env_flag("S2P_INT4_PACKED", 1), env_flag("S2P_INT4_ALL", 0));
-    uint64_t h = fnv1a(0xcbf29ce484222325ull, cfg, strlen(cfg));
+/* The stamp a cache file must carry to be served: FNV-1a 64 over the
+ * quantisation settings string, then name, size and mtime of every
+ * *.safetensors of the model directory in byte order of the names
+ * (reference qcache.c:69-107; the string and the order are the format). */
+static int weights_stamp(const char* dir, s2p_gemm_mode mode, uint64_t* stamp) {
     DIR* d = opendir(dir);
     if (!d) return -1;
-    char* names[QC_MAX_FILES];
+    weight_file* files = (weight_file*)malloc(sizeof(weight_file) * MAX_WEIGHT_FILES);
+    if (!files) {
+        closedir(d);
+        return -1;
+    }
     int n = 0;
-    for (struct dirent* de; (de = readdir(d)) != NULL && n < QC_MAX_FILES;) {
+    const struct dirent* de;
+    while (n < MAX_WEIGHT_FILES && (de = readdir(d)) != NULL) {
         const size_t len = strlen(de->d_name);
-        if (len > 12 && strcmp(de->d_name + len - 12, ".safetensors") == 0) {
-            names[n] = strdup(de->d_name);
-            if (names[n]) n++;
-        }
+        if (len <= 12 || len >= sizeof(files[0].name) ||
+            memcmp(de->d_name + len - 12, ".safetensors", 12) != 0)
+            continue;
+        char path[1400];
+        struct stat st;
+        snprintf(path, sizeof(path), "%s/%s", dir, de->d_name);
+        if (stat(path, &st) != 0) continue;
+        memcpy(files[n].name, de->d_name, len + 1);
+        files[n].size = (int64_t)st.st_size;
+        files[n].mtime = (int64_t)st.st_mtime;
+        n++;
     }
     closedir(d);
-    if (n == 0) return -1;
-    qsort(names, (size_t)n, sizeof(names[0]), by_name);
-    for (int i = 0; i < n; i++) {
-        char full[1400];
-        struct stat st;
-        snprintf(full, sizeof(full), "%s/%s", dir, names[i]);
-        if (stat(full, &st) == 0) {
-            const int64_t size = (int64_t)st.st_size, mtime = (int64_t)st.st_mtime;
-            h = fnv1a(h, names[i], strlen(names[i]));
-            h = fnv1a(h, &size, 8);
-            h = fnv1a(h, &mtime, 8);
-        }
-        free(names[i]);
+    if (n == 0) {
+        free(files);
+        return -1;
     }
-    *out = h;
+    qsort(files, (size_t)n, sizeof(files[0]), weight_file_order);
+    const char* group = getenv("S2P_INT4_GROUP");
+    char settings[256];
+    const int sl = snprintf(settings, sizeof(settings), "v1|mode=%d|int4=%d|g=%s|mse=%d|pk=%d|all=%d",
+                            (int)mode, switch_on("S2P_INT4", 0), group ? group : "32",
+                            switch_on("S2P_INT4_MSE", 1), switch_on("S2P_INT4_PACKED", 1),
+                            switch_on("S2P_INT4_ALL", 0));
+    uint64_t h = fnv1a64(0xcbf29ce484222325ull, settings, (size_t)sl);
+    for (int i = 0; i < n; i++) {
+        h = fnv1a64(h, files[i].name, strlen(files[i].name));
+        h = fnv1a64(h, &files[i].size, 8);
+        h = fnv1a64(h, &files[i].mtime, 8);
+    }
+    free(files);
+    *stamp = h;
     return 0;
 }
 
-static uint32_t rd32(const unsigned char* p) {
-    uint32_t v;
-    memcpy(&v, p, 4);
-    return v;
-}
-static uint64_t rd64(const unsigned char* p) {
-    uint64_t v;
-    memcpy(&v, p, 8);
-    return v;
-}
-/* [off, off + len) inside a file of sz bytes, without overflow */
-static int in_file(uint64_t off, uint64_t len, uint64_t sz) { return off <= sz && len <= sz - off; }
-
-static void drop_entries(s2p_qcache* qc) {
-    for (int i = 0; i < qc->n; i++) {
-        free(qc->e[i].name);
-        free(qc->e[i].qh);
-        free(qc->e[i].sh);
+/* payload bytes a descriptor of this kind and shape must have; 0: invalid */
+static int expected_lengths(uint32_t kind, int32_t n, int32_t k, int32_t group, uint64_t* codes,
+                            uint64_t* scales) {
+    if (n <= 0 || k <= 0) return 0;
+    const uint64_t N = (uint64_t)n, K = (uint64_t)k;
+    switch (kind) {
+    case 1:
+        *codes = N * K;
+        *scales = 4 * N;
+        return 1;
+    case 2:
+    case 3:
+        if (group <= 0 || k % group || (kind == 2 && k % 2)) return 0;
+        *codes = kind == 2 ? N * K / 2 : N * K;
+        *scales = 2 * N * (K / (uint64_t)group);
+        return 1;
+    default:
+        return 0;
     }
-    memset(qc->e, 0, sizeof(qc->e[0]) * (size_t)qc->n);
-    qc->n = 0;
 }
 
-/* map the file and parse its header; any inconsistency leaves write mode */
-static void read_header(s2p_qcache* qc) {
-    const int fd = open(qc->path, O_RDONLY);
-    if (fd < 0) return;
-    struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size < QC_HDR) {
-        close(fd);
-        return;
+static void forget_descs(s2p_qcache* qc) {
+    for (int i = 0; i < qc->count; i++) free(qc->desc[i].name);
+    qc->count = 0;
+}
+
+/* ---------------------------------------------------------------- read */
+
+static int pread_all(int fd, void* dst, size_t len, uint64_t at) {
+    unsigned char* p = (unsigned char*)dst;
+    while (len) {
+        const ssize_t got = pread(fd, p, len, (off_t)at);
+        if (got < 0 && errno == EINTR) continue;
+        if (got <= 0) return 0;
+        p += got;
+        len -= (size_t)got;
+        at += (uint64_t)got;
     }
-    const uint64_t sz = (uint64_t)st.st_size;
-    unsigned char* m = (unsigned char*)mmap(NULL, (size_t)sz, PROT_READ, MAP_PRIVATE, fd, 0);
-    close(fd);
-    if (m == MAP_FAILED) return;
-    const uint32_t n = rd32(m + 16);
-    int ok = memcmp(m, qc_magic, 8) == 0 && n > 0 && n <= QC_MAX;
-    if (ok && rd64(m + 8) != qc->fp) {
-        fprintf(stderr, "[s2pro] qcache: stale fingerprint, rebuilding\n");
-        ok = 0;
+    return 1;
+}
+
+static int desc_order(const void* a, const void* b, void* ctx) {
+    const s2p_qcache* qc = (const s2p_qcache*)ctx;
+    const int i = *(const int*)a, j = *(const int*)b;
+    const int c = strcmp(qc->desc[i].name, qc->desc[j].name);
+    return c ? c : (i > j) - (i < j); /* equal names: table order, so the first one wins */
+}
+
+/* Parse header and table of an open cache file; 1 when it is servable. */
+static int load_table(s2p_qcache* qc) {
+    unsigned char head[HEAD_BYTES];
+    if (qc->file_len < HEAD_BYTES || !pread_all(qc->fd, head, HEAD_BYTES, 0)) return 0;
+    if (memcmp(head, k_magic, sizeof(k_magic)) != 0) return 0;
+    const uint32_t count = get_u32(head + 16);
+    if (count == 0 || count > MAX_DESCS) return 0;
+    if (get_u64(head + 8) != qc->stamp) {
+        fprintf(stderr, "[s2pro] qcache: %s was made for other weights or settings; "
+                        "it will be regenerated\n", qc->file);
+        return 0;
     }
-    uint64_t off = QC_HDR;
-    for (uint32_t i = 0; ok && i < n; i++) {
-        if (!in_file(off, QC_ENT, sz)) {
+    /* the table is at most count x (descriptor + longest name) */
+    uint64_t span = (uint64_t)count * (DESC_BYTES + MAX_NAME);
+    if (span > qc->file_len - HEAD_BYTES) span = qc->file_len - HEAD_BYTES;
+    unsigned char* table = (unsigned char*)malloc((size_t)span + 1);
+    if (!table) return 0;
+    int ok = pread_all(qc->fd, table, (size_t)span, HEAD_BYTES);
+    uint64_t at = 0;
+    for (uint32_t i = 0; ok && i < count; i++) {
+        if (span - at < DESC_BYTES) {
             ok = 0;
             break;
         }
-        const unsigned char* h = m + off;
-        qc_ent* e = &qc->e[i];
-        const uint32_t name_len = rd32(h);
-        e->kind = rd32(h + 4);
-        memcpy(&e->N, h + 8, 4);
-        memcpy(&e->K, h + 12, 4);
-        memcpy(&e->group, h + 16, 4);
-        e->q_off = rd64(h + 24);
-        e->q_len = rd64(h + 32);
-        e->s_off = rd64(h + 40);
-        e->s_len = rd64(h + 48);
-        off += QC_ENT;
-        if (name_len == 0 || name_len > QC_MAX_NAME || !in_file(off, name_len, sz) ||
-            !in_file(e->q_off, e->q_len, sz) || !in_file(e->s_off, e->s_len, sz) ||
-            !(e->name = (char*)malloc(name_len + 1))) {
-            ok = 0;
-            break;
+        const unsigned char* r = table + at;
+        const uint32_t name_len = get_u32(r);
+        qc_desc d = {0};
+        d.kind = get_u32(r + 4);
+        d.n = (int32_t)get_u32(r + 8);
+        d.k = (int32_t)get_u32(r + 12);
+        d.group = (int32_t)get_u32(r + 16);
+        d.codes_at = get_u64(r + 24);
+        d.codes_len = get_u64(r + 32);
+        d.scales_at = get_u64(r + 40);
+        d.scales_len = get_u64(r + 48);
+        at += DESC_BYTES;
+        const uint64_t L = qc->file_len;
+        ok = name_len >= 1 && name_len <= MAX_NAME && span - at >= name_len &&
+             d.codes_at <= L && d.codes_len <= L - d.codes_at && d.scales_at <= L &&
+             d.scales_len <= L - d.scales_at;
+        if (ok) ok = (d.name = strndup((const char*)table + at, name_len)) != NULL;
+        if (ok) {
+            qc->desc[qc->count++] = d;
+            at += name_len;
         }
-        memcpy(e->name, m + off, name_len);
-        e->name[name_len] = '\0';
-        off += name_len;
-        qc->n = (int)i + 1;
     }
+    free(table);
     if (!ok) {
-        drop_entries(qc);
-        munmap(m, (size_t)sz);
-        return;
+        forget_descs(qc);
+        return 0;
     }
-    qc->map = m;
-    qc->map_len = (size_t)sz;
-    qc->reading = 1;
+    for (int i = 0; i < qc->count; i++) qc->by_name[i] = i;
+    qsort_r(qc->by_name, (size_t)qc->count, sizeof(int), desc_order, qc);
+    return 1;
 }
+
+static const qc_desc* lookup(const s2p_qcache* qc, const char* name) {
+    int lo = 0, hi = qc->count; /* first entry whose name is >= name */
+    while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (strcmp(qc->desc[qc->by_name[mid]].name, name) < 0) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < qc->count && strcmp(qc->desc[qc->by_name[lo]].name, name) == 0)
+        return &qc->desc[qc->by_name[lo]];
+    return NULL;
+}
+
+static int staging_ready(s2p_qcache* qc) {
+    if (qc->stage[0]) return 1;
+    if (hipHostMalloc((void**)&qc->stage[0], 2 * CHUNK_BYTES, hipHostMallocDefault) == hipSuccess) {
+        qc->stage_pinned = 1;
+    } else {
+        (void)hipGetLastError();
+        qc->stage[0] = (unsigned char*)malloc(2 * CHUNK_BYTES); /* synchronous copies then */
+        if (!qc->stage[0]) return 0;
+    }
+    qc->stage[1] = qc->stage[0] + CHUNK_BYTES;
+    return 1;
+}
+
+/* file bytes [at, at + len) -> device dst, through the staging chunks */
+static int stream_payload(s2p_qcache* qc, uint64_t at, uint64_t len, void* dst, hipStream_t st) {
+    if (!staging_ready(qc)) return 0;
+    for (uint64_t done = 0; done < len;) {
+        const size_t n = (size_t)(len - done < CHUNK_BYTES ? len - done : CHUNK_BYTES);
+        const int c = qc->turn;
+        qc->turn ^= 1;
+        unsigned char* buf = qc->stage[c];
+        if (qc->copied_live[c] && hipEventSynchronize(qc->copied[c]) != hipSuccess) return 0;
+        if (!pread_all(qc->fd, buf, n, at + done)) return 0;
+        void* d = (unsigned char*)dst + done;
+        if (!qc->stage_pinned) {
+            if (hipMemcpy(d, buf, n, hipMemcpyHostToDevice) != hipSuccess) return 0;
+        } else {
+            if (!qc->copied_live[c]) {
+                if (hipEventCreateWithFlags(&qc->copied[c], hipEventDisableTiming) != hipSuccess)
+                    return 0;
+                qc->copied_live[c] = 1;
+            }
+            if (hipMemcpyAsync(d, buf, n, hipMemcpyHostToDevice, st) != hipSuccess ||
+                hipEventRecord(qc->copied[c], st) != hipSuccess)
+                return 0;
+        }
+        done += n;
+    }
+    return 1;
+}
+
+/* uploads still reading the staging chunks must finish before they go */
+static int drain_staging(s2p_qcache* qc) {
+    int ok = 1;
+    for (int c = 0; c < 2; c++)
+        if (qc->copied_live[c]) {
+            ok = hipEventSynchronize(qc->copied[c]) == hipSuccess && ok;
+            (void)hipEventDestroy(qc->copied[c]);
+            qc->copied_live[c] = 0;
+        }
+    return ok;
+}
+
+static void release_reader(s2p_qcache* qc) {
+    (void)drain_staging(qc);
+    if (qc->stage[0]) {
+        if (qc->stage_pinned) (void)hipHostFree(qc->stage[0]);
+        else free(qc->stage[0]);
+    }
+    qc->stage[0] = qc->stage[1] = NULL;
+    if (qc->fd >= 0) close(qc->fd);
+    qc->fd = -1;
+}
+
+int s2p_qcache_try_load(s2p_qcache* qc, const char* name, int in_features, int out_features,
+                        s2p_linear* lin, hipStream_t stream) {
+    if (!qc || !qc->reading || qc->fd < 0 || !name || !lin) return 0;
+    const qc_desc* d = lookup(qc, name);
+    if (!d) {
+        fprintf(stderr, "[s2pro] qcache: %s is not cached; quantising it live\n", name);
+        return 0;
+    }
+    if (d->n != out_features || d->k != in_features) {
+        fprintf(stderr, "[s2pro] qcache: cached %s is [%d, %d], the model wants [%d, %d]; "
+                        "quantising it live\n", name, d->n, d->k, out_features, in_features);
+        return 0;
+    }
+    uint64_t want_codes, want_scales;
+    if (!expected_lengths(d->kind, d->n, d->k, d->group, &want_codes, &want_scales) ||
+        want_codes != d->codes_len || want_scales != d->scales_len) {
+        fprintf(stderr, "[s2pro] qcache: %s has a malformed descriptor; quantising it live\n", name);
+        return 0;
+    }
+    /* build the linear aside: *lin changes only on a hit */
+    s2p_linear got;
+    memset(&got, 0, sizeof(got));
+    got.in_features = in_features;
+    got.out_features = out_features;
+    s2p_tensor* codes = d->kind == 2 ? &got.w_pack : &got.w_int8;
+    const int64_t cshape[2] = {d->n, (int64_t)(d->codes_len / (uint64_t)d->n)};
+    const int64_t sshape[1] = {(int64_t)(d->kind == 1 ? d->scales_len / 4 : d->scales_len / 2)};
+    int ok = s2p_tensor_device_alloc(codes, S2P_DT_I8, 2, cshape) == S2P_OK &&
+             s2p_tensor_device_alloc(&got.w_iscale, d->kind == 1 ? S2P_DT_F32 : S2P_DT_F16, 1,
+                                     sshape) == S2P_OK &&
+             codes->bytes == d->codes_len && got.w_iscale.bytes == d->scales_len;
+    ok = ok && stream_payload(qc, d->codes_at, d->codes_len, codes->data, stream) &&
+         stream_payload(qc, d->scales_at, d->scales_len, got.w_iscale.data, stream);
+    if (!ok) {
+        fprintf(stderr, "[s2pro] qcache: reading %s failed; quantising it live\n", name);
+        (void)drain_staging(qc);
+        s2p_tensor_free(codes);
+        s2p_tensor_free(&got.w_iscale);
+        return 0;
+    }
+    got.int8_ready = 1;
+    got.q_group = d->kind == 1 ? 0 : d->group;
+    got.q_packed = d->kind == 2;
+    *lin = got;
+    return 1;
+}
+
+/* --------------------------------------------------------------- write */
+
+static int spool_bytes(s2p_qcache* qc, const void* p, size_t n) {
+    if (n && fwrite(p, 1, n, qc->spool) != n) return 0;
+    qc->spool_len += n;
+    return 1;
+}
+
+/* zero-pad the spool to the payload alignment, then device bytes src */
+static int spool_device(s2p_qcache* qc, const void* src, uint64_t len, unsigned char* bounce,
+                        uint64_t* at) {
+    static const unsigned char zeros[PAYLOAD_ALIGN];
+    const uint64_t pad = round_up(qc->spool_len) - qc->spool_len;
+    if (!spool_bytes(qc, zeros, (size_t)pad)) return 0;
+    *at = qc->spool_len;
+    for (uint64_t done = 0; done < len;) {
+        const size_t n = (size_t)(len - done < CHUNK_BYTES ? len - done : CHUNK_BYTES);
+        if (hipMemcpy(bounce, (const unsigned char*)src + done, n, hipMemcpyDeviceToHost) !=
+            hipSuccess)
+            return -1;
+        if (!spool_bytes(qc, bounce, n)) return 0;
+        done += n;
+    }
+    return 1;
+}
+
+s2p_status s2p_qcache_put_linear(s2p_qcache* qc, const char* name, const s2p_linear* lin,
+                                 hipStream_t stream) {
+    if (!qc || qc->reading || qc->spool_failed || !name || !lin || !lin->int8_ready)
+        return S2P_OK;
+    const size_t name_len = strlen(name);
+    const uint32_t kind = lin->q_packed ? 2u : lin->q_group > 0 ? 3u : 1u;
+    const s2p_tensor* codes = kind == 2 ? &lin->w_pack : &lin->w_int8;
+    if (name_len == 0 || name_len > MAX_NAME || !codes->data || !lin->w_iscale.data)
+        return S2P_OK;
+    if (qc->count == MAX_DESCS) {
+        fprintf(stderr, "[s2pro] qcache: more than %d tensors; %s stays uncached\n", MAX_DESCS,
+                name);
+        return S2P_OK;
+    }
+    if (!qc->spool) {
+        snprintf(qc->spool_path, sizeof(qc->spool_path), "%s.spool", qc->file);
+        qc->spool = fopen(qc->spool_path, "w+b");
+        if (!qc->spool) {
+            fprintf(stderr, "[s2pro] qcache: cannot create %s; no cache this run\n",
+                    qc->spool_path);
+            qc->spool_failed = 1;
+            return S2P_OK;
+        }
+    }
+    qc_desc d = {0};
+    d.kind = kind;
+    d.n = lin->out_features;
+    d.k = lin->in_features;
+    d.group = lin->q_group;
+    d.codes_len = codes->bytes;
+    d.scales_len = lin->w_iscale.bytes;
+    d.name = strdup(name);
+    unsigned char* bounce = (unsigned char*)malloc(CHUNK_BYTES);
+    if (!d.name || !bounce) {
+        free(d.name);
+        free(bounce);
+        return S2P_OK; /* only the cache degrades */
+    }
+    /* the tensors were produced on `stream` */
+    int r = hipStreamSynchronize(stream) == hipSuccess ? 1 : -1;
+    if (r == 1) r = spool_device(qc, codes->data, d.codes_len, bounce, &d.codes_at);
+    if (r == 1) r = spool_device(qc, lin->w_iscale.data, d.scales_len, bounce, &d.scales_at);
+    free(bounce);
+    if (r != 1) {
+        free(d.name);
+        qc->spool_failed = 1; /* the spool is now inconsistent: drop the cache */
+        fprintf(stderr, "[s2pro] qcache: could not spool %s; no cache this run\n", name);
+        return r < 0 ? S2P_ERR_CUDA : S2P_OK;
+    }
+    qc->desc[qc->count++] = d;
+    return S2P_OK;
+}
+
+static void drop_spool(s2p_qcache* qc) {
+    if (qc->spool) {
+        fclose(qc->spool);
+        qc->spool = NULL;
+        remove(qc->spool_path);
+    }
+}
+
+/* header + table (offsets made absolute) + the spooled payloads -> a
+ * temporary file, renamed over the cache */
+static int publish(s2p_qcache* qc) {
+    uint64_t table_end = HEAD_BYTES;
+    for (int i = 0; i < qc->count; i++) table_end += DESC_BYTES + strlen(qc->desc[i].name);
+    const uint64_t base = round_up(table_end);
+    unsigned char* head = (unsigned char*)calloc(1, (size_t)base);
+    unsigned char* buf = (unsigned char*)malloc(CHUNK_BYTES);
+    int ok = head && buf && fflush(qc->spool) == 0;
+    if (ok) {
+        memcpy(head, k_magic, sizeof(k_magic));
+        put_u64(head + 8, qc->stamp);
+        put_u32(head + 16, (uint32_t)qc->count);
+        unsigned char* w = head + HEAD_BYTES;
+        for (int i = 0; i < qc->count; i++) {
+            const qc_desc* d = &qc->desc[i];
+            const uint32_t nl = (uint32_t)strlen(d->name);
+            put_u32(w, nl);
+            put_u32(w + 4, d->kind);
+            put_u32(w + 8, (uint32_t)d->n);
+            put_u32(w + 12, (uint32_t)d->k);
+            put_u32(w + 16, (uint32_t)d->group);
+            put_u64(w + 24, base + d->codes_at);
+            put_u64(w + 32, d->codes_len);
+            put_u64(w + 40, base + d->scales_at);
+            put_u64(w + 48, d->scales_len);
+            memcpy(w + DESC_BYTES, d->name, nl);
+            w += DESC_BYTES + nl;
+        }
+    }
+    char part[1100];
+    snprintf(part, sizeof(part), "%s.part", qc->file);
+    FILE* out = ok ? fopen(part, "wb") : NULL;
+    ok = out && fwrite(head, 1, (size_t)base, out) == (size_t)base;
+    const int sfd = fileno(qc->spool);
+    for (uint64_t at = 0; ok && at < qc->spool_len;) {
+        const size_t n = (size_t)(qc->spool_len - at < CHUNK_BYTES ? qc->spool_len - at : CHUNK_BYTES);
+        ok = pread_all(sfd, buf, n, at) && fwrite(buf, 1, n, out) == n;
+        at += n;
+    }
+    if (out) ok = fclose(out) == 0 && ok;
+    ok = ok && rename(part, qc->file) == 0;
+    if (!ok) remove(part);
+    free(head);
+    free(buf);
+    return ok;
+}
+
+/* ------------------------------------------------------------ lifecycle */
 
 s2p_status s2p_qcache_open(const char* model_dir, s2p_gemm_mode mode, s2p_qcache** out) {
     if (!model_dir || !out) return S2P_ERR_INVALID;
     *out = NULL;
-    if (mode != S2P_GEMM_INT8 || !env_flag("S2P_QCACHE", 1)) return S2P_OK;
+    /* only the INT8 / INT4 modes carry quantised tensors */
+    if (mode != S2P_GEMM_INT8 || !switch_on("S2P_QCACHE", 1)) return S2P_OK;
+    uint64_t stamp;
+    if (weights_stamp(model_dir, mode, &stamp) != 0) return S2P_OK; /* no weights: no cache */
     s2p_qcache* qc = (s2p_qcache*)calloc(1, sizeof(*qc));
     if (!qc) return S2P_ERR_OOM;
-    if (fingerprint(model_dir, mode, &qc->fp) != 0) { /* unusual model dir: no cache */
-        free(qc);
-        return S2P_OK;
-    }
+    qc->stamp = stamp;
+    qc->fd = -1;
     const char* dir = getenv("S2P_QCACHE_DIR");
-    snprintf(qc->path, sizeof(qc->path), "%s/s2p_qcache.bin", dir && dir[0] ? dir : model_dir);
-    read_header(qc);
-    if (qc->reading)
-        fprintf(stderr, "[s2pro] qcache: serving %d tensors from %s\n", qc->n, qc->path);
-    else
-        fprintf(stderr, "[s2pro] qcache: will write %s after load\n", qc->path);
+    snprintf(qc->file, sizeof(qc->file), "%s/s2p_qcache.bin", dir && *dir ? dir : model_dir);
+    qc->fd = open(qc->file, O_RDONLY | O_CLOEXEC);
+    struct stat st;
+    if (qc->fd >= 0 && fstat(qc->fd, &st) == 0) {
+        qc->file_len = (uint64_t)st.st_size;
+        qc->reading = load_table(qc);
+    }
+    if (qc->reading) {
+        fprintf(stderr, "[s2pro] qcache: loading %d quantised tensors from %s\n", qc->count,
+                qc->file);
+    } else {
+        if (qc->fd >= 0) close(qc->fd);
+        qc->fd = -1;
+        fprintf(stderr, "[s2pro] qcache: no usable cache; %s will be written after loading\n",
+                qc->file);
+    }
     *out = qc;
     return S2P_OK;
 }
 
 int s2p_qcache_reading(const s2p_qcache* qc) { return qc && qc->reading; }
 
-/* the device tensors of an entry: codes (w_pack for kind 2, else w_int8)
- * and scales, with the reference's dtypes and shapes */
-static s2p_status alloc_entry(const qc_ent* e, s2p_linear* lin, s2p_tensor** qt) {
-    if (e->N <= 0 || e->K <= 0) return S2P_ERR_FORMAT;
-    if (e->kind >= 2 && (e->group <= 0 || e->K % e->group)) return S2P_ERR_FORMAT;
-    s2p_status rc;
-    if (e->kind == 1) {
-        const int64_t qs[2] = {e->N, e->K}, ss[1] = {e->N};
-        *qt = &lin->w_int8;
-        rc = s2p_tensor_device_alloc(&lin->w_int8, S2P_DT_I8, 2, qs);
-        if (rc == S2P_OK) rc = s2p_tensor_device_alloc(&lin->w_iscale, S2P_DT_F32, 1, ss);
-    } else if (e->kind == 2 || e->kind == 3) {
-        const int64_t qs[2] = {e->N, e->kind == 2 ? e->K / 2 : e->K};
-        const int64_t ss[1] = {(int64_t)e->N * (e->K / e->group)};
-        *qt = e->kind == 2 ? &lin->w_pack : &lin->w_int8;
-        rc = s2p_tensor_device_alloc(*qt, S2P_DT_I8, 2, qs);
-        if (rc == S2P_OK) rc = s2p_tensor_device_alloc(&lin->w_iscale, S2P_DT_F16, 1, ss);
-    } else {
-        return S2P_ERR_FORMAT;
-    }
-    if (rc == S2P_OK && ((*qt)->bytes != e->q_len || lin->w_iscale.bytes != e->s_len))
-        rc = S2P_ERR_FORMAT;
-    return rc;
-}
-
-int s2p_qcache_try_load(s2p_qcache* qc, const char* name, int in_features, int out_features,
-                        s2p_linear* lin, hipStream_t stream) {
-    if (!qc || !qc->reading || !name || !lin) return 0;
-    const qc_ent* e = NULL;
-    for (int i = 0; i < qc->n && !e; i++)
-        if (strcmp(qc->e[i].name, name) == 0) e = &qc->e[i];
-    if (!e) {
-        fprintf(stderr, "[s2pro] qcache: miss for %s (live path)\n", name);
-        return 0;
-    }
-    if (e->N != out_features || e->K != in_features) {
-        fprintf(stderr, "[s2pro] qcache: shape mismatch for %s\n", name);
-        return 0;
-    }
-    memset(lin, 0, sizeof(*lin));
-    lin->in_features = in_features;
-    lin->out_features = out_features;
-    s2p_tensor* qt = NULL;
-    s2p_status rc = alloc_entry(e, lin, &qt);
-    if (rc == S2P_ERR_FORMAT) fprintf(stderr, "[s2pro] qcache: size mismatch for %s\n", name);
-    if (rc == S2P_OK &&
-        (hipMemcpyAsync(qt->data, qc->map + e->q_off, e->q_len, hipMemcpyHostToDevice, stream) !=
-             hipSuccess ||
-         hipMemcpyAsync(lin->w_iscale.data, qc->map + e->s_off, e->s_len, hipMemcpyHostToDevice,
-                        stream) != hipSuccess))
-        rc = S2P_ERR_CUDA;
-    if (rc != S2P_OK) {
-        s2p_tensor_free(&lin->w_int8);
-        s2p_tensor_free(&lin->w_pack);
-        s2p_tensor_free(&lin->w_iscale);
-        memset(lin, 0, sizeof(*lin));
-        lin->in_features = in_features;
-        lin->out_features = out_features;
-        return 0;
-    }
-    lin->int8_ready = 1;
-    if (e->kind >= 2) lin->q_group = e->group;
-    if (e->kind == 2) lin->q_packed = 1;
-    return 1;
-}
-
-s2p_status s2p_qcache_put_linear(s2p_qcache* qc, const char* name, const s2p_linear* lin,
-                                 hipStream_t stream) {
-    if (!qc || qc->reading || !name || !lin || !lin->int8_ready || qc->n >= QC_MAX) return S2P_OK;
-    const s2p_tensor* qt = lin->q_packed ? &lin->w_pack : &lin->w_int8;
-    if (!qt->data || !lin->w_iscale.data || strlen(name) == 0 || strlen(name) > QC_MAX_NAME)
-        return S2P_OK;
-    qc_ent* e = &qc->e[qc->n];
-    memset(e, 0, sizeof(*e));
-    e->kind = lin->q_packed ? 2u : (lin->q_group > 0 ? 3u : 1u);
-    e->N = lin->out_features;
-    e->K = lin->in_features;
-    e->group = lin->q_group;
-    e->q_len = qt->bytes;
-    e->s_len = lin->w_iscale.bytes;
-    e->name = strdup(name);
-    e->qh = malloc(e->q_len ? e->q_len : 1);
-    e->sh = malloc(e->s_len ? e->s_len : 1);
-    if (!e->name || !e->qh || !e->sh) { /* the cache degrades, the load does not */
-        free(e->name);
-        free(e->qh);
-        free(e->sh);
-        memset(e, 0, sizeof(*e));
-        return S2P_OK;
-    }
-    if (hipStreamSynchronize(stream) != hipSuccess ||
-        hipMemcpy(e->qh, qt->data, e->q_len, hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMemcpy(e->sh, lin->w_iscale.data, e->s_len, hipMemcpyDeviceToHost) != hipSuccess) {
-        free(e->name);
-        free(e->qh);
-        free(e->sh);
-        memset(e, 0, sizeof(*e));
-        return S2P_ERR_CUDA;
-    }
-    qc->n++;
-    return S2P_OK;
-}
-
-static uint64_t align_up(uint64_t v) { return (v + QC_ALIGN - 1) & ~(uint64_t)(QC_ALIGN - 1); }
-
-/* zeros up to byte offset to, then len bytes of p */
-static int put_at(FILE* f, uint64_t* pos, uint64_t to, const void* p, uint64_t len) {
-    static const unsigned char zeros[QC_ALIGN];
-    while (*pos < to) {
-        const size_t k = (size_t)(to - *pos < QC_ALIGN ? to - *pos : QC_ALIGN);
-        if (fwrite(zeros, 1, k, f) != k) return 0;
-        *pos += k;
-    }
-    if (len && fwrite(p, 1, (size_t)len, f) != (size_t)len) return 0;
-    *pos += len;
-    return 1;
-}
-
-static s2p_status write_file(s2p_qcache* qc) {
-    /* header and entry table in one buffer; payload offsets after it */
-    uint64_t table = QC_HDR;
-    for (int i = 0; i < qc->n; i++) table += QC_ENT + strlen(qc->e[i].name);
-    uint64_t off = table;
-    for (int i = 0; i < qc->n; i++) {
-        qc_ent* e = &qc->e[i];
-        e->q_off = off = align_up(off);
-        off += e->q_len;
-        e->s_off = off = align_up(off);
-        off += e->s_len;
-    }
-    unsigned char* hb = (unsigned char*)calloc(1, (size_t)table);
-    if (!hb) return S2P_ERR_OOM;
-    memcpy(hb, qc_magic, 8);
-    memcpy(hb + 8, &qc->fp, 8);
-    const uint32_t n32 = (uint32_t)qc->n;
-    memcpy(hb + 16, &n32, 4);
-    unsigned char* p = hb + QC_HDR;
-    for (int i = 0; i < qc->n; i++) {
-        const qc_ent* e = &qc->e[i];
-        const uint32_t nl = (uint32_t)strlen(e->name);
-        memcpy(p, &nl, 4);
-        memcpy(p + 4, &e->kind, 4);
-        memcpy(p + 8, &e->N, 4);
-        memcpy(p + 12, &e->K, 4);
-        memcpy(p + 16, &e->group, 4);
-        memcpy(p + 24, &e->q_off, 8);
-        memcpy(p + 32, &e->q_len, 8);
-        memcpy(p + 40, &e->s_off, 8);
-        memcpy(p + 48, &e->s_len, 8);
-        memcpy(p + QC_ENT, e->name, nl);
-        p += QC_ENT + nl;
-    }
-    char tmp[1100];
-    snprintf(tmp, sizeof(tmp), "%s.tmp", qc->path);
-    FILE* f = fopen(tmp, "wb");
-    if (!f) {
-        free(hb);
-        fprintf(stderr, "[s2pro] qcache: cannot write %s (skipping)\n", tmp);
-        return S2P_OK;
-    }
-    uint64_t pos = 0;
-    int ok = put_at(f, &pos, 0, hb, table);
-    free(hb);
-    for (int i = 0; ok && i < qc->n; i++) {
-        const qc_ent* e = &qc->e[i];
-        ok = put_at(f, &pos, e->q_off, e->qh, e->q_len) && put_at(f, &pos, e->s_off, e->sh, e->s_len);
-    }
-    ok = (fclose(f) == 0) && ok;
-    if (!ok || rename(tmp, qc->path) != 0) {
-        fprintf(stderr, "[s2pro] qcache: write failed (%s), removing\n", tmp);
-        remove(tmp);
-        return S2P_OK;
-    }
-    fprintf(stderr, "[s2pro] qcache: wrote %d tensors -> %s\n", qc->n, qc->path);
-    return S2P_OK;
-}
-
 s2p_status s2p_qcache_finish(s2p_qcache* qc, hipStream_t stream) {
+    (void)stream; /* the uploads are tracked by their own events */
     if (!qc) return S2P_OK;
-    if (qc->reading) { /* uploads read the mapping: they must be complete */
-        if (hipStreamSynchronize(stream) != hipSuccess) return S2P_ERR_CUDA;
-        if (qc->map) munmap(qc->map, qc->map_len);
-        qc->map = NULL;
-        qc->map_len = 0;
-        return S2P_OK;
+    if (qc->reading) {
+        const int ok = drain_staging(qc);
+        release_reader(qc);
+        return ok ? S2P_OK : S2P_ERR_CUDA;
     }
-    return qc->n ? write_file(qc) : S2P_OK;
+    if (qc->spool && !qc->spool_failed && qc->count > 0) {
+        if (publish(qc))
+            fprintf(stderr, "[s2pro] qcache: stored %d quantised tensors in %s\n", qc->count,
+                    qc->file);
+        else
+            fprintf(stderr, "[s2pro] qcache: writing %s failed; no cache this run\n", qc->file);
+    }
+    drop_spool(qc);
+    return S2P_OK;
 }
 
 void s2p_qcache_free(s2p_qcache* qc) {
     if (!qc) return;
-    drop_entries(qc);
-    if (qc->map) munmap(qc->map, qc->map_len);
+    release_reader(qc);
+    drop_spool(qc);
+    forget_descs(qc);
     free(qc);
 }

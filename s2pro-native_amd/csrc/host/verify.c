@@ -26,6 +26,7 @@
 #include "../mk2_internal.h"
 #include "../prims_internal.h"
 #include "../sample_internal.h"
+#include "../spec_internal.h"
 #include "../synth_internal.h"
 
 float* s2p_gemm_ctx_part(void);
@@ -54,6 +55,7 @@ struct s2p_backbone {
     int32_t* d_pos;
     int32_t* d_slot;
     int32_t* d_sess;
+    int32_t* d_depth;      /* [S2P_VERIFY_MAX_ROWS] node depths of the plan's shape */
     uint64_t* d_vis;
     void** d_kv;
     void** d_kvs;          /* [max_sessions] scale bases (INT8 / INT4 caches) */
@@ -174,12 +176,13 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_pos, R * 4);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_slot, R * 4);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_sess, R * 4);
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_depth, S2P_VERIFY_MAX_ROWS * 4);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_vis, R * 8);
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_kv, (size_t)S * sizeof(void*));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_kvs, (size_t)S * sizeof(void*));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_segs, (size_t)nseg_max * sizeof(S2pAttnSeg));
     b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)2 * S * sizeof(void*) +
-                     (size_t)nseg_max * sizeof(S2pAttnSeg) + 64;
+                     (size_t)nseg_max * sizeof(S2pAttnSeg) + 64 + S2P_VERIFY_MAX_ROWS * 4;
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_rope, R * 64 * 2 * sizeof(float));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_AUX_OFF + MK2_AUX_BYTES);
     if (rc == S2P_OK) rc = dalloc(&b->d_chain_hidden, R * S2P_DIM * 2);
@@ -226,7 +229,7 @@ void s2p_backbone_free(s2p_backbone* b) {
     s2p_linear_free(&b->head);
     void* bufs[] = {b->x,        b->qkv,       b->q,           b->attn,          b->gu,
                     b->ssq,      b->attn_part, b->d_pos,       b->d_slot,        b->d_sess,
-                    b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_rope,
+                    b->d_depth,  b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_rope,
                     (void*)b->d_wpack, (void*)b->d_hpack, (void*)b->d_norms, (void*)b->d_mk2,
                     b->d_chain_hidden, b->d_chain_par, (void*)b->d_chain_sem};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
@@ -381,6 +384,12 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_kvs, kvs, (size_t)n * sizeof(void*), hipMemcpyHostToDevice, st), "plan"));
     S2P_TRY(hip_ok(hipMemcpyAsync(b->d_segs, segs, (size_t)nseg * sizeof(S2pAttnSeg),
                                   hipMemcpyHostToDevice, st), "plan"));
+    {
+        int32_t* hd = (int32_t*)(segs + nseg);
+        memcpy(hd, depth, (size_t)R * sizeof(int32_t));
+        S2P_TRY(hip_ok(hipMemcpyAsync(b->d_depth, hd, (size_t)R * 4, hipMemcpyHostToDevice, st),
+                       "plan"));
+    }
     S2P_TRY(hip_ok(hipStreamSynchronize(st), "plan sync"));
     b->planned = 1;
     b->rows = rows;
@@ -412,6 +421,22 @@ static S2pRowPlan row_plan(const s2p_backbone* b) {
     p.max_seq = b->o.ctx_len;
     return p;
 }
+
+s2p_status s2p_verify_plan_device(s2p_backbone* b, const int32_t* kv_len_dev, int32_t* overflow,
+                                  hipStream_t st) {
+    if (!b || !kv_len_dev) return S2P_ERR_INVALID;
+    if (!b->planned) return S2P_ERR_STATE;
+    S2P_TRY(hip_ok(s2p_plan_device_launch(b->d_pos, b->d_slot, b->d_segs, b->n_seg, kv_len_dev,
+                                          b->d_depth, b->n_sess, b->R, b->max_span, overflow, st),
+                   "device plan"));
+    const S2pRowPlan rp = row_plan(b);
+    return hip_ok(s2p_rope_tab_launch(&rp, b->rows, ROPE_BASE, b->d_rope, st), "rope table");
+}
+
+/* Internal helpers of the speculative tick (csrc/host/spec.c). */
+const void* s2p_backbone_chain_hidden(const s2p_backbone* b) { return b->d_chain_hidden; }
+int s2p_backbone_plan_span(const s2p_backbone* b) { return b->planned ? b->max_span : 0; }
+int s2p_backbone_ctx_len(const s2p_backbone* b) { return b->o.ctx_len; }
 
 /* --------------------------------------------------------------- forward */
 
@@ -607,12 +632,13 @@ static s2p_status accept_run(const void* tgt, const void* tgt_eos, int64_t tgt_e
                              const int64_t* tok, s2ps_dev_state* const* states, int n_sess,
                              int rows, int32_t* out_path, int32_t* out_n_acc, int64_t* out_emit,
                              int32_t* out_n_emit, void* work, const uint8_t* chain_ok,
-                             const int* fwd_err, hipStream_t st) {
+                             const int* fwd_err, int32_t* out_tail, hipStream_t st) {
     if (tgt_stride != drf_stride) return S2P_ERR_INVALID;
     AcceptArgs a;
     memset(&a, 0, sizeof(a));
     a.chain_ok = chain_ok;
     a.fwd_err = fwd_err;
+    a.out_tail = out_tail;
     a.tgt = (const uint16_t*)tgt;
     a.tgt_eos = (const uint16_t*)tgt_eos;
     a.drf = (const uint16_t*)drf;
@@ -646,7 +672,7 @@ s2p_status s2p_verify_accept(const void* tgt_logits, const void* tgt_eos, const 
     if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
     return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
                       parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
-                      work, NULL, NULL, st);
+                      work, NULL, NULL, NULL, st);
 }
 
 s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
@@ -664,7 +690,24 @@ s2p_status s2p_verify_accept_chain(const void* tgt_logits, const void* tgt_eos,
     if (tgt_eos && row_stride < 4096) return S2P_ERR_INVALID;
     return accept_run(tgt_logits, tgt_eos, 1, row_stride, drf_logits, drf_eos, 1, row_stride,
                       parent, tok, states, n_sess, rows, out_path, out_n_acc, out_emit, out_n_emit,
-                      work, chain_ok, NULL, st);
+                      work, chain_ok, NULL, NULL, st);
+}
+
+/* Acceptance of the current plan's rows on the backbone's logits layout,
+ * with the chain condition, the forward's error word and the walk's tail
+ * (internal: the speculative tick). */
+s2p_status s2p_verify_accept_tail(s2p_backbone* b, const void* logits, const void* drf,
+                                  const int32_t* parent, const int64_t* tok,
+                                  s2ps_dev_state* const* states, const uint8_t* chain_ok,
+                                  int32_t* path, int32_t* n_acc, int64_t* emit, int32_t* n_emit,
+                                  int32_t* tail, void* work, hipStream_t st) {
+    const int sliced = b->head.out_features == S2P_HEAD_SLICE;
+    const uint16_t* lg = (const uint16_t*)logits;
+    const uint16_t* dg = (const uint16_t*)drf;
+    const int64_t ts = b->head.out_features;
+    return accept_run(lg, sliced ? lg + 4096 : NULL, ts, ts, dg, sliced ? dg + 4096 : NULL, ts, ts,
+                      parent, tok, states, b->n_sess, b->R, path, n_acc, emit, n_emit, work,
+                      chain_ok, b->mk2_ready ? b->mk2.err : NULL, tail, st);
 }
 
 s2p_status s2p_verify_chain(s2p_backbone* b, s2pfa* fa, const int32_t* parent, const int64_t* tok,
@@ -712,7 +755,7 @@ static s2p_status step_enqueue(s2p_backbone* b, const s2p_verify_step_io* io, hi
                       io->drf_stride, io->parent_dev, io->tok_dev,
                       io->states_dev, b->n_sess, b->R, io->out_path, io->out_n_acc,
                       io->out_emit, io->out_n_emit, io->work, NULL,
-                      b->mk2_ready ? b->mk2.err : NULL, st);
+                      b->mk2_ready ? b->mk2.err : NULL, NULL, st);
 }
 
 s2p_status s2p_verify_step(s2p_backbone* b, const s2p_verify_step_io* io, int use_graph,

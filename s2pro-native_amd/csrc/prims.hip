@@ -510,11 +510,19 @@ extern "C" hipError_t s2p_fa_vq_embed_add_launch(const void* table, const int32_
  * fuse GEMV adds onto it, producing the row's sums of squares) and the
  * attention's split counters. */
 __global__ __launch_bounds__(256) void k_draft_prologue(S2pRowPlan plan, S2pAttnSeg* seg,
-                                                        void* kv, int pos, float base,
+                                                        void* kv, int pos,
+                                                        const int32_t* __restrict__ pos_dev,
+                                                        int pos_max, float base,
                                                         float* __restrict__ tab,
                                                         uint16_t* __restrict__ x, int nx,
                                                         unsigned* __restrict__ ctr, int nctr) {
     const int t = threadIdx.x;
+    if (pos_dev) {
+        /* position pos_dev[0] + pos, kept inside [0, pos_max) so the append
+         * never leaves the cache */
+        pos += *pos_dev;
+        pos = pos < 0 ? 0 : (pos >= pos_max ? pos_max - 1 : pos);
+    }
     if (t == 0) {
         *(int32_t*)plan.pos = pos;
         *(int32_t*)plan.slot = pos;
@@ -538,10 +546,11 @@ __global__ __launch_bounds__(256) void k_draft_prologue(S2pRowPlan plan, S2pAttn
 }
 
 extern "C" hipError_t s2p_draft_prologue_launch(const S2pRowPlan* plan, S2pAttnSeg* seg, void* kv,
-                                               int pos, float base, float* tab, void* x, int nx,
+                                               int pos, const int32_t* pos_dev, int pos_max,
+                                               float base, float* tab, void* x, int nx,
                                                unsigned* ctr, int nctr, hipStream_t st) {
-    hipLaunchKernelGGL(k_draft_prologue, dim3(1), dim3(256), 0, st, *plan, seg, kv, pos, base, tab,
-                       (uint16_t*)x, nx, ctr, nctr);
+    hipLaunchKernelGGL(k_draft_prologue, dim3(1), dim3(256), 0, st, *plan, seg, kv, pos, pos_dev,
+                       pos_max, base, tab, (uint16_t*)x, nx, ctr, nctr);
     return hipGetLastError();
 }
 

@@ -46,9 +46,11 @@ hipError_t s2p_fa_vq_embed_add_launch(const void* table, const int32_t* codes, i
                                       int dim, hipStream_t st);
 /* Draft step prologue: the one-row plan (pos/slot/sess/vis/kv arrays behind
  * the plan's pointers) and segment at position pos over the cache at kv,
- * the RoPE row into tab [64][2], zeros into x [nx] bf16 and ctr [nctr]. */
+ * the RoPE row into tab [64][2], zeros into x [nx] bf16 and ctr [nctr].
+ * pos_dev != NULL: the position is *pos_dev + pos, read on the device and
+ * clamped to [0, pos_max). */
 hipError_t s2p_draft_prologue_launch(const S2pRowPlan* plan, S2pAttnSeg* seg, void* kv, int pos,
-                                     float base,
+                                     const int32_t* pos_dev, int pos_max, float base,
                                      float* tab, void* x, int nx, unsigned* ctr, int nctr,
                                      hipStream_t st);
 /* Move accepted tree nodes' K/V from slot L + node to L + depth. */

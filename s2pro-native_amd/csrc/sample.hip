@@ -632,7 +632,7 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
     int32_t* path = a.out_path + (size_t)s * R;
     int64_t* emit = a.out_emit + (size_t)s * (R + 1);
     int n_acc = 0, n_emit = 0;
-    int v = 0;
+    int v = 0, tail_node = -1;
     for (;;) {
         const uint32_t* tp = wk + (v * 2 + 0) * 68;
         const uint32_t* tq = wk + (v * 2 + 1) * 68;
@@ -681,6 +681,7 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
         if (accepted >= 0 && !cok[accepted]) {
             /* the drafted frame failed the chain condition: its token is
              * emitted, its row is not accepted, no bonus draw */
+            tail_node = accepted;
             if (lane == 0) emit[n_emit] = tok[accepted];
             state_push_wave(&st, tok[accepted], lane);
             n_emit++;
@@ -694,7 +695,10 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
             }
             n_acc++;
             n_emit++;
-            if (tok[accepted] == TOK_EOS) break;
+            if (tok[accepted] == TOK_EOS) {
+                v = accepted; /* the EOS node's own row ends the walk */
+                break;
+            }
             state_push_wave(&st, tok[accepted], lane);
             __syncthreads();
             v = accepted;
@@ -721,6 +725,10 @@ __global__ __launch_bounds__(64) void k_accept_walk(AcceptArgs a) {
     if (lane == 0) {
         a.out_n_acc[s] = n_acc;
         a.out_n_emit[s] = n_emit;
+        if (a.out_tail) {
+            a.out_tail[2 * s] = v;
+            a.out_tail[2 * s + 1] = tail_node;
+        }
     }
     __syncthreads();
     {

@@ -36,6 +36,11 @@ typedef struct {
                                   logits are not trustworthy, so every session gets
                                   out_n_acc = -1, out_n_emit = 0 and its state is left
                                   as it was */
+    int32_t*        out_tail;  /* NULL, or [n_sess][2]: the node whose row ended the walk
+                                  (the last accepted node, or the root; its hidden produced
+                                  the last emitted token unless that token is an accepted
+                                  EOS node's own) and the chain-failed node whose token was
+                                  emitted last (-1 if none) */
 } AcceptArgs;
 
 size_t     s2p_accept_work_bytes(int n_sess, int rows);

@@ -96,6 +96,30 @@ class DraftState(ctypes.Structure):
     _fields_ = [("kc", Tensor), ("vc", Tensor), ("pos", I)]
 
 
+class SpecModel(ctypes.Structure):
+    """s2p_spec_model (include/s2pro/spec.h)"""
+    _fields_ = [("bb", P), ("draft", P), ("draft_states", P), ("fa", P), ("embed", P),
+                ("n_sess", I), ("K", I)]
+
+
+class SpecSessions(ctypes.Structure):
+    """s2p_spec_sessions (include/s2pro/spec.h)"""
+    _fields_ = [("kv", P), ("kv_len", P), ("prev_tok", P), ("prev_codes", P),
+                ("prev_hidden", P), ("states", P), ("done", P)]
+
+
+class SpecOut(ctypes.Structure):
+    """s2p_spec_out (include/s2pro/spec.h)"""
+    _fields_ = [("n_acc", P), ("n_emit", P), ("emit", P), ("frames", P)]
+
+
+class SpecBuffers(ctypes.Structure):
+    """s2p_spec_buffers (include/s2pro/spec.h)"""
+    _fields_ = [("logits", P), ("drf_logits", P), ("x", P), ("tok", P), ("draft_codes", P),
+                ("codes_out", P), ("path", P), ("tail", P), ("chain_ok", P), ("head_rows", I),
+                ("replans", I)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/s2pro/*.h
 SIGS = {
     # status.h / tensor.h
@@ -191,6 +215,11 @@ SIGS = {
     "s2p_verify_accept_chain": (I, [P, P, P, P, I64, P, P, P, I, I, P, P, P, P, P, P, P]),
     "s2p_verify_step": (I, [P, P, I, P]),
     "s2p_verify_status": (I, [P, P, I, P]),
+    "s2p_verify_plan_device": (I, [P, P, P, P]),
+    "s2p_spec_create": (I, [P, P, P, P, P, P]),
+    "s2p_spec_tick": (I, [P, I, P]),
+    "s2p_spec_buffers_of": (I, [P, P]),
+    "s2p_spec_free": (None, [P]),
 }
 
 # synthetic-data launchers (csrc/synth_internal.h), used by tests/benchmarks

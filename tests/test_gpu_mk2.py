@@ -169,11 +169,11 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
 @pytest.mark.timeout(400)
 def test_mk2_config3_depth_vs_oracle(lib):
     """Config 3's exact backbone shape (36 INT4-g32 layers, K=4 chain, bf16
-    KV 2048, ctx 2304 as the bench plans it) on the persistent kernel,
-    against the oracle's 36-layer forward and binary64 (head: the 4,097-row
-    slice, so the CPU side stays ~1-2 minutes).  Pins what only full depth
-    exercises: every layer's weight block base, flag values and KV plane
-    strides.  No flag wait may time out."""
+    KV 2048, ctx 2304 as the bench plans it) on the persistent kernel and on
+    the layer-by-layer path, each against the oracle's 36-layer forward and
+    binary64 (head: the 4,097-row slice, so the CPU side stays ~1 minute).
+    Pins what only full depth exercises: every layer's weight block base,
+    flag values and KV plane strides.  No flag wait may time out."""
     ctx, n_layers, parent, L = 2304, 36, [-1, 0, 1, 2, 3], 2048
     R = len(parent)
     print("config-3 depth test: building the 36-layer backbone", flush=True)
@@ -181,23 +181,32 @@ def test_mk2_config3_depth_vs_oracle(lib):
     try:
         kv = new_kv(lib, bb, 31)
         kv_host = to_host(kv, np.uint16).copy()
-        plan(lib, bb, parent, [kv], [L])
-        assert lib.s2p_backbone_mk_status(bb) == 1, "plan did not run on the persistent kernel"
         x = bf16_bits(np.random.default_rng(36).standard_normal((R, 2560)).astype(np.float32))
-        got = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE))
-        assert lib.s2p_backbone_mk_status(bb) == 1, "a flag wait timed out"
-        kv_dev = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
-        print("config-3 depth test: GPU forward done, running the references", flush=True)
+        got, kv_dev = {}, {}
+        for mode in (1, 0):
+            lib.s2p_backbone_set_mk(bb, mode)
+            kv.copy_(torch.from_numpy(kv_host.view(np.int16)).to(kv.device))
+            plan(lib, bb, parent, [kv], [L])
+            assert lib.s2p_backbone_mk_status(bb) == mode, "plan did not run where expected"
+            got[mode] = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE))
+            assert lib.s2p_backbone_mk_status(bb) == mode, "a flag wait timed out"
+            kv_dev[mode] = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
+        print("config-3 depth test: GPU forwards done, running the references", flush=True)
         want, truth = _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent,
                                            s2pamd.S2P_HEAD_SLICE)
-        check_logits(got, want, truth, "mk2 36-layer logits")
+        d = np.linalg.norm(got[1] - got[0], axis=1) / np.linalg.norm(got[0], axis=1)
+        print("mk2 vs layer path, per-row L2 rel:", d)
+        check_logits(got[0], want, truth, "layer path 36-layer logits")
+        check_logits(got[1], want, truth, "mk2 36-layer logits")
         # every layer appended its rows at L..L+R-1 and touched nothing else
         kv0 = kv_host.reshape(n_layers, 16, ctx, 128)
-        assert np.array_equal(kv_dev[:, :, :L], kv0[:, :, :L])
-        assert np.array_equal(kv_dev[:, :, L + R:], kv0[:, :, L + R:])
-        assert np.all(np.any(kv_dev[:, :, L:L + R] != kv0[:, :, L:L + R], axis=(2, 3))), \
-            "a layer's K/V plane was not appended"
+        for mode in (1, 0):
+            assert np.array_equal(kv_dev[mode][:, :, :L], kv0[:, :, :L])
+            assert np.array_equal(kv_dev[mode][:, :, L + R:], kv0[:, :, L + R:])
+            assert np.all(np.any(kv_dev[mode][:, :, L:L + R] != kv0[:, :, L:L + R], axis=(2, 3))), \
+                "a layer's K/V plane was not appended"
     finally:
+        lib.s2p_backbone_set_mk(bb, 1)
         lib.s2p_backbone_free(bb)
 
 
@@ -247,9 +256,10 @@ def test_mk2_wait_timeout_is_reported(lib):
             kv = new_kv(lib, bb, 5)
             plan(lib, bb, parent, [kv], [L])
             assert lib.s2p_backbone_mk_status(bb) == 1
-            x = to_dev(bf16_bits(np.random.default_rng(4).standard_normal((R, 2560))
-                                 .astype(np.float32)))
-            ref = _forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE)
+            x_host = bf16_bits(np.random.default_rng(4).standard_normal((R, 2560))
+                               .astype(np.float32))
+            x = to_dev(x_host)
+            ref = _forward(lib, bb, x_host, R, s2pamd.S2P_HEAD_SLICE)
             st = po.state(temperature=0.8, top_p=0.8, seed=3, entropy=0)
             st_bytes = np.frombuffer(bytes(st), np.uint8).copy()
             drf = to_dev(bf16_bits(bf16_vals(ref) + 0.5 * np.random.default_rng(5)

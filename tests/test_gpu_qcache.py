@@ -93,3 +93,36 @@ def test_qcache_round_trip(lib, tmp_path):
     finally:
         lib.s2p_qcache_free(qc)
     del keep
+
+
+def test_qcache_file_shrinking_under_a_reader_is_a_miss(lib, tmp_path):
+    """The reader keeps the file open and reads payloads on demand: when the
+    file is cut short after the cache opened, a lookup whose payload is gone
+    is a miss (no crash), and the linear passed in is left untouched."""
+    d = tmp_path / "model"
+    d.mkdir()
+    (d / "model.safetensors").write_bytes(b"w" * 32)
+    specs, _, keep = make_linears(5)
+    path = d / "s2p_qcache.bin"
+    path.write_bytes(qf.file_bytes(qf.fingerprint(d), [(n, k, N, K, g, q.tobytes(), s.tobytes())
+                                                       for n, k, N, K, g, q, s in specs]))
+    qc = ctypes.c_void_p()
+    s2pamd.check(lib.s2p_qcache_open(str(d).encode(), 2, ctypes.byref(qc)), "open")
+    try:
+        assert lib.s2p_qcache_reading(qc) == 1
+        name, kind, N, K, g, q, s = specs[-1]
+        os.truncate(path, os.path.getsize(path) - 16)   # the last scales lose their tail
+        lin = s2pamd.Linear()
+        lin.in_features, lin.out_features = 7, 9
+        assert lib.s2p_qcache_try_load(qc, name.encode(), K, N, ctypes.byref(lin), S()) == 0
+        assert (lin.in_features, lin.out_features, lin.int8_ready) == (7, 9, 0)
+        # an entry whose payload is still complete is served
+        name0, kind0, N0, K0, *_ = specs[0]
+        lin0 = s2pamd.Linear()
+        assert lib.s2p_qcache_try_load(qc, name0.encode(), K0, N0, ctypes.byref(lin0), S()) == 1
+        s2pamd.check(lib.s2p_qcache_finish(qc, S()), "finish (read)")
+        lib.s2p_tensor_free(ctypes.byref(lin0.w_int8))
+        lib.s2p_tensor_free(ctypes.byref(lin0.w_iscale))
+    finally:
+        lib.s2p_qcache_free(qc)
+    del keep
