@@ -295,6 +295,10 @@ void s2p_backbone_set_mk(s2p_backbone* b, int on) {
 void s2p_backbone_set_mk_spin(s2p_backbone* b, unsigned spins) {
     b->mk2_spin = spins;
     if (b->mk2_ready) b->mk2.spin_limit = spins ? spins : MK2_SPIN_LIMIT;
+    if (b->g_valid) { /* the captured step holds the old limit in its kernel arguments */
+        (void)hipGraphExecDestroy(b->gexec);
+        b->g_valid = 0;
+    }
 }
 
 s2p_status s2p_verify_status(s2p_backbone* b, int32_t* out, int clear, hipStream_t st) {

@@ -14,7 +14,7 @@ import f64_forward as f64
 import s2pamd
 import pyoracle as po
 from gpu_util import P, S, assert_close_rel, bf16_bits, bf16_vals, d2h, empty, to_dev, to_host
-from test_gpu_verify import (check_logits, f64_weights, host_layer, host_linear, make_backbone,
+from test_gpu_verify import (check_logits, check_rms, f64_weights, host_layer, host_linear, make_backbone,
                              new_kv, oracle_forward, plan)
 
 pytestmark = pytest.mark.gpu
@@ -166,18 +166,39 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
     return want, truth
 
 
+def check_depth(got, want, truth, what):
+    """The accuracy criterion at full depth.  Over 36 random-init layers the
+    reference order itself lands 2.8-3.1e-2 (per-row L2) from the binary64
+    forward, because every layer rounds its stages to bf16; any other order
+    of the same roundings lands as far, on its own side (the layer-by-layer
+    path, which rounds at the reference's points, is 2.7-3.1e-2 from it).
+    So at this depth the GPU must be per row no less accurate than the
+    reference order (error against binary64 at most 1.25x the oracle's) and
+    over all rows (check_rms).  A wrong layer offset, flag or plane stride
+    moves a row by O(1), far outside this."""
+    tn = np.linalg.norm(truth, axis=1)
+    e_gpu = np.linalg.norm(got - truth, axis=1) / tn
+    e_ref = np.linalg.norm(bf16_vals(want) - truth, axis=1) / tn
+    d = np.linalg.norm(got - bf16_vals(want), axis=1) / tn
+    for r in range(len(got)):
+        print(f"{what} row {r}: gpu vs binary64 {e_gpu[r]:.3e}, oracle vs binary64 "
+              f"{e_ref[r]:.3e}, gpu vs oracle {d[r]:.3e}")
+    assert np.all(e_gpu <= 1.25 * e_ref), (what, e_gpu, e_ref)
+    check_rms(got, bf16_vals(want), truth, what)
+
+
 @pytest.mark.timeout(400)
 def test_mk2_config3_depth_vs_oracle(lib):
-    """Config 3's exact backbone shape (36 INT4-g32 layers, K=4 chain, bf16
-    KV 2048, ctx 2304 as the bench plans it) on the persistent kernel and on
-    the layer-by-layer path, each against the oracle's 36-layer forward and
-    binary64 (head: the 4,097-row slice, so the CPU side stays ~1 minute).
-    Pins what only full depth exercises: every layer's weight block base,
-    flag values and KV plane strides.  No flag wait may time out."""
+    """Config 3 exactly (36 INT4-g32 layers, the full 155,776-row INT4 head,
+    K=4 chain, bf16 KV 2048, ctx 2304 as the bench plans it) on the
+    persistent kernel and on the layer-by-layer path, each against the
+    oracle's 36-layer forward and binary64 (check_depth).  Pins what only
+    full depth exercises: every layer's weight block base, flag values and
+    KV plane strides.  No flag wait may time out."""
     ctx, n_layers, parent, L = 2304, 36, [-1, 0, 1, 2, 3], 2048
     R = len(parent)
     print("config-3 depth test: building the 36-layer backbone", flush=True)
-    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 8, 1, ctx, 2026)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB, 8, 1, ctx, 2026)
     try:
         kv = new_kv(lib, bb, 31)
         kv_host = to_host(kv, np.uint16).copy()
@@ -188,16 +209,16 @@ def test_mk2_config3_depth_vs_oracle(lib):
             kv.copy_(torch.from_numpy(kv_host.view(np.int16)).to(kv.device))
             plan(lib, bb, parent, [kv], [L])
             assert lib.s2p_backbone_mk_status(bb) == mode, "plan did not run where expected"
-            got[mode] = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_HEAD_SLICE))
+            got[mode] = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_VOCAB))
             assert lib.s2p_backbone_mk_status(bb) == mode, "a flag wait timed out"
             kv_dev[mode] = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
         print("config-3 depth test: GPU forwards done, running the references", flush=True)
         want, truth = _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent,
-                                           s2pamd.S2P_HEAD_SLICE)
+                                           s2pamd.S2P_VOCAB)
         d = np.linalg.norm(got[1] - got[0], axis=1) / np.linalg.norm(got[0], axis=1)
         print("mk2 vs layer path, per-row L2 rel:", d)
-        check_logits(got[0], want, truth, "layer path 36-layer logits")
-        check_logits(got[1], want, truth, "mk2 36-layer logits")
+        check_depth(got[0], want, truth, "layer path, 36 layers + full head")
+        check_depth(got[1], want, truth, "mk2, 36 layers + full head")
         # every layer appended its rows at L..L+R-1 and touched nothing else
         kv0 = kv_host.reshape(n_layers, 16, ctx, 128)
         for mode in (1, 0):
@@ -205,34 +226,6 @@ def test_mk2_config3_depth_vs_oracle(lib):
             assert np.array_equal(kv_dev[mode][:, :, L + R:], kv0[:, :, L + R:])
             assert np.all(np.any(kv_dev[mode][:, :, L:L + R] != kv0[:, :, L:L + R], axis=(2, 3))), \
                 "a layer's K/V plane was not appended"
-    finally:
-        lib.s2p_backbone_set_mk(bb, 1)
-        lib.s2p_backbone_free(bb)
-
-
-@pytest.mark.timeout(200)
-def test_mk2_config3_full_head_vs_layer_path(lib):
-    """Config 3 end to end (36 layers, the full 155,776-row head): the
-    persistent kernel and the layer-by-layer path agree per row within the
-    logits bar, and neither run timed out."""
-    ctx, n_layers, parent, L = 2304, 36, [-1, 0, 1, 2, 3], 2048
-    R = len(parent)
-    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB, 8, 1, ctx, 7)
-    try:
-        kv = new_kv(lib, bb, 11)
-        kv_host = to_host(kv, np.uint16).copy()
-        x = bf16_bits(np.random.default_rng(1).standard_normal((R, 2560)).astype(np.float32))
-        out = {}
-        for mode in (1, 0):
-            lib.s2p_backbone_set_mk(bb, mode)
-            kv.copy_(torch.from_numpy(kv_host.view(np.int16)).to(kv.device))
-            plan(lib, bb, parent, [kv], [L])
-            assert lib.s2p_backbone_mk_status(bb) == mode
-            out[mode] = bf16_vals(_forward(lib, bb, x, R, s2pamd.S2P_VOCAB))
-            assert lib.s2p_backbone_mk_status(bb) == mode, "a flag wait timed out"
-        rel = np.linalg.norm(out[1] - out[0], axis=1) / np.linalg.norm(out[0], axis=1)
-        print("36-layer full head, mk2 vs layer path, per-row L2 rel:", rel)
-        assert np.all(rel < 1e-2), rel
     finally:
         lib.s2p_backbone_set_mk(bb, 1)
         lib.s2p_backbone_free(bb)
