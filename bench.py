@@ -147,8 +147,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS),
-                    help="config3 (the headline metric) or the batch / tree configs 4, 5")
+    ap.add_argument("--workload", default="config3", choices=sorted(WORKLOADS) + ["tick"],
+                    help="config3 (the headline metric), the batch / tree configs 4, 5, or "
+                         "tick: the composed speculative tick on the config-3 backbone")
     ap.add_argument("--kv-bits", type=int, default=16, choices=[16, 8, 4],
                     help="session KV cache: bf16 (16) or the INT8 / INT4 quantised cache")
     ap.add_argument("--copy-calib", action="store_true",
@@ -173,6 +174,9 @@ def main():
         return
     import s2pamd
     lib = s2pamd.load()
+    if args.workload == "tick":
+        tick_bench(lib, args)
+        return
     dev = torch.device("cuda:0")
     side = torch.cuda.Stream()
     torch.cuda.synchronize()
@@ -375,6 +379,107 @@ def main():
     if headline and not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
+
+
+def tick_bench(lib, args):
+    """The composed speculative tick (s2p_spec_tick) on config 3's backbone
+    (36L INT4-g32, full head, bf16 KV 2048, one session, K = 4) with a random
+    draft model (bf16, the trainer's shapes), a random INT4 fast-AR decoder
+    and a random bf16 token embedding: draft steps + draft head + draft
+    sampling + drafted frames' fast-AR codes, the verify forward, the chain
+    condition, acceptance, the last frame's codes and the session update,
+    replayed from one graph.  Reported beside the headline, not as it."""
+    import tempfile
+    import torch
+    import s2pamd
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import draft_util as du
+    dev = torch.device("cuda:0")
+    K_, L0 = K, CTX
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        S = s2pamd.stream_ptr()
+        opts = s2pamd.BackboneOpts(N_LAYERS, s2pamd.WQ_INT4, s2pamd.WQ_INT4, s2pamd.S2P_VOCAB,
+                                   16, 1, 4096, 16)
+        bb = ctypes.c_void_p()
+        s2pamd.check(lib.s2p_backbone_create_random(ctypes.byref(opts), 2026, S, ctypes.byref(bb)))
+        fa = ctypes.c_void_p()
+        s2pamd.check(lib.s2pfa_create_random(ctypes.byref(fa), s2pamd.WQ_INT4, 16, 17, S))
+        with tempfile.TemporaryDirectory() as td:
+            path = os.path.join(td, "draft.safetensors")
+            du.write_safetensors(path, du.make_weights(3))
+            dm = s2pamd.DraftModel()
+            s2pamd.check(lib.s2p_draft_load(ctypes.byref(dm), path.encode()), "draft")
+        dst = (s2pamd.DraftState * 1)()
+        s2pamd.check(lib.s2p_draft_state_init(ctypes.byref(dst[0])))
+        embed = torch.empty(155776 * 2560, dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(embed), embed.numel(), 0.0, 0.05,
+                                                   23, S))
+        kv = torch.empty(lib.s2p_backbone_kv_bytes(bb) // 2, dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(kv), kv.numel(), 0.0, 1.0, 5, S))
+        r = np.random.default_rng(0)
+        kv_len = torch.tensor([L0], dtype=torch.int32, device=dev)
+        prev_tok = torch.tensor([151678 + 17], dtype=torch.int64, device=dev)
+        prev_codes = torch.from_numpy(r.integers(0, 4096, (1, 10)).astype(np.int32)).to(dev)
+        prev_hidden = torch.empty(2560, dtype=torch.int16, device=dev)
+        s2pamd.hip_check(lib.s2p_synth_bf16_normal(s2pamd.dptr(prev_hidden), 2560, 0.0, 1.0, 7, S))
+        st = StateBytes.make(0.8, 0.8, 1.1, 16, seed=1, entropy=1)
+        st_buf = torch.from_numpy(np.frombuffer(bytes(st), np.uint8).copy()).to(dev)
+        states = torch.tensor([st_buf.data_ptr()], dtype=torch.int64, device=dev)
+        done = torch.zeros(1, dtype=torch.uint8, device=dev)
+        n_acc = torch.zeros(1, dtype=torch.int32, device=dev)
+        n_emit = torch.zeros(1, dtype=torch.int32, device=dev)
+        emit = torch.zeros(K_ + 2, dtype=torch.int64, device=dev)
+        frames = torch.zeros((K_ + 2) * 10, dtype=torch.int32, device=dev)
+        kvp = (ctypes.c_void_p * 1)(kv.data_ptr())
+        m = s2pamd.SpecModel(bb, ctypes.addressof(dm), ctypes.addressof(dst), fa,
+                             embed.data_ptr(), 1, K_)
+        ss = s2pamd.SpecSessions(ctypes.addressof(kvp), kv_len.data_ptr(), prev_tok.data_ptr(),
+                                 prev_codes.data_ptr(), prev_hidden.data_ptr(),
+                                 states.data_ptr(), done.data_ptr())
+        o = s2pamd.SpecOut(n_acc.data_ptr(), n_emit.data_ptr(), emit.data_ptr(),
+                           frames.data_ptr())
+        sp = ctypes.c_void_p()
+        lens = np.array([L0], np.int32)
+        s2pamd.check(lib.s2p_spec_create(ctypes.byref(sp), ctypes.byref(m), ctypes.byref(ss),
+                                         lens.ctypes.data, ctypes.byref(o), S), "spec create")
+        for _ in range(max(2, args.warmup // 5)):
+            s2pamd.check(lib.s2p_spec_tick(sp, 1, S), "tick")
+        side.synchronize()
+        steps = max(5, args.steps // 10)
+        emitted = 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        for _ in range(steps):
+            s2pamd.check(lib.s2p_spec_tick(sp, 1, S), "tick")
+        e1.record(side)
+        side.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        emitted = int(kv_len.cpu()[0]) - L0  # frames advanced over warmup + timed ticks
+        mk_status = lib.s2p_backbone_mk_status(bb)
+        buf = s2pamd.SpecBuffers()
+        s2pamd.check(lib.s2p_spec_buffers_of(sp, ctypes.byref(buf)))
+        lib.s2p_spec_free(sp)
+        lib.s2p_draft_state_free(ctypes.byref(dst[0]))
+        lib.s2p_draft_free(ctypes.byref(dm))
+        lib.s2pfa_free(fa)
+        lib.s2p_backbone_free(bb)
+    if mk_status < 0:
+        print(json.dumps({"error": "a flag wait timed out during the ticks"}), flush=True)
+        sys.exit(3)
+    total = steps + max(2, args.warmup // 5)
+    print(json.dumps({
+        "metric": "speculative ticks/s (config-3 backbone, K=4, draft + fast-AR chain)",
+        "value": round(1e3 / ms, 3), "unit": "ticks/s", "n_gpus": 1, "steps": steps,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init backbone, draft, fast-AR and embedding)",
+        "config": {"workload": "tick: 36L INT4-g32 + full INT4 head, bf16 KV from 2048, b=1, "
+                               "K=4 drafts (random draft model), chain condition, T0.8 p0.8",
+                   "global_batch": 1, "seq_len": L0, "parallelism": "single GPU"},
+        "frames_per_tick": round(emitted / total, 3), "host_replans": buf.replans,
+        "mk_status": int(mk_status)}), flush=True)
 
 
 class StateBytes(ctypes.Structure):

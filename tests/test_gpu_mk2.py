@@ -135,6 +135,7 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
     pos = np.array([L + d for d in depth], np.int32)
     chain = all(parent[i] == i - 1 for i in range(1, R))
     xo = np.array(x, np.uint16, copy=True)
+    appended = np.zeros((n_layers, 16, R, 128), np.uint16)
     x64 = f64.bf(x)
     kv = kv_host.reshape(n_layers, 16, ctx, 128)
     t0 = time.time()
@@ -145,6 +146,8 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
         kc = np.ascontiguousarray(kv[l, :8])
         vc = np.ascontiguousarray(kv[l, 8:])
         po.layer(lw, xo, R, kc, vc, ctx, L, pos, None if chain else vis)
+        appended[l, :8] = kc[:, L:L + R]
+        appended[l, 8:] = vc[:, L:L + R]
         W = {}
         (w_qkv, w_o, w_gu, w_2), norms = keep[:4], keep[4]
         Lr = lib.s2p_backbone_layer(bb, l).contents
@@ -163,7 +166,7 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
     want = po.linear_fwd(head, po.rms_norm(xo, fnorm, R, 2560), R)
     hl = lib.s2p_backbone_head(bb).contents
     truth = f64.rms(x64, f64.bf(fnorm)) @ f64.dequant(hw, hs, hl.out_features, hl.in_features).T
-    return want, truth
+    return want, truth, appended
 
 
 def check_depth(got, want, truth, what):
@@ -213,19 +216,31 @@ def test_mk2_config3_depth_vs_oracle(lib):
             assert lib.s2p_backbone_mk_status(bb) == mode, "a flag wait timed out"
             kv_dev[mode] = to_host(kv, np.uint16).reshape(n_layers, 16, ctx, 128)
         print("config-3 depth test: GPU forwards done, running the references", flush=True)
-        want, truth = _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent,
-                                           s2pamd.S2P_VOCAB)
+        want, truth, appended = _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L,
+                                                     parent, s2pamd.S2P_VOCAB)
         d = np.linalg.norm(got[1] - got[0], axis=1) / np.linalg.norm(got[0], axis=1)
         print("mk2 vs layer path, per-row L2 rel:", d)
         check_depth(got[0], want, truth, "layer path, 36 layers + full head")
         check_depth(got[1], want, truth, "mk2, 36 layers + full head")
-        # every layer appended its rows at L..L+R-1 and touched nothing else
+        # every layer appended its rows at L..L+R-1 (the first two layers,
+        # before the orders drift apart, within 2e-2 of the oracle's rows)
+        # and touched nothing else
         kv0 = kv_host.reshape(n_layers, 16, ctx, 128)
+        bad = []
         for mode in (1, 0):
+            new_rows = kv_dev[mode][:, :, L:L + R]
+            same = np.all(new_rows == kv0[:, :, L:L + R], axis=(2, 3))
+            for l, h in zip(*np.nonzero(same)):
+                bad.append(f"{'mk2' if mode else 'layer path'}: layer {l} plane {h} not appended")
+            for l in range(2):
+                a, w = bf16_vals(new_rows[l]), bf16_vals(appended[l])
+                rel = np.linalg.norm(a - w) / np.linalg.norm(w)
+                print(f"{'mk2' if mode else 'layer path'} layer {l} appended K/V vs oracle: {rel:.3e}")
+                if rel > 2e-2:
+                    bad.append(f"{'mk2' if mode else 'layer path'}: layer {l} appended rows {rel:.3e}")
             assert np.array_equal(kv_dev[mode][:, :, :L], kv0[:, :, :L])
             assert np.array_equal(kv_dev[mode][:, :, L + R:], kv0[:, :, L + R:])
-            assert np.all(np.any(kv_dev[mode][:, :, L:L + R] != kv0[:, :, L:L + R], axis=(2, 3))), \
-                "a layer's K/V plane was not appended"
+        assert not bad, "\n".join(bad[:40])
     finally:
         lib.s2p_backbone_set_mk(bb, 1)
         lib.s2p_backbone_free(bb)

@@ -327,9 +327,12 @@ def test_spec_graph_equals_eager(lib, tmp_path):
             finally:
                 t.free()
     torch.cuda.synchronize()
+    R = 5
     for a, b in zip(*runs):
         for k in a:
             va, vb = a[k], b[k]
+            if k == "drf":  # a session's last draft row (a leaf's) is never written
+                va, vb = va.reshape(-1, R, va.shape[-1])[:, :R - 1], vb.reshape(-1, R, vb.shape[-1])[:, :R - 1]
             if isinstance(va, list):
                 assert all(np.array_equal(x, y) for x, y in zip(va, vb)), k
             else:
