@@ -143,8 +143,8 @@ def _streamed_references(lib, bb, n_layers, x, kv_host, ctx, L, parent, head_row
         lw, keep = host_layer(lib, bb, l)
         kc0 = f64.bf(kv[l, :8])
         vc0 = f64.bf(kv[l, 8:])
-        kc = np.ascontiguousarray(kv[l, :8])
-        vc = np.ascontiguousarray(kv[l, 8:])
+        kc = kv[l, :8].copy()  # (a contiguous slice: without the copy the layer
+        vc = kv[l, 8:].copy()  # would write into the caller's cache)
         po.layer(lw, xo, R, kc, vc, ctx, L, pos, None if chain else vis)
         appended[l, :8] = kc[:, L:L + R]
         appended[l, 8:] = vc[:, L:L + R]
