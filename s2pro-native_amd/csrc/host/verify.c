@@ -526,7 +526,7 @@ static s2p_status mk2_pack_all(s2p_backbone* b, hipStream_t st) {
  * is not served by it (the layer-by-layer path runs instead): more than
  * MK2_MAX_ROWS rows, quantised caches, INT8 weights. */
 static int mk2_build(s2p_backbone* b, hipStream_t st) {
-    if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS || b->kvb != 16 ||
+    if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS || (b->kvb != 16 && b->kvb != 8) ||
         b->o.quant != S2P_WQ_INT4_G32 || b->o.head_quant != S2P_WQ_INT4_G32 ||
         b->head.out_features > 39 * 16 * MK2_NWG || b->n_seg > 8 ||
         b->o.n_layers > MK2_MAX_LAYERS)
@@ -568,6 +568,7 @@ static int mk2_build(s2p_backbone* b, hipStream_t st) {
     A->state = b->d_mk2 + MK2_STATE_WORD;
     A->err = (int*)(b->d_mk2 + MK2_ERR_WORD);
     A->spin_limit = b->mk2_spin ? b->mk2_spin : MK2_SPIN_LIMIT;
+    A->kvb = b->kvb;
     A->plan = row_plan(b);
     A->segs = b->d_segs;
     A->n_seg = b->n_seg;

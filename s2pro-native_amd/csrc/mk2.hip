@@ -667,9 +667,47 @@ S2P_DEV void io_store(const Mk2Args& A, LDSP(unsigned char)* smem, uint16_t* dst
 #define A_SEG (A_VIS + 64)         /* the segment record */
 #define A_NW (A_VIS + 256)         /* q-norm then k-norm weights [2][128] bf16 */
 #define A_PST 136
+/* INT8 caches: the split's old rows as loaded (free until the scores) */
+#define A_R8K A_SP                 /* [128][128] int8 K codes */
+#define A_R8V (A_SP + 16 * 1024)   /* [128][128] int8 V codes */
+#define A_R8KS (A_SP + 32 * 1024)  /* [128][4] f16 K group scales */
+#define A_R8VS (A_SP + 33 * 1024)  /* [128][4] f16 V group scales */
+/* INT8 caches, kept through the unit in the GEMV bias table's space (free
+ * during attention): every row's group scales as f32, and the new slots'
+ * codes and scales as appended */
+#define A_KS8 L_BIAS               /* [128][4] f32 */
+#define A_VS8 (L_BIAS + 2048)      /* [128][4] f32 */
+#define A_NEW8 (L_BIAS + 4096)     /* [8 slots][K, V][128] int8 */
+#define A_NEW8S (L_BIAS + 6144)    /* [8 slots][K, V][4] f16 */
 #define SVX(t, d) ((t) * 128 + ((((d) >> 3) ^ (((t) >> 2) & 6)) << 3) + ((d) & 7))
 #define SKX(t, ch) ((t) * 128 + (((ch) ^ ((t) & 15)) << 3))
 static_assert(A_NW + 512 <= L_INV && sizeof(S2pAttnSeg) <= 192, "attention LDS overlaps the shared state");
+static_assert(A_R8VS + 1024 <= A_RAW && A_NEW8S + 128 <= L_TOTAL, "INT8 attention LDS");
+
+/* Quantise elements (lane, lane + 64) of one 128-wide K or V row as the
+ * INT8 append does (reference kernels.cu:541-579, this build's
+ * s2pk_kv_append8): per 32-element group, scale = f16(max|x| / 127), code =
+ * rint(x / scale) clamped to +-127.  Returns the two codes; lanes 0 and 32
+ * write the group scales of elements lane and lane + 64 (groups lane / 32
+ * and 2 + lane / 32) into hs[4]. */
+S2P_DEV void q8_row(float x0, float x1, int lane, int* c0, int* c1, LDSP(uint16_t)* hs) {
+#pragma clang fp contract(off)
+    const float xs[2] = {x0, x1};
+    int cs[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float a = fabsf(xs[h]);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        const uint16_t hv = f2h(__fdiv_rn(a, 127.f));
+        const float sc = h2f(hv);
+        int q = sc > 0.f ? (int)rintf(__fdiv_rn(xs[h], sc)) : 0;
+        cs[h] = max(-127, min(127, q));
+        if ((lane & 31) == 0) hs[2 * h + (lane >> 5)] = hv;
+    }
+    *c0 = cs[0];
+    *c1 = cs[1];
+}
 
 /* direct-to-LDS 16-byte load of lane's chunk (LDS base is wave-uniform:
  * lane l lands at base + 16 l) */
@@ -723,7 +761,22 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         const uint16_t* vp = kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
         const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, g.span);
         const int oend = min(p1, g.L);
-        if (oend > p0) {
+        if (A.kvb == 8 && oend > p0) {
+            /* INT8: codes (128 B a row) and group scales (8 B a row) of K and
+             * V, rows past the old range clamped (their LDS rows are
+             * overwritten by the new slots or zeroed) */
+            const size_t pk = ((size_t)l * 16 + kvh) * A.plan.max_seq, pv = pk + (size_t)8 * A.plan.max_seq;
+            const int8_t* cb = (const int8_t*)g.kv;
+            const uint16_t* sb = (const uint16_t*)A.plan.kvs[g.sess];
+            for (int i = 0; i < 16; i++) { /* rows 8i .. 8i + 7 */
+                const int pos = min(p0 + 8 * i + (lane >> 3), oend - 1);
+                dma16(cb + (pk + pos) * 128 + 16 * (lane & 7), (LDSP(void)*)(smem + A_R8K + i * 1024), false);
+                dma16(cb + (pv + pos) * 128 + 16 * (lane & 7), (LDSP(void)*)(smem + A_R8V + i * 1024), false);
+            }
+            const int pr = min(p0 + 2 * lane, oend - 1); /* rows 2 lane, 2 lane + 1 */
+            dma16(sb + (pk + pr) * 4, (LDSP(void)*)(smem + A_R8KS), false);
+            dma16(sb + (pv + pr) * 4, (LDSP(void)*)(smem + A_R8VS), false);
+        } else if (oend > p0) {
             for (int i = 0; i < 32; i++) { /* rows 4i .. 4i + 3 */
                 const int t = 4 * i + (lane >> 4);
                 const int pos = min(p0 + t, oend - 1);
@@ -775,7 +828,35 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
     TRACE(l, 20);
     /* 2. items: qk-norm + RoPE from LDS into the q rows and the K / V
      * tiles; rows past the split's end zeroed (their P is 0, stale LDS could
-     * be Inf / NaN) */
+     * be Inf / NaN).  INT8 caches: the old rows' codes into the tiles as
+     * bf16 (exact) and their scales as f32; the new slots quantised as the
+     * append does, their codes into the tiles and the append staging. */
+    const bool q8 = A.kvb == 8;
+    LDSP(float)* s_ks8 = (LDSP(float)*)(smem + A_KS8);
+    LDSP(float)* s_vs8 = (LDSP(float)*)(smem + A_VS8);
+    if (q8) {
+        const int nold = max(0, min(p1, L) - p0);
+        for (int i = tidx; i < nold * 32; i += NTH) { /* 8 codes of K or V a thread */
+            const int isv = i >= nold * 16, j = isv ? i - nold * 16 : i;
+            const int tr = j >> 4, ch = j & 15;
+            const uint64_t w = *(const LDSP(uint64_t)*)(smem + (isv ? A_R8V : A_R8K) + tr * 128 + ch * 8);
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float lo = (float)(int8_t)(w >> (16 * e)), hi = (float)(int8_t)(w >> (16 * e + 8));
+                o[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+            }
+            const s2p_u32x4 v = {o[0], o[1], o[2], o[3]};
+            if (isv) *(LDSP(s2p_u32x4)*)(s_v + SVX(tr, 8 * ch)) = v;
+            else *(LDSP(s2p_u32x4)*)(s_k + SKX(tr, ch)) = v;
+        }
+        for (int i = tidx; i < 128 * 8; i += NTH) { /* scales: old rows, zero past them */
+            const int isv = i >= 512, j = i & 511, tr = j >> 2;
+            const float v = tr < nold ? h2f(((const LDSP(uint16_t)*)(smem + (isv ? A_R8VS : A_R8KS)))[j]) : 0.f;
+            (isv ? s_vs8 : s_ks8)[j] = v;
+        }
+        __syncthreads(); /* (the new slots' scales below overwrite zeros) */
+    }
     for (int it = wave; it < nit; it += NWAVE) {
         const bool isq = it < nq;
         const LDSP(uint16_t)* rv = isq ? s_raw + it * 128 : s_raw + 32 * 128 + (it - nq) * 256;
@@ -790,6 +871,25 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         if (isq) {
             s_q[SKX(it, lane >> 3) + (lane & 7)] = b0;
             s_q[SKX(it, (lane + 64) >> 3) + (lane & 7)] = b1;
+        } else if (q8) {
+            const int t = s0 + (it - nq) - p0, j = it - nq;
+            LDSP(int8_t)* nc = (LDSP(int8_t)*)(smem + A_NEW8) + j * 256;
+            LDSP(uint16_t)* ns8 = (LDSP(uint16_t)*)(smem + A_NEW8S) + j * 8;
+            int c0, c1;
+            q8_row(bf2f(b0), bf2f(b1), lane, &c0, &c1, ns8);
+            s_k[SKX(t, lane >> 3) + (lane & 7)] = f2bf((float)c0);
+            s_k[SKX(t, (lane + 64) >> 3) + (lane & 7)] = f2bf((float)c1);
+            nc[lane] = (int8_t)c0;
+            nc[lane + 64] = (int8_t)c1;
+            q8_row(bf2f(rv[128 + lane]), bf2f(rv[128 + lane + 64]), lane, &c0, &c1, ns8 + 4);
+            s_v[SVX(t, lane)] = f2bf((float)c0);
+            s_v[SVX(t, lane + 64)] = f2bf((float)c1);
+            nc[128 + lane] = (int8_t)c0;
+            nc[128 + lane + 64] = (int8_t)c1;
+            if (lane < 4) {
+                s_ks8[t * 4 + lane] = h2f(ns8[lane]);
+                s_vs8[t * 4 + lane] = h2f(ns8[4 + lane]);
+            }
         } else {
             const int t = s0 + (it - nq) - p0;
             s_k[SKX(t, lane >> 3) + (lane & 7)] = b0;
@@ -810,7 +910,25 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         /* the new slots' K / V rows appended to the cache; split 0 keeps an
          * inspection copy of the roped q rows */
         uint16_t* kvb = (uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
-        for (int j = 0; j < nnew; j++) {
+        if (q8) {
+            /* codes (16 B a lane: lanes 0-7 K, 8-15 V) and scales (lanes 16, 17) */
+            const size_t pk = ((size_t)l * 16 + kvh) * A.plan.max_seq, pv = pk + (size_t)8 * A.plan.max_seq;
+            int8_t* cb = (int8_t*)g.kv;
+            uint16_t* sb = (uint16_t*)A.plan.kvs[g.sess];
+            for (int j = 0; j < nnew; j++) {
+                const size_t slot = (size_t)(s0 + j);
+                if (lane < 16) {
+                    const bool isv = lane >= 8;
+                    coh_st128(cb + ((isv ? pv : pk) + slot) * 128 + 16 * (lane & 7),
+                              *(const LDSP(s2p_u32x4)*)(smem + A_NEW8 + j * 256 + (isv ? 128 : 0) + 16 * (lane & 7)));
+                } else if (lane < 18) {
+                    const bool isv = lane == 17;
+                    coh_st64(sb + ((isv ? pv : pk) + slot) * 4,
+                             *(const LDSP(uint64_t)*)(smem + A_NEW8S + j * 16 + (isv ? 8 : 0)));
+                }
+            }
+        }
+        for (int j = 0; j < (q8 ? 0 : nnew); j++) {
             const int slot = s0 + j, t = slot - p0;
             if (lane < 32) {
                 const int ch = lane & 15;
@@ -831,6 +949,25 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
     const int t = 16 * wave + c, pos = p0 + t;
     const float scale = 0.08838834764831845f;
     s2p_f32x4 sc[2];
+    if (q8) {
+        /* one MFMA per 32-dim group (the codes are exact in bf16), then the
+         * group scales of the position in group order:
+         * s = sum_g ks[t][g] (q_g . k_g) (kernels.cu:625-700's order) */
+        const s2p_f32x4 kst = *(const LDSP(s2p_f32x4)*)(s_ks8 + t * 4);
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            s2p_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++) {
+                const s2p_u32x4 qa = *(const LDSP(s2p_u32x4)*)(s_q + SKX(16 * qt + c, 4 * ch + qq));
+                const s2p_u32x4 kb = *(const LDSP(s2p_u32x4)*)(s_k + SKX(t, 4 * ch + qq));
+                const s2p_f32x4 pg = mfma16x16x32(qa, kb, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int i = 0; i < 4; i++) d[i] = fmaf(pg[i], kst[ch], d[i]);
+            }
+            sc[qt] = d;
+        }
+    } else {
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
         s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -841,6 +978,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             acc = mfma16x16x32(qa, kb, acc);
         }
         sc[qt] = acc;
+    }
     }
     /* visibility: lane (qq, c) element i is q vector 16 qt + 4 qq + i (row
      * 4 qt + qq), position pos */
@@ -895,8 +1033,26 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         const s2p_u32x4 bv = {bw[0], bw[1], bw[2], bw[3]};
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
-            const s2p_u32x4 pa = *(const LDSP(s2p_u32x4)*)(s_p + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
-            const s2p_u32x4 pl = *(const LDSP(s2p_u32x4)*)(s_pl + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
+            s2p_u32x4 pa = *(const LDSP(s2p_u32x4)*)(s_p + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
+            s2p_u32x4 pl = *(const LDSP(s2p_u32x4)*)(s_pl + (16 * qt + c) * A_PST + 32 * ch + 8 * qq);
+            if (q8) {
+                /* the V group scale rides in P: p' = (hi + lo) x vs[t][g] for this
+                 * wave's output group g = wave / 2, split again into bf16 hi + lo */
+                const int g8 = wave >> 1, t0 = 32 * ch + 8 * qq;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t hw = pa[e], lw = pl[e];
+                    float v2[2];
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const float pv = bf2f((uint16_t)(hw >> (16 * h))) + bf2f((uint16_t)(lw >> (16 * h)));
+                        v2[h] = pv * s_vs8[(t0 + 2 * e + h) * 4 + g8];
+                    }
+                    const uint16_t h0 = f2bf(v2[0]), h1 = f2bf(v2[1]);
+                    pa[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    pl[e] = (uint32_t)f2bf(v2[0] - bf2f(h0)) | ((uint32_t)f2bf(v2[1] - bf2f(h1)) << 16);
+                }
+            }
             o[qt] = mfma16x16x32(pl, bv, o[qt]);
             o[qt] = mfma16x16x32(pa, bv, o[qt]);
         }
