@@ -716,7 +716,7 @@ S2P_DEV void dma16(const void* g, LDSP(void)* base, bool coherent) {
     else __builtin_amdgcn_global_load_lds(g, base, 16, 0, 0);
 }
 
-template <bool IO>
+template <bool IO, bool Q8>
 S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32_t epoch,
                        LDSP(unsigned char)* smem) {
 #pragma clang fp contract(off)
@@ -761,7 +761,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         const uint16_t* vp = kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
         const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, g.span);
         const int oend = min(p1, g.L);
-        if (A.kvb == 8 && oend > p0) {
+        if (Q8 && oend > p0) {
             /* INT8: codes (128 B a row) and group scales (8 B a row) of K and
              * V, rows past the old range clamped (their LDS rows are
              * overwritten by the new slots or zeroed) */
@@ -831,7 +831,7 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
      * be Inf / NaN).  INT8 caches: the old rows' codes into the tiles as
      * bf16 (exact) and their scales as f32; the new slots quantised as the
      * append does, their codes into the tiles and the append staging. */
-    const bool q8 = A.kvb == 8;
+    constexpr bool q8 = Q8;
     LDSP(float)* s_ks8 = (LDSP(float)*)(smem + A_KS8);
     LDSP(float)* s_vs8 = (LDSP(float)*)(smem + A_VS8);
     if (q8) {
@@ -1188,12 +1188,12 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
  * handed out in the same round of workgroups: a round holds
  * floor(gridDim / nsplit) whole groups, split sp of the round's group i on
  * workgroup i * nsplit + sp. */
-template <bool IO>
+template <bool IO, bool Q8>
 S2P_DEV void attn_phase(const Mk2Args& A, int l, uint32_t epoch, LDSP(unsigned char)* smem) {
     const int ns = A.nsplit, ng = A.n_seg * 8, gpr = (int)gridDim.x / ns;
     const int gi = (int)blockIdx.x / ns, sp = (int)blockIdx.x - gi * ns;
     if (gi >= gpr) return;
-    for (int grp = gi; grp < ng; grp += gpr) attn_unit<IO>(A, l, grp % A.n_seg, grp / A.n_seg, sp, epoch, smem);
+    for (int grp = gi; grp < ng; grp += gpr) attn_unit<IO, Q8>(A, l, grp % A.n_seg, grp / A.n_seg, sp, epoch, smem);
 }
 
 /* ---- head: the ring continues over this wave's head units ---- */
@@ -1264,6 +1264,8 @@ S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* sm
 }
 
 /* ---- the kernel ---- */
+/* Q8: the sessions' caches are INT8 codes + group scales (A.kvb == 8) */
+template <bool Q8>
 __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     LDSP(unsigned char)* smem = (LDSP(unsigned char)*)smem_raw;
@@ -1306,7 +1308,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
             /* attention */
-            attn_phase<false>(A, l, epoch, smem);
+            attn_phase<false, Q8>(A, l, epoch, smem);
             /* O */
             __syncthreads();
             c_gemv<PO>(S, A, l, cw, C, smem, M);
@@ -1385,7 +1387,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                      flag_val(epoch, l, MK2_F_Q), l);
             TRACE(l, 2);
             /* attention */
-            attn_phase<true>(A, l, epoch, smem);
+            attn_phase<true, Q8>(A, l, epoch, smem);
             TRACE(l, 3);
             /* O: attn -> x += wo attn */
             flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8 * A.nsplit, flag_val(epoch, l, MK2_F_ATT));
@@ -1527,9 +1529,14 @@ extern "C" int s2p_mk2_supported(void) {
     bool ok = hipGetDevice(&dev) == hipSuccess &&
               hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
               cus == MK2_NWG &&
-              hipFuncSetAttribute((const void*)k_mk2, hipFuncAttributeMaxDynamicSharedMemorySize,
+              hipFuncSetAttribute((const void*)k_mk2<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)L_TOTAL) == hipSuccess &&
-              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2, NTH, L_TOTAL) ==
+              hipFuncSetAttribute((const void*)k_mk2<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)L_TOTAL) == hipSuccess &&
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2<false>, NTH, L_TOTAL) ==
+                  hipSuccess &&
+              per_cu >= 1 &&
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2<true>, NTH, L_TOTAL) ==
                   hipSuccess &&
               per_cu >= 1;
     (void)hipGetLastError();
@@ -1542,8 +1549,10 @@ extern "C" hipError_t s2p_mk2_launch(const Mk2Args* args, hipStream_t st) {
     if (!args || args->rows < 1 || args->rows > MK2_MAX_ROWS || args->n_seg > 8 ||
         args->nsplit < 1 || args->nsplit > MK2_MAX_SPLIT ||
         args->n_seg * 8 * args->nsplit > MK2_ATT_MAX || args->n_layers > MK2_MAX_LAYERS ||
-        args->head_tiles > 39 * MK2_NWG)
+        args->head_tiles > 39 * MK2_NWG || (args->kvb != 16 && args->kvb != 8) ||
+        (args->kvb == 8 && !args->plan.kvs))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mk2, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    if (args->kvb == 8) hipLaunchKernelGGL(k_mk2<true>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    else hipLaunchKernelGGL(k_mk2<false>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
     return hipGetLastError();
 }

@@ -140,13 +140,27 @@ def _step(item, state, report, where):
 
 
 def check(asm_text, begin="CPATH_BEGIN", end="IOPATH_BEGIN"):
-    """Returns (violations, stats) for the path from the block holding the
-    `begin` marker (blocks holding `end` are not entered)."""
+    """Returns (violations, stats) for the paths from every block holding
+    the `begin` marker (one per instantiation of the kernel; blocks holding
+    `end` are not entered); stats are summed over them."""
     blocks, succ = blocks_of(parse(asm_text.split("\n")))
     starts = [i for i, b in enumerate(blocks) if any(begin in t for _, t in b)]
-    if len(starts) != 1:
-        raise ValueError(f"expected one '{begin}' marker, found {len(starts)}")
+    if not starts:
+        raise ValueError(f"no '{begin}' marker")
+    bad, total = [], {"paths": len(starts), "blocks": 0, "slot_loads": 0, "slot_waits": 0,
+                      "iterations": 0}
+    for st in starts:
+        b, s = _check_from(blocks, succ, st, end)
+        bad += b
+        for k in ("blocks", "slot_loads", "slot_waits"):
+            total[k] += s[k]
+        total["iterations"] = max(total["iterations"], s["iterations"])
+    return sorted(set(bad)), total
+
+
+def _check_from(blocks, succ, start, end):
     stop = {i for i, b in enumerate(blocks) if any(end in t for _, t in b)}
+    starts = [start]
     reach, todo = set(), [starts[0]]
     while todo:
         x = todo.pop()
