@@ -108,12 +108,19 @@ def step(ks):
 
 
 def check_appended(got, want, st, what, bw):
-    """Dequantised appended rows: every element within one quantisation step
-    (a code that rounded the other way) plus 2e-2 relative of the oracle's,
-    and the rms difference within 2e-2 (INT4, whose steps are 18x larger:
-    6e-2) of the rows' rms."""
+    """Dequantised appended rows: every element within two quantisation steps
+    plus 2e-2 relative of the oracle's, and the rms difference within 2e-2
+    (INT4, whose steps are 18x larger: 6e-2) of the rows' rms.  Two steps:
+    the K / V being quantised come out of the GEMVs in another rounding order
+    (the persistent kernel applies the RMSNorm's inverse RMS after the dot
+    product; the layer path sums in its own order from layer 1 on), and an
+    element that moved by a bf16 unit next to a rounding boundary of the code
+    moves its code by one step, and its group scale (the group maximum) moves too:
+    measured up to 2.0 steps for both forwards on a 6-row plan."""
     err = np.abs(got - want)
-    assert np.all(err <= 1.01 * st + 2e-2 * np.abs(want)), f"{what}: beyond one step"
+    bad = err > 2.01 * st + 2e-2 * np.abs(want)
+    assert not np.any(bad), (f"{what}: beyond two steps at {np.argwhere(bad)[:4].tolist()}: "
+                             f"got {got[bad][:4]}, want {want[bad][:4]}, step {st[bad][:4]}")
     rel = np.sqrt(np.mean(err ** 2) / np.mean(want ** 2))
     assert rel <= (2e-2 if bw == 8 else 6e-2), f"{what}: rms difference {rel:.3g}"
 
