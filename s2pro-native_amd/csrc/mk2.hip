@@ -850,12 +850,14 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             if (isv) *(LDSP(s2p_u32x4)*)(s_v + SVX(tr, 8 * ch)) = v;
             else *(LDSP(s2p_u32x4)*)(s_k + SKX(tr, ch)) = v;
         }
-        for (int i = tidx; i < 128 * 8; i += NTH) { /* scales: old rows, zero past them */
+        /* scales: the old rows', zeros past the split's end; the new slots'
+         * rows [nold, p1 - p0) are written by their items below */
+        const int nend = max(p1, p0) - p0;
+        for (int i = tidx; i < 128 * 8; i += NTH) {
             const int isv = i >= 512, j = i & 511, tr = j >> 2;
-            const float v = tr < nold ? h2f(((const LDSP(uint16_t)*)(smem + (isv ? A_R8VS : A_R8KS)))[j]) : 0.f;
-            (isv ? s_vs8 : s_ks8)[j] = v;
+            if (tr < nold) (isv ? s_vs8 : s_ks8)[j] = h2f(((const LDSP(uint16_t)*)(smem + (isv ? A_R8VS : A_R8KS)))[j]);
+            else if (tr >= nend) (isv ? s_vs8 : s_ks8)[j] = 0.f;
         }
-        __syncthreads(); /* (the new slots' scales below overwrite zeros) */
     }
     for (int it = wave; it < nit; it += NWAVE) {
         const bool isq = it < nq;

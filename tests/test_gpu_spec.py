@@ -331,6 +331,8 @@ def test_spec_graph_equals_eager(lib, tmp_path):
     for a, b in zip(*runs):
         for k in a:
             va, vb = a[k], b[k]
+            if k == "tok":  # entry 0 of a session (the root) is not a drafted token
+                va, vb = va.reshape(-1, R)[:, 1:], vb.reshape(-1, R)[:, 1:]
             if k == "drf":  # a session's last draft row (a leaf's) is never written
                 va, vb = va.reshape(-1, R, va.shape[-1])[:, :R - 1], vb.reshape(-1, R, vb.shape[-1])[:, :R - 1]
             if isinstance(va, list):
