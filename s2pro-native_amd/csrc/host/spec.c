@@ -164,6 +164,8 @@ s2p_status s2p_spec_create(s2p_spec** out, const s2p_spec_model* m, const s2p_sp
         /* tokens and draft logits rows no tick writes (the roots', the
          * leaves') read as zeros */
         if (rc == S2P_OK) rc = hip_ok(hipMemsetAsync(sp->tok, 0, rows * 8, st), "clear");
+        if (rc == S2P_OK) rc = hip_ok(hipMemsetAsync(sp->draft_codes, 0, rows * 9 * 4, st), "clear");
+        if (rc == S2P_OK) rc = hip_ok(hipMemsetAsync(sp->path, 0, rows * 4, st), "clear");
         if (rc == S2P_OK) rc = hip_ok(hipMemsetAsync(sp->drf, 0, rows * W * 2, st), "clear");
         if (rc == S2P_OK) rc = hip_ok(hipStreamSynchronize(st), "create sync");
     }
