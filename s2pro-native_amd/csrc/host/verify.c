@@ -526,7 +526,7 @@ static s2p_status mk2_pack_all(s2p_backbone* b, hipStream_t st) {
  * is not served by it (the layer-by-layer path runs instead): more than
  * MK2_MAX_ROWS rows, quantised caches, INT8 weights. */
 static int mk2_build(s2p_backbone* b, hipStream_t st) {
-    if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS || (b->kvb != 16 && b->kvb != 8) ||
+    if (!b->mk2_enabled || b->rows > MK2_MAX_ROWS ||
         b->o.quant != S2P_WQ_INT4_G32 || b->o.head_quant != S2P_WQ_INT4_G32 ||
         b->head.out_features > 39 * 16 * MK2_NWG || b->n_seg > 8 ||
         b->o.n_layers > MK2_MAX_LAYERS)

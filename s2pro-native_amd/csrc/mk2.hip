@@ -685,11 +685,12 @@ static_assert(A_NW + 512 <= L_INV && sizeof(S2pAttnSeg) <= 192, "attention LDS o
 static_assert(A_R8VS + 1024 <= A_RAW && A_NEW8S + 128 <= L_TOTAL, "INT8 attention LDS");
 
 /* Quantise elements (lane, lane + 64) of one 128-wide K or V row as the
- * INT8 append does (reference kernels.cu:541-579, this build's
- * s2pk_kv_append8): per 32-element group, scale = f16(max|x| / 127), code =
- * rint(x / scale) clamped to +-127.  Returns the two codes; lanes 0 and 32
+ * INT8 / INT4 append does (reference kernels.cu:541-579, this build's
+ * s2pk_kv_append8): per 32-element group, scale = f16(max|x| / QMAX), code =
+ * rint(x / scale) clamped to +-QMAX (127 / 7).  Returns the two codes; lanes 0 and 32
  * write the group scales of elements lane and lane + 64 (groups lane / 32
  * and 2 + lane / 32) into hs[4]. */
+template <int QMAX>
 S2P_DEV void q8_row(float x0, float x1, int lane, int* c0, int* c1, LDSP(uint16_t)* hs) {
 #pragma clang fp contract(off)
     const float xs[2] = {x0, x1};
@@ -699,10 +700,10 @@ S2P_DEV void q8_row(float x0, float x1, int lane, int* c0, int* c1, LDSP(uint16_
         float a = fabsf(xs[h]);
 #pragma unroll
         for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-        const uint16_t hv = f2h(__fdiv_rn(a, 127.f));
+        const uint16_t hv = f2h(__fdiv_rn(a, (float)QMAX));
         const float sc = h2f(hv);
         int q = sc > 0.f ? (int)rintf(__fdiv_rn(xs[h], sc)) : 0;
-        cs[h] = max(-127, min(127, q));
+        cs[h] = max(-QMAX, min(QMAX, q));
         if ((lane & 31) == 0) hs[2 * h + (lane >> 5)] = hv;
     }
     *c0 = cs[0];
@@ -716,7 +717,7 @@ S2P_DEV void dma16(const void* g, LDSP(void)* base, bool coherent) {
     else __builtin_amdgcn_global_load_lds(g, base, 16, 0, 0);
 }
 
-template <bool IO, bool Q8>
+template <bool IO, int KVB>
 S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32_t epoch,
                        LDSP(unsigned char)* smem) {
 #pragma clang fp contract(off)
@@ -761,17 +762,19 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         const uint16_t* vp = kvb + (size_t)(8 + kvh) * A.plan.max_seq * 128;
         const int p0 = sp * A.split_pos, p1 = min(p0 + A.split_pos, g.span);
         const int oend = min(p1, g.L);
-        if (Q8 && oend > p0) {
-            /* INT8: codes (128 B a row) and group scales (8 B a row) of K and
-             * V, rows past the old range clamped (their LDS rows are
-             * overwritten by the new slots or zeroed) */
+        if (KVB != 16 && oend > p0) {
+            /* INT8 / INT4: codes (EL = 128 / 64 B a row) and group scales
+             * (8 B a row) of K and V, rows past the old range clamped (their
+             * LDS rows are overwritten by the new slots or zeroed) */
+            constexpr int EL = KVB == 8 ? 128 : 64, RPL = 1024 / EL; /* rows a 1 KB load */
             const size_t pk = ((size_t)l * 16 + kvh) * A.plan.max_seq, pv = pk + (size_t)8 * A.plan.max_seq;
             const int8_t* cb = (const int8_t*)g.kv;
             const uint16_t* sb = (const uint16_t*)A.plan.kvs[g.sess];
-            for (int i = 0; i < 16; i++) { /* rows 8i .. 8i + 7 */
-                const int pos = min(p0 + 8 * i + (lane >> 3), oend - 1);
-                dma16(cb + (pk + pos) * 128 + 16 * (lane & 7), (LDSP(void)*)(smem + A_R8K + i * 1024), false);
-                dma16(cb + (pv + pos) * 128 + 16 * (lane & 7), (LDSP(void)*)(smem + A_R8V + i * 1024), false);
+            for (int i = 0; i < 128 / RPL; i++) {
+                const int pos = min(p0 + RPL * i + lane / (EL / 16), oend - 1);
+                const int off = 16 * (lane % (EL / 16));
+                dma16(cb + (pk + pos) * EL + off, (LDSP(void)*)(smem + A_R8K + i * 1024), false);
+                dma16(cb + (pv + pos) * EL + off, (LDSP(void)*)(smem + A_R8V + i * 1024), false);
             }
             const int pr = min(p0 + 2 * lane, oend - 1); /* rows 2 lane, 2 lane + 1 */
             dma16(sb + (pk + pr) * 4, (LDSP(void)*)(smem + A_R8KS), false);
@@ -831,7 +834,8 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
      * be Inf / NaN).  INT8 caches: the old rows' codes into the tiles as
      * bf16 (exact) and their scales as f32; the new slots quantised as the
      * append does, their codes into the tiles and the append staging. */
-    constexpr bool q8 = Q8;
+    constexpr bool q8 = KVB != 16;
+    constexpr int EL8 = KVB == 8 ? 128 : 64; /* code bytes a row */
     LDSP(float)* s_ks8 = (LDSP(float)*)(smem + A_KS8);
     LDSP(float)* s_vs8 = (LDSP(float)*)(smem + A_VS8);
     if (q8) {
@@ -839,12 +843,24 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
         for (int i = tidx; i < nold * 32; i += NTH) { /* 8 codes of K or V a thread */
             const int isv = i >= nold * 16, j = isv ? i - nold * 16 : i;
             const int tr = j >> 4, ch = j & 15;
-            const uint64_t w = *(const LDSP(uint64_t)*)(smem + (isv ? A_R8V : A_R8K) + tr * 128 + ch * 8);
             uint32_t o[4];
+            if constexpr (KVB == 8) {
+                const uint64_t w = *(const LDSP(uint64_t)*)(smem + (isv ? A_R8V : A_R8K) + tr * 128 + ch * 8);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float lo = (float)(int8_t)(w >> (16 * e)), hi = (float)(int8_t)(w >> (16 * e + 8));
-                o[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+                for (int e = 0; e < 4; e++) {
+                    const float lo = (float)(int8_t)(w >> (16 * e)), hi = (float)(int8_t)(w >> (16 * e + 8));
+                    o[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+                }
+            } else {
+                /* element 2b in the low nibble of byte b, both nibbles the
+                 * two's complement the append writes */
+                const uint32_t w = *(const LDSP(uint32_t)*)(smem + (isv ? A_R8V : A_R8K) + tr * 64 + ch * 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int8_t by = (int8_t)(w >> (8 * e));
+                    const float lo = (float)((int8_t)(by << 4) >> 4), hi = (float)(by >> 4);
+                    o[e] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+                }
             }
             const s2p_u32x4 v = {o[0], o[1], o[2], o[3]};
             if (isv) *(LDSP(s2p_u32x4)*)(s_v + SVX(tr, 8 * ch)) = v;
@@ -877,17 +893,28 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
             const int t = s0 + (it - nq) - p0, j = it - nq;
             LDSP(int8_t)* nc = (LDSP(int8_t)*)(smem + A_NEW8) + j * 256;
             LDSP(uint16_t)* ns8 = (LDSP(uint16_t)*)(smem + A_NEW8S) + j * 8;
+            constexpr int QMAX = KVB == 8 ? 127 : 7;
+            /* codes as stored: INT8 one a byte; INT4 element 2b in the low
+             * nibble of byte b (the pair's high element from the next lane) */
+            auto put = [&](LDSP(int8_t)* row, int e, int c) __attribute__((always_inline)) {
+                if constexpr (KVB == 8) {
+                    row[e] = (int8_t)c;
+                } else {
+                    const int hi = __shfl_down(c, 1, 64);
+                    if ((e & 1) == 0) row[e >> 1] = (int8_t)((c & 0xF) | ((hi & 0xF) << 4));
+                }
+            };
             int c0, c1;
-            q8_row(bf2f(b0), bf2f(b1), lane, &c0, &c1, ns8);
+            q8_row<QMAX>(bf2f(b0), bf2f(b1), lane, &c0, &c1, ns8);
             s_k[SKX(t, lane >> 3) + (lane & 7)] = f2bf((float)c0);
             s_k[SKX(t, (lane + 64) >> 3) + (lane & 7)] = f2bf((float)c1);
-            nc[lane] = (int8_t)c0;
-            nc[lane + 64] = (int8_t)c1;
-            q8_row(bf2f(rv[128 + lane]), bf2f(rv[128 + lane + 64]), lane, &c0, &c1, ns8 + 4);
+            put(nc, lane, c0);
+            put(nc, lane + 64, c1);
+            q8_row<QMAX>(bf2f(rv[128 + lane]), bf2f(rv[128 + lane + 64]), lane, &c0, &c1, ns8 + 4);
             s_v[SVX(t, lane)] = f2bf((float)c0);
             s_v[SVX(t, lane + 64)] = f2bf((float)c1);
-            nc[128 + lane] = (int8_t)c0;
-            nc[128 + lane + 64] = (int8_t)c1;
+            put(nc + 128, lane, c0);
+            put(nc + 128, lane + 64, c1);
             if (lane < 4) {
                 s_ks8[t * 4 + lane] = h2f(ns8[lane]);
                 s_vs8[t * 4 + lane] = h2f(ns8[4 + lane]);
@@ -913,18 +940,21 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
          * inspection copy of the roped q rows */
         uint16_t* kvb = (uint16_t*)g.kv + (size_t)l * A.plan.layer_stride;
         if (q8) {
-            /* codes (16 B a lane: lanes 0-7 K, 8-15 V) and scales (lanes 16, 17) */
+            /* codes (16 B a lane: K then V, EL8 / 16 lanes each) and scales
+             * (the next two lanes) */
+            constexpr int CL = EL8 / 16;
             const size_t pk = ((size_t)l * 16 + kvh) * A.plan.max_seq, pv = pk + (size_t)8 * A.plan.max_seq;
             int8_t* cb = (int8_t*)g.kv;
             uint16_t* sb = (uint16_t*)A.plan.kvs[g.sess];
             for (int j = 0; j < nnew; j++) {
                 const size_t slot = (size_t)(s0 + j);
-                if (lane < 16) {
-                    const bool isv = lane >= 8;
-                    coh_st128(cb + ((isv ? pv : pk) + slot) * 128 + 16 * (lane & 7),
-                              *(const LDSP(s2p_u32x4)*)(smem + A_NEW8 + j * 256 + (isv ? 128 : 0) + 16 * (lane & 7)));
-                } else if (lane < 18) {
-                    const bool isv = lane == 17;
+                if (lane < 2 * CL) {
+                    const bool isv = lane >= CL;
+                    const int c16 = 16 * (lane % CL);
+                    coh_st128(cb + ((isv ? pv : pk) + slot) * EL8 + c16,
+                              *(const LDSP(s2p_u32x4)*)(smem + A_NEW8 + j * 256 + (isv ? 128 : 0) + c16));
+                } else if (lane < 2 * CL + 2) {
+                    const bool isv = lane == 2 * CL + 1;
                     coh_st64(sb + ((isv ? pv : pk) + slot) * 4,
                              *(const LDSP(uint64_t)*)(smem + A_NEW8S + j * 16 + (isv ? 8 : 0)));
                 }
@@ -1190,12 +1220,12 @@ S2P_DEV void attn_unit(const Mk2Args& A, int l, int seg, int kvh, int sp, uint32
  * handed out in the same round of workgroups: a round holds
  * floor(gridDim / nsplit) whole groups, split sp of the round's group i on
  * workgroup i * nsplit + sp. */
-template <bool IO, bool Q8>
+template <bool IO, int KVB>
 S2P_DEV void attn_phase(const Mk2Args& A, int l, uint32_t epoch, LDSP(unsigned char)* smem) {
     const int ns = A.nsplit, ng = A.n_seg * 8, gpr = (int)gridDim.x / ns;
     const int gi = (int)blockIdx.x / ns, sp = (int)blockIdx.x - gi * ns;
     if (gi >= gpr) return;
-    for (int grp = gi; grp < ng; grp += gpr) attn_unit<IO, Q8>(A, l, grp % A.n_seg, grp / A.n_seg, sp, epoch, smem);
+    for (int grp = gi; grp < ng; grp += gpr) attn_unit<IO, KVB>(A, l, grp % A.n_seg, grp / A.n_seg, sp, epoch, smem);
 }
 
 /* ---- head: the ring continues over this wave's head units ---- */
@@ -1266,8 +1296,9 @@ S2P_DEV void head_reduce(const Mk2Args& A, const Ctx& C, LDSP(unsigned char)* sm
 }
 
 /* ---- the kernel ---- */
-/* Q8: the sessions' caches are INT8 codes + group scales (A.kvb == 8) */
-template <bool Q8>
+/* KVB: the sessions' caches, bf16 (16) or INT8 / INT4 codes with f16 group
+ * scales (8 / 4, A.kvb) */
+template <int KVB>
 __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     LDSP(unsigned char)* smem = (LDSP(unsigned char)*)smem_raw;
@@ -1310,7 +1341,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
             __syncthreads();
             reduce_phase<PQ>(smem, M, wg);
             /* attention */
-            attn_phase<false, Q8>(A, l, epoch, smem);
+            attn_phase<false, KVB>(A, l, epoch, smem);
             /* O */
             __syncthreads();
             c_gemv<PO>(S, A, l, cw, C, smem, M);
@@ -1389,7 +1420,7 @@ __global__ __launch_bounds__(NTH) void k_mk2(const Mk2Args A) {
                      flag_val(epoch, l, MK2_F_Q), l);
             TRACE(l, 2);
             /* attention */
-            attn_phase<true, Q8>(A, l, epoch, smem);
+            attn_phase<true, KVB>(A, l, epoch, smem);
             TRACE(l, 3);
             /* O: attn -> x += wo attn */
             flags_wait(A, MK2_F_ATT, 0, A.n_seg * 8 * A.nsplit, flag_val(epoch, l, MK2_F_ATT));
@@ -1531,16 +1562,15 @@ extern "C" int s2p_mk2_supported(void) {
     bool ok = hipGetDevice(&dev) == hipSuccess &&
               hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
               cus == MK2_NWG &&
-              hipFuncSetAttribute((const void*)k_mk2<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+              hipFuncSetAttribute((const void*)k_mk2<16>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)L_TOTAL) == hipSuccess &&
-              hipFuncSetAttribute((const void*)k_mk2<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+              hipFuncSetAttribute((const void*)k_mk2<8>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)L_TOTAL) == hipSuccess &&
-              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2<false>, NTH, L_TOTAL) ==
-                  hipSuccess &&
-              per_cu >= 1 &&
-              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_mk2<true>, NTH, L_TOTAL) ==
-                  hipSuccess &&
-              per_cu >= 1;
+              hipFuncSetAttribute((const void*)k_mk2<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)L_TOTAL) == hipSuccess;
+    for (const void* f : {(const void*)k_mk2<16>, (const void*)k_mk2<8>, (const void*)k_mk2<4>})
+        ok = ok && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, NTH, L_TOTAL) == hipSuccess &&
+             per_cu >= 1;
     (void)hipGetLastError();
     g_mk2_ok = ok ? 1 : 0;
     return ok ? 0 : -1;
@@ -1551,10 +1581,11 @@ extern "C" hipError_t s2p_mk2_launch(const Mk2Args* args, hipStream_t st) {
     if (!args || args->rows < 1 || args->rows > MK2_MAX_ROWS || args->n_seg > 8 ||
         args->nsplit < 1 || args->nsplit > MK2_MAX_SPLIT ||
         args->n_seg * 8 * args->nsplit > MK2_ATT_MAX || args->n_layers > MK2_MAX_LAYERS ||
-        args->head_tiles > 39 * MK2_NWG || (args->kvb != 16 && args->kvb != 8) ||
-        (args->kvb == 8 && !args->plan.kvs))
+        args->head_tiles > 39 * MK2_NWG || (args->kvb != 16 && args->kvb != 8 && args->kvb != 4) ||
+        (args->kvb != 16 && !args->plan.kvs))
         return hipErrorInvalidValue;
-    if (args->kvb == 8) hipLaunchKernelGGL(k_mk2<true>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
-    else hipLaunchKernelGGL(k_mk2<false>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    if (args->kvb == 8) hipLaunchKernelGGL(k_mk2<8>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    else if (args->kvb == 4) hipLaunchKernelGGL(k_mk2<4>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
+    else hipLaunchKernelGGL(k_mk2<16>, dim3(MK2_NWG), dim3(NTH), L_TOTAL, st, *args);
     return hipGetLastError();
 }

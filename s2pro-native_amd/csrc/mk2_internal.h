@@ -97,9 +97,10 @@ typedef struct {
     uint32_t* state;               /* [0] launch epoch, [1] workgroups done (monotonic) */
     int* err;                      /* sticky: a wait timed out */
     unsigned spin_limit;           /* polls per flag wait before it gives up */
-    int kvb;                       /* session caches: 16 = bf16, 8 = INT8 codes [layers][16]
-                                    * [ctx][128] with f16 group scales [layers][16][ctx][4]
-                                    * behind plan.kvs (slowar_internal.h:177-179) */
+    int kvb;                       /* session caches: 16 = bf16; 8 / 4 = INT8 / INT4 codes
+                                    * [layers][16][ctx][128 / 64] with f16 group scales
+                                    * [layers][16][ctx][4] behind plan.kvs
+                                    * (slowar_internal.h:177-179) */
     /* attention */
     S2pRowPlan plan;
     const S2pAttnSeg* segs;

@@ -130,11 +130,14 @@ def deq(kc, ks, bw):
 
 
 @pytest.mark.parametrize("bw,parent,lens,ctx", [(8, [-1, 0, 1, 2, 3], [300], 384),
-                                                # INT8 plans of <= 6 rows run on the persistent
-                                                # kernel: 17 splits, a 6-node tree, two segments
+                                                # INT8 / INT4 plans of <= 6 rows run on the
+                                                # persistent kernel: 17 splits, a 6-node tree,
+                                                # two segments
                                                 (8, [-1, 0, 1, 2, 3], [2043], 2304),
                                                 (8, [-1, 0, 0, 1, 1, 2], [301], 640),
                                                 (8, [-1, 0, 1], [500, 777], 1024),
+                                                (4, [-1, 0, 1, 2, 3], [2043], 2304),
+                                                (4, [-1, 0, 0, 1, 1, 2], [301], 640),
                                                 (4, [-1, 0, 1, 2, 3], [129], 384),
                                                 (8, TREE16, [130, 301], 384),
                                                 # 8 segments over a 4608-slot span: the
@@ -153,7 +156,7 @@ def test_verify_forward_kv8_vs_oracle(lib, bw, parent, lens, ctx):
         mk = lib.s2p_backbone_mk_status(bb)
         print(f"kv{bw}: {n} sessions x {R} rows, lens {lens}, "
               f"{'persistent kernel' if mk == 1 else 'layer path'}", flush=True)
-        assert mk == (1 if bw == 8 and n * R <= 6 else 0)
+        assert mk == (1 if n * R <= 6 else 0)
         x = bf16_bits(np.random.default_rng(9).standard_normal((n * R, 2560)).astype(np.float32))
         logits = empty((n * R, s2pamd.S2P_HEAD_SLICE))
         s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
