@@ -104,12 +104,56 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         }
     }
 
-    /* window c of the activations into LDS: the raw rows go straight to
-     * their slots (16-byte direct-to-LDS loads, one per row and wave, all in
-     * flight together), then every lane transforms its 8-element block b =
-     * lane of the rows in place (RMSNorm, k-slot order, group sums: a group's
-     * 4 blocks sit in adjacent lanes) */
-    auto stage = [&](int c) __attribute__((always_inline)) {
+    /* window c of the activations into LDS, transformed there (RMSNorm with
+     * the rule's roundings, k-slot order, group sums: a group's 4 blocks sit
+     * in adjacent lanes).  Two ways to bring the raw rows in:
+     * - stage_lds: straight to their LDS slots at staging time (16-byte
+     *   direct-to-LDS loads, one per row and wave, all in flight together),
+     *   then every lane transforms its 8-element block b = lane in place;
+     * - stage_regs (five column tiles, M = 65..80): wave w holds rows w,
+     *   w + 8, ... of the window in registers, loaded one window ahead by
+     *   prefetch() so they land while the previous window multiplies
+     *   (measured 38.3 -> 35.8 us per launch at M = 68).  At six tiles no
+     *   registers are left for them, and at three tiles it measured slower
+     *   (26.4 -> 29.3 us at M = 40). */
+    constexpr bool PF = MT == 5;
+    constexpr int RPW = PF ? 2 * MT : 1; /* rows per wave: M <= 16 MT */
+    s2p_u32x4 raw[RPW];
+    s2p_u32x4 wn4p = {0u, 0u, 0u, 0u};
+    auto zero_tail = [&](int gn) __attribute__((always_inline)) {
+        if (gn < G4_WIN)
+            for (int i = tid; i < M * 3 * (G4_WIN - gn); i += 64 * G4_WAVES) {
+                const int row = i / (G4_WIN - gn), g = gn + i % (G4_WIN - gn);
+                L.X3[row * L.xg + g] = 0;
+            }
+    };
+    auto prefetch = [&](int c) __attribute__((always_inline)) {
+        if constexpr (PF) {
+            const int nb = min(G4_WIN, G - c * G4_WIN) * 4;
+            const size_t k0 = (size_t)c * G4_WIN * 32;
+#pragma unroll
+            for (int j = 0; j < RPW; j++) {
+                const int m = wave + G4_WAVES * j;
+                raw[j] = (m < M && lane < nb) ? *(const s2p_u32x4*)(a.x + (size_t)m * a.ldx + k0 + lane * 8)
+                                              : (s2p_u32x4){0u, 0u, 0u, 0u};
+            }
+            if (a.xmode == GEMV_X_NORM && lane < nb) wn4p = *(const s2p_u32x4*)(a.norm_w + k0 + lane * 8);
+        }
+    };
+    auto stage_regs = [&](int c) __attribute__((always_inline)) {
+        const int gn = min(G4_WIN, G - c * G4_WIN);
+        const int nb = gn * 4;
+        __syncthreads(); /* the previous window is no longer read */
+        zero_tail(gn);
+        vm_drain(); /* this wave's rows (and the weights issued before) landed */
+#pragma unroll
+        for (int j = 0; j < RPW; j++) {
+            const int m = wave + G4_WAVES * j;
+            if (m < M) gv_stage_one<GEMV_W_INT4>(a, L, m, lane, lane < nb, raw[j], wn4p);
+        }
+        __syncthreads();
+    };
+    auto stage_lds = [&](int c) __attribute__((always_inline)) {
         const int gn = min(G4_WIN, G - c * G4_WIN);
         const int nb = gn * 4;
         const size_t k0 = (size_t)c * G4_WIN * 32;
@@ -121,11 +165,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
                     (LDS(void)*)(L.x + m * L.xs), 16, 0, 0);
         s2p_u32x4 wn4 = {0u, 0u, 0u, 0u};
         if (a.xmode == GEMV_X_NORM && lane < nb) wn4 = *(const s2p_u32x4*)(a.norm_w + k0 + lane * 8);
-        if (gn < G4_WIN)
-            for (int i = tid; i < M * 3 * (G4_WIN - gn); i += 64 * G4_WAVES) {
-                const int row = i / (G4_WIN - gn), g = gn + i % (G4_WIN - gn);
-                L.X3[row * L.xg + g] = 0;
-            }
+        zero_tail(gn);
         vm_drain(); /* this wave's rows (and the weights issued before) landed */
         __syncthreads();
         for (int m = wave; m < M; m += G4_WAVES) {
@@ -136,6 +176,13 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         }
         __syncthreads();
     };
+    auto stage = [&](int c) __attribute__((always_inline)) {
+        if constexpr (PF)
+            stage_regs(c);
+        else
+            stage_lds(c);
+    };
+    prefetch(c0);
 
     s2p_f32x4 acc[MT], corr[MT];
 #pragma unroll
@@ -150,11 +197,17 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     const int ce = c0 + nch;
     for (int c = c0; c < ce; c += 2) {
         stage(c);
-        if (c + 1 < ce) load_c(b1, c + 1);
+        if (c + 1 < ce) {
+            prefetch(c + 1);
+            load_c(b1, c + 1);
+        }
         mult(b0, c);
         if (c + 1 >= ce) break;
         stage(c + 1);
-        if (c + 2 < ce) load_c(b0, c + 2);
+        if (c + 2 < ce) {
+            prefetch(c + 2);
+            load_c(b0, c + 2);
+        }
         mult(b1, c + 1);
     }
 
