@@ -32,11 +32,37 @@
 #include "s2pro/kernels.h"
 #include "s2pro/slowar_kernels.h"
 
-template <int MQT, int W>
+/* Position splits are sized so that the grid stays within AT_MAX_BLOCKS
+ * blocks (two per CU): a block's fixed costs (q load or the fused prologue,
+ * the wave merge, the partial store) are paid once per block, so at configs
+ * 4 / 5 (8 x 4096 / 4 x 8192 positions) 512 blocks ran the layer's
+ * attention in 34 / 85 us against 54 / 112 us with 4096. */
+#ifndef AT_MAX_BLOCKS
+#define AT_MAX_BLOCKS 512
+#endif
+
+/* Blocks are numbered (segment fastest, then kv head, then split) and the
+ * numbering is laid over the 8 XCDs in contiguous chunks: workgroup i runs
+ * on XCD i % 8 and takes the (i / 8)-th block of chunk i % 8.  The
+ * segments of one session (a draft tree of more than 8 rows has several)
+ * read the same K/V positions of a kv head; this way they run together on
+ * one XCD and the second and third reads hit its L2. */
+template <int MQT, int W, int MODE>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    attn_block<MQT, W, false>(a, blockIdx.x, blockIdx.y, blockIdx.z,
-                              (LDS(unsigned char)*)smem_raw);
+    const int lin = (int)blockIdx.x;
+    const int total = a.nseg * a.kvh_n * a.nsplit;
+#ifdef AT_NO_XCD
+    const int b = lin;
+#else
+    /* chunk x of the numbering (the first total % 8 chunks one block
+     * longer) goes to XCD x; bijective for lin < total */
+    const int q = total >> 3, r = total & 7, xcd = lin & 7, j = lin >> 3;
+    const int b = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
+#endif
+    const int seg = b % a.nseg, rest = b / a.nseg;
+    attn_block<MQT, W, false, MODE>(a, seg, rest % a.kvh_n, rest / a.kvh_n,
+                                    (LDS(unsigned char)*)smem_raw);
 }
 
 /* merge split partials (one thread per output element) */
@@ -60,13 +86,21 @@ static int64_t part_floats(int rows, int qh, int nsplit) {
     return (int64_t)rows * qh * nsplit * (AT_HD + 2);
 }
 
-template <int MQT, int W>
+template <int MQT, int W, int MODE>
 static void attn_launch(const AttnArgs& a, dim3 grid, hipStream_t st) {
     /* once per instantiation (thread-safe static initialisation) */
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void*)k_attn<MQT, W>, hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES_W(W));
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)k_attn<MQT, W, MODE>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, AT_LDS_BYTES_W(W));
     (void)attr;
-    hipLaunchKernelGGL((k_attn<MQT, W>), grid, dim3(64 * W), AT_LDS_BYTES_W(W), st, a);
+    hipLaunchKernelGGL((k_attn<MQT, W, MODE>), grid, dim3(64 * W), AT_LDS_BYTES_W(W), st, a);
+}
+
+template <int MQT, int W>
+static void attn_launch_mode(const AttnArgs& a, dim3 grid, hipStream_t st) {
+    if (a.mode == AM_CONTIG) attn_launch<MQT, W, AM_CONTIG>(a, grid, st);
+    else if (a.mode == AM_PTRS) attn_launch<MQT, W, AM_PTRS>(a, grid, st);
+    else attn_launch<MQT, W, AM_PLAN>(a, grid, st);
 }
 
 static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
@@ -75,7 +109,7 @@ static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
     const int tiles = (max_span + AT_TILE * W - 1) / (AT_TILE * W);
     int tpw = 1; /* tiles per wave per split */
     if (a.part && part_cap > 0) {
-        while ((int64_t)n_seg * a.kvh_n * ((tiles + tpw - 1) / tpw) > 4096) tpw *= 2;
+        while ((int64_t)n_seg * a.kvh_n * ((tiles + tpw - 1) / tpw) > AT_MAX_BLOCKS) tpw *= 2;
         int nsplit = (tiles + tpw - 1) / tpw;
         while (nsplit > 1 && part_floats(a.rows, a.qh, nsplit) > part_cap) {
             tpw *= 2;
@@ -87,9 +121,11 @@ static hipError_t attn_run(AttnArgs a, int n_seg, int max_nrows, int max_span,
     a.split_pos = tpw * AT_TILE * W;
     a.nsplit = (max_span + a.split_pos - 1) / a.split_pos;
     if (a.nsplit < 1) a.nsplit = 1;
-    dim3 grid((unsigned)n_seg, (unsigned)a.kvh_n, (unsigned)a.nsplit);
-    if (max_nrows <= 4) attn_launch<1, W>(a, grid, st);
-    else attn_launch<2, W>(a, grid, st);
+    a.nseg = n_seg;
+    const int total = n_seg * a.kvh_n * a.nsplit;
+    const dim3 grid((unsigned)total);
+    if (max_nrows <= 4) attn_launch_mode<1, W>(a, grid, st);
+    else attn_launch_mode<2, W>(a, grid, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1 || a.counters) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,

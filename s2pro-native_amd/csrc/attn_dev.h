@@ -53,7 +53,8 @@ struct AttnArgs {
     S2pRowPlan plan;
     const S2pAttnSeg* segs;
     int layer;
-    /* splitting */
+    /* splitting: nseg segments x kvh_n kv heads x nsplit position splits */
+    int nseg;
     int nsplit;
     int split_pos;
     float* part;
@@ -81,17 +82,21 @@ struct SegInfo {
     const uint64_t* vis; /* NULL: causal */
 };
 
+/* MODE is a compile-time constant: each caller kind gets its own kernel,
+ * with no run-time branch over the modes */
+template <int MODE>
 S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
     SegInfo s;
     s.vis = nullptr;
-    if (a.mode == AM_CONTIG) {
+    s.first = 0;
+    if constexpr (MODE == AM_CONTIG) {
         s.row0 = seg * AT_SEG_ROWS;
         s.nrows = min(AT_SEG_ROWS, a.rows - s.row0);
         s.L = a.pos0 + s.row0;
         s.span = min(s.L + s.nrows, a.max_seq); /* never read past the cache */
         s.kp = a.kc + (size_t)kvh * a.max_seq * AT_HD;
         s.vp = a.vc + (size_t)kvh * a.max_seq * AT_HD;
-    } else if (a.mode == AM_PTRS) {
+    } else if constexpr (MODE == AM_PTRS) {
         s.row0 = seg;
         s.L = a.pos[seg];
         /* a position outside the cache attends nothing (and reads nothing) */
@@ -191,7 +196,7 @@ S2P_DEV void attn_merge_one(const float* part, uint16_t* out, int rows, int qh, 
 /* COH: the q / qkv / RoPE-table reads bypass the L2 (the persistent
  * kernel, where their producer ran in the same launch); the layer kernel
  * reads them through the caches */
-template <int MQT, int W = AT_WAVES, bool COH = true>
+template <int MQT, int W, bool COH, int MODE>
 __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsigned char)* smem) {
     constexpr int SVB = AT_SV_BYTES_W(W), SPB = AT_SP_BYTES_W(W), SMLB = AT_SML_BYTES_W(W);
     LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
@@ -210,7 +215,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int qq = lane >> 4, c = lane & 15;
-    const SegInfo S = resolve(a, seg, kvh);
+    const SegInfo S = resolve<MODE>(a, seg, kvh);
     const int p_begin = sp * a.split_pos;
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
@@ -254,7 +259,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
 
     /* Q operands: A row i = c -> query vector qv = 16 qt + c */
     s2p_u32x4 qa[MQT][4];
-    if (a.qkv) {
+    if (MODE == AM_PLAN && a.qkv) {
         /* fused qk-norm + RoPE + K/V append, one wave per (row, head) item:
          * the block's 4 q heads of its segment's rows (to LDS), then the k/v
          * of every new slot of the session inside the block's positions (a

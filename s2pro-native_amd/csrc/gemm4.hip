@@ -44,6 +44,19 @@ static __host__ __device__ size_t g4_lds_bytes(int M) {
     return x + x3 + G4_WAVES * 1024 + GEMV_MAX_M * 4 + 16;
 }
 
+#ifdef S2P_DIAG
+/* diagnostics build: wall clock per workgroup at the stages of the kernel
+ * (start, staged, first window, multiplied, partials stored, counted, merged) */
+__device__ uint64_t g4_probe[4096 * 8];
+extern "C" hipError_t s2p_g4_probe_get(uint64_t* host, int n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g4_probe), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+}
+#define G4_STAMP(i) \
+    if (threadIdx.x == 0) g4_probe[(blockIdx.y * gridDim.x + blockIdx.x) * 8 + (i)] = wall_clock64();
+#else
+#define G4_STAMP(i)
+#endif
+
 template <int MT>
 __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
 #pragma clang fp contract(off)
@@ -51,6 +64,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     LDS(unsigned char)* smem = (LDS(unsigned char)*)smem4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    G4_STAMP(0);
     const int q = lane >> 4, r = lane & 15;
     const int M = a.M, G = a.K >> 5;
     const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
@@ -195,8 +209,10 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
                                            corr);
     };
     const int ce = c0 + nch;
+    G4_STAMP(1);
     for (int c = c0; c < ce; c += 2) {
         stage(c);
+        if (c == c0) G4_STAMP(2);
         if (c + 1 < ce) {
             prefetch(c + 1);
             load_c(b1, c + 1);
@@ -218,6 +234,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) v[t][i] = 16.0f * acc[t][i] - 24.0f * corr[t][i];
+    G4_STAMP(3);
     uint16_t* Y = a.y;
     if (a.splits > 1) {
         /* K-split handoff as in the GEMV engine's split-K path: this
@@ -240,22 +257,28 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         }
         vm_drain();
         __syncthreads();
+        G4_STAMP(4);
         if (tid == 0) {
-            /* acquire-release at agent scope: the partials of every split
-             * that arrived before are visible to this workgroup's reads */
+            /* the partials were written through and their stores have
+             * completed; the last arriver reads them with agent-scope
+             * (L2-bypassing) loads, so a relaxed count suffices (an
+             * acquire-release one adds an L2 writeback and invalidate,
+             * ~2 us, to every workgroup) */
             const unsigned prev = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1u,
-                                                         __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *L.flag = prev == (unsigned)(a.splits - 1);
         }
         __syncthreads();
+        G4_STAMP(5);
         if (*L.flag) {
             /* threads 0..255 take block 2x, 256..511 block 2x + 1 */
             const int fb = blockIdx.x * 2 + (tid >> 8);
-            if (fb < a.nrb) gv_fixup<GEMV_W_INT4, false>(a, fb, Y, tid & 255);
+            if (fb < a.nrb) gv_fixup<GEMV_W_INT4, false, 4>(a, fb, Y, tid & 255);
             vm_drain();
             if (tid == 0)
                 __hip_atomic_store(&a.counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
+            G4_STAMP(6);
         }
         return;
     }

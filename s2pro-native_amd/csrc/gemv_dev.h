@@ -543,27 +543,39 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
     }
 }
 
-/* deterministic split-order sum of the partials p[k * stride], k < S, with
- * the loads of 16 splits in flight at a time */
-S2P_DEV float gv_sum_splits(const float* p, size_t stride, int S) {
-    float s = 0.f;
-    for (int k0 = 0; k0 < S; k0 += 16) {
-        float v[16];
+/* deterministic split-order sums of the partials p[j][k * stride], k < S,
+ * for NB outputs at once, the loads of 8 splits of every output in flight
+ * together.  !ok[j]: out[j] = 0, nothing read. */
+template <int NB>
+S2P_DEV void gv_sum_splits_n(const float* const (&p)[NB], const bool (&ok)[NB], size_t stride,
+                             int S, float (&out)[NB]) {
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            v[j] = k0 + j < S ? __hip_atomic_load(p + (size_t)(k0 + j) * stride, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)
+    for (int j = 0; j < NB; j++) out[j] = 0.f;
+    for (int k0 = 0; k0 < S; k0 += 8) {
+        float v[NB][8];
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                v[j][k] = ok[j] && k0 + k < S
+                              ? __hip_atomic_load(p[j] + (size_t)(k0 + k) * stride,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                               : 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            if (k0 + j < S) s += v[j];
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (k0 + k < S) out[j] += v[j][k];
     }
-    return s;
 }
 
 /* last arrival at row block rb: sum the splits and run the epilogue (on
- * 256 threads: thread tid of them) */
-template <int WFMT, bool COH>
+ * 256 threads: thread tid of them).  A thread takes FB outputs per round
+ * (output idx = base + 256 j + tid), every load of the round in flight
+ * before any sum, so a round costs one memory latency.  FB > 1 needs the
+ * registers: k_gemm4 (up to 96 rows: 24 outputs per thread) uses 4,
+ * the GEMV engine (16 rows) 1. */
+template <int WFMT, bool COH, int FB = 1>
 __device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y, int tid = threadIdx.x) {
 #pragma clang fp contract(off)
     const int lane = tid & 63;
@@ -572,45 +584,79 @@ __device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y, int tid = threa
     const float* part = a.part;
     if (a.epi == GEMV_EPI_SWIGLU) {
         const int F = a.N >> 1;
-        for (int idx = tid; idx < M * 32; idx += 256) {
-            const int m = idx >> 5, j = idx & 31;
-            const float* p0 = part + ((size_t)m * a.nrb + rb) * 64;
-            float g = gv_sum_splits(p0 + j, stride, S);
-            float u = gv_sum_splits(p0 + 32 + j, stride, S);
-            if (WFMT == GEMV_W_INT8) {
-                g *= ((const float*)a.s)[rb * 32 + j];
-                u *= ((const float*)a.s)[F + rb * 32 + j];
+        for (int base = 0; base < M * 32; base += 256 * FB) {
+            const float* pp[2 * FB];
+            bool ok[2 * FB];
+            float gu[2 * FB];
+#pragma unroll
+            for (int j = 0; j < FB; j++) {
+                const int idx = base + 256 * j + tid;
+                const int m = idx >> 5, c = idx & 31;
+                ok[2 * j] = ok[2 * j + 1] = idx < M * 32;
+                pp[2 * j] = part + ((size_t)m * a.nrb + rb) * 64 + c;
+                pp[2 * j + 1] = pp[2 * j] + 32;
             }
-            if (rb * 32 + j < F)
-                coh_st16(Y + (size_t)m * a.ldy + rb * 32 + j, silu_mul_bf16(f2bf(g), f2bf(u)));
+            gv_sum_splits_n<2 * FB>(pp, ok, stride, S, gu);
+#pragma unroll
+            for (int j = 0; j < FB; j++) {
+                const int idx = base + 256 * j + tid;
+                if (!ok[2 * j]) continue;
+                const int m = idx >> 5, c = idx & 31;
+                float g = gu[2 * j], u = gu[2 * j + 1];
+                if (WFMT == GEMV_W_INT8) {
+                    g *= ((const float*)a.s)[rb * 32 + c];
+                    u *= ((const float*)a.s)[F + rb * 32 + c];
+                }
+                if (rb * 32 + c < F)
+                    coh_st16(Y + (size_t)m * a.ldy + rb * 32 + c, silu_mul_bf16(f2bf(g), f2bf(u)));
+            }
         }
         return;
     }
-    for (int base = 0; base < M * 64; base += 256) {
-        const int idx = base + tid;
-        const int m = idx >> 6, l = idx & 63;
-        const int n = rb * 64 + l;
-        float ssq = 0.f;
-        if (m < M && n < a.N) {
-            float s = gv_sum_splits(part + ((size_t)m * a.nrb + rb) * 64 + l, stride, S);
-            if (WFMT == GEMV_W_INT8) s *= ((const float*)a.s)[n];
-            const uint16_t yb = f2bf(s);
-            uint16_t* yp = Y + (size_t)m * a.ldy + n;
-            if (a.epi == GEMV_EPI_RESID) {
-                const uint16_t xo = f2bf(__fadd_rn(bf2f(ld_act16<COH>(yp)), bf2f(yb)));
-                coh_st16(yp, xo);
-                const float xv = bf2f(xo);
-                ssq = xv * xv;
-            } else {
-                coh_st16(yp, yb);
-            }
+    for (int base = 0; base < M * 64; base += 256 * FB) {
+        const float* pp[FB];
+        bool ok[FB];
+        float sv[FB];
+        uint16_t yold[FB];
+#pragma unroll
+        for (int j = 0; j < FB; j++) {
+            const int idx = base + 256 * j + tid;
+            const int m = idx >> 6, l = idx & 63;
+            const int n = rb * 64 + l;
+            ok[j] = m < M && n < a.N;
+            pp[j] = part + ((size_t)m * a.nrb + rb) * 64 + l;
+            yold[j] = ok[j] && a.epi == GEMV_EPI_RESID
+                          ? ld_act16<COH>(Y + (size_t)m * a.ldy + n)
+                          : (uint16_t)0;
         }
-        if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
-            /* one wave = one row m = the block's 64 columns = four
-             * sum-of-squares blocks of 16 */
-            const float tot = sum_lanes16(ssq);
-            if ((lane & 15) == 0 && m < M)
-                coh_stf(a.ssq_out + (size_t)(rb * 4 + (lane >> 4)) * GEMV_MAX_M + m, tot);
+        gv_sum_splits_n<FB>(pp, ok, stride, S, sv);
+#pragma unroll
+        for (int j = 0; j < FB; j++) {
+            const int idx = base + 256 * j + tid;
+            const int m = idx >> 6, l = idx & 63;
+            const int n = rb * 64 + l;
+            float ssq = 0.f;
+            if (ok[j]) {
+                float sj = sv[j];
+                if (WFMT == GEMV_W_INT8) sj *= ((const float*)a.s)[n];
+                const uint16_t yb = f2bf(sj);
+                uint16_t* yp = Y + (size_t)m * a.ldy + n;
+                if (a.epi == GEMV_EPI_RESID) {
+                    const uint16_t xo = f2bf(__fadd_rn(bf2f(yold[j]), bf2f(yb)));
+                    coh_st16(yp, xo);
+                    const float xv = bf2f(xo);
+                    ssq = xv * xv;
+                } else {
+                    coh_st16(yp, yb);
+                }
+            }
+            if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                /* one wave = one row m = the block's 64 columns = four
+                 * sum-of-squares blocks of 16 (wave-uniform: idx >> 6) */
+                const float tot = sum_lanes16(ssq);
+                if ((lane & 15) == 0 && m < M)
+                    coh_stf(a.ssq_out + (size_t)(rb * 4 + (lane >> 4)) * GEMV_MAX_M + m, tot);
+            }
         }
     }
 }
