@@ -47,6 +47,15 @@
  * segments of one session (a draft tree of more than 8 rows has several)
  * read the same K/V positions of a kv head; this way they run together on
  * one XCD and the second and third reads hit its L2. */
+#ifdef S2P_DIAG
+/* diagnostics build: wall clock per block (logical number) at the stages of
+ * attn_block, for the last launch */
+__device__ uint64_t g_at_probe[4096 * 8];
+extern "C" hipError_t s2p_at_probe_get(uint64_t* host, int n) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_at_probe), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
 template <int MQT, int W, int MODE>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void k_attn(AttnArgs a) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -61,6 +70,9 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int b = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
 #endif
     const int seg = b % a.nseg, rest = b / a.nseg;
+#ifdef S2P_DIAG
+    a.probe = b < 4096 ? g_at_probe : nullptr;
+#endif
     attn_block<MQT, W, false, MODE>(a, seg, rest % a.kvh_n, rest / a.kvh_n,
                                     (LDS(unsigned char)*)smem_raw);
 }

@@ -10,6 +10,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "coh.h"
 #include "common.h"
 #include "prims_dev.h"
@@ -119,13 +121,17 @@ S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
     return s;
 }
 
-S2P_DEV bool visible(const SegInfo& s, int rl, int j) {
+/* may row rl see slot j: the prefix, then the causal chain or the row's
+ * tree mask word vw = s.vis[row0 + rl], which the caller loads once (any
+ * value when s.vis is NULL), so the tile loop makes no memory access */
+S2P_DEV bool visible_w(const SegInfo& s, uint64_t vw, int rl, int j) {
     if (rl >= s.nrows || j >= s.span) return false;
     if (j < s.L) return true;
     const int b = j - s.L;
     if (!s.vis) return b <= rl;
-    return b < 64 && ((s.vis[s.row0 + rl] >> b) & 1ull);
+    return b < 64 && ((vw >> b) & 1ull);
 }
+
 
 S2P_DEV float max16(float v) {
     /* every lane of the 16-lane row gets the max (DPP moves; max is exact,
@@ -216,14 +222,22 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int qq = lane >> 4, c = lane & 15;
     const SegInfo S = resolve<MODE>(a, seg, kvh);
+    /* the mask words of this lane's rows 4 qt + qq, loaded once and first
+     * (every later load is then younger, so the tile loop's waits can count
+     * the prefetches in flight) */
+    uint64_t vw[MQT];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++) {
+        const int rl = 4 * qt + ((threadIdx.x & 63) >> 4);
+        vw[qt] = S.vis && rl < S.nrows ? S.vis[S.row0 + rl] : 0ull;
+    }
     const int p_begin = sp * a.split_pos;
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
     const int qrow_stride = a.qh * AT_HD;
 #ifdef S2P_DIAG
     uint64_t* const probe =
-        a.probe ? a.probe + ((size_t)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 8
-                : nullptr;
+        a.probe ? a.probe + ((size_t)(sp * a.kvh_n + kvh) * a.nseg + seg) * 8 : nullptr;
 #else
     uint64_t* const probe = nullptr; /* stage clocks: diagnostics build only */
 #endif
@@ -236,7 +250,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
      * of load i fills bytes 16 l of the load's 1 KB = slot l % 16 of row
      * 4 i + l / 16) */
     s2p_u32x4 kr[2][4];
-    auto issue_tile = [&](int tb) __attribute__((always_inline)) {
+    auto issue_k = [&](int tb) __attribute__((always_inline)) {
 #pragma unroll
         for (int ps = 0; ps < 2; ps++) {
             const int pos = min(tb + 16 * ps + c, p_end - 1);
@@ -244,15 +258,24 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             for (int ch = 0; ch < 4; ch++)
                 kr[ps][ch] = gld_nt128(S.kp + (size_t)pos * AT_HD + 32 * ch + 8 * qq);
         }
+    };
+    /* V into registers (lane l of load i holds the 16 bytes that go to
+     * bytes 16 l of the wave's 1 KB row group i in LDS), written to LDS just
+     * before its P V: loads the compiler counts, so the tile loop's waits
+     * leave the next tile's loads in flight */
+    s2p_u32x4 vt[8];
+    auto issue_v = [&](int tb) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int t = 4 * i + (lane >> 4);
             const int pos = min(tb + t, p_end - 1);
             const int k = (lane & 15) ^ ((t >> 2) & 6);
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(S.vp + (size_t)pos * AT_HD + 8 * k),
-                (LDS(void)*)(s_v + wave * (AT_TILE * 128) + i * 512), 16, 0, 0);
+            vt[i] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * k);
         }
+    };
+    auto issue_tile = [&](int tb) __attribute__((always_inline)) {
+        issue_k(tb);
+        issue_v(tb);
     };
     const int tb0 = p_begin + wave * AT_TILE;
     bool early = false; /* first tile issued before the fused prologue */
@@ -387,12 +410,15 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int tb = tb0; tb < p_end; tb += W * AT_TILE) {
-        if (!(early && tb == tb0)) issue_tile(tb);
-        if (probe && tb == p_begin) {
-            vm_drain();
-            stamp(1);
-        }
+    /* software pipeline over this wave's tiles: the next tile's K loads
+     * (into kr, free once the scores are issued) fly during this tile's
+     * softmax and P V, its V loads (into vt, free once this tile's V is in
+     * LDS) during this P V and the next scores and softmax */
+    if (!early && tb0 < p_end) issue_tile(tb0);
+    auto tile_step = [&](int tb, auto nxt_c) __attribute__((always_inline)) {
+        constexpr bool nxt = decltype(nxt_c)::value; /* a next tile follows */
+        const int tn = tb + W * AT_TILE;
+        if (probe && tb == p_begin) stamp(1); /* prologue done, first scores next */
         /* scores */
         s2p_f32x4 sc[MQT][2];
 #pragma unroll
@@ -404,12 +430,18 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(qa[qt][ch], kr[ps][ch], acc);
                 sc[qt][ps] = acc;
             }
-        /* online softmax; lane (qq, c) holds rows 4 qq + v of each q tile */
+        if constexpr (nxt) issue_k(tn);
+        /* online softmax; lane (qq, c) holds rows 4 qq + v of each q tile.
+         * O is rescaled only when some row of the wave raised its maximum:
+         * otherwise every factor is e^0 = 1 exactly and the products would
+         * change nothing (past the first tiles of a split, the usual case) */
+        float corr[MQT][4];
+        bool raised = false;
 #pragma unroll
         for (int qt = 0; qt < MQT; qt++) {
             const int rl = 4 * qt + qq;
-            const bool vis0 = visible(S, rl, tb + c) && tb + c < p_end;
-            const bool vis1 = visible(S, rl, tb + 16 + c) && tb + 16 + c < p_end;
+            const bool vis0 = visible_w(S, vw[qt], rl, tb + c) && tb + c < p_end;
+            const bool vis1 = visible_w(S, vw[qt], rl, tb + 16 + c) && tb + 16 + c < p_end;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const float t0 = vis0 ? sc[qt][0][v] * scale : -INFINITY;
@@ -417,12 +449,11 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 const float tm = max16(fmaxf(t0, t1));
                 const float mn = fmaxf(m[qt][v], tm);
                 const float ms = mn == -INFINITY ? 0.f : mn;
-                const float corr = __expf(m[qt][v] - ms);
+                corr[qt][v] = __expf(m[qt][v] - ms);
+                raised |= corr[qt][v] != 1.0f;
                 const float p0 = __expf(t0 - ms), p1 = __expf(t1 - ms);
-                l[qt][v] = l[qt][v] * corr + p0 + p1;
+                l[qt][v] = l[qt][v] * corr[qt][v] + p0 + p1;
                 m[qt][v] = mn;
-#pragma unroll
-                for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr;
                 /* P = hi + lo, both bf16: 16 significant bits into the PV MFMA */
                 const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
                 SP(wave, 16 * qt + 4 * qq + v, c) = h0;
@@ -431,7 +462,20 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
                 SPL(wave, 16 * qt + 4 * qq + v, 16 + c) = f2bf(p1 - bf2f(h1));
             }
         }
-        vm_drain(); /* the V tile has landed in LDS */
+        if (__any(raised)) {
+#pragma unroll
+            for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr[qt][v];
+        }
+        /* this tile's V into the wave's LDS buffer (free: the previous
+         * tile's P V has read it), then the next tile's V loads */
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            *(LDS(s2p_u32x4)*)(s_v + wave * (AT_TILE * 128) + i * 512 + lane * 8) = vt[i];
+        if constexpr (nxt) issue_v(tn);
         wave_sync_lds();
         s2p_u32x4 pa[MQT], pl[MQT];
 #pragma unroll
@@ -454,6 +498,15 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             }
         }
         wave_sync_lds();
+    };
+    /* the tiles with a successor run in a loop whose every iteration issues
+     * the next tile's loads (so the compiler's waits count them), the last
+     * tile after it */
+    if (tb0 < p_end) {
+        int tb = tb0;
+        for (; tb + W * AT_TILE < p_end; tb += W * AT_TILE)
+            tile_step(tb, std::integral_constant<bool, true>{});
+        tile_step(tb, std::integral_constant<bool, false>{});
     }
 
     stamp(2);
