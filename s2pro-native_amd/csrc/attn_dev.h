@@ -121,6 +121,16 @@ S2P_DEV SegInfo resolve(const AttnArgs& a, int seg, int kvh) {
     return s;
 }
 
+/* ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+ * i % 4 of the 8-byte chunks addressed by lanes i / 4, 4 + i / 4, 8 + i / 4,
+ * 12 + i / 4 (a 4 x 4 transpose of 16-bit elements per group of lanes;
+ * measured on the part with an index pattern) */
+S2P_DEV s2p_u32x2 ds_read_tr16(const LDS(uint16_t)* p) {
+    typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS(s16x4)*)p);
+    return __builtin_bit_cast(s2p_u32x2, v);
+}
+
 /* may row rl see slot j: the prefix, then the causal chain or the row's
  * tree mask word vw = s.vis[row0 + rl], which the caller loads once (any
  * value when s.vis is NULL), so the tile loop makes no memory access */
@@ -210,11 +220,13 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     LDS(uint16_t)* s_pl = (LDS(uint16_t)*)(smem + SVB + SPB);
     LDS(float)* s_ml = (LDS(float)*)(smem + SVB + 2 * SPB);
     LDS(int)* s_flag = (LDS(int)*)(smem + SVB + 2 * SPB + SMLB);
-/* V tile of wave w: 32 positions x 16 chunks of 16 bytes, chunk (t, k)
- * stored at slot k ^ 2 (t / 8 % 4) of row t (rows of 256 B, so the PV
- * gather of 8 rows x 16 columns hits distinct banks) */
-#define SV(w, t, d) \
-    s_v[(w) * (AT_TILE * 128) + (t) * 128 + ((((d) >> 3) ^ (((t) >> 2) & 6)) << 3) + ((d) & 7)]
+/* V tile of wave w: 32 positions x 16 chunks of 16 bytes (8 dims), chunk
+ * (t, k) stored at slot k ^ vsw(t) of row t (rows of 256 B).  The P V
+ * operand is read with transposing loads (ds_read_b64_tr_b16): a read
+ * touches 16 rows (8 G + k, G < 4, k < 4) at the same two chunks, and vsw
+ * spreads them over 8 slot pairs (2-way at most). */
+#define VSW(t) ((((t) & 3) | ((((t) >> 3) & 1) << 2)) << 1)
+#define SVOFF(w, t, d) ((w) * (AT_TILE * 128) + (t) * 128 + ((((d) >> 3) ^ VSW(t)) << 3) + ((d) & 7))
 #define SP(w, r, c) s_p[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
 #define SPL(w, r, c) s_pl[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
 #define SML(w, qv, k) s_ml[((w) * 32 + (qv)) * 2 + (k)]
@@ -269,8 +281,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         for (int i = 0; i < 8; i++) {
             const int t = 4 * i + (lane >> 4);
             const int pos = min(tb + t, p_end - 1);
-            const int k = (lane & 15) ^ ((t >> 2) & 6);
-            vt[i] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * k);
+            vt[i] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * (lane & 15));
         }
     };
     auto issue_tile = [&](int tb) __attribute__((always_inline)) {
@@ -474,7 +485,7 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
          * tile's P V has read it), then the next tile's V loads */
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            *(LDS(s2p_u32x4)*)(s_v + wave * (AT_TILE * 128) + i * 512 + lane * 8) = vt[i];
+            *(LDS(s2p_u32x4)*)(s_v + SVOFF(wave, 4 * i + (lane >> 4), 8 * (lane & 15))) = vt[i];
         if constexpr (nxt) issue_v(tn);
         wave_sync_lds();
         s2p_u32x4 pa[MQT], pl[MQT];
@@ -485,12 +496,14 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         }
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            uint32_t b[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                b[e] = (uint32_t)SV(wave, 8 * qq + 2 * e, 16 * dt + c) |
-                       ((uint32_t)SV(wave, 8 * qq + 2 * e + 1, 16 * dt + c) << 16);
-            const s2p_u32x4 bv = {b[0], b[1], b[2], b[3]};
+            /* B operand (k = position 8 qq + j, n = dim 16 dt + c) by two
+             * transposing reads: lane 4 k + m of a 16-lane group supplies the
+             * 4 dims 16 dt + 4 m.. of row 8 qq + k (+ 4), and lane c receives
+             * dim 16 dt + c of the group's 4 rows */
+            const int k4 = c >> 2, m4 = c & 3;
+            const s2p_u32x2 b0 = ds_read_tr16(s_v + SVOFF(wave, 8 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x2 b1 = ds_read_tr16(s_v + SVOFF(wave, 8 * qq + 4 + k4, 16 * dt + 4 * m4));
+            const s2p_u32x4 bv = {b0.x, b0.y, b1.x, b1.y};
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++) {
                 o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
@@ -736,7 +749,8 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     const bool merged = *s_flag != 0;
     __syncthreads();
     return merged;
-#undef SV
+#undef SVOFF
+#undef VSW
 #undef SP
 #undef SPL
 #undef SML
