@@ -362,11 +362,14 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
                               : (unsigned)(((a.N + 15) / 16 + G4_WAVES - 1) / G4_WAVES);
     /* 64-row fixup blocks of the split handoff (SWIGLU: 32 gate + 32 up) */
     const int nrb = a.epi == GEMV_EPI_SWIGLU ? (a.N >> 1) / 32 : (a.N + 63) / 64;
-    /* too few row blocks to fill the chip: split K over about one workgroup
-     * per CU (needs the caller's split-K scratch: partials and counters) */
+    /* too few row blocks to fill the chip: split K over at most one
+     * workgroup per CU (needs the caller's split-K scratch: partials and
+     * counters).  One workgroup fits a CU, so a grid past the CU count runs
+     * in two rounds: gate_up (152 row blocks) split in two took 44.5 us at
+     * M = 40, unsplit (five windows a workgroup, no handoff) about half */
     const int nch = ((a.K >> 5) + G4_WIN - 1) / G4_WIN;
     const int cus = s2p_cu_count();
-    int ks = (int)(((unsigned)cus + nblk - 1) / nblk);
+    int ks = (int)((unsigned)cus / nblk);
     if (ks > nch) ks = nch;
     if (ks < 1) ks = 1;
     int cps = (nch + ks - 1) / ks;
