@@ -337,8 +337,10 @@ def main():
             abytes = sum(2 * M * (lin.in_features + lin.out_features) for lin in lins)
             per_launch = (wbytes + abytes) / len(lins)
             kern_gbs = per_launch / avg_launch_s / 1e9
-            kern_name = (f"k_gemv3<INT4, MT={(M + 15) // 16}> (all 145 weight GEMVs of a step, "
-                         f"layer path)")
+            # M <= 16 rows run on the GEMV engine, 16 < M <= 96 on k_gemm4
+            mt = (M + 15) // 16
+            kern_name = ((f"k_gemv3<INT4, MT={mt}>" if M <= 16 else f"k_gemm4<MT={mt}>") +
+                         " (all 145 weight GEMVs of a step, layer path)")
         lib.s2p_backbone_free(bb)
 
     w, kvb, alg = step_alg_bytes(lens, M, args.kv_bits)
