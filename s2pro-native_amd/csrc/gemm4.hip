@@ -36,10 +36,13 @@
 
 static __host__ __device__ size_t g4_xs() { return (size_t)G4_WIN * 32 + GV_XPAD; }
 static __host__ __device__ size_t g4_xg() { return (size_t)gv_round32(G4_WIN) + 8; }
-/* x [M][xs] bf16 | X3 [M][3][xg] bf16 | scale staging [waves][16][16] f32 |
- * inverse RMS [GEMV_MAX_M] f32 */
+/* x [M][xs] bf16 (two of them up to four column tiles: the next window's
+ * rows land in the second while the first multiplies) | X3 [M][3][xg] bf16 |
+ * scale staging [waves][16][16] f32 | inverse RMS [GEMV_MAX_M] f32 */
+static __host__ __device__ bool g4_dbuf(int M) { return (M + 15) / 16 <= 4; }
+static __host__ __device__ size_t g4_xbytes(int M) { return ((size_t)M * g4_xs() * 2 + 15) & ~(size_t)15; }
 static __host__ __device__ size_t g4_lds_bytes(int M) {
-    const size_t x = ((size_t)M * g4_xs() * 2 + 15) & ~(size_t)15;
+    const size_t x = g4_xbytes(M) * (g4_dbuf(M) ? 2 : 1);
     const size_t x3 = ((size_t)M * 3 * g4_xg() * 2 + 15) & ~(size_t)15;
     return x + x3 + G4_WAVES * 1024 + GEMV_MAX_M * 4 + 16;
 }
@@ -87,8 +90,9 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     GvLds L;
     L.xs = (int)g4_xs();
     L.xg = (int)g4_xg();
+    constexpr bool DB = MT <= 4; /* g4_dbuf */
     L.x = (LDS(uint16_t)*)smem;
-    size_t off = ((size_t)M * L.xs * 2 + 15) & ~(size_t)15;
+    size_t off = g4_xbytes(M) * (DB ? 2 : 1);
     L.X3 = (LDS(uint16_t)*)(smem + off);
     off += ((size_t)M * 3 * L.xg * 2 + 15) & ~(size_t)15;
     L.sc = (LDS(float)*)(smem + off + (size_t)wave * 1024);
@@ -210,6 +214,62 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     };
     const int ce = c0 + nch;
     G4_STAMP(1);
+    if constexpr (DB) {
+        /* double-buffered windows: the raw rows of window c + 1 go to the
+         * other x buffer (direct-to-LDS) right after window c is staged, so
+         * they land while c multiplies; staging then only waits, transforms
+         * in place and publishes */
+        GvLds Lb[2] = {L, L};
+        Lb[1].x = (LDS(uint16_t)*)(smem + g4_xbytes(M));
+        s2p_u32x4 wnb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        auto issue = [&](int c, int bsel) __attribute__((always_inline)) {
+            const int nb = min(G4_WIN, G - c * G4_WIN) * 4;
+            const size_t k0 = (size_t)c * G4_WIN * 32;
+            for (int m = wave; m < M; m += G4_WAVES)
+                if (lane < nb)
+                    __builtin_amdgcn_global_load_lds(
+                        (const void*)(a.x + (size_t)m * a.ldx + k0 + lane * 8),
+                        (LDS(void)*)(Lb[bsel].x + m * L.xs), 16, 0, 0);
+            if (a.xmode == GEMV_X_NORM && lane < nb)
+                wnb[bsel] = *(const s2p_u32x4*)(a.norm_w + k0 + lane * 8);
+        };
+        auto stage_db = [&](int c, int bsel) __attribute__((always_inline)) {
+            const int gn = min(G4_WIN, G - c * G4_WIN);
+            const int nb = gn * 4;
+            __syncthreads(); /* the previous window (and its X3) is no longer read */
+            zero_tail(gn);
+            vm_drain(); /* this wave's rows of window c (and the weights issued before) landed */
+            __syncthreads();
+            for (int m = wave; m < M; m += G4_WAVES) {
+                const bool ok = lane < nb;
+                const s2p_u32x4 rw = ok ? *(const LDS(s2p_u32x4)*)(Lb[bsel].x + m * L.xs + lane * 8)
+                                        : (s2p_u32x4){0u, 0u, 0u, 0u};
+                gv_stage_one<GEMV_W_INT4>(a, Lb[bsel], m, lane, ok, rw, wnb[bsel]);
+            }
+            __syncthreads();
+        };
+        auto mult_db = [&](const GvBuf& B, int c, int bsel) __attribute__((always_inline)) {
+            gv_compute<GEMV_W_INT4, MT, false>(B, Lb[bsel], 0, min(G4_WIN, G - c * G4_WIN), M, 0, q,
+                                               r, acc, corr);
+        };
+        issue(c0, 0);
+        for (int c = c0; c < ce; c += 2) {
+            stage_db(c, 0);
+            if (c == c0) G4_STAMP(2);
+            if (c + 1 < ce) {
+                issue(c + 1, 1);
+                load_c(b1, c + 1);
+            }
+            mult_db(b0, c, 0);
+            if (c + 1 >= ce) break;
+            stage_db(c + 1, 1);
+            if (c + 2 < ce) {
+                issue(c + 2, 0);
+                load_c(b0, c + 2);
+            }
+            mult_db(b1, c + 1, 1);
+        }
+    } else
     for (int c = c0; c < ce; c += 2) {
         stage(c);
         if (c == c0) G4_STAMP(2);
