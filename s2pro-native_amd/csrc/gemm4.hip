@@ -333,7 +333,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         if (*L.flag) {
             /* threads 0..255 take block 2x, 256..511 block 2x + 1 */
             const int fb = blockIdx.x * 2 + (tid >> 8);
-            if (fb < a.nrb) gv_fixup<GEMV_W_INT4, false, 4>(a, fb, Y, tid & 255);
+            if (fb < a.nrb) gv_fixup4<3>(a, fb, Y, tid & 255);
             vm_drain();
             if (tid == 0)
                 __hip_atomic_store(&a.counters[blockIdx.x], 0u, __ATOMIC_RELAXED,

@@ -543,119 +543,113 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
     }
 }
 
-/* deterministic split-order sums of the partials p[j][k * stride], k < S,
- * for NB outputs at once, the loads of 8 splits of every output in flight
- * together.  !ok[j]: out[j] = 0, nothing read. */
-template <int NB>
-S2P_DEV void gv_sum_splits_n(const float* const (&p)[NB], const bool (&ok)[NB], size_t stride,
-                             int S, float (&out)[NB]) {
-#pragma unroll
-    for (int j = 0; j < NB; j++) out[j] = 0.f;
-    for (int k0 = 0; k0 < S; k0 += 8) {
-        float v[NB][8];
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                v[j][k] = ok[j] && k0 + k < S
-                              ? __hip_atomic_load(p[j] + (size_t)(k0 + k) * stride,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : 0.f;
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                if (k0 + k < S) out[j] += v[j][k];
-    }
-}
-
-/* last arrival at row block rb: sum the splits and run the epilogue (on
- * 256 threads: thread tid of them).  A thread takes FB outputs per round
- * (output idx = base + 256 j + tid), every load of the round in flight
- * before any sum, so a round costs one memory latency.  FB > 1 needs the
- * registers: k_gemm4 (up to 96 rows: 24 outputs per thread) uses 4,
- * the GEMV engine (16 rows) 1. */
-template <int WFMT, bool COH, int FB = 1>
-__device__ void gv_fixup(const GemvArgs& a, int rb, uint16_t* Y, int tid = threadIdx.x) {
+/* last arrival at row block rb: sum the splits in split order and run the
+ * epilogue (on 256 threads: thread tid of them).  A thread takes FB groups
+ * of four adjacent outputs per round, each split's four partials as one
+ * 16-byte agent-scope load (two 8-byte loads), every load of a round in
+ * flight before any sum: at 48 rows (FB = 3) a 64-row block takes one round
+ * of memory latency, where one output a thread per round took three. */
+template <int FB, int WFMT = GEMV_W_INT4, bool COH = false>
+__device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid) {
 #pragma clang fp contract(off)
     const int lane = tid & 63;
     const int M = a.M, S = a.splits;
     const size_t stride = (size_t)M * a.nrb * 64;
     const float* part = a.part;
-    if (a.epi == GEMV_EPI_SWIGLU) {
-        const int F = a.N >> 1;
-        for (int base = 0; base < M * 32; base += 256 * FB) {
-            const float* pp[2 * FB];
-            bool ok[2 * FB];
-            float gu[2 * FB];
+    const bool swiglu = a.epi == GEMV_EPI_SWIGLU;
+    /* items: (m, 4 outputs); SWIGLU: 8 gate groups a row (each with its up
+     * group 32 later), else 16 groups a row */
+    const int per_row = swiglu ? 8 : 16;
+    const int items = M * per_row;
+    for (int base = 0; base < items; base += 256 * FB) {
+        s2p_f32x4 g[FB], u[FB];
+        uint16_t yold[FB][4];
 #pragma unroll
-            for (int j = 0; j < FB; j++) {
-                const int idx = base + 256 * j + tid;
-                const int m = idx >> 5, c = idx & 31;
-                ok[2 * j] = ok[2 * j + 1] = idx < M * 32;
-                pp[2 * j] = part + ((size_t)m * a.nrb + rb) * 64 + c;
-                pp[2 * j + 1] = pp[2 * j] + 32;
+        for (int j = 0; j < FB; j++) {
+            g[j] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            u[j] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+            const int idx = base + 256 * j + tid;
+            const int m = idx / per_row, l4 = (idx % per_row) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = rb * 64 + l4 + e;
+                yold[j][e] = !swiglu && idx < items && a.epi == GEMV_EPI_RESID && n < a.N
+                                 ? ld_act16<COH>(Y + (size_t)m * a.ldy + n)
+                                 : (uint16_t)0;
             }
-            gv_sum_splits_n<2 * FB>(pp, ok, stride, S, gu);
+        }
+        for (int k0 = 0; k0 < S; k0 += 4) {
+            s2p_u32x4 vg[FB][4], vu[FB][4];
 #pragma unroll
             for (int j = 0; j < FB; j++) {
                 const int idx = base + 256 * j + tid;
-                if (!ok[2 * j]) continue;
-                const int m = idx >> 5, c = idx & 31;
-                float g = gu[2 * j], u = gu[2 * j + 1];
-                if (WFMT == GEMV_W_INT8) {
-                    g *= ((const float*)a.s)[rb * 32 + c];
-                    u *= ((const float*)a.s)[F + rb * 32 + c];
+                const bool ok = idx < items;
+                const int m = idx / per_row, l4 = (idx % per_row) * 4;
+                const float* p0 = part + ((size_t)m * a.nrb + rb) * 64 + l4;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const bool ld = ok && k0 + k < S;
+                    vg[j][k] = ld ? coh_ld128(p0 + (size_t)(k0 + k) * stride) : (s2p_u32x4){0u, 0u, 0u, 0u};
+                    vu[j][k] = ld && swiglu ? coh_ld128(p0 + 32 + (size_t)(k0 + k) * stride)
+                                            : (s2p_u32x4){0u, 0u, 0u, 0u};
                 }
-                if (rb * 32 + c < F)
-                    coh_st16(Y + (size_t)m * a.ldy + rb * 32 + c, silu_mul_bf16(f2bf(g), f2bf(u)));
             }
+#pragma unroll
+            for (int j = 0; j < FB; j++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (k0 + k >= S) break;
+                    const s2p_f32x4 fg = __builtin_bit_cast(s2p_f32x4, vg[j][k]);
+                    const s2p_f32x4 fu = __builtin_bit_cast(s2p_f32x4, vu[j][k]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        g[j][e] += fg[e];
+                        if (swiglu) u[j][e] += fu[e];
+                    }
+                }
         }
-        return;
-    }
-    for (int base = 0; base < M * 64; base += 256 * FB) {
-        const float* pp[FB];
-        bool ok[FB];
-        float sv[FB];
-        uint16_t yold[FB];
 #pragma unroll
         for (int j = 0; j < FB; j++) {
             const int idx = base + 256 * j + tid;
-            const int m = idx >> 6, l = idx & 63;
-            const int n = rb * 64 + l;
-            ok[j] = m < M && n < a.N;
-            pp[j] = part + ((size_t)m * a.nrb + rb) * 64 + l;
-            yold[j] = ok[j] && a.epi == GEMV_EPI_RESID
-                          ? ld_act16<COH>(Y + (size_t)m * a.ldy + n)
-                          : (uint16_t)0;
-        }
-        gv_sum_splits_n<FB>(pp, ok, stride, S, sv);
-#pragma unroll
-        for (int j = 0; j < FB; j++) {
-            const int idx = base + 256 * j + tid;
-            const int m = idx >> 6, l = idx & 63;
-            const int n = rb * 64 + l;
+            const bool ok = idx < items;
+            const int m = idx / per_row, l4 = (idx % per_row) * 4;
             float ssq = 0.f;
-            if (ok[j]) {
-                float sj = sv[j];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (swiglu) {
+                    const int c = l4 + e; /* gate row rb * 32 + c */
+                    const int F = a.N >> 1;
+                    if (!ok || rb * 32 + c >= F) continue;
+                    float gg = g[j][e], uu = u[j][e];
+                    if (WFMT == GEMV_W_INT8) {
+                        gg *= ((const float*)a.s)[rb * 32 + c];
+                        uu *= ((const float*)a.s)[F + rb * 32 + c];
+                    }
+                    coh_st16(Y + (size_t)m * a.ldy + rb * 32 + c, silu_mul_bf16(f2bf(gg), f2bf(uu)));
+                    continue;
+                }
+                const int n = rb * 64 + l4 + e;
+                if (!ok || n >= a.N) continue;
+                float sj = g[j][e];
                 if (WFMT == GEMV_W_INT8) sj *= ((const float*)a.s)[n];
                 const uint16_t yb = f2bf(sj);
                 uint16_t* yp = Y + (size_t)m * a.ldy + n;
                 if (a.epi == GEMV_EPI_RESID) {
-                    const uint16_t xo = f2bf(__fadd_rn(bf2f(yold[j]), bf2f(yb)));
+                    const uint16_t xo = f2bf(__fadd_rn(bf2f(yold[j][e]), bf2f(yb)));
                     coh_st16(yp, xo);
                     const float xv = bf2f(xo);
-                    ssq = xv * xv;
+                    ssq += xv * xv;
                 } else {
                     coh_st16(yp, yb);
                 }
             }
-            if (a.epi == GEMV_EPI_RESID && a.ssq_out) {
-                /* one wave = one row m = the block's 64 columns = four
-                 * sum-of-squares blocks of 16 (wave-uniform: idx >> 6) */
-                const float tot = sum_lanes16(ssq);
-                if ((lane & 15) == 0 && m < M)
-                    coh_stf(a.ssq_out + (size_t)(rb * 4 + (lane >> 4)) * GEMV_MAX_M + m, tot);
+            if (!swiglu && a.epi == GEMV_EPI_RESID && a.ssq_out) {
+                /* a 16-column sum-of-squares block is 4 adjacent lanes (same m:
+                 * 16 items a row, rows start at multiples of 16 lanes) */
+                ssq += __shfl_xor(ssq, 1, 64);
+                ssq += __shfl_xor(ssq, 2, 64);
+                if ((lane & 3) == 0 && ok)
+                    coh_stf(a.ssq_out + (size_t)(rb * 4 + (l4 >> 4)) * GEMV_MAX_M + m, ssq);
             }
         }
     }
@@ -797,7 +791,7 @@ __device__ void gv_block(const GemvArgs& a, int p, int P, int sp, LDS(unsigned c
         GV_PROBE(5);
         const bool last = *L.flag != 0;
         if (last) {
-            gv_fixup<WFMT, COH>(a, rb, Y);
+            gv_fixup4<1, WFMT, COH>(a, rb, Y, threadIdx.x);
             vm_drain();
             GV_PROBE(6);
             if (tid == 0)
