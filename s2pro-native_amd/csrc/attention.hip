@@ -85,6 +85,254 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
     attn_merge_one<false>(part, out, rows, qh, nsplit, blockIdx.x, blockIdx.y, threadIdx.x);
 }
 
+/* ---- tree segments: one block per (session, kv head, split) ----
+ * A draft tree of R > 8 rows per session (config 5: 17) in 8-row segments
+ * has every segment read its session's K/V again.  Here one block takes all
+ * R <= 32 rows of the session: its 4 waves are the 4 query heads of the GQA
+ * group (wave g: head 4 kvh + g, q tiles of 16 rows), and share each
+ * 32-position K/V tile through LDS, so the K/V are read once.  The q rows
+ * come roped from the q buffer (k_qkrope_append ran before).  Per tile:
+ * S = Q K^T (K from LDS), online softmax, P (bf16 hi + lo) through LDS,
+ * O += P V with V read by transposing loads.  Every wave ends with its
+ * head's (m, l, O) over the split: the partial, merged by k_attn_combine. */
+#define TR_KOFF(t, ch) ((t) * 128 + ((((ch) ^ ((t) & 15))) << 3))
+#define TR_VSW(t) ((((t) & 3) | ((((t) >> 3) & 1) << 2)) << 1)
+#define TR_VOFF(t, d) ((t) * 128 + ((((d) >> 3) ^ TR_VSW(t)) << 3) + ((d) & 7))
+#define TR_LDS_BYTES (4 * AT_TILE * 128 * 2 + 2 * 4 * 32 * AT_PSTRIDE * 2)
+
+template <int MQT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_tree(AttnArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    LDS(unsigned char)* smem = (LDS(unsigned char)*)smem_raw;
+    LDS(uint16_t)* s_k = (LDS(uint16_t)*)smem;                           /* [2][32][128] */
+    LDS(uint16_t)* s_v = s_k + 2 * AT_TILE * 128;                         /* [2][32][128] */
+    LDS(uint16_t)* s_p = s_v + 2 * AT_TILE * 128;                         /* [4 waves][32][PSTRIDE] */
+    LDS(uint16_t)* s_pl = s_p + 4 * 32 * AT_PSTRIDE;
+    const int lin = (int)blockIdx.x;
+    const int total = a.nseg * a.kvh_n * a.nsplit;
+    const int qd = total >> 3, rd = total & 7, xcd = lin & 7, jd = lin >> 3;
+    const int b = xcd < rd ? xcd * (qd + 1) + jd : rd * (qd + 1) + (xcd - rd) * qd + jd;
+    const int seg = b % a.nseg, rest = b / a.nseg;
+    const int kvh = rest % a.kvh_n, sp = rest / a.kvh_n;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qq = lane >> 4, c = lane & 15;
+    const SegInfo S = resolve<AM_PLAN>(a, seg, kvh);
+    const int h = 4 * kvh + wave;
+    const int p_begin = sp * a.split_pos;
+    const int p_end = min(p_begin + a.split_pos, S.span);
+    const float scale = 0.08838834764831845f;
+
+    /* this lane's rows of the score / output tiles: 16 qt + 4 qq + v */
+    uint64_t vw[MQT][4];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int r = 16 * qt + 4 * qq + v;
+            vw[qt][v] = S.vis && r < S.nrows ? S.vis[S.row0 + r] : 0ull;
+        }
+    /* Q operand (A): row c of tile qt, dims 32 ch + 8 qq .. + 7 */
+    s2p_u32x4 qa[MQT][4];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++) {
+        const int r = 16 * qt + c;
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++)
+            qa[qt][ch] = r < S.nrows ? *(const s2p_u32x4*)(a.q + (size_t)(S.row0 + r) * (a.qh * AT_HD) +
+                                                             h * AT_HD + 32 * ch + 8 * qq)
+                                     : (s2p_u32x4){0u, 0u, 0u, 0u};
+    }
+
+    /* the block's K/V tile loads: chunk i = tid, tid + 256 of the tile's
+     * 512 16-byte chunks (row i / 16, chunk i % 16) of K, then of V */
+    s2p_u32x4 ld[4];
+    auto load_tile = [&](int tb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = tid + 256 * j, t = i >> 4, ch = i & 15;
+            const int pos = min(tb + t, p_end - 1);
+            ld[j] = gld_nt128(S.kp + (size_t)pos * AT_HD + 8 * ch);
+            ld[2 + j] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * ch);
+        }
+    };
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = tid + 256 * j, t = i >> 4, ch = i & 15;
+            *(LDS(s2p_u32x4)*)(s_k + buf * AT_TILE * 128 + TR_KOFF(t, ch)) = ld[j];
+            *(LDS(s2p_u32x4)*)(s_v + buf * AT_TILE * 128 + TR_VOFF(t, 8 * ch)) = ld[2 + j];
+        }
+    };
+
+    float m[MQT][4], l[MQT][4];
+    s2p_f32x4 o[MQT][8];
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            m[qt][v] = -INFINITY;
+            l[qt][v] = 0.f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int ntile = p_end > p_begin ? (p_end - p_begin + AT_TILE - 1) / AT_TILE : 0;
+    if (ntile > 0) {
+        load_tile(p_begin);
+        store_tile(0);
+        if (ntile > 1) load_tile(p_begin + AT_TILE);
+    }
+    __syncthreads();
+    for (int ti = 0; ti < ntile; ti++) {
+        const int tb = p_begin + ti * AT_TILE, buf = ti & 1;
+        const LDS(uint16_t)* kt = s_k + buf * AT_TILE * 128;
+        const LDS(uint16_t)* vt = s_v + buf * AT_TILE * 128;
+        /* scores: K operand (B) = row 16 ps + c, dims 32 ch + 8 qq .. */
+        s2p_f32x4 sc[MQT][2];
+#pragma unroll
+        for (int ps = 0; ps < 2; ps++) {
+            s2p_u32x4 kb[4];
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++)
+                kb[ch] = *(const LDS(s2p_u32x4)*)(kt + TR_KOFF(16 * ps + c, 4 * ch + qq));
+#pragma unroll
+            for (int qt = 0; qt < MQT; qt++) {
+                s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(qa[qt][ch], kb[ch], acc);
+                sc[qt][ps] = acc;
+            }
+        }
+        /* online softmax (rows 16 qt + 4 qq + v, positions tb + c, + 16) */
+        float corr[MQT][4];
+        bool raised = false;
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = 16 * qt + 4 * qq + v;
+                const bool vis0 = visible_w(S, vw[qt][v], r, tb + c) && tb + c < p_end;
+                const bool vis1 = visible_w(S, vw[qt][v], r, tb + 16 + c) && tb + 16 + c < p_end;
+                const float t0 = vis0 ? sc[qt][0][v] * scale : -INFINITY;
+                const float t1 = vis1 ? sc[qt][1][v] * scale : -INFINITY;
+                const float tm = max16(fmaxf(t0, t1));
+                const float mn = fmaxf(m[qt][v], tm);
+                const float ms = mn == -INFINITY ? 0.f : mn;
+                corr[qt][v] = __expf(m[qt][v] - ms);
+                raised |= corr[qt][v] != 1.0f;
+                const float p0 = __expf(t0 - ms), p1 = __expf(t1 - ms);
+                l[qt][v] = l[qt][v] * corr[qt][v] + p0 + p1;
+                m[qt][v] = mn;
+                const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
+                LDS(uint16_t)* prow = s_p + (wave * 32 + 16 * qt + 4 * qq + v) * AT_PSTRIDE;
+                LDS(uint16_t)* plrow = s_pl + (wave * 32 + 16 * qt + 4 * qq + v) * AT_PSTRIDE;
+                prow[c] = h0;
+                prow[16 + c] = h1;
+                plrow[c] = f2bf(p0 - bf2f(h0));
+                plrow[16 + c] = f2bf(p1 - bf2f(h1));
+            }
+        if (__any(raised)) {
+#pragma unroll
+            for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr[qt][v];
+        }
+        wave_sync_lds();
+        s2p_u32x4 pa[MQT], pl[MQT];
+#pragma unroll
+        for (int qt = 0; qt < MQT; qt++) {
+            pa[qt] = *(const LDS(s2p_u32x4)*)(s_p + (wave * 32 + 16 * qt + c) * AT_PSTRIDE + 8 * qq);
+            pl[qt] = *(const LDS(s2p_u32x4)*)(s_pl + (wave * 32 + 16 * qt + c) * AT_PSTRIDE + 8 * qq);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const int k4 = c >> 2, m4 = c & 3;
+            const s2p_u32x2 b0 = ds_read_tr16(vt + TR_VOFF(8 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x2 b1 = ds_read_tr16(vt + TR_VOFF(8 * qq + 4 + k4, 16 * dt + 4 * m4));
+            const s2p_u32x4 bv = {b0.x, b0.y, b1.x, b1.y};
+#pragma unroll
+            for (int qt = 0; qt < MQT; qt++) {
+                o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+            }
+        }
+        /* the next tile into the other buffer (its previous tile was read
+         * before the last barrier), then the one after into registers */
+        if (ti + 1 < ntile) store_tile(buf ^ 1);
+        __syncthreads();
+        if (ti + 2 < ntile) load_tile(tb + 2 * AT_TILE);
+    }
+
+    /* the partial of this wave's head: (m, l) and the unnormalised O */
+    const int nrows = S.nrows;
+#pragma unroll
+    for (int qt = 0; qt < MQT; qt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int r = 16 * qt + 4 * qq + v;
+            const float lt = sum16(l[qt][v]);
+            if (r >= nrows) continue;
+            const size_t pi = ((size_t)(S.row0 + r) * a.qh + h) * a.nsplit + sp;
+            float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) coh_stf(po + 16 * dt + c, o[qt][dt][v]);
+            if (c == 0)
+                coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(m[qt][v]) |
+                                              ((uint64_t)__float_as_uint(lt) << 32));
+        }
+}
+
+extern "C" hipError_t s2p_attn_tree_launch(const void* q, void* out, const S2pRowPlan* plan,
+                                           const S2pAttnSeg* segs, int n_seg, int rows,
+                                           int max_nrows, int layer, int max_span, float* part,
+                                           int64_t part_cap, hipStream_t st) {
+    if (rows <= 0 || n_seg <= 0) return hipSuccess;
+    if (max_nrows < 1 || max_nrows > 32 || max_span <= 0) return hipErrorInvalidValue;
+    AttnArgs a = {};
+    a.mode = AM_PLAN;
+    a.q = (const uint16_t*)q;
+    a.out = (uint16_t*)out;
+    a.rows = rows;
+    a.qh = 32;
+    a.kvh_n = 8;
+    a.plan = *plan;
+    a.segs = segs;
+    a.layer = layer;
+    a.part = part;
+    /* splits of whole 32-position tiles, as many as keep the grid within
+     * AT_MAX_BLOCKS blocks and the partials within part_cap floats */
+    const int tiles = (max_span + AT_TILE - 1) / AT_TILE;
+    int ns = (int)(AT_MAX_BLOCKS / ((int64_t)n_seg * 8));
+    if (ns < 1) ns = 1;
+    if (ns > tiles) ns = tiles;
+    while (ns > 1 && (int64_t)rows * 32 * ns * (AT_HD + 2) > part_cap) ns--;
+    const int tps = (tiles + ns - 1) / ns;
+    a.split_pos = tps * AT_TILE;
+    a.nsplit = (max_span + a.split_pos - 1) / a.split_pos;
+    a.nseg = n_seg;
+    const int total = n_seg * 8 * a.nsplit;
+    if (max_nrows <= 16) {
+        static const hipError_t attr = hipFuncSetAttribute(
+            (const void*)k_attn_tree<1>, hipFuncAttributeMaxDynamicSharedMemorySize, TR_LDS_BYTES);
+        (void)attr;
+        hipLaunchKernelGGL(k_attn_tree<1>, dim3((unsigned)total), dim3(256), TR_LDS_BYTES, st, a);
+    } else {
+        static const hipError_t attr = hipFuncSetAttribute(
+            (const void*)k_attn_tree<2>, hipFuncAttributeMaxDynamicSharedMemorySize, TR_LDS_BYTES);
+        (void)attr;
+        hipLaunchKernelGGL(k_attn_tree<2>, dim3((unsigned)total), dim3(256), TR_LDS_BYTES, st, a);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,
+                       a.rows, a.qh, a.nsplit);
+    return hipGetLastError();
+}
+
 /* the split merge for other attention kernels with the same partial layout
  * (the INT8 / INT4 KV decode) */
 extern "C" hipError_t s2p_attn_combine_launch(const float* part, uint16_t* out, int rows, int qh,

@@ -60,6 +60,11 @@ struct s2p_backbone {
     void** d_kv;
     void** d_kvs;          /* [max_sessions] scale bases (INT8 / INT4 caches) */
     S2pAttnSeg* d_segs;
+    /* bf16 caches, 8 < R <= 32 rows a session: one segment a session for the
+     * tree attention kernel (every segment of <= 8 rows would read the
+     * session's K/V again) */
+    S2pAttnSeg* d_tsegs;
+    int tree;
     void* h_stage;
     size_t stage_bytes;
     int planned, rows, n_sess, R, n_seg, max_span;
@@ -181,8 +186,10 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_kv, (size_t)S * sizeof(void*));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_kvs, (size_t)S * sizeof(void*));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_segs, (size_t)nseg_max * sizeof(S2pAttnSeg));
+    if (rc == S2P_OK) rc = dalloc((void**)&b->d_tsegs, (size_t)S * sizeof(S2pAttnSeg));
     b->stage_bytes = R * (4 + 4 + 4 + 8) + (size_t)2 * S * sizeof(void*) +
-                     (size_t)nseg_max * sizeof(S2pAttnSeg) + 64 + S2P_VERIFY_MAX_ROWS * 4;
+                     (size_t)nseg_max * sizeof(S2pAttnSeg) + 64 + S2P_VERIFY_MAX_ROWS * 4 +
+                     (size_t)S * sizeof(S2pAttnSeg) + 64;
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_rope, R * 64 * 2 * sizeof(float));
     if (rc == S2P_OK) rc = dalloc((void**)&b->d_mk2, MK2_AUX_OFF + MK2_AUX_BYTES);
     if (rc == S2P_OK) rc = dalloc(&b->d_chain_hidden, R * S2P_DIM * 2);
@@ -230,6 +237,7 @@ void s2p_backbone_free(s2p_backbone* b) {
     void* bufs[] = {b->x,        b->qkv,       b->q,           b->attn,          b->gu,
                     b->ssq,      b->attn_part, b->d_pos,       b->d_slot,        b->d_sess,
                     b->d_depth,  b->d_vis,    (void*)b->d_kv, (void*)b->d_kvs, (void*)b->d_segs, (void*)b->d_rope,
+                    (void*)b->d_tsegs,
                     (void*)b->d_wpack, (void*)b->d_hpack, (void*)b->d_norms, (void*)b->d_mk2,
                     b->d_chain_hidden, b->d_chain_par, (void*)b->d_chain_sem};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
@@ -393,6 +401,22 @@ s2p_status s2p_verify_plan(s2p_backbone* b, const s2p_verify_batch* vb, hipStrea
         memcpy(hd, depth, (size_t)R * sizeof(int32_t));
         S2P_TRY(hip_ok(hipMemcpyAsync(b->d_depth, hd, (size_t)R * 4, hipMemcpyHostToDevice, st),
                        "plan"));
+        b->tree = b->kvb == 16 && R > 8 && R <= 32;
+        if (b->tree) {
+            S2pAttnSeg* ts = (S2pAttnSeg*)(((uintptr_t)(hd + R) + 63) & ~(uintptr_t)63);
+            for (int s = 0; s < n; s++) {
+                ts[s] = segs[0];
+                ts[s].sess = s;
+                ts[s].L = vb->kv_len[s];
+                ts[s].row0 = s * R;
+                ts[s].nrows = R;
+                ts[s].span = vb->kv_len[s] + R;
+                ts[s].first = s * R;
+                ts[s].kv = vb->kv[s];
+            }
+            S2P_TRY(hip_ok(hipMemcpyAsync(b->d_tsegs, ts, (size_t)n * sizeof(S2pAttnSeg),
+                                          hipMemcpyHostToDevice, st), "plan"));
+        }
     }
     S2P_TRY(hip_ok(hipStreamSynchronize(st), "plan sync"));
     b->planned = 1;
@@ -433,6 +457,11 @@ s2p_status s2p_verify_plan_device(s2p_backbone* b, const int32_t* kv_len_dev, in
     S2P_TRY(hip_ok(s2p_plan_device_launch(b->d_pos, b->d_slot, b->d_segs, b->n_seg, kv_len_dev,
                                           b->d_depth, b->n_sess, b->R, b->max_span, overflow, st),
                    "device plan"));
+    if (b->tree) /* the per-session segments too (positions rewritten alike) */
+        S2P_TRY(hip_ok(s2p_plan_device_launch(b->d_pos, b->d_slot, b->d_tsegs, b->n_sess,
+                                              kv_len_dev, b->d_depth, b->n_sess, b->R,
+                                              b->max_span, overflow, st),
+                       "device plan"));
     const S2pRowPlan rp = row_plan(b);
     return hip_ok(s2p_rope_tab_launch(&rp, b->rows, ROPE_BASE, b->d_rope, st), "rope table");
 }
@@ -608,6 +637,15 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
             S2P_TRY(hip_ok(s2p_attn8_plan_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
                                                  b->max_span, b->attn_part, b->kvb, st),
                            "attention8"));
+        } else if (b->tree) {
+            /* trees of 9..32 rows: qk-norm + RoPE + append, then one block
+             * per (session, kv head, split) */
+            S2P_TRY(hip_ok(s2p_qkrope_append_launch(b->qkv, b->q, L->q_norm.data, L->k_norm.data,
+                                                    &plan, M, l, NORM_EPS, ROPE_BASE, st),
+                           "qk-norm / rope / append"));
+            S2P_TRY(hip_ok(s2p_attn_tree_launch(b->q, b->attn, &plan, b->d_tsegs, b->n_sess, M, b->R,
+                                                l, b->max_span, b->attn_part, b->attn_part_floats, st),
+                           "tree attention"));
         } else
         S2P_TRY(hip_ok(s2p_attn_plan_fused_launch(b->q, b->attn, &plan, b->d_segs, b->n_seg, M, l,
                                                   b->max_span, b->attn_part, b->qkv,

@@ -73,6 +73,14 @@ hipError_t s2p_attn_plan_launch(const void* q, void* out, const S2pRowPlan* plan
  * rows are written to) and, with counters ([n_seg * 8], zero between calls),
  * with the split merge done by the last split of each block. */
 /* qn_w = kn_w = NULL: RoPE without qk-norm (a model without qk-norm) */
+/* Tree attention over bf16 caches (csrc/attention.hip): segs [n_seg] hold
+ * one segment a session of max_nrows <= 32 rows; q holds the roped rows
+ * (k_qkrope_append ran); partials in part (part_cap floats), merged into
+ * out by k_attn_combine. */
+hipError_t s2p_attn_tree_launch(const void* q, void* out, const S2pRowPlan* plan,
+                                const S2pAttnSeg* segs, int n_seg, int rows, int max_nrows,
+                                int layer, int max_span, float* part, int64_t part_cap,
+                                hipStream_t st);
 hipError_t s2p_attn_plan_fused_launch(void* q, void* out, const S2pRowPlan* plan,
                                       const S2pAttnSeg* segs, int n_seg, int rows, int layer,
                                       int max_span, float* part, const void* qkv,
