@@ -138,3 +138,48 @@ def test_attention_plan_mode(lib, parent, L, max_seq):
     err = np.abs(got - exact)
     assert err.max() < 2e-2, (f"max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}; "
                               f"rows with err>2e-2: {sorted(set(np.nonzero(err > 2e-2)[0].tolist()))}")
+
+
+@pytest.mark.parametrize("R,Ls,max_seq", [(12, (300, 77), 512), (17, (1000, 2048), 2304),
+                                          (32, (520, 31), 640)])
+def test_attention_tree_kernel(lib, R, Ls, max_seq):
+    """The tree attention kernel (one block per session, kv head and split;
+    waves on the group's query heads) vs binary64, two sessions of different
+    lengths, random trees of 12 (one q tile a wave), 17 and 32 rows (two)."""
+    import ctypes
+    import torch
+    rng = np.random.default_rng(R * 7 + Ls[0])
+    parent = [-1] + [int(rng.integers(0, i)) for i in range(1, R)]
+    vis1 = _tree_masks(parent)
+    n = len(Ls)
+    kvs = [bf16_bits(rng.standard_normal((16, max_seq, 128)).astype(np.float32)) for _ in range(n)]
+    q = bf16_bits(rng.standard_normal((n * R, 4096)).astype(np.float32) * 2)
+    kvd = [to_dev(k) for k in kvs]
+    kvp = to_dev(np.array([k.data_ptr() for k in kvd], np.int64))
+    posd = to_dev(np.concatenate([np.full(R, L, np.int32) for L in Ls]))
+    slotd = to_dev(np.concatenate([np.arange(L, L + R, dtype=np.int32) for L in Ls]))
+    sessd = to_dev(np.repeat(np.arange(n, dtype=np.int32), R))
+    visd = to_dev(np.concatenate([vis1] * n))
+    plan = RowPlan(posd.data_ptr(), slotd.data_ptr(), sessd.data_ptr(), visd.data_ptr(),
+                   kvp.data_ptr(), None, 16 * max_seq * 128, max_seq)
+    segs = [AttnSeg(s, L, s * R, R, L + R, s * R, kvd[s].data_ptr()) for s, L in enumerate(Ls)]
+    seg_arr = (AttnSeg * n)(*segs)
+    segd = to_dev(np.frombuffer(bytes(seg_arr), np.uint8).copy())
+    span = min(((max(Ls) + R + 511) // 512) * 512, max_seq)
+    fn = lib.s2p_attn_tree_launch
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_int64,
+                                                                ctypes.c_void_p]
+    nf = lib.s2pk_attention_part_floats(n * R, 32, span)
+    part = empty((nf,), dtype=torch.float32)
+    out = empty((n * R, 4096))
+    s2pamd.hip_check(fn(P(to_dev(q)), P(out), ctypes.byref(plan), P(segd), n, n * R, R, 0, span,
+                        P(part), nf, S()))
+    got = bf16_vals(to_host(out, np.uint16))
+    for s, L in enumerate(Ls):
+        kc = np.ascontiguousarray(kvs[s][:8])
+        vc = np.ascontiguousarray(kvs[s][8:])
+        exact = po.attention_f64(q[s * R:(s + 1) * R], kc, vc, R, 32, 8, 128, L, max_seq, vis1)
+        err = np.abs(got[s * R:(s + 1) * R] - exact)
+        assert err.max() < 2e-2, (f"session {s}: max err {err.max():.4g} at "
+                                  f"{np.unravel_index(err.argmax(), err.shape)}")
