@@ -158,7 +158,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; --gpus must be 1 "
-                          "(sessions shard across GPUs with no collectives, see DESIGN.md)"}))
+                          "(sessions shard across GPUs with no collectives: one process per GPU, "
+                          "each on its own sessions)"}))
         sys.exit(2)
 
     import torch

@@ -1,4 +1,4 @@
-"""Draft model (src/draft/draft.c) on the CPU: the bf16 GEMM
+"""Draft model (reference src/draft/draft.c) on the CPU: the bf16 GEMM
 contract and the draft step of the oracle against binary64 truth and closed
 forms, and the safetensors loader's error paths (they fail before any device
 work, so no GPU is needed)."""

@@ -1,4 +1,4 @@
-"""Draft model on the GPU: s2p_gemm_bf16 (the bf16 path of
+"""Draft model on the GPU (reference src/draft/draft.c): s2p_gemm_bf16 (the bf16 path of
 the GEMV engine) against the oracle and binary64, and s2p_draft_load +
 s2p_draft_step against the oracle's draft step and binary64 truth.
 
