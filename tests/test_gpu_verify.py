@@ -215,28 +215,41 @@ def test_verify_chain_vs_oracle(lib, quant, n_layers, L):
         lib.s2p_backbone_free(bb)
 
 
-def test_verify_tree_two_sessions_vs_oracle(lib):
-    """Config 5 shape on 2 layers: 16-node tree + root, two sessions with
-    different prefix lengths, tree visibility masks."""
+TREE32 = [-1] + [int(p) for p in np.random.default_rng(32).integers(0, np.arange(1, 32))]
+
+
+@pytest.mark.parametrize("tree", [TREE16, TREE32], ids=["17-node", "32-node"])
+def test_verify_tree_two_sessions_vs_oracle(lib, tree):
+    """Config 5 shape on 2 layers: a 16-node tree + root (and the largest
+    tree of the per-session attention kernel, 32 nodes), two sessions with
+    different prefix lengths, tree visibility masks; the rows' K/V appended
+    to their slots and nothing else touched."""
     ctx, n_layers = 512, 2
-    R = len(TREE16)
+    R = len(tree)
     bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 2 * R, 2, ctx, 99)
     try:
         kvs = [new_kv(lib, bb, 5), new_kv(lib, bb, 6)]
         hosts = [to_host(k, np.uint16).copy() for k in kvs]
         lens = [130, 301]
-        plan(lib, bb, TREE16, kvs, lens)
+        plan(lib, bb, tree, kvs, lens)
         x = bf16_bits(np.random.default_rng(8).standard_normal((2 * R, 2560)).astype(np.float32))
         logits = empty((2 * R, s2pamd.S2P_HEAD_SLICE))
         s2pamd.check(lib.s2p_verify_forward(bb, P(to_dev(x)), P(logits), S()), "forward")
         got = bf16_vals(to_host(logits, np.uint16))
         W, fn, head = f64_weights(lib, bb, n_layers)
         for s in range(2):
-            want, _ = oracle_forward(lib, bb, n_layers, x[s * R:(s + 1) * R], hosts[s], ctx,
-                                     lens[s], TREE16, s2pamd.S2P_HEAD_SLICE)
+            want, kv_ref = oracle_forward(lib, bb, n_layers, x[s * R:(s + 1) * R], hosts[s], ctx,
+                                          lens[s], tree, s2pamd.S2P_HEAD_SLICE)
             truth = f64.forward(W, fn, head, x[s * R:(s + 1) * R],
-                                hosts[s].reshape(n_layers, 16, ctx, 128), lens[s], TREE16)
-            check_logits(got[s * R:(s + 1) * R], want, truth, f"tree session {s}")
+                                hosts[s].reshape(n_layers, 16, ctx, 128), lens[s], tree)
+            check_logits(got[s * R:(s + 1) * R], want, truth, f"{R}-row tree session {s}")
+            L = lens[s]
+            kv_dev = to_host(kvs[s], np.uint16).reshape(n_layers, 16, ctx, 128)
+            kv_ref = kv_ref.reshape(n_layers, 16, ctx, 128)
+            assert np.array_equal(kv_dev[:, :, :L], kv_ref[:, :, :L])
+            assert np.array_equal(kv_dev[:, :, L + R:], kv_ref[:, :, L + R:])
+            assert_close_rel(bf16_vals(kv_dev[:, :, L:L + R]), bf16_vals(kv_ref[:, :, L:L + R]),
+                             rel=2e-2, floor_frac=2e-2, what=f"session {s} appended K/V")
     finally:
         lib.s2p_backbone_free(bb)
 
