@@ -405,3 +405,37 @@ def test_verify_stages_one_layer(lib, quant, L):
         assert_close_rel(bf16_vals(g_x), bf16_vals(x_out), what="layer output")
     finally:
         lib.s2p_backbone_free(bb)
+
+
+def test_verify_plan_device_tree(lib):
+    """s2p_verify_plan_device on a 17-row tree plan (per-session tree
+    attention segments): lengths advanced on the device give the same logits,
+    bit for bit, as a host plan at those lengths."""
+    ctx, n_layers = 512, 1
+    R = len(TREE16)
+    bb = make_backbone(lib, n_layers, s2pamd.WQ_INT4, s2pamd.S2P_HEAD_SLICE, 2 * R, 2, ctx, 7)
+    try:
+        kvs = [new_kv(lib, bb, 11), new_kv(lib, bb, 12)]
+        base = [to_host(k, np.uint16).copy() for k in kvs]
+        x = bf16_bits(np.random.default_rng(3).standard_normal((2 * R, 2560)).astype(np.float32))
+        xd = to_dev(x)
+        new_lens = [140, 333]
+        # device-advanced plan: planned at shorter lengths (same 512-slot span bucket)
+        plan(lib, bb, TREE16, kvs, [100, 300])
+        lend = to_dev(np.asarray(new_lens, np.int32))
+        ovf = to_dev(np.zeros(1, np.int32))
+        s2pamd.check(lib.s2p_verify_plan_device(bb, P(lend), P(ovf), S()), "plan device")
+        la = empty((2 * R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(xd), P(la), S()), "forward a")
+        got_a = to_host(la, np.uint16)
+        assert int(to_host(ovf, np.int32)[0]) == 0
+        # host plan at the new lengths on fresh copies of the same caches
+        for k, h in zip(kvs, base):
+            k.copy_(torch.from_numpy(h.view(np.int16)).to(k.device))
+        plan(lib, bb, TREE16, kvs, new_lens)
+        lb = empty((2 * R, s2pamd.S2P_HEAD_SLICE))
+        s2pamd.check(lib.s2p_verify_forward(bb, P(xd), P(lb), S()), "forward b")
+        got_b = to_host(lb, np.uint16)
+        assert np.array_equal(got_a, got_b)
+    finally:
+        lib.s2p_backbone_free(bb)
