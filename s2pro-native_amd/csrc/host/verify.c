@@ -640,8 +640,9 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
         } else if (b->tree) {
             /* trees of 9..32 rows: qk-norm + RoPE + append, then one block
              * per (session, kv head, split) */
-            S2P_TRY(hip_ok(s2p_qkrope_append_launch(b->qkv, b->q, L->q_norm.data, L->k_norm.data,
-                                                    &plan, M, l, NORM_EPS, ROPE_BASE, st),
+            S2P_TRY(hip_ok(s2p_qkrope_append_tab_launch(b->qkv, b->q, L->q_norm.data,
+                                                        L->k_norm.data, &plan, M, l, NORM_EPS,
+                                                        b->d_rope, st),
                            "qk-norm / rope / append"));
             S2P_TRY(hip_ok(s2p_attn_tree_launch(b->q, b->attn, &plan, b->d_tsegs, b->n_sess, M, b->R,
                                                 l, b->max_span, b->attn_part, b->attn_part_floats, st),

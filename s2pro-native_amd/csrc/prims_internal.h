@@ -35,6 +35,12 @@ typedef struct {
     const void* kv; /* the session's KV base (plan.kv[sess]), so the kernel has it at hand */
 } S2pAttnSeg;
 
+/* s2p_qkrope_append_launch with (cos, sin) from a RoPE table [rows][64][2]
+ * (s2p_rope_tab_launch of the same plan) */
+hipError_t s2p_qkrope_append_tab_launch(const void* qkv, void* q_out, const void* qn_w,
+                                        const void* kn_w, const S2pRowPlan* plan, int rows,
+                                        int layer, float eps, const float* rope_tab,
+                                        hipStream_t st);
 hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
                                     const void* kn_w, const S2pRowPlan* plan, int rows,
                                     int layer, float eps, float base, hipStream_t st);
