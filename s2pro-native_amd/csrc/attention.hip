@@ -61,14 +61,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int lin = (int)blockIdx.x;
     const int total = a.nseg * a.kvh_n * a.nsplit;
-#ifdef AT_NO_XCD
-    const int b = lin;
-#else
     /* chunk x of the numbering (the first total % 8 chunks one block
      * longer) goes to XCD x; bijective for lin < total */
     const int q = total >> 3, r = total & 7, xcd = lin & 7, j = lin >> 3;
     const int b = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
-#endif
     const int seg = b % a.nseg, rest = b / a.nseg;
 #ifdef S2P_DIAG
     a.probe = b < 4096 ? g_at_probe : nullptr;
