@@ -66,7 +66,8 @@ def test_int4p_gemv_vs_oracle(lib, engine, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(40, 6144, 2560), (68, 2560, 4096), (128, 256, 2560),
                                    (17, 9728, 2560), (96, 4097, 2560), (80, 4097, 2560),
-                                   (33, 2560, 9728)])
+                                   (33, 2560, 9728), (24, 512, 640), (64, 300, 1152),
+                                   (70, 1000, 1152)])
 def test_int4p_gemm_large_m(lib, M, N, K):
     r = np.random.default_rng(2000 + M)
     packed, scales = rand_int4(r, N, K)
