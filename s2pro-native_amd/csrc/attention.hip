@@ -87,14 +87,40 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
  * R <= 32 rows of the session: its 4 waves are the 4 query heads of the GQA
  * group (wave g: head 4 kvh + g, q tiles of 16 rows), and share each
  * 32-position K/V tile through LDS, so the K/V are read once.  The q rows
- * come roped from the q buffer (k_qkrope_append ran before).  Per tile:
- * S = Q K^T (K from LDS), online softmax, P (bf16 hi + lo) through LDS,
- * O += P V with V read by transposing loads.  Every wave ends with its
- * head's (m, l, O) over the split: the partial, merged by k_attn_combine. */
+ * come roped from the q buffer (k_qkrope_append ran before).
+ * The scores are computed transposed, S^T = K Q^T: lane (G, c) (G = lane /
+ * 16, c = lane % 16) holds query 16 qt + c at positions 16 ps + 4 G + v,
+ * so a query's softmax runs in its own lanes (8 values each, then the 4
+ * lanes c + 16 G) and the 8 values are, packed, the B operand of
+ * O^T = V^T P^T (k slot 8 G + 4 ps + v <-> position 16 ps + 4 G + v): P
+ * never goes through LDS.  P is split hi + lo, both bf16 (16 significant
+ * bits into the MFMA).  V comes by transposing LDS reads.  Every wave ends
+ * with its head's (m, l, O) over the split: the partial, merged by
+ * k_attn_combine. */
 #define TR_KOFF(t, ch) ((t) * 128 + ((((ch) ^ ((t) & 15))) << 3))
-#define TR_VSW(t) ((((t) & 3) | ((((t) >> 3) & 1) << 2)) << 1)
+/* a transposing V read touches rows 4 G + k (or 16 + 4 G + k), G, k < 4, at
+ * two adjacent 16-byte chunks: the swizzle gives the 16 rows 8 distinct
+ * chunk pairs (2-way, the minimum for 512 bytes) */
+#define TR_VSW(t) (((t) & 7) << 1)
 #define TR_VOFF(t, d) ((t) * 128 + ((((d) >> 3) ^ TR_VSW(t)) << 3) + ((d) & 7))
-#define TR_LDS_BYTES (4 * AT_TILE * 128 * 2 + 2 * 4 * 32 * AT_PSTRIDE * 2)
+#define TR_LDS_BYTES (4 * AT_TILE * 128 * 2)
+
+/* max / sum over the lanes c, c + 16, c + 32, c + 48 (row swaps, VALU) */
+S2P_DEV float xg_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+S2P_DEV float xg_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+S2P_DEV uint32_t pk_bf(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
 
 template <int MQT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_tree(AttnArgs a) {
@@ -103,8 +129,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     LDS(unsigned char)* smem = (LDS(unsigned char)*)smem_raw;
     LDS(uint16_t)* s_k = (LDS(uint16_t)*)smem;                           /* [2][32][128] */
     LDS(uint16_t)* s_v = s_k + 2 * AT_TILE * 128;                         /* [2][32][128] */
-    LDS(uint16_t)* s_p = s_v + 2 * AT_TILE * 128;                         /* [4 waves][32][PSTRIDE] */
-    LDS(uint16_t)* s_pl = s_p + 4 * 32 * AT_PSTRIDE;
     const int lin = (int)blockIdx.x;
     const int total = a.nseg * a.kvh_n * a.nsplit;
     const int qd = total >> 3, rd = total & 7, xcd = lin & 7, jd = lin >> 3;
@@ -119,23 +143,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
 
-    /* this lane's rows of the score / output tiles: 16 qt + 4 qq + v */
-    uint64_t vw[MQT][4];
-#pragma unroll
-    for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int r = 16 * qt + 4 * qq + v;
-            vw[qt][v] = S.vis && r < S.nrows ? S.vis[S.row0 + r] : 0ull;
-        }
-    /* Q operand (A): row c of tile qt, dims 32 ch + 8 qq .. + 7 */
-    s2p_u32x4 qa[MQT][4];
+    /* this lane's query rows 16 qt + c: mask words, Q operand (B: query c,
+     * dims 32 ch + 8 qq .. + 7) */
+    uint64_t vw[MQT];
+    s2p_u32x4 qb[MQT][4];
 #pragma unroll
     for (int qt = 0; qt < MQT; qt++) {
         const int r = 16 * qt + c;
+        vw[qt] = S.vis && r < S.nrows ? S.vis[S.row0 + r] : 0ull;
 #pragma unroll
         for (int ch = 0; ch < 4; ch++)
-            qa[qt][ch] = r < S.nrows ? *(const s2p_u32x4*)(a.q + (size_t)(S.row0 + r) * (a.qh * AT_HD) +
+            qb[qt][ch] = r < S.nrows ? *(const s2p_u32x4*)(a.q + (size_t)(S.row0 + r) * (a.qh * AT_HD) +
                                                              h * AT_HD + 32 * ch + 8 * qq)
                                      : (s2p_u32x4){0u, 0u, 0u, 0u};
     }
@@ -161,20 +179,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     };
 
-    float m[MQT][4], l[MQT][4];
+    /* m, l per query (l: this lane's positions only, summed at the end);
+     * o[qt][dt]: O^T, dims 16 dt + 4 qq + v of query 16 qt + c */
+    float m[MQT], l[MQT];
     s2p_f32x4 o[MQT][8];
 #pragma unroll
     for (int qt = 0; qt < MQT; qt++) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            m[qt][v] = -INFINITY;
-            l[qt][v] = 0.f;
-        }
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
 
     const int ntile = p_end > p_begin ? (p_end - p_begin + AT_TILE - 1) / AT_TILE : 0;
+    /* tiles wholly inside the prefix (and the split) need no mask */
+    const int open_end = min(S.L, p_end);
     if (ntile > 0) {
         load_tile(p_begin);
         store_tile(0);
@@ -185,75 +204,83 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int tb = p_begin + ti * AT_TILE, buf = ti & 1;
         const LDS(uint16_t)* kt = s_k + buf * AT_TILE * 128;
         const LDS(uint16_t)* vt = s_v + buf * AT_TILE * 128;
-        /* scores: K operand (B) = row 16 ps + c, dims 32 ch + 8 qq .. */
+        /* S^T: K operand (A) = row 16 ps + c, dims 32 ch + 8 qq .. */
         s2p_f32x4 sc[MQT][2];
 #pragma unroll
         for (int ps = 0; ps < 2; ps++) {
-            s2p_u32x4 kb[4];
+            s2p_u32x4 ka[4];
 #pragma unroll
             for (int ch = 0; ch < 4; ch++)
-                kb[ch] = *(const LDS(s2p_u32x4)*)(kt + TR_KOFF(16 * ps + c, 4 * ch + qq));
+                ka[ch] = *(const LDS(s2p_u32x4)*)(kt + TR_KOFF(16 * ps + c, 4 * ch + qq));
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++) {
                 s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(qa[qt][ch], kb[ch], acc);
+                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(ka[ch], qb[qt][ch], acc);
                 sc[qt][ps] = acc;
             }
         }
-        /* online softmax (rows 16 qt + 4 qq + v, positions tb + c, + 16) */
-        float corr[MQT][4];
+        const bool open = tb + AT_TILE <= open_end;
+        /* online softmax of query 16 qt + c over positions tb + 16 ps + 4 qq + v */
+        float corr[MQT];
+        s2p_u32x4 ph[MQT], pl[MQT];
         bool raised = false;
 #pragma unroll
-        for (int qt = 0; qt < MQT; qt++)
+        for (int qt = 0; qt < MQT; qt++) {
+            const int r = 16 * qt + c;
+            float t[2][4];
+            float tm = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int r = 16 * qt + 4 * qq + v;
-                const bool vis0 = visible_w(S, vw[qt][v], r, tb + c) && tb + c < p_end;
-                const bool vis1 = visible_w(S, vw[qt][v], r, tb + 16 + c) && tb + 16 + c < p_end;
-                const float t0 = vis0 ? sc[qt][0][v] * scale : -INFINITY;
-                const float t1 = vis1 ? sc[qt][1][v] * scale : -INFINITY;
-                const float tm = max16(fmaxf(t0, t1));
-                const float mn = fmaxf(m[qt][v], tm);
-                const float ms = mn == -INFINITY ? 0.f : mn;
-                corr[qt][v] = __expf(m[qt][v] - ms);
-                raised |= corr[qt][v] != 1.0f;
-                const float p0 = __expf(t0 - ms), p1 = __expf(t1 - ms);
-                l[qt][v] = l[qt][v] * corr[qt][v] + p0 + p1;
-                m[qt][v] = mn;
-                const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
-                LDS(uint16_t)* prow = s_p + (wave * 32 + 16 * qt + 4 * qq + v) * AT_PSTRIDE;
-                LDS(uint16_t)* plrow = s_pl + (wave * 32 + 16 * qt + 4 * qq + v) * AT_PSTRIDE;
-                prow[c] = h0;
-                prow[16 + c] = h1;
-                plrow[c] = f2bf(p0 - bf2f(h0));
-                plrow[16 + c] = f2bf(p1 - bf2f(h1));
-            }
+            for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int pos = tb + 16 * ps + 4 * qq + v;
+                    const bool vis = open || (visible_w(S, vw[qt], r, pos) && pos < p_end);
+                    t[ps][v] = vis ? sc[qt][ps][v] * scale : -INFINITY;
+                    tm = fmaxf(tm, t[ps][v]);
+                }
+            tm = xg_max(tm);
+            const float mn = fmaxf(m[qt], tm);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            corr[qt] = __expf(m[qt] - ms);
+            raised |= corr[qt] != 1.0f;
+            float ls = 0.f;
+            float p[2][4], lo[2][4];
+#pragma unroll
+            for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    p[ps][v] = __expf(t[ps][v] - ms);
+                    ls += p[ps][v];
+                    lo[ps][v] = p[ps][v] - bf2f(f2bf(p[ps][v]));
+                }
+            l[qt] = l[qt] * corr[qt] + ls;
+            m[qt] = mn;
+            ph[qt] = (s2p_u32x4){pk_bf(p[0][0], p[0][1]), pk_bf(p[0][2], p[0][3]),
+                                 pk_bf(p[1][0], p[1][1]), pk_bf(p[1][2], p[1][3])};
+            pl[qt] = (s2p_u32x4){pk_bf(lo[0][0], lo[0][1]), pk_bf(lo[0][2], lo[0][3]),
+                                 pk_bf(lo[1][0], lo[1][1]), pk_bf(lo[1][2], lo[1][3])};
+        }
         if (__any(raised)) {
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++)
 #pragma unroll
-                for (int v = 0; v < 4; v++)
+                for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-                    for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr[qt][v];
+                    for (int v = 0; v < 4; v++) o[qt][dt][v] *= corr[qt];
         }
-        wave_sync_lds();
-        s2p_u32x4 pa[MQT], pl[MQT];
-#pragma unroll
-        for (int qt = 0; qt < MQT; qt++) {
-            pa[qt] = *(const LDS(s2p_u32x4)*)(s_p + (wave * 32 + 16 * qt + c) * AT_PSTRIDE + 8 * qq);
-            pl[qt] = *(const LDS(s2p_u32x4)*)(s_pl + (wave * 32 + 16 * qt + c) * AT_PSTRIDE + 8 * qq);
-        }
+        /* O^T += V^T P^T: A row c = dim 16 dt + c, k slots 8 qq + j =
+         * positions 4 qq + j (j < 4), 16 + 4 qq + j - 4 */
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const int k4 = c >> 2, m4 = c & 3;
-            const s2p_u32x2 b0 = ds_read_tr16(vt + TR_VOFF(8 * qq + k4, 16 * dt + 4 * m4));
-            const s2p_u32x2 b1 = ds_read_tr16(vt + TR_VOFF(8 * qq + 4 + k4, 16 * dt + 4 * m4));
-            const s2p_u32x4 bv = {b0.x, b0.y, b1.x, b1.y};
+            const s2p_u32x2 b0 = ds_read_tr16(vt + TR_VOFF(4 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x2 b1 = ds_read_tr16(vt + TR_VOFF(16 + 4 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x4 va = {b0.x, b0.y, b1.x, b1.y};
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++) {
-                o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
-                o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(va, pl[qt], o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(va, ph[qt], o[qt][dt]);
             }
         }
         /* the next tile into the other buffer (its previous tile was read
@@ -266,20 +293,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     /* the partial of this wave's head: (m, l) and the unnormalised O */
     const int nrows = S.nrows;
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++)
+    for (int qt = 0; qt < MQT; qt++) {
+        const int r = 16 * qt + c;
+        const float lt = xg_sum(l[qt]);
+        if (r >= nrows) continue;
+        const size_t pi = ((size_t)(S.row0 + r) * a.qh + h) * a.nsplit + sp;
+        float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int r = 16 * qt + 4 * qq + v;
-            const float lt = sum16(l[qt][v]);
-            if (r >= nrows) continue;
-            const size_t pi = ((size_t)(S.row0 + r) * a.qh + h) * a.nsplit + sp;
-            float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) coh_stf(po + 16 * dt + c, o[qt][dt][v]);
-            if (c == 0)
-                coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(m[qt][v]) |
-                                              ((uint64_t)__float_as_uint(lt) << 32));
-        }
+        for (int dt = 0; dt < 8; dt++)
+            coh_st128(po + 16 * dt + 4 * qq, __builtin_bit_cast(s2p_u32x4, o[qt][dt]));
+        if (qq == 0)
+            coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(m[qt]) |
+                                          ((uint64_t)__float_as_uint(lt) << 32));
+    }
 }
 
 extern "C" hipError_t s2p_attn_tree_launch(const void* q, void* out, const S2pRowPlan* plan,
