@@ -84,18 +84,20 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
 /* ---- tree segments: one block per (session, kv head, split) ----
  * A draft tree of R > 8 rows per session (config 5: 17) in 8-row segments
  * has every segment read its session's K/V again.  Here one block takes all
- * R <= 32 rows of the session: its 4 waves are the 4 query heads of the GQA
- * group (wave g: head 4 kvh + g, q tiles of 16 rows), and share each
- * 32-position K/V tile through LDS, so the K/V are read once.  The q rows
- * come roped from the q buffer (k_qkrope_append ran before).
+ * R <= 32 rows of the session's GQA group (4 query heads): waves 0..3 take
+ * rows 0..15 of one head each, wave 4 + e rows 16 + 4 e .. + 3 of all four
+ * heads (so a 17-row tree runs 5 waves, not 8 half-empty q tiles).  The
+ * waves share each 32-position K/V tile through LDS, so the K/V are read
+ * once.  The q rows come roped from the q buffer (k_qkrope_append ran
+ * before).
  * The scores are computed transposed, S^T = K Q^T: lane (G, c) (G = lane /
- * 16, c = lane % 16) holds query 16 qt + c at positions 16 ps + 4 G + v,
+ * 16, c = lane % 16) holds query vector c at positions 16 ps + 4 G + v,
  * so a query's softmax runs in its own lanes (8 values each, then the 4
  * lanes c + 16 G) and the 8 values are, packed, the B operand of
  * O^T = V^T P^T (k slot 8 G + 4 ps + v <-> position 16 ps + 4 G + v): P
  * never goes through LDS.  P is split hi + lo, both bf16 (16 significant
- * bits into the MFMA).  V comes by transposing LDS reads.  Every wave ends
- * with its head's (m, l, O) over the split: the partial, merged by
+ * bits into the MFMA).  V comes by transposing LDS reads.  Every query
+ * vector ends with its (m, l, O) over the split: the partial, merged by
  * k_attn_combine. */
 #define TR_KOFF(t, ch) ((t) * 128 + ((((ch) ^ ((t) & 15))) << 3))
 /* a transposing V read touches rows 4 G + k (or 16 + 4 G + k), G, k < 4, at
@@ -122,8 +124,7 @@ S2P_DEV uint32_t pk_bf(float lo, float hi) {
     return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-template <int MQT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_tree(AttnArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_attn_tree(AttnArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) unsigned char smem_raw[];
     LDS(unsigned char)* smem = (LDS(unsigned char)*)smem_raw;
@@ -136,60 +137,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int seg = b % a.nseg, rest = b / a.nseg;
     const int kvh = rest % a.kvh_n, sp = rest / a.kvh_n;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = (int)blockDim.x;
     const int qq = lane >> 4, c = lane & 15;
     const SegInfo S = resolve<AM_PLAN>(a, seg, kvh);
-    const int h = 4 * kvh + wave;
+    /* this lane's query vector: waves 0..3 rows c of head 4 kvh + wave;
+     * wave 4 + e rows 16 + 4 e + c / 4 of head 4 kvh + c % 4 */
+    const int r = wave < 4 ? c : 16 + 4 * (wave - 4) + (c >> 2);
+    const int h = 4 * kvh + (wave < 4 ? wave : (c & 3));
     const int p_begin = sp * a.split_pos;
     const int p_end = min(p_begin + a.split_pos, S.span);
     const float scale = 0.08838834764831845f;
 
-    /* this lane's query rows 16 qt + c: mask words, Q operand (B: query c,
-     * dims 32 ch + 8 qq .. + 7) */
-    uint64_t vw[MQT];
-    s2p_u32x4 qb[MQT][4];
+    /* mask word and Q operand (B: query vector c, dims 32 ch + 8 qq .. + 7) */
+    const uint64_t vw = S.vis && r < S.nrows ? S.vis[S.row0 + r] : 0ull;
+    s2p_u32x4 qb[4];
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++) {
-        const int r = 16 * qt + c;
-        vw[qt] = S.vis && r < S.nrows ? S.vis[S.row0 + r] : 0ull;
-#pragma unroll
-        for (int ch = 0; ch < 4; ch++)
-            qb[qt][ch] = r < S.nrows ? *(const s2p_u32x4*)(a.q + (size_t)(S.row0 + r) * (a.qh * AT_HD) +
-                                                             h * AT_HD + 32 * ch + 8 * qq)
-                                     : (s2p_u32x4){0u, 0u, 0u, 0u};
-    }
+    for (int ch = 0; ch < 4; ch++)
+        qb[ch] = r < S.nrows ? *(const s2p_u32x4*)(a.q + (size_t)(S.row0 + r) * (a.qh * AT_HD) +
+                                                    h * AT_HD + 32 * ch + 8 * qq)
+                             : (s2p_u32x4){0u, 0u, 0u, 0u};
 
-    /* the block's K/V tile loads: chunk i = tid, tid + 256 of the tile's
-     * 512 16-byte chunks (row i / 16, chunk i % 16) of K, then of V */
+    /* the block's K/V tile loads: chunks i = tid, tid + nthr (< 512) of the
+     * tile's 512 16-byte chunks (row i / 16, chunk i % 16) of K, then of V */
     s2p_u32x4 ld[4];
     auto load_tile = [&](int tb) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int i = tid + 256 * j, t = i >> 4, ch = i & 15;
+            const int i = tid + nthr * j, t = (i >> 4) & 31, ch = i & 15;
             const int pos = min(tb + t, p_end - 1);
-            ld[j] = gld_nt128(S.kp + (size_t)pos * AT_HD + 8 * ch);
-            ld[2 + j] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * ch);
+            if (i < 512) {
+                ld[j] = gld_nt128(S.kp + (size_t)pos * AT_HD + 8 * ch);
+                ld[2 + j] = gld_nt128(S.vp + (size_t)pos * AT_HD + 8 * ch);
+            }
         }
     };
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int i = tid + 256 * j, t = i >> 4, ch = i & 15;
-            *(LDS(s2p_u32x4)*)(s_k + buf * AT_TILE * 128 + TR_KOFF(t, ch)) = ld[j];
-            *(LDS(s2p_u32x4)*)(s_v + buf * AT_TILE * 128 + TR_VOFF(t, 8 * ch)) = ld[2 + j];
+            const int i = tid + nthr * j, t = (i >> 4) & 31, ch = i & 15;
+            if (i < 512) {
+                *(LDS(s2p_u32x4)*)(s_k + buf * AT_TILE * 128 + TR_KOFF(t, ch)) = ld[j];
+                *(LDS(s2p_u32x4)*)(s_v + buf * AT_TILE * 128 + TR_VOFF(t, 8 * ch)) = ld[2 + j];
+            }
         }
     };
 
-    /* m, l per query (l: this lane's positions only, summed at the end);
-     * o[qt][dt]: O^T, dims 16 dt + 4 qq + v of query 16 qt + c */
-    float m[MQT], l[MQT];
-    s2p_f32x4 o[MQT][8];
+    /* m, l of the query (l: this lane's positions only, summed at the end);
+     * o[dt]: O^T, dims 16 dt + 4 qq + v of the query */
+    float m = -INFINITY, l = 0.f;
+    s2p_f32x4 o[8];
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++) {
-        m[qt] = -INFINITY;
-        l[qt] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
-    }
+    for (int dt = 0; dt < 8; dt++) o[dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int ntile = p_end > p_begin ? (p_end - p_begin + AT_TILE - 1) / AT_TILE : 0;
     /* tiles wholly inside the prefix (and the split) need no mask */
@@ -205,69 +203,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const LDS(uint16_t)* kt = s_k + buf * AT_TILE * 128;
         const LDS(uint16_t)* vt = s_v + buf * AT_TILE * 128;
         /* S^T: K operand (A) = row 16 ps + c, dims 32 ch + 8 qq .. */
-        s2p_f32x4 sc[MQT][2];
+        s2p_f32x4 sc[2];
 #pragma unroll
         for (int ps = 0; ps < 2; ps++) {
             s2p_u32x4 ka[4];
 #pragma unroll
             for (int ch = 0; ch < 4; ch++)
                 ka[ch] = *(const LDS(s2p_u32x4)*)(kt + TR_KOFF(16 * ps + c, 4 * ch + qq));
+            s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int qt = 0; qt < MQT; qt++) {
-                s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(ka[ch], qb[qt][ch], acc);
-                sc[qt][ps] = acc;
-            }
+            for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(ka[ch], qb[ch], acc);
+            sc[ps] = acc;
         }
         const bool open = tb + AT_TILE <= open_end;
-        /* online softmax of query 16 qt + c over positions tb + 16 ps + 4 qq + v */
-        float corr[MQT];
-        s2p_u32x4 ph[MQT], pl[MQT];
-        bool raised = false;
+        /* online softmax of the query over positions tb + 16 ps + 4 qq + v */
+        float t[2][4];
+        float tm = -INFINITY;
 #pragma unroll
-        for (int qt = 0; qt < MQT; qt++) {
-            const int r = 16 * qt + c;
-            float t[2][4];
-            float tm = -INFINITY;
+        for (int ps = 0; ps < 2; ps++)
 #pragma unroll
-            for (int ps = 0; ps < 2; ps++)
+            for (int v = 0; v < 4; v++) {
+                const int pos = tb + 16 * ps + 4 * qq + v;
+                const bool vis = open || (visible_w(S, vw, r, pos) && pos < p_end);
+                t[ps][v] = vis ? sc[ps][v] * scale : -INFINITY;
+                tm = fmaxf(tm, t[ps][v]);
+            }
+        tm = xg_max(tm);
+        const float mn = fmaxf(m, tm);
+        const float ms = mn == -INFINITY ? 0.f : mn;
+        const float corr = __expf(m - ms);
+        float ls = 0.f;
+        float p[2][4], lo[2][4];
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int pos = tb + 16 * ps + 4 * qq + v;
-                    const bool vis = open || (visible_w(S, vw[qt], r, pos) && pos < p_end);
-                    t[ps][v] = vis ? sc[qt][ps][v] * scale : -INFINITY;
-                    tm = fmaxf(tm, t[ps][v]);
-                }
-            tm = xg_max(tm);
-            const float mn = fmaxf(m[qt], tm);
-            const float ms = mn == -INFINITY ? 0.f : mn;
-            corr[qt] = __expf(m[qt] - ms);
-            raised |= corr[qt] != 1.0f;
-            float ls = 0.f;
-            float p[2][4], lo[2][4];
+        for (int ps = 0; ps < 2; ps++)
 #pragma unroll
-            for (int ps = 0; ps < 2; ps++)
+            for (int v = 0; v < 4; v++) {
+                p[ps][v] = __expf(t[ps][v] - ms);
+                ls += p[ps][v];
+                lo[ps][v] = p[ps][v] - bf2f(f2bf(p[ps][v]));
+            }
+        l = l * corr + ls;
+        m = mn;
+        const s2p_u32x4 ph = {pk_bf(p[0][0], p[0][1]), pk_bf(p[0][2], p[0][3]),
+                              pk_bf(p[1][0], p[1][1]), pk_bf(p[1][2], p[1][3])};
+        const s2p_u32x4 pl = {pk_bf(lo[0][0], lo[0][1]), pk_bf(lo[0][2], lo[0][3]),
+                              pk_bf(lo[1][0], lo[1][1]), pk_bf(lo[1][2], lo[1][3])};
+        if (__any(corr != 1.0f)) {
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    p[ps][v] = __expf(t[ps][v] - ms);
-                    ls += p[ps][v];
-                    lo[ps][v] = p[ps][v] - bf2f(f2bf(p[ps][v]));
-                }
-            l[qt] = l[qt] * corr[qt] + ls;
-            m[qt] = mn;
-            ph[qt] = (s2p_u32x4){pk_bf(p[0][0], p[0][1]), pk_bf(p[0][2], p[0][3]),
-                                 pk_bf(p[1][0], p[1][1]), pk_bf(p[1][2], p[1][3])};
-            pl[qt] = (s2p_u32x4){pk_bf(lo[0][0], lo[0][1]), pk_bf(lo[0][2], lo[0][3]),
-                                 pk_bf(lo[1][0], lo[1][1]), pk_bf(lo[1][2], lo[1][3])};
-        }
-        if (__any(raised)) {
+            for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-            for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-                for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++) o[qt][dt][v] *= corr[qt];
+                for (int v = 0; v < 4; v++) o[dt][v] *= corr;
         }
         /* O^T += V^T P^T: A row c = dim 16 dt + c, k slots 8 qq + j =
          * positions 4 qq + j (j < 4), 16 + 4 qq + j - 4 */
@@ -277,11 +262,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             const s2p_u32x2 b0 = ds_read_tr16(vt + TR_VOFF(4 * qq + k4, 16 * dt + 4 * m4));
             const s2p_u32x2 b1 = ds_read_tr16(vt + TR_VOFF(16 + 4 * qq + k4, 16 * dt + 4 * m4));
             const s2p_u32x4 va = {b0.x, b0.y, b1.x, b1.y};
-#pragma unroll
-            for (int qt = 0; qt < MQT; qt++) {
-                o[qt][dt] = mfma16x16x32(va, pl[qt], o[qt][dt]);
-                o[qt][dt] = mfma16x16x32(va, ph[qt], o[qt][dt]);
-            }
+            o[dt] = mfma16x16x32(va, pl, o[dt]);
+            o[dt] = mfma16x16x32(va, ph, o[dt]);
         }
         /* the next tile into the other buffer (its previous tile was read
          * before the last barrier), then the one after into registers */
@@ -290,22 +272,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         if (ti + 2 < ntile) load_tile(tb + 2 * AT_TILE);
     }
 
-    /* the partial of this wave's head: (m, l) and the unnormalised O */
-    const int nrows = S.nrows;
+    /* the partial of this lane's query: (m, l) and the unnormalised O */
+    const float lt = xg_sum(l);
+    if (r >= S.nrows) return;
+    const size_t pi = ((size_t)(S.row0 + r) * a.qh + h) * a.nsplit + sp;
+    float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++) {
-        const int r = 16 * qt + c;
-        const float lt = xg_sum(l[qt]);
-        if (r >= nrows) continue;
-        const size_t pi = ((size_t)(S.row0 + r) * a.qh + h) * a.nsplit + sp;
-        float* po = a.part + (size_t)a.rows * a.qh * a.nsplit * 2 + pi * AT_HD;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-            coh_st128(po + 16 * dt + 4 * qq, __builtin_bit_cast(s2p_u32x4, o[qt][dt]));
-        if (qq == 0)
-            coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(m[qt]) |
-                                          ((uint64_t)__float_as_uint(lt) << 32));
-    }
+    for (int dt = 0; dt < 8; dt++)
+        coh_st128(po + 16 * dt + 4 * qq, __builtin_bit_cast(s2p_u32x4, o[dt]));
+    if (qq == 0)
+        coh_st64(a.part + pi * 2, (uint64_t)__float_as_uint(m) | ((uint64_t)__float_as_uint(lt) << 32));
 }
 
 extern "C" hipError_t s2p_attn_tree_launch(const void* q, void* out, const S2pRowPlan* plan,
@@ -337,17 +313,12 @@ extern "C" hipError_t s2p_attn_tree_launch(const void* q, void* out, const S2pRo
     a.nsplit = (max_span + a.split_pos - 1) / a.split_pos;
     a.nseg = n_seg;
     const int total = n_seg * 8 * a.nsplit;
-    if (max_nrows <= 16) {
-        static const hipError_t attr = hipFuncSetAttribute(
-            (const void*)k_attn_tree<1>, hipFuncAttributeMaxDynamicSharedMemorySize, TR_LDS_BYTES);
-        (void)attr;
-        hipLaunchKernelGGL(k_attn_tree<1>, dim3((unsigned)total), dim3(256), TR_LDS_BYTES, st, a);
-    } else {
-        static const hipError_t attr = hipFuncSetAttribute(
-            (const void*)k_attn_tree<2>, hipFuncAttributeMaxDynamicSharedMemorySize, TR_LDS_BYTES);
-        (void)attr;
-        hipLaunchKernelGGL(k_attn_tree<2>, dim3((unsigned)total), dim3(256), TR_LDS_BYTES, st, a);
-    }
+    /* 4 waves (rows 0..15 of the 4 heads), then a wave per 4 more rows */
+    const int waves = 4 + (max_nrows > 16 ? (max_nrows - 16 + 3) / 4 : 0);
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)k_attn_tree, hipFuncAttributeMaxDynamicSharedMemorySize, TR_LDS_BYTES);
+    (void)attr;
+    hipLaunchKernelGGL(k_attn_tree, dim3((unsigned)total), dim3(64 * waves), TR_LDS_BYTES, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.rows, a.qh), dim3(AT_HD), 0, st, a.part, a.out,
