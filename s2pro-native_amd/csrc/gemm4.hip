@@ -18,8 +18,8 @@
  *   - the next chunk's weights are in flight while a window is staged and
  *     multiplied; two waves per SIMD hide each other's latencies;
  *   - when the row blocks are too few to fill the chip, K is split over
- *     workgroups and the last split to arrive at a 64-row block sums the
- *     splits in order and runs the epilogue (the GEMV engine's handoff).
+ *     workgroups, which store partials; a second launch (k_g4_merge, every
+ *     CU) sums the splits in order and runs the epilogue.
  * Per group the dequantisation (9 VALU per 8 weights) is shared by the MT
  * column tiles, so at M = 68 the MFMA work, not the weight stream, sets the
  * pace.  Accumulation order per output is fixed (window by window, group by
@@ -49,7 +49,7 @@ static __host__ __device__ size_t g4_lds_bytes(int M) {
 
 #ifdef S2P_DIAG
 /* diagnostics build: wall clock per workgroup at the stages of the kernel
- * (start, staged, first window, multiplied, partials stored, counted, merged) */
+ * (start, staged, first window, multiplied) */
 __device__ uint64_t g4_probe[4096 * 8];
 extern "C" hipError_t s2p_g4_probe_get(uint64_t* host, int n) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(g4_probe), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
@@ -297,14 +297,12 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     G4_STAMP(3);
     uint16_t* Y = a.y;
     if (a.splits > 1) {
-        /* K-split handoff as in the GEMV engine's split-K path: this
-         * split's partial rows (the 64-row block layout: wave w holds rows
-         * 16w..16w+15, SWIGLU gate rows then up rows) written through to
-         * memory, arrival counted once the stores completed, and the last
-         * split to arrive sums the splits in order and runs the epilogue */
-        /* the workgroup's 128 rows are two 64-row fixup blocks: block h
-         * holds tiles 4h..4h+3, or (SWIGLU) gate tiles 2h, 2h+1 then the
-         * matching up tiles */
+        /* K split: this split's partial rows in the 64-row block layout of
+         * the merge (wave w holds rows 16w..16w+15, SWIGLU gate rows then up
+         * rows), plain stores; k_g4_merge, the next launch, sums the splits
+         * in order and runs the epilogue.  The workgroup's 128 rows are two
+         * 64-row blocks: block h holds tiles 4h..4h+3, or (SWIGLU) gate
+         * tiles 2h, 2h+1 then the matching up tiles */
         const int h = swiglu ? (wave & 3) >> 1 : wave >> 2;
         const int row = swiglu ? (wave >= 4 ? 32 : 0) + (wave & 1) * 16 : (wave & 3) * 16;
         const int rb = blockIdx.x * 2 + h;
@@ -313,32 +311,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
             const int m = t * 16 + r;
             if (m >= M || rb >= a.nrb) continue;
             float* dst = &a.part[(((size_t)sp * M + m) * a.nrb + rb) * 64 + row + q * 4];
-            coh_st128(dst, __builtin_bit_cast(s2p_u32x4, v[t]));
-        }
-        vm_drain();
-        __syncthreads();
-        G4_STAMP(4);
-        if (tid == 0) {
-            /* the partials were written through and their stores have
-             * completed; the last arriver reads them with agent-scope
-             * (L2-bypassing) loads, so a relaxed count suffices (an
-             * acquire-release one adds an L2 writeback and invalidate,
-             * ~2 us, to every workgroup) */
-            const unsigned prev = __hip_atomic_fetch_add(&a.counters[blockIdx.x], 1u,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *L.flag = prev == (unsigned)(a.splits - 1);
-        }
-        __syncthreads();
-        G4_STAMP(5);
-        if (*L.flag) {
-            /* threads 0..255 take block 2x, 256..511 block 2x + 1 */
-            const int fb = blockIdx.x * 2 + (tid >> 8);
-            if (fb < a.nrb) gv_fixup4<3>(a, fb, Y, tid & 255);
-            vm_drain();
-            if (tid == 0)
-                __hip_atomic_store(&a.counters[blockIdx.x], 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            G4_STAMP(6);
+            *(s2p_f32x4*)dst = v[t];
         }
         return;
     }
@@ -394,6 +367,17 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     }
 }
 
+/* the K-split merge: 64-row block blockIdx.x, its items (4 adjacent
+ * outputs of one row m) blockIdx.y * 512 + tid, + 256, then every
+ * gridDim.y * 512 (every split's partials in flight together, summed in
+ * split order, then the epilogue) */
+#define G4_MERGE_FB 2
+__global__ __launch_bounds__(256) void k_g4_merge(GemvArgs a) {
+    gv_fixup4<G4_MERGE_FB, GEMV_W_INT4, false, true>(a, blockIdx.x, a.y, threadIdx.x,
+                                                     blockIdx.y * 256 * G4_MERGE_FB,
+                                                     gridDim.y * 256 * G4_MERGE_FB);
+}
+
 template <int MT>
 static hipError_t g4_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     /* once per instantiation (thread-safe static initialisation) */
@@ -420,11 +404,11 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const unsigned nblk = a.epi == GEMV_EPI_SWIGLU
                               ? (unsigned)(((a.N >> 1) / 16 + 3) / 4)
                               : (unsigned)(((a.N + 15) / 16 + G4_WAVES - 1) / G4_WAVES);
-    /* 64-row fixup blocks of the split handoff (SWIGLU: 32 gate + 32 up) */
+    /* 64-row blocks of the split merge (SWIGLU: 32 gate + 32 up) */
     const int nrb = a.epi == GEMV_EPI_SWIGLU ? (a.N >> 1) / 32 : (a.N + 63) / 64;
     /* too few row blocks to fill the chip: split K over at most one
-     * workgroup per CU (needs the caller's split-K scratch: partials and
-     * counters).  One workgroup fits a CU, so a grid past the CU count runs
+     * workgroup per CU (needs the caller's split-K scratch for the
+     * partials).  One workgroup fits a CU, so a grid past the CU count runs
      * in two rounds: gate_up (152 row blocks) split in two took 44.5 us at
      * M = 40, unsplit (five windows a workgroup, no handoff) about half */
     const int nch = ((a.K >> 5) + G4_WIN - 1) / G4_WIN;
@@ -435,19 +419,24 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     int cps = (nch + ks - 1) / ks;
     ks = (nch + cps - 1) / cps;
     b.nrb = nrb;
-    if (ks > 1 && (!a.part || !a.counters || (int)nblk > GV_COUNTERS ||
-                   (int64_t)ks * a.M * nrb * 64 > a.part_cap)) {
+    if (ks > 1 && (!a.part || (int64_t)ks * a.M * nrb * 64 > a.part_cap)) {
         ks = 1;
         cps = nch;
     }
     b.splits = ks;
     b.win = cps;
     const dim3 grid(nblk, (unsigned)ks);
+    hipError_t err;
     switch ((a.M + 15) / 16) {
-        case 2: return g4_launch_mt<2>(b, grid, lds, st);
-        case 3: return g4_launch_mt<3>(b, grid, lds, st);
-        case 4: return g4_launch_mt<4>(b, grid, lds, st);
-        case 5: return g4_launch_mt<5>(b, grid, lds, st);
-        default: return g4_launch_mt<6>(b, grid, lds, st);
+        case 2: err = g4_launch_mt<2>(b, grid, lds, st); break;
+        case 3: err = g4_launch_mt<3>(b, grid, lds, st); break;
+        case 4: err = g4_launch_mt<4>(b, grid, lds, st); break;
+        case 5: err = g4_launch_mt<5>(b, grid, lds, st); break;
+        default: err = g4_launch_mt<6>(b, grid, lds, st); break;
     }
+    if (err != hipSuccess || ks == 1) return err;
+    const int items = a.M * (a.epi == GEMV_EPI_SWIGLU ? 8 : 16);
+    const unsigned ny = (unsigned)((items + 256 * G4_MERGE_FB - 1) / (256 * G4_MERGE_FB));
+    hipLaunchKernelGGL(k_g4_merge, dim3((unsigned)nrb, ny), dim3(256), 0, st, b);
+    return hipGetLastError();
 }

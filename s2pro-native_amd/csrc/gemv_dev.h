@@ -549,8 +549,12 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
  * 16-byte agent-scope load (two 8-byte loads), every load of a round in
  * flight before any sum: at 48 rows (FB = 3) a 64-row block takes one round
  * of memory latency, where one output a thread per round took three. */
-template <int FB, int WFMT = GEMV_W_INT4, bool COH = false>
-__device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid) {
+/* PLAIN: the partials come from an earlier launch (plain 16-byte loads);
+ * items base0, base0 + 256 FB, ... of the block go to this thread group
+ * (base0 = 0 and step 256 FB: all of them) */
+template <int FB, int WFMT = GEMV_W_INT4, bool COH = false, bool PLAIN = false>
+__device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid, int base0 = 0,
+                          int bstep = 256 * FB) {
 #pragma clang fp contract(off)
     const int lane = tid & 63;
     const int M = a.M, S = a.splits;
@@ -561,7 +565,7 @@ __device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid) {
      * group 32 later), else 16 groups a row */
     const int per_row = swiglu ? 8 : 16;
     const int items = M * per_row;
-    for (int base = 0; base < items; base += 256 * FB) {
+    for (int base = base0; base < items; base += bstep) {
         s2p_f32x4 g[FB], u[FB];
         uint16_t yold[FB][4];
 #pragma unroll
@@ -578,35 +582,53 @@ __device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid) {
                                  : (uint16_t)0;
             }
         }
-        for (int k0 = 0; k0 < S; k0 += 4) {
-            s2p_u32x4 vg[FB][4], vu[FB][4];
+        /* splits in sets of four, summed in split order */
+        auto issue = [&](int k0, s2p_u32x4 (&vg)[FB][4], int off) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < FB; j++) {
                 const int idx = base + 256 * j + tid;
                 const bool ok = idx < items;
                 const int m = idx / per_row, l4 = (idx % per_row) * 4;
-                const float* p0 = part + ((size_t)m * a.nrb + rb) * 64 + l4;
+                const float* p0 = part + ((size_t)m * a.nrb + rb) * 64 + l4 + off;
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const bool ld = ok && k0 + k < S;
-                    vg[j][k] = ld ? coh_ld128(p0 + (size_t)(k0 + k) * stride) : (s2p_u32x4){0u, 0u, 0u, 0u};
-                    vu[j][k] = ld && swiglu ? coh_ld128(p0 + 32 + (size_t)(k0 + k) * stride)
-                                            : (s2p_u32x4){0u, 0u, 0u, 0u};
-                }
+                for (int k = 0; k < 4; k++)
+                    vg[j][k] = !(ok && k0 + k < S) ? (s2p_u32x4){0u, 0u, 0u, 0u}
+                               : PLAIN ? *(const s2p_u32x4*)(p0 + (size_t)(k0 + k) * stride)
+                                       : coh_ld128(p0 + (size_t)(k0 + k) * stride);
             }
+        };
+        auto accum = [&](int k0, const s2p_u32x4 (&vg)[FB][4], s2p_f32x4 (&dst)[FB])
+            __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < FB; j++)
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     if (k0 + k >= S) break;
-                    const s2p_f32x4 fg = __builtin_bit_cast(s2p_f32x4, vg[j][k]);
-                    const s2p_f32x4 fu = __builtin_bit_cast(s2p_f32x4, vu[j][k]);
+                    const s2p_f32x4 f = __builtin_bit_cast(s2p_f32x4, vg[j][k]);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        g[j][e] += fg[e];
-                        if (swiglu) u[j][e] += fu[e];
-                    }
+                    for (int e = 0; e < 4; e++) dst[j][e] += f[e];
                 }
+        };
+        if (swiglu) {
+            /* gate and up partials (32 rows apart), one set at a time */
+            for (int k0 = 0; k0 < S; k0 += 4) {
+                s2p_u32x4 vg[FB][4], vu[FB][4];
+                issue(k0, vg, 0);
+                issue(k0, vu, 32);
+                accum(k0, vg, g);
+                accum(k0, vu, u);
+            }
+        } else {
+            /* the next set's loads in flight while the current one is summed */
+            s2p_u32x4 ga[FB][4], gb[FB][4];
+            issue(0, ga, 0);
+            for (int k0 = 0; k0 < S; k0 += 8) {
+                if (k0 + 4 < S) issue(k0 + 4, gb, 0);
+                accum(k0, ga, g);
+                if (k0 + 4 >= S) break;
+                if (k0 + 8 < S) issue(k0 + 8, ga, 0);
+                accum(k0 + 4, gb, g);
+            }
         }
 #pragma unroll
         for (int j = 0; j < FB; j++) {
