@@ -368,14 +368,15 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
 }
 
 /* the K-split merge: 64-row block blockIdx.x, its items (4 adjacent
- * outputs of one row m) blockIdx.y * 512 + tid, + 256, then every
- * gridDim.y * 512 (every split's partials in flight together, summed in
- * split order, then the epilogue) */
-#define G4_MERGE_FB 2
-__global__ __launch_bounds__(256) void k_g4_merge(GemvArgs a) {
-    gv_fixup4<G4_MERGE_FB, GEMV_W_INT4, false, true>(a, blockIdx.x, a.y, threadIdx.x,
-                                                     blockIdx.y * 256 * G4_MERGE_FB,
-                                                     gridDim.y * 256 * G4_MERGE_FB);
+ * outputs of one row m) blockIdx.y * G4_MERGE_T + tid, then every
+ * gridDim.y * G4_MERGE_T (every split's partials in flight together, summed
+ * in split order, then the epilogue) */
+#ifndef G4_MERGE_T
+#define G4_MERGE_T 256
+#endif
+__global__ __launch_bounds__(G4_MERGE_T) void k_g4_merge(GemvArgs a) {
+    gv_fixup4<1, GEMV_W_INT4, false, true>(a, blockIdx.x, a.y, threadIdx.x, blockIdx.y * G4_MERGE_T,
+                                           gridDim.y * G4_MERGE_T);
 }
 
 template <int MT>
@@ -436,7 +437,7 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     }
     if (err != hipSuccess || ks == 1) return err;
     const int items = a.M * (a.epi == GEMV_EPI_SWIGLU ? 8 : 16);
-    const unsigned ny = (unsigned)((items + 256 * G4_MERGE_FB - 1) / (256 * G4_MERGE_FB));
-    hipLaunchKernelGGL(k_g4_merge, dim3((unsigned)nrb, ny), dim3(256), 0, st, b);
+    const unsigned ny = (unsigned)((items + G4_MERGE_T - 1) / G4_MERGE_T);
+    hipLaunchKernelGGL(k_g4_merge, dim3((unsigned)nrb, ny), dim3(G4_MERGE_T), 0, st, b);
     return hipGetLastError();
 }
