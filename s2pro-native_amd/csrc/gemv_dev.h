@@ -636,33 +636,50 @@ __device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid, int b
             const bool ok = idx < items;
             const int m = idx / per_row, l4 = (idx % per_row) * 4;
             float ssq = 0.f;
+            /* the item's 4 adjacent outputs: one 8-byte store when all 4
+             * exist and the address allows, else one at a time */
+            uint16_t ov[4] = {0, 0, 0, 0};
+            const int F = a.N >> 1;
+            const int n0 = swiglu ? rb * 32 + l4 : rb * 64 + l4;
+            const int nlim = swiglu ? F : a.N;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
+                if (!ok || n0 + e >= nlim) continue;
                 if (swiglu) {
-                    const int c = l4 + e; /* gate row rb * 32 + c */
-                    const int F = a.N >> 1;
-                    if (!ok || rb * 32 + c >= F) continue;
                     float gg = g[j][e], uu = u[j][e];
                     if (WFMT == GEMV_W_INT8) {
-                        gg *= ((const float*)a.s)[rb * 32 + c];
-                        uu *= ((const float*)a.s)[F + rb * 32 + c];
+                        gg *= ((const float*)a.s)[n0 + e];
+                        uu *= ((const float*)a.s)[F + n0 + e];
                     }
-                    coh_st16(Y + (size_t)m * a.ldy + rb * 32 + c, silu_mul_bf16(f2bf(gg), f2bf(uu)));
+                    ov[e] = silu_mul_bf16(f2bf(gg), f2bf(uu));
                     continue;
                 }
-                const int n = rb * 64 + l4 + e;
-                if (!ok || n >= a.N) continue;
                 float sj = g[j][e];
-                if (WFMT == GEMV_W_INT8) sj *= ((const float*)a.s)[n];
+                if (WFMT == GEMV_W_INT8) sj *= ((const float*)a.s)[n0 + e];
                 const uint16_t yb = f2bf(sj);
-                uint16_t* yp = Y + (size_t)m * a.ldy + n;
                 if (a.epi == GEMV_EPI_RESID) {
                     const uint16_t xo = f2bf(__fadd_rn(bf2f(yold[j][e]), bf2f(yb)));
-                    coh_st16(yp, xo);
+                    ov[e] = xo;
                     const float xv = bf2f(xo);
                     ssq += xv * xv;
                 } else {
-                    coh_st16(yp, yb);
+                    ov[e] = yb;
+                }
+            }
+            if (ok) {
+                uint16_t* yp = Y + (size_t)m * a.ldy + n0;
+                if (n0 + 3 < nlim && ((uintptr_t)yp & 7) == 0) {
+                    const uint64_t w = (uint64_t)ov[0] | ((uint64_t)ov[1] << 16) |
+                                       ((uint64_t)ov[2] << 32) | ((uint64_t)ov[3] << 48);
+                    if (PLAIN) *(uint64_t*)yp = w;
+                    else coh_st64(yp, w);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (n0 + e >= nlim) break;
+                        if (PLAIN) yp[e] = ov[e];
+                        else coh_st16(yp + e, ov[e]);
+                    }
                 }
             }
             if (!swiglu && a.epi == GEMV_EPI_RESID && a.ssq_out) {
@@ -670,8 +687,11 @@ __device__ void gv_fixup4(const GemvArgs& a, int rb, uint16_t* Y, int tid, int b
                  * 16 items a row, rows start at multiples of 16 lanes) */
                 ssq += __shfl_xor(ssq, 1, 64);
                 ssq += __shfl_xor(ssq, 2, 64);
-                if ((lane & 3) == 0 && ok)
-                    coh_stf(a.ssq_out + (size_t)(rb * 4 + (l4 >> 4)) * GEMV_MAX_M + m, ssq);
+                if ((lane & 3) == 0 && ok) {
+                    float* sp = a.ssq_out + (size_t)(rb * 4 + (l4 >> 4)) * GEMV_MAX_M + m;
+                    if (PLAIN) *sp = ssq;
+                    else coh_stf(sp, ssq);
+                }
             }
         }
     }
