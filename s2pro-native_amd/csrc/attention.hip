@@ -107,23 +107,6 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
 #define TR_VOFF(t, d) ((t) * 128 + ((((d) >> 3) ^ TR_VSW(t)) << 3) + ((d) & 7))
 #define TR_LDS_BYTES (4 * AT_TILE * 128 * 2)
 
-/* max / sum over the lanes c, c + 16, c + 32, c + 48 (row swaps, VALU) */
-S2P_DEV float xg_max(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-S2P_DEV float xg_sum(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-S2P_DEV uint32_t pk_bf(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
-
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_attn_tree(AttnArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) unsigned char smem_raw[];

@@ -162,6 +162,25 @@ S2P_DEV float sum16(float v) {
     return v;
 }
 
+/* max / sum over the lanes c, c + 16, c + 32, c + 48 (row swaps, VALU);
+ * every lane gets the result */
+S2P_DEV float xg_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+S2P_DEV float xg_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+/* two floats as a bf16 pair (RNE), the first in the low half */
+S2P_DEV uint32_t pk_bf(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
 S2P_DEV void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -217,30 +236,27 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     constexpr int SVB = AT_SV_BYTES_W(W), SPB = AT_SP_BYTES_W(W), SMLB = AT_SML_BYTES_W(W);
     LDS(uint16_t)* s_v = (LDS(uint16_t)*)smem;
     LDS(uint16_t)* s_p = (LDS(uint16_t)*)(smem + SVB);
-    LDS(uint16_t)* s_pl = (LDS(uint16_t)*)(smem + SVB + SPB);
     LDS(float)* s_ml = (LDS(float)*)(smem + SVB + 2 * SPB);
     LDS(int)* s_flag = (LDS(int)*)(smem + SVB + 2 * SPB + SMLB);
 /* V tile of wave w: 32 positions x 16 chunks of 16 bytes (8 dims), chunk
- * (t, k) stored at slot k ^ vsw(t) of row t (rows of 256 B).  The P V
+ * (t, k) stored at slot k ^ vsw(t) of row t (rows of 256 B).  The Vt
  * operand is read with transposing loads (ds_read_b64_tr_b16): a read
- * touches 16 rows (8 G + k, G < 4, k < 4) at the same two chunks, and vsw
- * spreads them over 8 slot pairs (2-way at most). */
-#define VSW(t) ((((t) & 3) | ((((t) >> 3) & 1) << 2)) << 1)
+ * touches 16 rows (4 G + k, or 16 + 4 G + k; G, k < 4) at the same two
+ * chunks, and vsw spreads them over 8 slot pairs (2-way at most). */
+#define VSW(t) (((t) & 7) << 1)
 #define SVOFF(w, t, d) ((w) * (AT_TILE * 128) + (t) * 128 + ((((d) >> 3) ^ VSW(t)) << 3) + ((d) & 7))
-#define SP(w, r, c) s_p[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
-#define SPL(w, r, c) s_pl[((w) * 32 + (r)) * AT_PSTRIDE + (c)]
 #define SML(w, qv, k) s_ml[((w) * 32 + (qv)) * 2 + (k)]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int qq = lane >> 4, c = lane & 15;
     const SegInfo S = resolve<MODE>(a, seg, kvh);
-    /* the mask words of this lane's rows 4 qt + qq, loaded once and first
-     * (every later load is then younger, so the tile loop's waits can count
-     * the prefetches in flight) */
+    /* the mask words of this lane's query rows 4 qt + c / 4 (query vector
+     * 16 qt + c), loaded once and first (every later load is then younger,
+     * so the tile loop's waits can count the prefetches in flight) */
     uint64_t vw[MQT];
 #pragma unroll
     for (int qt = 0; qt < MQT; qt++) {
-        const int rl = 4 * qt + ((threadIdx.x & 63) >> 4);
+        const int rl = 4 * qt + (c >> 2);
         vw[qt] = S.vis && rl < S.nrows ? S.vis[S.row0 + rl] : 0ull;
     }
     const int p_begin = sp * a.split_pos;
@@ -408,18 +424,23 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
         }
     }
 
-    float m[MQT][4], l[MQT][4];
+    /* The scores are computed transposed, S^T = K Q^T: lane (qq, c) holds
+     * query vector 16 qt + c at positions 16 ps + 4 qq + v, so a query's
+     * softmax runs over its own 8 values and then the lanes c + 16 G, and
+     * the 8 values, packed, are the B operand of O^T = V^T P^T (k slot
+     * 8 qq + 4 ps + v <-> position 16 ps + 4 qq + v): P never goes through
+     * LDS.  m, l per query vector (l: this lane's positions, summed at the
+     * end); o[qt][dt]: O^T, dims 16 dt + 4 qq + v of query vector 16 qt + c */
+    float m[MQT], l[MQT];
     s2p_f32x4 o[MQT][8];
 #pragma unroll
     for (int qt = 0; qt < MQT; qt++) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            m[qt][v] = -INFINITY;
-            l[qt][v] = 0.f;
-        }
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
+    const int open_end = min(S.L, p_end); /* tiles below it need no mask */
 
     /* software pipeline over this wave's tiles: the next tile's K loads
      * (into kr, free once the scores are issued) fly during this tile's
@@ -438,48 +459,63 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             for (int ps = 0; ps < 2; ps++) {
                 s2p_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(qa[qt][ch], kr[ps][ch], acc);
+                for (int ch = 0; ch < 4; ch++) acc = mfma16x16x32(kr[ps][ch], qa[qt][ch], acc);
                 sc[qt][ps] = acc;
             }
         if constexpr (nxt) issue_k(tn);
-        /* online softmax; lane (qq, c) holds rows 4 qq + v of each q tile.
-         * O is rescaled only when some row of the wave raised its maximum:
-         * otherwise every factor is e^0 = 1 exactly and the products would
-         * change nothing (past the first tiles of a split, the usual case) */
-        float corr[MQT][4];
+        /* online softmax of query vector 16 qt + c over positions
+         * tb + 16 ps + 4 qq + v.  O is rescaled only when some query of the
+         * wave raised its maximum: otherwise every factor is e^0 = 1 exactly
+         * and the products would change nothing (past the first tiles of a
+         * split, the usual case) */
+        const bool open = tb + AT_TILE <= open_end;
+        float corr[MQT];
+        s2p_u32x4 ph[MQT], pl[MQT];
         bool raised = false;
 #pragma unroll
         for (int qt = 0; qt < MQT; qt++) {
-            const int rl = 4 * qt + qq;
-            const bool vis0 = visible_w(S, vw[qt], rl, tb + c) && tb + c < p_end;
-            const bool vis1 = visible_w(S, vw[qt], rl, tb + 16 + c) && tb + 16 + c < p_end;
+            const int rl = 4 * qt + (c >> 2);
+            float t[2][4];
+            float tm = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float t0 = vis0 ? sc[qt][0][v] * scale : -INFINITY;
-                const float t1 = vis1 ? sc[qt][1][v] * scale : -INFINITY;
-                const float tm = max16(fmaxf(t0, t1));
-                const float mn = fmaxf(m[qt][v], tm);
-                const float ms = mn == -INFINITY ? 0.f : mn;
-                corr[qt][v] = __expf(m[qt][v] - ms);
-                raised |= corr[qt][v] != 1.0f;
-                const float p0 = __expf(t0 - ms), p1 = __expf(t1 - ms);
-                l[qt][v] = l[qt][v] * corr[qt][v] + p0 + p1;
-                m[qt][v] = mn;
-                /* P = hi + lo, both bf16: 16 significant bits into the PV MFMA */
-                const uint16_t h0 = f2bf(p0), h1 = f2bf(p1);
-                SP(wave, 16 * qt + 4 * qq + v, c) = h0;
-                SP(wave, 16 * qt + 4 * qq + v, 16 + c) = h1;
-                SPL(wave, 16 * qt + 4 * qq + v, c) = f2bf(p0 - bf2f(h0));
-                SPL(wave, 16 * qt + 4 * qq + v, 16 + c) = f2bf(p1 - bf2f(h1));
-            }
+            for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int pos = tb + 16 * ps + 4 * qq + v;
+                    const bool vis = open || (visible_w(S, vw[qt], rl, pos) && pos < p_end);
+                    t[ps][v] = vis ? sc[qt][ps][v] * scale : -INFINITY;
+                    tm = fmaxf(tm, t[ps][v]);
+                }
+            tm = xg_max(tm);
+            const float mn = fmaxf(m[qt], tm);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            corr[qt] = __expf(m[qt] - ms);
+            raised |= corr[qt] != 1.0f;
+            float ls = 0.f;
+            float p[2][4], lo[2][4];
+#pragma unroll
+            for (int ps = 0; ps < 2; ps++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    p[ps][v] = __expf(t[ps][v] - ms);
+                    ls += p[ps][v];
+                    /* P = hi + lo, both bf16: 16 significant bits into the MFMA */
+                    lo[ps][v] = p[ps][v] - bf2f(f2bf(p[ps][v]));
+                }
+            l[qt] = l[qt] * corr[qt] + ls;
+            m[qt] = mn;
+            ph[qt] = (s2p_u32x4){pk_bf(p[0][0], p[0][1]), pk_bf(p[0][2], p[0][3]),
+                                 pk_bf(p[1][0], p[1][1]), pk_bf(p[1][2], p[1][3])};
+            pl[qt] = (s2p_u32x4){pk_bf(lo[0][0], lo[0][1]), pk_bf(lo[0][2], lo[0][3]),
+                                 pk_bf(lo[1][0], lo[1][1]), pk_bf(lo[1][2], lo[1][3])};
         }
         if (__any(raised)) {
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++)
 #pragma unroll
-                for (int v = 0; v < 4; v++)
+                for (int dt = 0; dt < 8; dt++)
 #pragma unroll
-                    for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= corr[qt][v];
+                    for (int v = 0; v < 4; v++) o[qt][dt][v] *= corr[qt];
         }
         /* this tile's V into the wave's LDS buffer (free: the previous
          * tile's P V has read it), then the next tile's V loads */
@@ -488,26 +524,21 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
             *(LDS(s2p_u32x4)*)(s_v + SVOFF(wave, 4 * i + (lane >> 4), 8 * (lane & 15))) = vt[i];
         if constexpr (nxt) issue_v(tn);
         wave_sync_lds();
-        s2p_u32x4 pa[MQT], pl[MQT];
-#pragma unroll
-        for (int qt = 0; qt < MQT; qt++) {
-            pa[qt] = *(const LDS(s2p_u32x4)*)&SP(wave, 16 * qt + c, 8 * qq);
-            pl[qt] = *(const LDS(s2p_u32x4)*)&SPL(wave, 16 * qt + c, 8 * qq);
-        }
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            /* B operand (k = position 8 qq + j, n = dim 16 dt + c) by two
-             * transposing reads: lane 4 k + m of a 16-lane group supplies the
-             * 4 dims 16 dt + 4 m.. of row 8 qq + k (+ 4), and lane c receives
-             * dim 16 dt + c of the group's 4 rows */
+            /* A operand (row c = dim 16 dt + c, k slots 8 qq + j = positions
+             * 4 qq + j, then 16 + 4 qq + j) by two transposing reads: lane
+             * 4 k + m of a 16-lane group supplies the 4 dims 16 dt + 4 m.. of
+             * row 4 qq + k (+ 16), and lane c receives dim 16 dt + c of the
+             * group's 4 rows */
             const int k4 = c >> 2, m4 = c & 3;
-            const s2p_u32x2 b0 = ds_read_tr16(s_v + SVOFF(wave, 8 * qq + k4, 16 * dt + 4 * m4));
-            const s2p_u32x2 b1 = ds_read_tr16(s_v + SVOFF(wave, 8 * qq + 4 + k4, 16 * dt + 4 * m4));
-            const s2p_u32x4 bv = {b0.x, b0.y, b1.x, b1.y};
+            const s2p_u32x2 b0 = ds_read_tr16(s_v + SVOFF(wave, 4 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x2 b1 = ds_read_tr16(s_v + SVOFF(wave, 16 + 4 * qq + k4, 16 * dt + 4 * m4));
+            const s2p_u32x4 va = {b0.x, b0.y, b1.x, b1.y};
 #pragma unroll
             for (int qt = 0; qt < MQT; qt++) {
-                o[qt][dt] = mfma16x16x32(pl[qt], bv, o[qt][dt]);
-                o[qt][dt] = mfma16x16x32(pa[qt], bv, o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(va, pl[qt], o[qt][dt]);
+                o[qt][dt] = mfma16x16x32(va, ph[qt], o[qt][dt]);
             }
         }
         wave_sync_lds();
@@ -523,57 +554,44 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     }
 
     stamp(2);
-    /* ---- merge the 4 waves ---- */
+    /* ---- merge the W waves ---- */
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            l[qt][v] = sum16(l[qt][v]);
-            if (c == 0) {
-                SML(wave, 16 * qt + 4 * qq + v, 0) = m[qt][v];
-                SML(wave, 16 * qt + 4 * qq + v, 1) = l[qt][v];
-            }
+    for (int qt = 0; qt < MQT; qt++) {
+        l[qt] = xg_sum(l[qt]);
+        if (qq == 0) {
+            SML(wave, 16 * qt + c, 0) = m[qt];
+            SML(wave, 16 * qt + c, 1) = l[qt];
         }
+    }
     __syncthreads();
-    float ltot[MQT][4], mtot[MQT][4];
+    float ltot[MQT], mtot[MQT];
 #pragma unroll
-    for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int qv = 16 * qt + 4 * qq + v;
-            float M = -INFINITY;
+    for (int qt = 0; qt < MQT; qt++) {
+        const int qv = 16 * qt + c;
+        float M = -INFINITY;
 #pragma unroll 4
-            for (int w = 0; w < W; w++) M = fmaxf(M, SML(w, qv, 0));
-            const float Ms = M == -INFINITY ? 0.f : M;
-            float lt = 0.f;
+        for (int w = 0; w < W; w++) M = fmaxf(M, SML(w, qv, 0));
+        const float Ms = M == -INFINITY ? 0.f : M;
+        float lt = 0.f;
 #pragma unroll 4
-            for (int w = 0; w < W; w++) lt += __expf(SML(w, qv, 0) - Ms) * SML(w, qv, 1);
-            const float f = __expf(m[qt][v] - Ms);
+        for (int w = 0; w < W; w++) lt += __expf(SML(w, qv, 0) - Ms) * SML(w, qv, 1);
+        const float f = __expf(m[qt] - Ms);
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) o[qt][dt][v] *= f;
-            ltot[qt][v] = lt;
-            mtot[qt][v] = M;
-        }
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) o[qt][dt][v] *= f;
+        ltot[qt] = lt;
+        mtot[qt] = M;
+    }
     /* sum O over waves through LDS (reusing the V tiles: 2 x 16 KB) */
     LDS(float)* s_o = (LDS(float)*)s_v;
-    const int ostride = 32 * AT_HD;
-    auto put = [&](int slot) {
+    /* O of the 32 query vectors as [q vector][dim] */
+    auto put = [&]() {
 #pragma unroll
         for (int qt = 0; qt < MQT; qt++)
 #pragma unroll
             for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c] = o[qt][dt][v];
-    };
-    auto add = [&](int slot) {
-#pragma unroll
-        for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    o[qt][dt][v] += s_o[slot * ostride + (16 * qt + 4 * qq + v) * AT_HD + 16 * dt + c];
+                *(LDS(s2p_f32x4)*)(s_o + (16 * qt + c) * AT_HD + 16 * dt + 4 * qq) = o[qt][dt];
     };
     /* the tree's hand-offs in a lane-major layout ([slot][qt][dt][lane] of
      * 16 bytes): one ds_write_b128 / ds_read_b128 per register quad,
@@ -613,35 +631,34 @@ __device__ bool attn_block(const AttnArgs& a, int seg, int kvh, int sp, LDS(unsi
     if (a.nsplit == 1) {
         if (wave == 0) {
 #pragma unroll
-            for (int qt = 0; qt < MQT; qt++)
+            for (int qt = 0; qt < MQT; qt++) {
+                const int qv = 16 * qt + c;
+                const int rl = qv >> 2, g = qv & 3;
+                if (rl >= S.nrows) continue;
+                const int row = S.row0 + rl;
+                const int h = 4 * kvh + g;
+                const float inv = 1.0f / ltot[qt];
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int qv = 16 * qt + 4 * qq + v;
-                    const int rl = qv >> 2, g = qv & 3;
-                    if (rl >= S.nrows) continue;
-                    const int row = S.row0 + rl;
-                    const int h = 4 * kvh + g;
-                    const float inv = 1.0f / ltot[qt][v];
-#pragma unroll
-                    for (int dt = 0; dt < 8; dt++)
-                        coh_st16(a.out + (size_t)row * qrow_stride + h * AT_HD + 16 * dt + c,
-                                 f2bf(o[qt][dt][v] * inv));
+                for (int dt = 0; dt < 8; dt++) {
+                    const s2p_f32x4 y = o[qt][dt];
+                    coh_st64(a.out + (size_t)row * qrow_stride + h * AT_HD + 16 * dt + 4 * qq,
+                             (uint64_t)pk_bf(y[0] * inv, y[1] * inv) |
+                                 ((uint64_t)pk_bf(y[2] * inv, y[3] * inv) << 32));
                 }
+            }
         }
     } else {
         /* partial (m, l, O) of this split: O through LDS ([q vector][dim]), then
          * 16-byte write-through stores by the whole block */
         LDS(float)* s_mlw = (LDS(float)*)s_p; /* [32][2], free after the tiles */
         if (wave == 0) {
-            put(0);
-            if (c == 0) {
+            put();
+            if (qq == 0) {
 #pragma unroll
-                for (int qt = 0; qt < MQT; qt++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        s_mlw[(16 * qt + 4 * qq + v) * 2] = mtot[qt][v];
-                        s_mlw[(16 * qt + 4 * qq + v) * 2 + 1] = ltot[qt][v];
-                    }
+                for (int qt = 0; qt < MQT; qt++) {
+                    s_mlw[(16 * qt + c) * 2] = mtot[qt];
+                    s_mlw[(16 * qt + c) * 2 + 1] = ltot[qt];
+                }
             }
         }
         __syncthreads();
