@@ -33,6 +33,9 @@
 #define G4_WAVES 8
 #define G4_WIN 16 /* groups per window = one weight chunk (GV_CHG_INT4) */
 #define G4_MAX_M 96 /* six column tiles */
+#ifndef G4_PIPE
+#define G4_PIPE(MT) ((MT) != 5) /* five tiles: no registers left for it */
+#endif
 
 static __host__ __device__ size_t g4_xs() { return (size_t)G4_WIN * 32 + GV_XPAD; }
 static __host__ __device__ size_t g4_xg() { return (size_t)gv_round32(G4_WIN) + 8; }
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         corr[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
     }
     auto mult = [&](const GvBuf& B, int c) __attribute__((always_inline)) {
-        gv_compute<GEMV_W_INT4, MT, false>(B, L, 0, min(G4_WIN, G - c * G4_WIN), M, 0, q, r, acc,
+        gv_compute<GEMV_W_INT4, MT, false, G4_PIPE(MT)>(B, L, 0, min(G4_WIN, G - c * G4_WIN), M, 0, q, r, acc,
                                            corr);
     };
     const int ce = c0 + nch;
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
             __syncthreads();
         };
         auto mult_db = [&](const GvBuf& B, int c, int bsel) __attribute__((always_inline)) {
-            gv_compute<GEMV_W_INT4, MT, false>(B, Lb[bsel], 0, min(G4_WIN, G - c * G4_WIN), M, 0, q,
+            gv_compute<GEMV_W_INT4, MT, false, G4_PIPE(MT)>(B, Lb[bsel], 0, min(G4_WIN, G - c * G4_WIN), M, 0, q,
                                                r, acc, corr);
         };
         issue(c0, 0);

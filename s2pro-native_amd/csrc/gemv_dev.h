@@ -374,7 +374,11 @@ S2P_DEV s2p_f32x4 mfma16x16x16(s2p_u32x2 a, s2p_u32x2 b, s2p_f32x4 c) {
 }
 
 /* multiply one chunk: cg = chunk's first group within the staged window */
-template <int WFMT, int MT, bool TR = false>
+/* PIPE (untransposed INT4): a group's MT MFMAs are issued before the
+ * previous group's scale FMAs, so one MFMA latency per group is hidden
+ * behind the other's work instead of one per column tile exposed (same
+ * products, same accumulation order) */
+template <int WFMT, int MT, bool TR = false, bool PIPE = false>
 S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, int wave, int q,
                         int r, s2p_f32x4 (&acc)[MT], s2p_f32x4 (&corr)[MT]) {
     int mrow[MT];
@@ -466,6 +470,10 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
         wave_lds_sync();
         uint32_t kmask = 0x00780078u, kone = 0x3F803F80u;
         asm volatile("" : "+v"(kmask), "+v"(kone));
+        s2p_f32x4 rp[MT], sp4 = {0.f, 0.f, 0.f, 0.f}; /* PIPE: the pending group */
+#pragma unroll
+        for (int t = 0; t < MT; t++) rp[t] = (s2p_f32x4){0.f, 0.f, 0.f, 0.f};
+        bool pend = false;
 #pragma unroll
         for (int it = 0; it < GV_CHG_INT4 / 4; it++) {
             if (it * 4 >= gn) break;
@@ -478,16 +486,43 @@ S2P_DEV void gv_compute(const GvBuf& B, const GvLds& L, int cg, int gn, int M, i
                 const int g = it * 4 + j;
                 const s2p_u32x4 av = deq_int4(dj[j], kmask, kone);
                 const s2p_f32x4 s4 = *(const LDS(s2p_f32x4)*)(sc + g * 16 + 4 * q);
+                if constexpr (PIPE) {
+                    s2p_u32x4 bv[MT];
+                    s2p_f32x4 raw[MT];
 #pragma unroll
-                for (int t = 0; t < MT; t++) {
-                    const s2p_u32x4 bv =
-                        *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
-                    const s2p_f32x4 raw = mfma16x16x32(av, bv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+                    for (int t = 0; t < MT; t++)
+                        bv[t] = *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[t][i] = fmaf(s4[i], raw[i], acc[t][i]);
+                    for (int t = 0; t < MT; t++)
+                        raw[t] = mfma16x16x32(av, bv[t], (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+                    if (pend) {
+#pragma unroll
+                        for (int t = 0; t < MT; t++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc[t][i] = fmaf(sp4[i], rp[t][i], acc[t][i]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < MT; t++) rp[t] = raw[t];
+                    sp4 = s4;
+                    pend = true;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < MT; t++) {
+                        const s2p_u32x4 bv =
+                            *(const LDS(s2p_u32x4)*)(L.x + mrow[t] * L.xs + (cg + g) * 32 + q * 8);
+                        const s2p_f32x4 raw = mfma16x16x32(av, bv, (s2p_f32x4){0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[t][i] = fmaf(s4[i], raw[i], acc[t][i]);
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0); /* keep LDS reads from piling up */
+        }
+        if (PIPE && pend) {
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][i] = fmaf(sp4[i], rp[t][i], acc[t][i]);
         }
         /* bias correction: corr += S (16 rows x 16 groups) . X (16 groups x 16 cols) */
         const s2p_u32x2 ah = {shi[0], shi[1]};
