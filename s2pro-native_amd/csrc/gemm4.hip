@@ -332,10 +332,18 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
                 const s2p_f32x4 u = ex[(wave * MT + t) * 64 + lane];
                 const int m = t * 16 + r;
                 if (m >= M) continue;
+                uint16_t h[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = tile * 16 + 4 * q + i;
-                    Y[(size_t)m * a.ldy + n] = silu_mul_bf16(f2bf(v[t][i]), f2bf(u[i]));
+                for (int i = 0; i < 4; i++) h[i] = silu_mul_bf16(f2bf(v[t][i]), f2bf(u[i]));
+                /* outputs tile * 16 + 4 q .. + 3 of row m: one 8-byte store
+                 * where aligned (F is a multiple of 32) */
+                uint16_t* yp = Y + (size_t)m * a.ldy + tile * 16 + 4 * q;
+                if (((uintptr_t)yp & 7) == 0) {
+                    *(uint64_t*)yp = (uint64_t)h[0] | ((uint64_t)h[1] << 16) |
+                                     ((uint64_t)h[2] << 32) | ((uint64_t)h[3] << 48);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) yp[i] = h[i];
                 }
             }
         }
