@@ -76,8 +76,9 @@ S2P_FM_QUAL float s2p_expf(float xf) {
     const double LN2_HI = 6.93147180369123816490e-01; /* 0x3FE62E42FEE00000 */
     const double LN2_LO = 1.90821492927058770002e-10;
     double t = x * INV_LN2;
-    /* round-half-away to an integer; exact for |t| < 2^52 */
-    double kd = t >= 0.0 ? (double)(int64_t)(t + 0.5) : -(double)(int64_t)(0.5 - t);
+    /* round-half-away to an integer; exact for |t| < 2^52 (truncation of a
+     * double, the value a conversion to int64 and back gives in that range) */
+    double kd = t >= 0.0 ? __builtin_trunc(t + 0.5) : -__builtin_trunc(0.5 - t);
     const int k = (int)kd;
     const double r = (x - kd * LN2_HI) - kd * LN2_LO;
     /* Taylor series of exp(r), Horner form, degree 13 */

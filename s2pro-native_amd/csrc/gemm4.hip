@@ -319,22 +319,29 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
         return;
     }
     if (swiglu) {
-        __syncthreads(); /* the last window is no longer read: reuse x for the up tiles */
+        /* gate wave w and up wave w + 4 hold the two halves of the same
+         * outputs: each takes half the column tiles (the gate wave the first
+         * TH, the up wave the rest) and hands the other half of its values
+         * over through LDS, so both halves of the SiLU work run at once */
+        constexpr int TH = (MT + 1) / 2;
+        __syncthreads(); /* the last window is no longer read: reuse x for the exchange */
         LDS(s2p_f32x4)* ex = (LDS(s2p_f32x4)*)smem;
-        if (wave >= 4) {
+        const int pw = wave & 3;
 #pragma unroll
-            for (int t = 0; t < MT; t++) ex[((wave - 4) * MT + t) * 64 + lane] = v[t];
-        }
+        for (int t = 0; t < MT; t++)
+            if ((wave >= 4) == (t < TH)) ex[(pw * MT + t) * 64 + lane] = v[t];
         __syncthreads();
-        if (wave < 4 && active) {
+        if (active) {
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const s2p_f32x4 u = ex[(wave * MT + t) * 64 + lane];
+                if ((wave >= 4) != (t >= TH)) continue; /* uniform */
+                const s2p_f32x4 o = ex[(pw * MT + t) * 64 + lane];
+                const s2p_f32x4 gv = wave < 4 ? v[t] : o, uv = wave < 4 ? o : v[t];
                 const int m = t * 16 + r;
                 if (m >= M) continue;
                 uint16_t h[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) h[i] = silu_mul_bf16(f2bf(v[t][i]), f2bf(u[i]));
+                for (int i = 0; i < 4; i++) h[i] = silu_mul_bf16(f2bf(gv[i]), f2bf(uv[i]));
                 /* outputs tile * 16 + 4 q .. + 3 of row m: one 8-byte store
                  * where aligned (F is a multiple of 32) */
                 uint16_t* yp = Y + (size_t)m * a.ldy + tile * 16 + 4 * q;
