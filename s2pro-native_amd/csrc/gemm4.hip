@@ -63,6 +63,27 @@ extern "C" hipError_t s2p_g4_probe_get(uint64_t* host, int n) {
 #define G4_STAMP(i)
 #endif
 
+/* inverse RMS of activation row m from the producer's per-block sums of
+ * squares: lane l sums blocks l, l + 64, ... in order, then the wave's tree
+ * (the GEMV engine's order); every lane returns it */
+static __device__ float g4_inv_rms(const GemvArgs& a, int m, int lane) {
+#pragma clang fp contract(off)
+    float s = 0.f;
+    for (int b = lane; b < a.ssq_in_blocks; b += 64) s += a.ssq_in[(size_t)b * GEMV_MAX_M + m];
+    s = wave_sum_down(s);
+    return rsqrt_rule(s / (float)a.K + a.norm_eps);
+}
+
+/* the rows' inverse RMS once per launch, one wave a row, into inv_out (a
+ * k_gemm4 workgroup otherwise computes all M of them itself: a chain of a
+ * load round and M / 8 trees a wave, ~7 us at M = 68 in every workgroup) */
+__global__ __launch_bounds__(256) void k_g4_rms(GemvArgs a, float* inv_out) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (m >= a.M) return; /* uniform per wave */
+    const float v = g4_inv_rms(a, m, lane);
+    if (lane == 0) inv_out[m] = v;
+}
+
 template <int MT>
 __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
 #pragma clang fp contract(off)
@@ -117,11 +138,10 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     load_c(b0, c0); /* in flight during the inverse RMS and the first staging */
 
     if (a.xmode == GEMV_X_NORM) {
-        for (int m = wave; m < M; m += G4_WAVES) {
-            float s = 0.f;
-            for (int b = lane; b < a.ssq_in_blocks; b += 64) s += a.ssq_in[(size_t)b * GEMV_MAX_M + m];
-            s = wave_sum_down(s);
-            if (lane == 0) L.inv[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
+        if (a.inv_in) { /* from k_g4_rms, the launch before */
+            if (tid < M) L.inv[tid] = a.inv_in[tid];
+        } else {
+            for (int m = wave; m < M; m += G4_WAVES) L.inv[m] = g4_inv_rms(a, m, lane);
         }
     }
 
@@ -419,6 +439,15 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const size_t lds = g4_lds_bytes(a.M);
     if (lds > 160 * 1024) return hipErrorNotSupported;
     GemvArgs b = a;
+    b.inv_in = nullptr;
+    /* NORM: the rows' inverse RMS by k_g4_rms first, into the last
+     * GEMV_MAX_M floats of the split scratch (kept out of the partials) */
+    float* inv_buf = nullptr;
+    if (a.xmode == GEMV_X_NORM && a.part && a.part_cap >= 4 * GEMV_MAX_M) {
+        const int64_t at = (a.part_cap - GEMV_MAX_M) & ~(int64_t)63;
+        inv_buf = a.part + at;
+        b.part_cap = at;
+    }
     /* workgroups of 8 row tiles (SWIGLU: 4 gate + 4 up tiles) */
     const unsigned nblk = a.epi == GEMV_EPI_SWIGLU
                               ? (unsigned)(((a.N >> 1) / 16 + 3) / 4)
@@ -438,13 +467,19 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     int cps = (nch + ks - 1) / ks;
     ks = (nch + cps - 1) / cps;
     b.nrb = nrb;
-    if (ks > 1 && (!a.part || (int64_t)ks * a.M * nrb * 64 > a.part_cap)) {
+    if (ks > 1 && (!a.part || (int64_t)ks * a.M * nrb * 64 > b.part_cap)) {
         ks = 1;
         cps = nch;
     }
     b.splits = ks;
     b.win = cps;
     const dim3 grid(nblk, (unsigned)ks);
+    if (inv_buf) {
+        hipLaunchKernelGGL(k_g4_rms, dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0, st, b, inv_buf);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        b.inv_in = inv_buf;
+    }
     hipError_t err;
     switch ((a.M + 15) / 16) {
         case 2: err = g4_launch_mt<2>(b, grid, lds, st); break;

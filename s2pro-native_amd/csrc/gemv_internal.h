@@ -47,6 +47,7 @@ typedef struct {
     int64_t         part_cap;/* floats available at part */
     unsigned*       counters;/* [ceil(N/64)], zero between calls */
     int             engine;  /* GEMV_ENGINE_AUTO, or GEMV_ENGINE_SPLITK: the split-K engine only */
+    const float*    inv_in;  /* derived (k_gemm4, NORM): the rows' inverse RMS, [M] */
 #ifdef S2P_DIAG
     uint64_t*       probe;   /* diagnostics build (whole-K engine): [grid][8] stage clocks */
 #endif
