@@ -74,14 +74,27 @@ static __device__ float g4_inv_rms(const GemvArgs& a, int m, int lane) {
     return rsqrt_rule(s / (float)a.K + a.norm_eps);
 }
 
-/* the rows' inverse RMS once per launch, one wave a row, into inv_out (a
- * k_gemm4 workgroup otherwise computes all M of them itself: a chain of a
- * load round and M / 8 trees a wave, ~7 us at M = 68 in every workgroup) */
+/* the rows' inverse RMS once per launch into inv_out (a k_gemm4 workgroup
+ * otherwise computes all M of them itself: a chain of a load round and
+ * M / 8 trees a wave, ~7 us at M = 68 in every workgroup).  Workgroup g
+ * takes rows 4 g .. 4 g + 3: their block sums come in as one 16-byte load
+ * per block (coalesced; GEMV_MAX_M is a multiple of 4), then wave w sums
+ * row 4 g + w in the GEMV engine's order from LDS */
+#define G4_RMS_BLOCKS 1024
 __global__ __launch_bounds__(256) void k_g4_rms(GemvArgs a, float* inv_out) {
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+#pragma clang fp contract(off)
+    __shared__ s2p_f32x4 sb[G4_RMS_BLOCKS];
+    const int m0 = blockIdx.x * 4, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.ssq_in_blocks;
+    for (int b = threadIdx.x; b < nb; b += 256)
+        sb[b] = *(const s2p_f32x4*)(a.ssq_in + (size_t)b * GEMV_MAX_M + m0);
+    __syncthreads();
+    const int m = m0 + wave;
     if (m >= a.M) return; /* uniform per wave */
-    const float v = g4_inv_rms(a, m, lane);
-    if (lane == 0) inv_out[m] = v;
+    float s = 0.f;
+    for (int b = lane; b < nb; b += 64) s += sb[b][wave];
+    s = wave_sum_down(s);
+    if (lane == 0) inv_out[m] = rsqrt_rule(s / (float)a.K + a.norm_eps);
 }
 
 template <int MT>
@@ -443,7 +456,8 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     /* NORM: the rows' inverse RMS by k_g4_rms first, into the last
      * GEMV_MAX_M floats of the split scratch (kept out of the partials) */
     float* inv_buf = nullptr;
-    if (a.xmode == GEMV_X_NORM && a.part && a.part_cap >= 4 * GEMV_MAX_M) {
+    if (a.xmode == GEMV_X_NORM && a.part && a.part_cap >= 4 * GEMV_MAX_M &&
+        a.ssq_in_blocks <= G4_RMS_BLOCKS && (GEMV_MAX_M & 3) == 0) {
         const int64_t at = (a.part_cap - GEMV_MAX_M) & ~(int64_t)63;
         inv_buf = a.part + at;
         b.part_cap = at;
