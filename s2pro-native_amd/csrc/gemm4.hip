@@ -27,6 +27,7 @@
  * residual add with per-16-column sums of squares, SwiGLU. */
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "gemv_dev.h"
 
@@ -430,6 +431,83 @@ __global__ __launch_bounds__(G4_MERGE_T) void k_g4_merge(GemvArgs a) {
                                            gridDim.y * G4_MERGE_T);
 }
 
+/* the split merge of a RESID GEMM whose rows' inverse RMS the next GEMM
+ * wants (inv_out): workgroup m takes all of row m, so after the outputs
+ * (the same sums in split order and epilogue as k_g4_merge) it has every
+ * 16-column sum of squares of the row and writes inv_out[m] (the order and
+ * arithmetic of k_g4_rms) — no separate launch for it */
+__global__ __launch_bounds__(1024) void k_g4_merge_rows(GemvArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float sblk[G4_RMS_BLOCKS];
+    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int nit = a.N >> 2, S = a.splits;
+    const size_t stride = (size_t)a.M * a.nrb * 64;
+    uint16_t* Y = a.y;
+    for (int i0 = 0; i0 < nit; i0 += (int)blockDim.x) {
+        const int i = i0 + tid;
+        const bool ok = i < nit;
+        const int n0 = 4 * min(i, nit - 1), rb = n0 >> 6, l4 = n0 & 63;
+        const float* p0 = a.part + ((size_t)m * a.nrb + rb) * 64 + l4;
+        uint16_t* yp = Y + (size_t)m * a.ldy + n0;
+        uint16_t yold[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) yold[e] = yp[e];
+        s2p_f32x4 g = {0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < S; k0 += 8) {
+            s2p_f32x4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                v[j] = *(const s2p_f32x4*)(p0 + (size_t)min(k0 + j, S - 1) * stride);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (k0 + j >= S) break;
+#pragma unroll
+                for (int e = 0; e < 4; e++) g[e] += v[j][e];
+            }
+        }
+        float ssq = 0.f;
+        uint16_t ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint16_t xo = f2bf(__fadd_rn(bf2f(yold[e]), bf2f(f2bf(g[e]))));
+            ov[e] = xo;
+            const float xv = bf2f(xo);
+            ssq += xv * xv;
+        }
+        if (ok)
+            *(uint64_t*)yp = (uint64_t)ov[0] | ((uint64_t)ov[1] << 16) | ((uint64_t)ov[2] << 32) |
+                             ((uint64_t)ov[3] << 48);
+        /* a 16-column block is 4 adjacent lanes */
+        ssq += __shfl_xor(ssq, 1, 64);
+        ssq += __shfl_xor(ssq, 2, 64);
+        if ((lane & 3) == 0 && ok) {
+            if (a.ssq_out) a.ssq_out[(size_t)(n0 >> 4) * GEMV_MAX_M + m] = ssq;
+            sblk[n0 >> 4] = ssq;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float s = 0.f;
+        for (int b = lane; b < (a.N >> 4); b += 64) s += sblk[b];
+        s = wave_sum_down(s);
+        if (lane == 0) a.inv_out[m] = rsqrt_rule(s / (float)a.N + a.inv_eps);
+    }
+}
+
+extern "C" hipError_t s2p_g4_rms_launch(const float* ssq, int blocks, int M, int K, float eps,
+                                        float* inv, hipStream_t st) {
+    if (blocks > G4_RMS_BLOCKS || M > GEMV_MAX_M || (GEMV_MAX_M & 3)) return hipErrorInvalidValue;
+    GemvArgs r;
+    memset(&r, 0, sizeof(r));
+    r.ssq_in = ssq;
+    r.ssq_in_blocks = blocks;
+    r.M = M;
+    r.K = K;
+    r.norm_eps = eps;
+    hipLaunchKernelGGL(k_g4_rms, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, st, r, inv);
+    return hipGetLastError();
+}
+
 template <int MT>
 static hipError_t g4_launch_mt(const GemvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     /* once per instantiation (thread-safe static initialisation) */
@@ -452,11 +530,11 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
     const size_t lds = g4_lds_bytes(a.M);
     if (lds > 160 * 1024) return hipErrorNotSupported;
     GemvArgs b = a;
-    b.inv_in = nullptr;
-    /* NORM: the rows' inverse RMS by k_g4_rms first, into the last
-     * GEMV_MAX_M floats of the split scratch (kept out of the partials) */
+    /* NORM: the rows' inverse RMS as the producer wrote it (inv_in), else
+     * by k_g4_rms first, into the last GEMV_MAX_M floats of the split
+     * scratch (kept out of the partials) */
     float* inv_buf = nullptr;
-    if (a.xmode == GEMV_X_NORM && a.part && a.part_cap >= 4 * GEMV_MAX_M &&
+    if (a.xmode == GEMV_X_NORM && !a.inv_in && a.part && a.part_cap >= 4 * GEMV_MAX_M &&
         a.ssq_in_blocks <= G4_RMS_BLOCKS && (GEMV_MAX_M & 3) == 0) {
         const int64_t at = (a.part_cap - GEMV_MAX_M) & ~(int64_t)63;
         inv_buf = a.part + at;
@@ -502,9 +580,22 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         case 5: err = g4_launch_mt<5>(b, grid, lds, st); break;
         default: err = g4_launch_mt<6>(b, grid, lds, st); break;
     }
-    if (err != hipSuccess || ks == 1) return err;
+    if (err != hipSuccess) return err;
+    const bool want_inv = a.inv_out && a.epi == GEMV_EPI_RESID && a.ssq_out;
+    if (ks == 1) /* the kernel's epilogue wrote the sums of squares */
+        return want_inv ? s2p_g4_rms_launch(a.ssq_out, (a.N + 15) / 16, a.M, a.N, a.inv_eps,
+                                            a.inv_out, st)
+                        : hipSuccess;
+    if (want_inv && (a.N & 15) == 0 && a.N / 16 <= G4_RMS_BLOCKS) {
+        const int nit = a.N >> 2;
+        const unsigned th = (unsigned)(nit >= 1024 ? 1024 : ((nit + 63) / 64) * 64);
+        hipLaunchKernelGGL(k_g4_merge_rows, dim3((unsigned)a.M), dim3(th), 0, st, b);
+        return hipGetLastError();
+    }
     const int items = a.M * (a.epi == GEMV_EPI_SWIGLU ? 8 : 16);
     const unsigned ny = (unsigned)((items + G4_MERGE_T - 1) / G4_MERGE_T);
     hipLaunchKernelGGL(k_g4_merge, dim3((unsigned)nrb, ny), dim3(G4_MERGE_T), 0, st, b);
-    return hipGetLastError();
+    err = hipGetLastError();
+    if (err != hipSuccess || !want_inv) return err;
+    return s2p_g4_rms_launch(a.ssq_out, (a.N + 15) / 16, a.M, a.N, a.inv_eps, a.inv_out, st);
 }

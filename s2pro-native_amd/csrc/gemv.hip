@@ -325,16 +325,10 @@ static hipError_t gv3_launch(const GemvArgs& a, dim3 grid, dim3 block, size_t ld
     }
 }
 
-extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
+static hipError_t gemv_engines(const GemvArgs* ap, hipStream_t st) {
     GemvArgs a = *ap;
     dim3 grid;
     size_t lds = 0;
-    /* INT4 at 16 < M <= 96: the row-split GEMM with streamed activation
-     * windows (gemm4.hip) */
-    if (a.engine == GEMV_ENGINE_AUTO && a.gps == 0 && a.wfmt == GEMV_W_INT4 && a.M > 16) {
-        const hipError_t e4 = s2p_gemm4_launch(&a, st);
-        if (e4 != hipErrorNotSupported) return e4;
-    }
     if (a.engine != GEMV_ENGINE_SPLITK && a.gps == 0) {
         GemvArgs a3 = a;
         dim3 block;
@@ -375,6 +369,19 @@ extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
         case 7: return gv_launch_mt<GEMV_W_INT8, 7>(a, grid, lds, st);
         default: return gv_launch_mt<GEMV_W_INT8, 8>(a, grid, lds, st);
     }
+}
+
+extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
+    /* INT4 at 16 < M <= 96: the row-split GEMM with streamed activation
+     * windows (gemm4.hip), which writes inv_out itself */
+    if (ap->engine == GEMV_ENGINE_AUTO && ap->gps == 0 && ap->wfmt == GEMV_W_INT4 && ap->M > 16) {
+        const hipError_t e4 = s2p_gemm4_launch(ap, st);
+        if (e4 != hipErrorNotSupported) return e4;
+    }
+    const hipError_t e = gemv_engines(ap, st);
+    if (e != hipSuccess || !ap->inv_out || ap->epi != GEMV_EPI_RESID || !ap->ssq_out) return e;
+    return s2p_g4_rms_launch(ap->ssq_out, (ap->N + 15) / 16, ap->M, ap->N, ap->inv_eps,
+                             ap->inv_out, st);
 }
 
 extern "C" hipError_t s2p_gemv_generic_launch(int fmt, const void* w, const void* sc,

@@ -47,15 +47,22 @@ typedef struct {
     int64_t         part_cap;/* floats available at part */
     unsigned*       counters;/* [ceil(N/64)], zero between calls */
     int             engine;  /* GEMV_ENGINE_AUTO, or GEMV_ENGINE_SPLITK: the split-K engine only */
-    const float*    inv_in;  /* derived (k_gemm4, NORM): the rows' inverse RMS, [M] */
+    const float*    inv_in;  /* NORM (k_gemm4): the rows' inverse RMS, [M], when the producer
+                              * wrote it (NULL: computed here) */
+    float*          inv_out; /* RESID: also write the output rows' inverse RMS, [M] (NULL: no) */
+    float           inv_eps; /* RESID with inv_out: the epsilon of the norm that follows */
 #ifdef S2P_DIAG
     uint64_t*       probe;   /* diagnostics build (whole-K engine): [grid][8] stage clocks */
 #endif
 } GemvArgs;
 
 hipError_t s2p_gemv_launch(const GemvArgs* a, hipStream_t st);
-/* INT4, 16 < M <= 80 (gemm4.hip); hipErrorNotSupported outside that range */
+/* INT4, 16 < M <= 96 (gemm4.hip); hipErrorNotSupported outside that range */
 hipError_t s2p_gemm4_launch(const GemvArgs* a, hipStream_t st);
+/* inv[m] = the rule's inverse RMS of row m < M from per-16-column sums of
+ * squares ssq [blocks][GEMV_MAX_M] of rows of K values (gemm4.hip) */
+hipError_t s2p_g4_rms_launch(const float* ssq, int blocks, int M, int K, float eps, float* inv,
+                             hipStream_t st);
 /* resident-workgroup target the split-K engine plans for (4 per CU) */
 int s2p_gemv_slots(void);
 /* compute units of the current device, queried once per device */

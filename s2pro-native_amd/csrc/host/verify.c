@@ -169,7 +169,9 @@ s2p_status s2p_backbone_create_random(const s2p_backbone_opts* opts, uint64_t se
     if (rc == S2P_OK) rc = dalloc(&b->q, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
     if (rc == S2P_OK) rc = dalloc(&b->attn, R * S2P_Q_HEADS * S2P_HEAD_DIM * 2);
     if (rc == S2P_OK) rc = dalloc(&b->gu, R * 2 * S2P_FFN_DIM * 2);
-    if (rc == S2P_OK) rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M);
+    /* two sums-of-squares buffers, then the two rows' inverse RMS arrays */
+    if (rc == S2P_OK)
+        rc = dalloc((void**)&b->ssq, sizeof(float) * 2 * ((S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M + GEMV_MAX_M));
     b->attn_part_floats = s2p_attn_plan_part_floats((int)R, opts->ctx_len);
     if (b->kvb != 16) {
         const int64_t p8 = s2p_attn8_plan_part_floats((int)R, opts->ctx_len);
@@ -502,11 +504,19 @@ static void gemv_args(GemvArgs* ap, const s2p_linear* lin, int M, const void* x,
     *ap = a;
 }
 
+/* inv_out / inv_in: the output rows' inverse RMS written by a residual GEMV
+ * for the normed GEMV that reads them next (the row-split INT4 GEMM at
+ * 16 < M <= 96 only: elsewhere the consumer computes its own) */
 static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, void* y, int ldy,
                        int xmode, const void* norm_w, const float* ssq_in, int epi, float* ssq_out,
-                       hipStream_t st) {
+                       const float* inv_in, float* inv_out, hipStream_t st) {
     GemvArgs a;
     gemv_args(&a, lin, M, x, ldx, y, ldy, xmode, norm_w, ssq_in, epi, ssq_out);
+    if (M > 16 && M <= 96) {
+        a.inv_in = inv_in;
+        a.inv_out = inv_out;
+        a.inv_eps = NORM_EPS;
+    }
     return hip_ok(s2p_gemv_launch(&a, st), "verify gemv");
 }
 
@@ -622,11 +632,14 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
     const S2pRowPlan plan = row_plan(b);
     float* ssq_a = b->ssq;
     float* ssq_b = b->ssq + (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M;
+    float* inv_a = b->ssq + 2 * (S2P_DIM / GEMV_SSQ_COLS) * GEMV_MAX_M;
+    float* inv_b = inv_a + GEMV_MAX_M;
     S2P_TRY(hip_ok(s2p_resid_init_launch(x_in, b->x, ssq_a, M, S2P_DIM, st), "resid init"));
     for (int l = 0; l < b->o.n_layers; l++) {
         const s2p_slow_layer* L = &b->layers[l];
         S2P_TRY(gemv(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
-                     L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st));
+                     L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, l > 0 ? inv_a : NULL, NULL,
+                     st));
         if (b->kvb != 16) {
             /* quantised caches: prologue + quantise-on-append, then the
              * split attention and its combine */
@@ -654,14 +667,15 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
                                                   NORM_EPS, NULL, st),
                        "attention"));
         S2P_TRY(gemv(&L->wo, M, b->attn, S2P_Q_HEADS * S2P_HEAD_DIM, b->x, S2P_DIM, GEMV_X_PLAIN,
-                     NULL, NULL, GEMV_EPI_RESID, ssq_b, st));
+                     NULL, NULL, GEMV_EPI_RESID, ssq_b, NULL, inv_b, st));
         S2P_TRY(gemv(&L->gate_up, M, b->x, S2P_DIM, b->gu, S2P_FFN_DIM, GEMV_X_NORM,
-                     L->ffn_norm.data, ssq_b, GEMV_EPI_SWIGLU, NULL, st));
+                     L->ffn_norm.data, ssq_b, GEMV_EPI_SWIGLU, NULL, inv_b, NULL, st));
         S2P_TRY(gemv(&L->w2, M, b->gu, S2P_FFN_DIM, b->x, S2P_DIM, GEMV_X_PLAIN, NULL, NULL,
-                     GEMV_EPI_RESID, ssq_a, st));
+                     GEMV_EPI_RESID, ssq_a, NULL, inv_a, st));
     }
     return gemv(&b->head, M, b->x, S2P_DIM, logits, b->head.out_features, GEMV_X_NORM,
-                b->final_norm.data, ssq_a, GEMV_EPI_STORE, NULL, st);
+                b->final_norm.data, ssq_a, GEMV_EPI_STORE, NULL, b->o.n_layers > 0 ? inv_a : NULL,
+                NULL, st);
 }
 
 /* ------------------------------------------------------------ acceptance */
