@@ -581,6 +581,10 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         default: err = g4_launch_mt<6>(b, grid, lds, st); break;
     }
     if (err != hipSuccess) return err;
+    if (ks > 1 && a.deferred && a.epi == GEMV_EPI_STORE) { /* the consumer merges */
+        *a.deferred = ks;
+        return hipSuccess;
+    }
     const bool want_inv = a.inv_out && a.epi == GEMV_EPI_RESID && a.ssq_out;
     if (ks == 1) /* the kernel's epilogue wrote the sums of squares */
         return want_inv ? s2p_g4_rms_launch(a.ssq_out, (a.N + 15) / 16, a.M, a.N, a.inv_eps,

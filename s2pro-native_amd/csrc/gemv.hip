@@ -372,6 +372,7 @@ static hipError_t gemv_engines(const GemvArgs* ap, hipStream_t st) {
 }
 
 extern "C" hipError_t s2p_gemv_launch(const GemvArgs* ap, hipStream_t st) {
+    if (ap->deferred) *ap->deferred = 0; /* merged, unless k_gemm4 defers below */
     /* INT4 at 16 < M <= 96: the row-split GEMM with streamed activation
      * windows (gemm4.hip), which writes inv_out itself */
     if (ap->engine == GEMV_ENGINE_AUTO && ap->gps == 0 && ap->wfmt == GEMV_W_INT4 && ap->M > 16) {

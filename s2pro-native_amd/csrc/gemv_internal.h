@@ -51,6 +51,10 @@ typedef struct {
                               * wrote it (NULL: computed here) */
     float*          inv_out; /* RESID: also write the output rows' inverse RMS, [M] (NULL: no) */
     float           inv_eps; /* RESID with inv_out: the epsilon of the norm that follows */
+    int*            deferred;/* STORE (host pointer, may be NULL): a K-split k_gemm4 launch
+                              * leaves its partials [splits][M][ceil(N/64)][64] in part
+                              * unmerged and stores the split count here, else 0; the
+                              * consumer sums them in split order (the merge's values) */
 #ifdef S2P_DIAG
     uint64_t*       probe;   /* diagnostics build (whole-K engine): [grid][8] stage clocks */
 #endif

@@ -507,17 +507,34 @@ static void gemv_args(GemvArgs* ap, const s2p_linear* lin, int M, const void* x,
 /* inv_out / inv_in: the output rows' inverse RMS written by a residual GEMV
  * for the normed GEMV that reads them next (the row-split INT4 GEMM at
  * 16 < M <= 96 only: elsewhere the consumer computes its own) */
-static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, void* y, int ldy,
-                       int xmode, const void* norm_w, const float* ssq_in, int epi, float* ssq_out,
-                       const float* inv_in, float* inv_out, hipStream_t st) {
+static s2p_status gemv_ex(const s2p_linear* lin, int M, const void* x, int ldx, void* y,
+                          int ldy, int xmode, const void* norm_w, const float* ssq_in, int epi,
+                          float* ssq_out, const float* inv_in, float* inv_out,
+                          S2pQkvParts* parts, hipStream_t st) {
     GemvArgs a;
     gemv_args(&a, lin, M, x, ldx, y, ldy, xmode, norm_w, ssq_in, epi, ssq_out);
+    int deferred = 0;
     if (M > 16 && M <= 96) {
         a.inv_in = inv_in;
         a.inv_out = inv_out;
         a.inv_eps = NORM_EPS;
+        if (parts) a.deferred = &deferred;
     }
-    return hip_ok(s2p_gemv_launch(&a, st), "verify gemv");
+    S2P_TRY(hip_ok(s2p_gemv_launch(&a, st), "verify gemv"));
+    if (parts) {
+        parts->part = a.part;
+        parts->splits = deferred;
+        parts->M = M;
+        parts->nrb = (a.N + 63) / 64;
+    }
+    return S2P_OK;
+}
+
+static s2p_status gemv(const s2p_linear* lin, int M, const void* x, int ldx, void* y, int ldy,
+                       int xmode, const void* norm_w, const float* ssq_in, int epi, float* ssq_out,
+                       const float* inv_in, float* inv_out, hipStream_t st) {
+    return gemv_ex(lin, M, x, ldx, y, ldy, xmode, norm_w, ssq_in, epi, ssq_out, inv_in, inv_out,
+                   NULL, st);
 }
 
 /* Pack the weights into the persistent kernel's tile layout (once per
@@ -637,9 +654,14 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
     S2P_TRY(hip_ok(s2p_resid_init_launch(x_in, b->x, ssq_a, M, S2P_DIM, st), "resid init"));
     for (int l = 0; l < b->o.n_layers; l++) {
         const s2p_slow_layer* L = &b->layers[l];
-        S2P_TRY(gemv(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
-                     L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, l > 0 ? inv_a : NULL, NULL,
-                     st));
+        /* trees over bf16 caches: the qk-norm / RoPE / append kernel merges
+         * wqkv's K-split partials itself (one launch fewer; the fused
+         * attention prologue of the other plans measured slower reading them:
+         * every split's blocks reread the partials) */
+        S2pQkvParts qp = {NULL, 0, 0, 0};
+        S2P_TRY(gemv_ex(&L->wqkv, M, b->x, S2P_DIM, b->qkv, S2P_QKV_WIDTH, GEMV_X_NORM,
+                        L->attn_norm.data, ssq_a, GEMV_EPI_STORE, NULL, l > 0 ? inv_a : NULL,
+                        NULL, b->kvb == 16 && b->tree ? &qp : NULL, st));
         if (b->kvb != 16) {
             /* quantised caches: prologue + quantise-on-append, then the
              * split attention and its combine */
@@ -653,9 +675,9 @@ s2p_status s2p_verify_forward(s2p_backbone* b, const void* x_in, void* logits, h
         } else if (b->tree) {
             /* trees of 9..32 rows: qk-norm + RoPE + append, then one block
              * per (session, kv head, split) */
-            S2P_TRY(hip_ok(s2p_qkrope_append_tab_launch(b->qkv, b->q, L->q_norm.data,
-                                                        L->k_norm.data, &plan, M, l, NORM_EPS,
-                                                        b->d_rope, st),
+            S2P_TRY(hip_ok(s2p_qkrope_append_tab_parts_launch(b->qkv, &qp, b->q, L->q_norm.data,
+                                                              L->k_norm.data, &plan, M, l,
+                                                              NORM_EPS, b->d_rope, st),
                            "qk-norm / rope / append"));
             S2P_TRY(hip_ok(s2p_attn_tree_launch(b->q, b->attn, &plan, b->d_tsegs, b->n_sess, M, b->R,
                                                 l, b->max_span, b->attn_part, b->attn_part_floats, st),

@@ -331,14 +331,15 @@ __global__ __launch_bounds__(64) void k_qkrope_append(const uint16_t* __restrict
 /* the same with (cos, sin) from the plan's RoPE table (bit-identical: the
  * table holds rope_cs of the rows' positions), four (row, head) items a
  * block */
-__global__ __launch_bounds__(256) void k_qkrope_append_tab(const uint16_t* __restrict__ qkv,
+__global__ __launch_bounds__(256) void k_qkrope_append_tab(const uint16_t* qkv,
                                                            uint16_t* __restrict__ q_out,
                                                            const uint16_t* __restrict__ qn_w,
                                                            const uint16_t* __restrict__ kn_w,
                                                            S2pRowPlan plan, int layer, float eps,
-                                                           const float* __restrict__ rope_tab) {
+                                                           const float* __restrict__ rope_tab,
+                                                           S2pQkvParts parts) {
     qkrope_item_t<true>(qkv, q_out, qn_w, kn_w, plan, layer, eps, 0.f, blockIdx.x,
-                        blockIdx.y * 4 + (threadIdx.x >> 6), threadIdx.x & 63, rope_tab);
+                        blockIdx.y * 4 + (threadIdx.x >> 6), threadIdx.x & 63, rope_tab, parts);
 }
 
 extern "C" hipError_t s2p_qkrope_append_tab_launch(const void* qkv, void* q_out, const void* qn_w,
@@ -349,7 +350,22 @@ extern "C" hipError_t s2p_qkrope_append_tab_launch(const void* qkv, void* q_out,
     if (!rope_tab) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_qkrope_append_tab, dim3(rows, 10), dim3(256), 0, st,
                        (const uint16_t*)qkv, (uint16_t*)q_out, (const uint16_t*)qn_w,
-                       (const uint16_t*)kn_w, *plan, layer, eps, rope_tab);
+                       (const uint16_t*)kn_w, *plan, layer, eps, rope_tab,
+                       S2pQkvParts{nullptr, 0, 0, 0});
+    return hipGetLastError();
+}
+
+extern "C" hipError_t s2p_qkrope_append_tab_parts_launch(void* qkv, const S2pQkvParts* parts,
+                                                         void* q_out, const void* qn_w,
+                                                         const void* kn_w, const S2pRowPlan* plan,
+                                                         int rows, int layer, float eps,
+                                                         const float* rope_tab, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (!rope_tab || !parts || (parts->splits > 0 && (!parts->part || parts->M < rows)))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_qkrope_append_tab, dim3(rows, 10), dim3(256), 0, st,
+                       (const uint16_t*)qkv, (uint16_t*)q_out, (const uint16_t*)qn_w,
+                       (const uint16_t*)kn_w, *plan, layer, eps, rope_tab, *parts);
     return hipGetLastError();
 }
 

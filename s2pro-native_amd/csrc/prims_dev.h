@@ -51,21 +51,52 @@ S2P_DEV void qkrope_math(float v0, float v1, uint16_t w0, uint16_t w1, float c0,
     }
 }
 
+/* element n of fused qkv row `row` (the row width is 6144): the merged
+ * bf16 value, from the rows or summed from the deferred partials */
+template <bool COH>
+S2P_DEV uint16_t qkv_elem(const uint16_t* qkv, const S2pQkvParts& p, int row, int n) {
+#pragma clang fp contract(off)
+    if (p.splits > 0) {
+        const float* e = p.part + ((size_t)row * p.nrb + (n >> 6)) * 64 + (n & 63);
+        const size_t stride = (size_t)p.M * p.nrb * 64;
+        float s = 0.f;
+        if (p.splits <= 8) { /* every load in flight before the first add */
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = e[(size_t)min(k, p.splits - 1) * stride];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (k < p.splits) s += v[k];
+        } else {
+            for (int k = 0; k < p.splits; k++) s += e[(size_t)k * stride];
+        }
+        return f2bf(s);
+    }
+    return COH ? coh_ld16(qkv + (size_t)row * 6144 + n) : qkv[(size_t)row * 6144 + n];
+}
+
 /* qk-norm + RoPE of one (row, head) of the fused qkv output, one wave:
  * q heads 0..31 go to q_out, k heads 32..39 (with the matching v head) to
  * the row's KV slot of `layer` (kernels.cu:81-109, 114-168, 172-222). */
 template <bool TAB>
 S2P_DEV void qkrope_item_t(const uint16_t* qkv, uint16_t* q_out, const uint16_t* qn_w,
                            const uint16_t* kn_w, const S2pRowPlan& plan, int layer, float eps,
-                           float base, int row, int head, int lane, const float* rope_tab) {
+                           float base, int row, int head, int lane, const float* rope_tab,
+                           S2pQkvParts parts = S2pQkvParts{nullptr, 0, 0, 0}) {
 #pragma clang fp contract(off)
     const int QH = 32, KVH = 8, HD = 128;
     const int qkv_w = (QH + 2 * KVH) * HD;
     const bool is_q = head < QH;
     const int kh = head - QH;
-    const uint16_t* src = qkv + (size_t)row * qkv_w + (is_q ? head * HD : QH * HD + kh * HD);
+    const int n0 = is_q ? head * HD : QH * HD + kh * HD;
     const uint16_t* nw = is_q ? qn_w : kn_w;
-    const float v0 = bf2f(coh_ld16(src + lane)), v1 = bf2f(coh_ld16(src + lane + 64));
+    const uint16_t r0 = qkv_elem<true>(qkv, parts, row, n0 + lane);
+    const uint16_t r1 = qkv_elem<true>(qkv, parts, row, n0 + lane + 64);
+    if (parts.splits > 0) { /* the merged row, as the merge would have stored it */
+        coh_st16((uint16_t*)qkv + (size_t)row * qkv_w + n0 + lane, r0);
+        coh_st16((uint16_t*)qkv + (size_t)row * qkv_w + n0 + lane + 64, r1);
+    }
+    const float v0 = bf2f(r0), v1 = bf2f(r1);
     /* RoPE: element e = lane + 64*slot, pair e >> 1 */
     float cs[2][2];
 #pragma unroll
@@ -92,9 +123,15 @@ S2P_DEV void qkrope_item_t(const uint16_t* qkv, uint16_t* q_out, const uint16_t*
         uint16_t* vd = kvb + ((size_t)(KVH + kh) * plan.max_seq + slot) * HD;
         coh_st16(kd + lane, f2bf(o[0]));
         coh_st16(kd + lane + 64, f2bf(o[1]));
-        const uint16_t* vs = qkv + (size_t)row * qkv_w + (QH + KVH) * HD + kh * HD;
-        coh_st16(vd + lane, coh_ld16(vs + lane));
-        coh_st16(vd + lane + 64, coh_ld16(vs + lane + 64));
+        const int nv = (QH + KVH) * HD + kh * HD;
+        const uint16_t w0 = qkv_elem<true>(qkv, parts, row, nv + lane);
+        const uint16_t w1 = qkv_elem<true>(qkv, parts, row, nv + lane + 64);
+        if (parts.splits > 0) {
+            coh_st16((uint16_t*)qkv + (size_t)row * qkv_w + nv + lane, w0);
+            coh_st16((uint16_t*)qkv + (size_t)row * qkv_w + nv + lane + 64, w1);
+        }
+        coh_st16(vd + lane, w0);
+        coh_st16(vd + lane + 64, w1);
     }
 }
 

@@ -35,12 +35,28 @@ typedef struct {
     const void* kv; /* the session's KV base (plan.kv[sess]), so the kernel has it at hand */
 } S2pAttnSeg;
 
+/* The fused qkv rows as the wqkv GEMM left them when its K-split merge was
+ * deferred (splits > 0): fp32 partials [splits][M][nrb][64], element (row,
+ * n) at part[((k * M + row) * nrb + n / 64) * 64 + n % 64]; a consumer sums
+ * them in split order from 0 and rounds to bf16 (the merge's value) and
+ * stores the result into the qkv rows as the merge would have.  splits = 0:
+ * the qkv rows hold the merged values. */
+typedef struct {
+    const float* part;
+    int splits, M, nrb;
+} S2pQkvParts;
+
 /* s2p_qkrope_append_launch with (cos, sin) from a RoPE table [rows][64][2]
  * (s2p_rope_tab_launch of the same plan) */
 hipError_t s2p_qkrope_append_tab_launch(const void* qkv, void* q_out, const void* qn_w,
                                         const void* kn_w, const S2pRowPlan* plan, int rows,
                                         int layer, float eps, const float* rope_tab,
                                         hipStream_t st);
+/* the same over the wqkv GEMM's deferred partials (qkv receives the merged rows) */
+hipError_t s2p_qkrope_append_tab_parts_launch(void* qkv, const S2pQkvParts* parts, void* q_out,
+                                              const void* qn_w, const void* kn_w,
+                                              const S2pRowPlan* plan, int rows, int layer,
+                                              float eps, const float* rope_tab, hipStream_t st);
 hipError_t s2p_qkrope_append_launch(const void* qkv, void* q_out, const void* qn_w,
                                     const void* kn_w, const S2pRowPlan* plan, int rows,
                                     int layer, float eps, float base, hipStream_t st);
