@@ -152,7 +152,7 @@ __global__ __launch_bounds__(64 * G4_WAVES) void k_gemm4(GemvArgs a) {
     load_c(b0, c0); /* in flight during the inverse RMS and the first staging */
 
     if (a.xmode == GEMV_X_NORM) {
-        if (a.inv_in) { /* from k_g4_rms, the launch before */
+        if (a.inv_in) { /* written before this launch (the residual producer's merge, or k_g4_rms) */
             if (tid < M) L.inv[tid] = a.inv_in[tid];
         } else {
             for (int m = wave; m < M; m += G4_WAVES) L.inv[m] = g4_inv_rms(a, m, lane);
@@ -590,7 +590,8 @@ extern "C" hipError_t s2p_gemm4_launch(const GemvArgs* ap, hipStream_t st) {
         return want_inv ? s2p_g4_rms_launch(a.ssq_out, (a.N + 15) / 16, a.M, a.N, a.inv_eps,
                                             a.inv_out, st)
                         : hipSuccess;
-    if (want_inv && (a.N & 15) == 0 && a.N / 16 <= G4_RMS_BLOCKS) {
+    if (want_inv && (a.N & 15) == 0 && a.N / 16 <= G4_RMS_BLOCKS && (a.ldy & 3) == 0 &&
+        ((uintptr_t)a.y & 7) == 0) { /* k_g4_merge_rows stores four outputs at once */
         const int nit = a.N >> 2;
         const unsigned th = (unsigned)(nit >= 1024 ? 1024 : ((nit + 63) / 64) * 64);
         hipLaunchKernelGGL(k_g4_merge_rows, dim3((unsigned)a.M), dim3(th), 0, st, b);
