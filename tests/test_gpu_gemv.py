@@ -209,3 +209,24 @@ def test_linear_prepare_site_and_forward(lib):
     exact = po.int4p_gemv_f64(x, po.int4_pack(q_ref, N, K), s_ref, M, N, K)
     assert_close_rel(bf16_vals(to_host(y, np.uint16)), exact, what="prepared linear")
     lib.s2p_linear_free(ctypes_ref(lin))
+
+
+@pytest.mark.parametrize("M,blocks,K", [(68, 160, 2560), (40, 160, 2560), (17, 608, 9728)])
+def test_g4_rms_inverse_rms(lib, M, blocks, K):
+    """k_g4_rms: inv[m] = 1 / sqrt(sum of row m's per-16-column sums of
+    squares / K + eps), from the [blocks][128] layout the residual epilogues
+    write; against binary64 (the float sums differ only in their order)."""
+    r = np.random.default_rng(M + blocks)
+    ssq = np.zeros((blocks, 128), np.float32)
+    ssq[:, :M] = (r.random((blocks, M)) * 16.0).astype(np.float32)
+    ssq[:, 1] = 0.0  # a row of zeros: inv = 1 / sqrt(eps)
+    eps = 1e-6
+    inv = empty((M,), dtype=torch.float32)
+    fn = lib.s2p_g4_rms_launch
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                   ctypes.c_void_p, ctypes.c_void_p]
+    s2pamd.hip_check(fn(P(to_dev(ssq)), blocks, M, K, eps, P(inv), S()))
+    got = to_host(inv, np.float32).astype(np.float64)
+    exact = 1.0 / np.sqrt(ssq[:, :M].astype(np.float64).sum(axis=0) / K + eps)
+    assert np.all(np.abs(got - exact) <= 2e-6 * exact), np.max(np.abs(got - exact) / exact)
